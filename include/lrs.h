@@ -1,0 +1,134 @@
+/*
+ * lrs.h — C ABI of the MI355X (gfx950) batch-1 decode hot path of llama.rs.
+ *
+ * This is the drop-in boundary: a thin Rust `extern "C"` crate implements the
+ * reference's `llama_model::GpuMatmul` and `llama_model::GpuResidentDecode`
+ * traits on top of these calls.  All arguments are plain
+ * pointers and sizes; no HIP or torch type crosses the boundary.
+ *
+ * Conventions (mirroring the reference's error and ownership rules):
+ *  - Every call returns LRS_OK (0) or a negative LRS_E_* code; the message is
+ *    in lrs_last_error() (thread-local), which the Rust shim maps to
+ *    ModelError::Gpu(String) (crates/llama-model/src/error.rs:26-27).
+ *  - Weight bytes are borrowed only for the duration of the upload call and
+ *    copied to device memory; the caller may drop them afterwards
+ *    (crates/llama-vulkan/src/resident_forward.rs:1298-1299).
+ *  - Calls are synchronous unless named *_dev (those enqueue on the context's
+ *    stream and return at once) and are not re-entrant per context/model
+ *    (the reference backend is !Sync, resident_forward.rs:797, 835-854).
+ *  - GGUF type ids are those of crates/gguf/src/types.rs:84-107:
+ *    F32=0 F16=1 Q8_0=8 Q4_K=12 Q5_K=13 Q6_K=14.
+ */
+#ifndef LRS_H
+#define LRS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LRS_OK 0
+#define LRS_E_ARG (-1)          /* bad argument / shape (gpu.rs:149-164 checks) */
+#define LRS_E_HIP (-2)          /* HIP runtime error */
+#define LRS_E_OOM (-3)          /* device allocation failed */
+#define LRS_E_CTX_OVERFLOW (-4) /* KV cache full (attention.rs:36-40) */
+#define LRS_E_UNSUPPORTED (-5)  /* type / shape not supported */
+
+#define LRS_TYPE_F32 0u
+#define LRS_TYPE_F16 1u
+#define LRS_TYPE_Q8_0 8u
+#define LRS_TYPE_Q4_K 12u
+#define LRS_TYPE_Q5_K 13u
+#define LRS_TYPE_Q6_K 14u
+
+typedef struct lrs_ctx lrs_ctx;
+typedef struct lrs_weight lrs_weight;
+typedef struct lrs_model lrs_model;
+
+/* Message of the last failed call on this thread ("" if none).
+ * Replaces the String inside ModelError::Gpu (error.rs:26-27). */
+const char *lrs_last_error(void);
+
+/* Library version string, e.g. "lrs 0.1 gfx950". */
+const char *lrs_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* context                                                                  */
+/* ------------------------------------------------------------------------ */
+/* Opens a device and a stream.  device = -1 picks the device with the most
+ * free HBM, like pick_device (resident_forward.rs:1119-1133).
+ * Replaces VulkanContext::new + VulkanDevice::create (device.rs). */
+int lrs_ctx_create(int device, lrs_ctx **out);
+void lrs_ctx_destroy(lrs_ctx *ctx);
+/* Blocks until all work enqueued on the context's stream has finished. */
+int lrs_ctx_sync(lrs_ctx *ctx);
+/* Free / total HBM of the context's device, bytes. */
+int lrs_ctx_mem_info(lrs_ctx *ctx, size_t *free_bytes, size_t *total_bytes);
+
+/* ------------------------------------------------------------------------ */
+/* weights (QTensor / GpuRawWeights, crates/llama-model/src/gpu.rs:13-17,    */
+/* 128-248; upload = Uploader::tensor, llama-vulkan/src/tensor.rs:555-598)   */
+/* ------------------------------------------------------------------------ */
+/* Copies an n_out x n_in GGUF tensor (row-major blocks, len bytes) to HBM,
+ * repacking it to the device layout.  Types: Q8_0, Q4_K, Q5_K, Q6_K, F32, F16.
+ * Fails with LRS_E_ARG when n_in is not a multiple of the block size or len
+ * != n_out * n_in / block * type_size (gpu.rs:149-164). */
+int lrs_weight_upload(lrs_ctx *ctx, uint32_t ggml_type, const void *bytes, size_t len,
+                      uint32_t n_in, uint32_t n_out, lrs_weight **out);
+/* Fills an n_out x n_in tensor on the device with the library's seeded
+ * synthetic blocks (counter-based hash of (seed, block, byte); mode 0 = the
+ * benchmark distributions, 1 = zero-mean K-quants; f16 scales uniform in
+ * [d_lo, d_hi)).  Used for random-init models too large to build on the host.
+ * No reference counterpart: the reference loads weights from GGUF files. */
+int lrs_weight_generate(lrs_ctx *ctx, uint32_t ggml_type, uint64_t seed, int mode,
+                        float d_lo, float d_hi, uint32_t n_in, uint32_t n_out,
+                        lrs_weight **out);
+/* Copies a weight back to the host in GGUF byte layout (len must equal the
+ * GGUF size).  For round-trip checks. */
+int lrs_weight_download(lrs_ctx *ctx, const lrs_weight *w, void *dst, size_t len);
+/* GGUF bytes of the tensor (the algorithmic bytes one matvec reads). */
+size_t lrs_weight_gguf_bytes(const lrs_weight *w);
+void lrs_weight_free(lrs_weight *w);
+
+/* ------------------------------------------------------------------------ */
+/* kernel level                                                             */
+/* ------------------------------------------------------------------------ */
+/* ggml_cpu::dequant_to_f32 on the GPU (crates/ggml-cpu/src/dequant.rs:10-21),
+ * bit-exact: host GGUF bytes in, host f32 out (len/type_size*block floats). */
+int lrs_dequant_f32(lrs_ctx *ctx, uint32_t ggml_type, const void *bytes, size_t len,
+                    float *out);
+/* Dequantizes a resident weight to a device f32 buffer [n_out*n_in]. */
+int lrs_weight_dequant_dev(lrs_ctx *ctx, const lrs_weight *w, float *out_dev);
+
+/* y = W x for `cols` columns: x [cols*n_in] host f32, y [cols*n_out] host f32.
+ * GpuMatmul::matvec_q8_0 (crates/llama-model/src/gpu.rs:1057-1065) generalised
+ * to every resident type, and matmul::dispatch_{q8_0,q4_k,q5_k,q6_k}_matvec
+ * (crates/llama-vulkan/src/matmul.rs:36-430).  Activations stay f32 (no int8
+ * activation quantization).  Blocking. */
+int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y,
+                   uint32_t cols);
+/* Same on device buffers, enqueued on the context stream (async). */
+int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
+                   uint32_t cols);
+
+/* Matvec launch geometry override: lanes_per_row in {16,32,64}, rows per
+ * lane group in {1,2,4}, waves per workgroup in {1,2,4}; all 0 = automatic.
+ * Replaces the LLAMA_RS_MATVEC_GEOM knob (resident_forward.rs:164-176); the
+ * LRS_MATVEC_GEOM="lpr,rows,waves" environment variable sets the initial value. */
+int lrs_matvec_set_geom(int lanes_per_row, int rows, int waves);
+
+/* device memory + timing helpers for callers that keep buffers resident */
+int lrs_dev_alloc(lrs_ctx *ctx, size_t bytes, void **dptr);
+int lrs_dev_free(lrs_ctx *ctx, void *dptr);
+int lrs_copy_h2d(lrs_ctx *ctx, void *dst_dev, const void *src, size_t bytes);
+int lrs_copy_d2h(lrs_ctx *ctx, void *dst, const void *src_dev, size_t bytes);
+/* HIP events on the context stream: start, then stop returns elapsed ms. */
+int lrs_timer_start(lrs_ctx *ctx);
+int lrs_timer_stop(lrs_ctx *ctx, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

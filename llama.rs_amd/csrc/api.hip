@@ -1,0 +1,382 @@
+// api.hip — the extern "C" boundary of liblrs.so (declared in include/lrs.h).
+#include "lrs_internal.h"
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+namespace lrs {
+
+static thread_local std::string g_err;
+
+void set_error(const std::string &msg) { g_err = msg; }
+
+int fail(int code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    g_err = std::string("HIP error: ") + hipGetErrorString(e) + " in " + what;
+    return e == hipErrorOutOfMemory ? LRS_E_OOM : LRS_E_HIP;
+}
+
+// geometry check of gpu.rs:149-164: n_in multiple of the block, byte count
+static int check_shape(uint32_t t, size_t len, uint32_t n_in, uint32_t n_out, bool need_len) {
+    const int64_t be = block_elems(t), bb = block_bytes(t);
+    if (be < 0) return fail(LRS_E_UNSUPPORTED, "unsupported ggml type " + std::to_string(t));
+    if (n_in == 0 || n_out == 0) return fail(LRS_E_ARG, "empty tensor");
+    if (n_in % (uint32_t)be != 0)
+        return fail(LRS_E_ARG, "n_in=" + std::to_string(n_in) + " is not a multiple of the block size " +
+                                   std::to_string(be));
+    const size_t want = (size_t)(n_in / be) * (size_t)bb * n_out;
+    if (need_len && len != want)
+        return fail(LRS_E_ARG, "tensor has " + std::to_string(len) + " bytes, expected " +
+                                   std::to_string(want) + " for " + std::to_string(n_out) + "x" +
+                                   std::to_string(n_in));
+    return LRS_OK;
+}
+
+static int alloc_weight(lrs_ctx *ctx, uint32_t t, uint32_t n_in, uint32_t n_out, lrs_weight **out) {
+    lrs_weight *w = new lrs_weight();
+    w->ctx = ctx;
+    w->v.type = t;
+    w->v.n_in = n_in;
+    w->v.n_out = n_out;
+    w->v.nb = n_in / (uint32_t)block_elems(t);
+    const size_t nblk = (size_t)w->v.nb * n_out;
+    w->q_alloc = nblk * q_bytes_per_block(t);
+    w->d_alloc = has_d_array(t) ? nblk * 2 : 0;
+    hipError_t e = hipMalloc(&w->q, w->q_alloc);
+    if (e == hipSuccess && w->d_alloc) e = hipMalloc(&w->d, w->d_alloc);
+    if (e != hipSuccess) {
+        if (w->q) (void)hipFree(w->q);
+        delete w;
+        return hip_fail(e, "hipMalloc(weight)");
+    }
+    w->v.q = w->q;
+    w->v.d = w->d;
+    *out = w;
+    return LRS_OK;
+}
+
+}  // namespace lrs
+
+using namespace lrs;
+
+// per-context device scratch for the blocking host-buffer entry points
+struct lrs_ctx_scratch {
+    void *p = nullptr;
+    size_t n = 0;
+};
+static std::mutex g_scratch_mu;
+static std::unordered_map<lrs_ctx *, lrs_ctx_scratch> g_scratch;
+
+namespace lrs {
+static hipError_t scratch(lrs_ctx *ctx, size_t bytes, void **p) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    lrs_ctx_scratch &s = g_scratch[ctx];
+    if (s.n < bytes) {
+        if (s.p) {
+            hipError_t e = hipStreamSynchronize(ctx->stream);
+            if (e != hipSuccess) return e;
+            (void)hipFree(s.p);
+            s.p = nullptr;
+            s.n = 0;
+        }
+        size_t n = bytes < (1u << 20) ? (1u << 20) : bytes;
+        hipError_t e = hipMalloc(&s.p, n);
+        if (e != hipSuccess) return e;
+        s.n = n;
+    }
+    *p = s.p;
+    return hipSuccess;
+}
+}  // namespace lrs
+
+#define SETDEV(ctx) LRS_HIP(hipSetDevice((ctx)->device))
+
+extern "C" {
+
+const char *lrs_last_error(void) { return g_err.c_str(); }
+
+const char *lrs_version(void) { return "lrs 0.1 gfx950"; }
+
+int lrs_ctx_create(int device, lrs_ctx **out) {
+    if (!out) return fail(LRS_E_ARG, "null out");
+    int n = 0;
+    LRS_HIP(hipGetDeviceCount(&n));
+    if (n == 0) return fail(LRS_E_HIP, "no HIP device");
+    if (device < 0) {
+        size_t best = 0;
+        device = 0;
+        for (int i = 0; i < n; i++) {
+            size_t fr = 0, tot = 0;
+            if (hipSetDevice(i) == hipSuccess && hipMemGetInfo(&fr, &tot) == hipSuccess && fr > best) {
+                best = fr;
+                device = i;
+            }
+        }
+    }
+    if (device >= n) return fail(LRS_E_ARG, "device " + std::to_string(device) + " out of range");
+    LRS_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    LRS_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(LRS_E_UNSUPPORTED, std::string("liblrs is built for gfx950, device is ") +
+                                           prop.gcnArchName);
+    lrs_ctx *c = new lrs_ctx();
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&c->ev0);
+    if (e == hipSuccess) e = hipEventCreate(&c->ev1);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "stream/event create");
+    }
+    *out = c;
+    return LRS_OK;
+}
+
+void lrs_ctx_destroy(lrs_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        auto it = g_scratch.find(ctx);
+        if (it != g_scratch.end()) {
+            if (it->second.p) (void)hipFree(it->second.p);
+            g_scratch.erase(it);
+        }
+    }
+    (void)hipEventDestroy(ctx->ev0);
+    (void)hipEventDestroy(ctx->ev1);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+int lrs_ctx_sync(lrs_ctx *ctx) {
+    if (!ctx) return fail(LRS_E_ARG, "null ctx");
+    SETDEV(ctx);
+    LRS_HIP(hipStreamSynchronize(ctx->stream));
+    return LRS_OK;
+}
+
+int lrs_ctx_mem_info(lrs_ctx *ctx, size_t *free_bytes, size_t *total_bytes) {
+    if (!ctx) return fail(LRS_E_ARG, "null ctx");
+    SETDEV(ctx);
+    size_t f = 0, t = 0;
+    LRS_HIP(hipMemGetInfo(&f, &t));
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return LRS_OK;
+}
+
+int lrs_weight_upload(lrs_ctx *ctx, uint32_t t, const void *bytes, size_t len, uint32_t n_in,
+                      uint32_t n_out, lrs_weight **out) {
+    if (!ctx || !bytes || !out) return fail(LRS_E_ARG, "null argument");
+    int rc = check_shape(t, len, n_in, n_out, true);
+    if (rc) return rc;
+    SETDEV(ctx);
+    lrs_weight *w = nullptr;
+    rc = alloc_weight(ctx, t, n_in, n_out, &w);
+    if (rc) return rc;
+    hipError_t e;
+    if (!has_d_array(t)) {
+        e = hipMemcpyAsync(w->q, bytes, len, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    } else {
+        uint8_t *tmp = nullptr;
+        e = hipMalloc(&tmp, len);
+        if (e == hipSuccess) e = hipMemcpyAsync(tmp, bytes, len, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = launch_repack_from_gguf(tmp, w->v, w->q, w->d, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (tmp) (void)hipFree(tmp);
+    }
+    if (e != hipSuccess) {
+        lrs_weight_free(w);
+        return hip_fail(e, "weight upload");
+    }
+    *out = w;
+    return LRS_OK;
+}
+
+int lrs_weight_generate(lrs_ctx *ctx, uint32_t t, uint64_t seed, int mode, float d_lo, float d_hi,
+                        uint32_t n_in, uint32_t n_out, lrs_weight **out) {
+    if (!ctx || !out) return fail(LRS_E_ARG, "null argument");
+    if (t != T_Q8_0 && t != T_Q4_K && t != T_Q5_K && t != T_Q6_K)
+        return fail(LRS_E_UNSUPPORTED, "synthetic blocks exist for Q8_0/Q4_K/Q5_K/Q6_K only");
+    int rc = check_shape(t, 0, n_in, n_out, false);
+    if (rc) return rc;
+    SETDEV(ctx);
+    lrs_weight *w = nullptr;
+    rc = alloc_weight(ctx, t, n_in, n_out, &w);
+    if (rc) return rc;
+    hipError_t e = launch_generate(w->v, w->q, w->d, seed, mode, d_lo, d_hi, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        lrs_weight_free(w);
+        return hip_fail(e, "weight generate");
+    }
+    *out = w;
+    return LRS_OK;
+}
+
+size_t lrs_weight_gguf_bytes(const lrs_weight *w) {
+    if (!w) return 0;
+    return (size_t)w->v.nb * w->v.n_out * (size_t)block_bytes(w->v.type);
+}
+
+int lrs_weight_download(lrs_ctx *ctx, const lrs_weight *w, void *dst, size_t len) {
+    if (!ctx || !w || !dst) return fail(LRS_E_ARG, "null argument");
+    if (len != lrs_weight_gguf_bytes(w)) return fail(LRS_E_ARG, "download size mismatch");
+    SETDEV(ctx);
+    if (!has_d_array(w->v.type)) {
+        LRS_HIP(hipMemcpyAsync(dst, w->q, len, hipMemcpyDeviceToHost, ctx->stream));
+        LRS_HIP(hipStreamSynchronize(ctx->stream));
+        return LRS_OK;
+    }
+    uint8_t *tmp = nullptr;
+    LRS_HIP(hipMalloc(&tmp, len));
+    hipError_t e = launch_repack_to_gguf(w->v, tmp, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, tmp, len, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(tmp);
+    if (e != hipSuccess) return hip_fail(e, "weight download");
+    return LRS_OK;
+}
+
+void lrs_weight_free(lrs_weight *w) {
+    if (!w) return;
+    (void)hipSetDevice(w->ctx->device);
+    (void)hipStreamSynchronize(w->ctx->stream);
+    if (w->q) (void)hipFree(w->q);
+    if (w->d) (void)hipFree(w->d);
+    delete w;
+}
+
+int lrs_dequant_f32(lrs_ctx *ctx, uint32_t t, const void *bytes, size_t len, float *out) {
+    if (!ctx || !bytes || !out) return fail(LRS_E_ARG, "null argument");
+    const int64_t be = block_elems(t), bb = block_bytes(t);
+    if (be < 0) return fail(LRS_E_UNSUPPORTED, "unsupported ggml type " + std::to_string(t));
+    if (len == 0 || len % (size_t)bb != 0)
+        return fail(LRS_E_ARG, "byte count " + std::to_string(len) + " is not a multiple of the block size " +
+                                   std::to_string(bb));
+    const size_t nblk = len / (size_t)bb;
+    if (nblk * (size_t)be > 0xFFFFFFFFull) return fail(LRS_E_ARG, "tensor too large for one call");
+    lrs_weight *w = nullptr;
+    int rc = lrs_weight_upload(ctx, t, bytes, len, (uint32_t)(nblk * be), 1, &w);
+    if (rc) return rc;
+    float *dev = nullptr;
+    hipError_t e = hipMalloc(&dev, nblk * be * sizeof(float));
+    if (e == hipSuccess) e = launch_dequant(w->v, dev, ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(out, dev, nblk * be * sizeof(float), hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (dev) (void)hipFree(dev);
+    lrs_weight_free(w);
+    if (e != hipSuccess) return hip_fail(e, "dequant");
+    return LRS_OK;
+}
+
+int lrs_weight_dequant_dev(lrs_ctx *ctx, const lrs_weight *w, float *out_dev) {
+    if (!ctx || !w || !out_dev) return fail(LRS_E_ARG, "null argument");
+    SETDEV(ctx);
+    LRS_HIP(launch_dequant(w->v, out_dev, ctx->stream));
+    return LRS_OK;
+}
+
+static int matvec_check(const lrs_weight *w, uint32_t cols) {
+    if (cols == 0) return fail(LRS_E_ARG, "cols must be >= 1");
+    const uint32_t t = w->v.type;
+    if (t != T_Q8_0 && t != T_Q4_K && t != T_Q5_K && t != T_Q6_K)
+        return fail(LRS_E_UNSUPPORTED, "matvec supports Q8_0/Q4_K/Q5_K/Q6_K weights");
+    return LRS_OK;
+}
+
+int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
+                   uint32_t cols) {
+    if (!ctx || !w || !x_dev || !y_dev) return fail(LRS_E_ARG, "null argument");
+    int rc = matvec_check(w, cols);
+    if (rc) return rc;
+    SETDEV(ctx);
+    LRS_HIP(launch_matvec(w->v, x_dev, y_dev, cols, nullptr, ctx->stream));
+    return LRS_OK;
+}
+
+int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y, uint32_t cols) {
+    if (!ctx || !w || !x || !y) return fail(LRS_E_ARG, "null argument");
+    int rc = matvec_check(w, cols);
+    if (rc) return rc;
+    SETDEV(ctx);
+    const size_t xb = (size_t)cols * w->v.n_in * sizeof(float);
+    const size_t yb = (size_t)cols * w->v.n_out * sizeof(float);
+    void *buf = nullptr;
+    LRS_HIP(scratch(ctx, xb + yb + 256, &buf));
+    float *xd = (float *)buf;
+    float *yd = (float *)((char *)buf + ((xb + 255) & ~(size_t)255));
+    LRS_HIP(hipMemcpyAsync(xd, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    LRS_HIP(launch_matvec(w->v, xd, yd, cols, nullptr, ctx->stream));
+    LRS_HIP(hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
+    LRS_HIP(hipStreamSynchronize(ctx->stream));
+    return LRS_OK;
+}
+
+int lrs_matvec_set_geom(int lanes_per_row, int rows, int waves) {
+    if (set_matvec_geom(lanes_per_row, rows, waves) != 0)
+        return fail(LRS_E_ARG, "geometry must be lanes_per_row in {16,32,64}, rows in {1,2,4}, "
+                               "waves in {1,2,4} (or all 0)");
+    return LRS_OK;
+}
+
+int lrs_dev_alloc(lrs_ctx *ctx, size_t bytes, void **dptr) {
+    if (!ctx || !dptr) return fail(LRS_E_ARG, "null argument");
+    SETDEV(ctx);
+    LRS_HIP(hipMalloc(dptr, bytes ? bytes : 1));
+    return LRS_OK;
+}
+
+int lrs_dev_free(lrs_ctx *ctx, void *dptr) {
+    if (!ctx) return fail(LRS_E_ARG, "null ctx");
+    SETDEV(ctx);
+    LRS_HIP(hipStreamSynchronize(ctx->stream));
+    if (dptr) LRS_HIP(hipFree(dptr));
+    return LRS_OK;
+}
+
+int lrs_copy_h2d(lrs_ctx *ctx, void *dst_dev, const void *src, size_t bytes) {
+    if (!ctx || (bytes && (!dst_dev || !src))) return fail(LRS_E_ARG, "null argument");
+    SETDEV(ctx);
+    LRS_HIP(hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    LRS_HIP(hipStreamSynchronize(ctx->stream));
+    return LRS_OK;
+}
+
+int lrs_copy_d2h(lrs_ctx *ctx, void *dst, const void *src_dev, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src_dev))) return fail(LRS_E_ARG, "null argument");
+    SETDEV(ctx);
+    LRS_HIP(hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    LRS_HIP(hipStreamSynchronize(ctx->stream));
+    return LRS_OK;
+}
+
+int lrs_timer_start(lrs_ctx *ctx) {
+    if (!ctx) return fail(LRS_E_ARG, "null ctx");
+    SETDEV(ctx);
+    LRS_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+    return LRS_OK;
+}
+
+int lrs_timer_stop(lrs_ctx *ctx, float *ms) {
+    if (!ctx || !ms) return fail(LRS_E_ARG, "null argument");
+    SETDEV(ctx);
+    LRS_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+    LRS_HIP(hipEventSynchronize(ctx->ev1));
+    LRS_HIP(hipEventElapsedTime(ms, ctx->ev0, ctx->ev1));
+    return LRS_OK;
+}
+
+}  // extern "C"

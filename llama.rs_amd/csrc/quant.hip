@@ -1,0 +1,316 @@
+// quant.hip — device-layout repack, seeded synthetic blocks and bit-exact
+// dequant for the GGUF block types on the decode path (gfx950).
+//
+// Dequant follows ggml_cpu::dequant_to_f32 (crates/ggml-cpu/src/dequant.rs:
+// 58-258) element by element with the same f32 operation order; the library
+// is compiled with -ffp-contract=off, so d1*q - m1 rounds twice as in Rust.
+#include "lrs_internal.h"
+
+namespace lrs {
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+
+__device__ __forceinline__ uint16_t rd16(const uint8_t *p) {
+    return (uint16_t)(p[0] | ((uint16_t)p[1] << 8));
+}
+
+// ---------------------------------------------------------------------------
+// GGUF byte offset of byte `i` of the device q-part of a block
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t q_to_gguf_off(uint32_t t, uint32_t i) {
+    return t == T_Q8_0 ? i + 2 : i;  // Q6_K q-part = GGUF bytes 0..207
+}
+
+// repack: one thread per q-part byte / per d entry
+__global__ void k_repack_from_gguf(const uint8_t *__restrict__ g, uint32_t t, uint64_t n_blocks,
+                                   uint8_t *__restrict__ q, uint16_t *__restrict__ d) {
+    const uint32_t qb = (uint32_t)q_bytes_per_block(t), gb = (uint32_t)block_bytes(t);
+    const uint64_t nq = n_blocks * qb;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nq;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t b = i / qb;
+        uint32_t o = (uint32_t)(i - b * qb);
+        q[i] = g[b * gb + q_to_gguf_off(t, o)];
+    }
+    if (d) {
+        const uint32_t doff = t == T_Q6_K ? 208 : 0;
+        for (uint64_t b = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < n_blocks;
+             b += (uint64_t)gridDim.x * blockDim.x)
+            d[b] = rd16(g + b * gb + doff);
+    }
+}
+
+__global__ void k_repack_to_gguf(const uint8_t *__restrict__ q, const uint16_t *__restrict__ d,
+                                 uint32_t t, uint64_t n_blocks, uint8_t *__restrict__ g) {
+    const uint32_t qb = (uint32_t)q_bytes_per_block(t), gb = (uint32_t)block_bytes(t);
+    const uint64_t nq = n_blocks * qb;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nq;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t b = i / qb;
+        uint32_t o = (uint32_t)(i - b * qb);
+        g[b * gb + q_to_gguf_off(t, o)] = q[i];
+    }
+    if (d) {
+        const uint32_t doff = t == T_Q6_K ? 208 : 0;
+        for (uint64_t b = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < n_blocks;
+             b += (uint64_t)gridDim.x * blockDim.x) {
+            g[b * gb + doff] = (uint8_t)(d[b] & 0xFF);
+            g[b * gb + doff + 1] = (uint8_t)(d[b] >> 8);
+        }
+    }
+}
+
+static unsigned grid_for(uint64_t n, unsigned bs) {
+    uint64_t g = (n + bs - 1) / bs;
+    if (g > 65536u * 4u) g = 65536u * 4u;
+    if (g == 0) g = 1;
+    return (unsigned)g;
+}
+
+hipError_t launch_repack_from_gguf(const uint8_t *gguf_dev, WeightView w, uint8_t *q, uint16_t *d,
+                                   hipStream_t s) {
+    uint64_t nblk = (uint64_t)w.n_out * w.nb;
+    uint64_t n = nblk * q_bytes_per_block(w.type);
+    hipLaunchKernelGGL(k_repack_from_gguf, dim3(grid_for(n, 256)), dim3(256), 0, s, gguf_dev,
+                       w.type, nblk, q, has_d_array(w.type) ? d : nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_to_gguf(WeightView w, uint8_t *gguf_dev, hipStream_t s) {
+    uint64_t nblk = (uint64_t)w.n_out * w.nb;
+    uint64_t n = nblk * q_bytes_per_block(w.type);
+    hipLaunchKernelGGL(k_repack_to_gguf, dim3(grid_for(n, 256)), dim3(256), 0, s, w.q, w.d,
+                       w.type, nblk, gguf_dev);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// seeded synthetic blocks: the same counter-based hash and field rules as the
+// host generator, so any block can be regenerated bit-identically on the CPU
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t hsh(uint64_t seed, uint64_t blk, uint32_t j) {
+    return mix64(seed * 0x9E3779B97F4A7C15ULL + blk * 0xD1B54A32D192ED03ULL +
+                 (uint64_t)j * 0x8CB92BA72F3D8DD7ULL + 0x2545F4914F6CDD1DULL);
+}
+__device__ __forceinline__ float h_unif(uint64_t h, float lo, float hi) {
+    float u = __fmul_rn((float)(uint32_t)(h >> 40), 1.0f / 16777216.0f);
+    float span = __fsub_rn(hi, lo);
+    return __fadd_rn(lo, __fmul_rn(span, u));
+}
+// binary16 round-to-nearest-even narrowing, integer-only
+__device__ __forceinline__ uint16_t f2h_rne(float f) {
+    uint32_t x = __float_as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u, exp = (x >> 23) & 0xFFu, man = x & 0x7FFFFFu;
+    if (exp == 0xFF) return (uint16_t)(sign | (man ? (0x7E00u | (man >> 13)) : 0x7C00u));
+    int32_t e = (int32_t)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        uint32_t m = man | 0x800000u, sh = (uint32_t)(14 - e);
+        uint32_t q = m >> sh, rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (man >> 13), rem = man & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+__device__ __forceinline__ uint8_t hbyte(uint64_t h) { return (uint8_t)(h >> 56); }
+
+__device__ uint16_t gen_d16(uint32_t t, uint64_t seed, uint64_t blk, int mode, float lo, float hi,
+                            bool is_min) {
+    if (t == T_Q6_K) return f2h_rne(h_unif(hsh(seed, blk, 208), lo, hi));
+    if (!is_min) return f2h_rne(h_unif(hsh(seed, blk, 0), lo, hi));
+    if (mode == 1) {
+        float d = h2f(f2h_rne(h_unif(hsh(seed, blk, 0), lo, hi)));
+        return f2h_rne(__fmul_rn(d, t == T_Q4_K ? 7.5f : 15.5f));
+    }
+    return f2h_rne(h_unif(hsh(seed, blk, 1), lo, hi));
+}
+
+// GGUF byte `o` of synthetic block `blk`
+__device__ uint8_t gen_byte(uint32_t t, uint64_t seed, uint64_t blk, uint32_t o, int mode,
+                            float lo, float hi) {
+    switch (t) {
+    case T_Q8_0: {
+        if (o < 2) {
+            uint16_t v = gen_d16(t, seed, blk, mode, lo, hi, false);
+            return (uint8_t)(o == 0 ? (v & 0xFF) : (v >> 8));
+        }
+        uint64_t h = hsh(seed, blk, o - 1);
+        int q = (int)(((h >> 32) * 255ULL) >> 32) - 127;
+        return (uint8_t)(int8_t)q;
+    }
+    case T_Q4_K:
+    case T_Q5_K: {
+        if (o < 4) {
+            uint16_t v = gen_d16(t, seed, blk, mode, lo, hi, o >= 2);
+            return (uint8_t)((o & 1) ? (v >> 8) : (v & 0xFF));
+        }
+        if (o < 16 && mode == 1) {
+            // packed 6-bit scales with mins equal to scales
+            uint32_t k = o - 4;  // 0..11
+            auto sc = [&](uint32_t j) { return (uint32_t)(hbyte(hsh(seed, blk, 4 + j)) & 63); };
+            if (k < 4) return (uint8_t)((sc(k) & 63) | ((sc(k + 4) >> 4) << 6));
+            if (k < 8) return (uint8_t)((sc(k - 4) & 63) | ((sc(k) >> 4) << 6));
+            uint32_t j = k - 8;
+            return (uint8_t)((sc(j + 4) & 15) | ((sc(j + 4) & 15) << 4));
+        }
+        return hbyte(hsh(seed, blk, o));
+    }
+    case T_Q6_K: {
+        if (o < 192) return hbyte(hsh(seed, blk, o));
+        if (o < 208) return (uint8_t)(int8_t)((int)(hsh(seed, blk, o) >> 57) - 64);
+        uint16_t v = gen_d16(t, seed, blk, mode, lo, hi, false);
+        return (uint8_t)(o == 208 ? (v & 0xFF) : (v >> 8));
+    }
+    default:
+        return 0;
+    }
+}
+
+__global__ void k_generate(uint32_t t, uint64_t n_blocks, uint64_t seed, int mode, float lo,
+                           float hi, uint8_t *__restrict__ q, uint16_t *__restrict__ d) {
+    const uint32_t qb = (uint32_t)q_bytes_per_block(t);
+    const uint64_t nw = n_blocks * qb / 4;  // q-part sizes are multiples of 4 bytes
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nw;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t byte = i * 4;
+        uint64_t b = byte / qb;
+        uint32_t o = (uint32_t)(byte - b * qb);
+        uint32_t v = 0;
+        for (int k = 0; k < 4; k++)
+            v |= (uint32_t)gen_byte(t, seed, b, q_to_gguf_off(t, o + k), mode, lo, hi) << (8 * k);
+        reinterpret_cast<uint32_t *>(q)[i] = v;
+    }
+    if (d) {
+        for (uint64_t b = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < n_blocks;
+             b += (uint64_t)gridDim.x * blockDim.x)
+            d[b] = gen_d16(t, seed, b, mode, lo, hi, false);
+    }
+}
+
+hipError_t launch_generate(WeightView w, uint8_t *q, uint16_t *d, uint64_t seed, int mode,
+                           float d_lo, float d_hi, hipStream_t s) {
+    uint64_t nblk = (uint64_t)w.n_out * w.nb;
+    uint64_t n = nblk * q_bytes_per_block(w.type) / 4;
+    hipLaunchKernelGGL(k_generate, dim3(grid_for(n, 256)), dim3(256), 0, s, w.type, nblk, seed,
+                       mode, d_lo, d_hi, q, has_d_array(w.type) ? d : nullptr);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// dequant (bit-exact with dequant.rs)
+// ---------------------------------------------------------------------------
+// K-quant 6-bit (scale, min) of sub-block j: dequant.rs:101-110
+__device__ __forceinline__ void scale_min_k4(uint32_t j, const uint8_t *s, uint32_t &sc,
+                                             uint32_t &m) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+// element e (0..255) of block b of a resident weight
+__device__ __forceinline__ float deq_elem(const WeightView &w, uint64_t b, uint32_t e) {
+    switch (w.type) {
+    case T_Q8_0: {
+        // dequant.rs:58-76
+        const uint8_t *qs = w.q + b * Q8_QBYTES;
+        return __fmul_rn((float)(int8_t)qs[e], h2f(w.d[b]));
+    }
+    case T_Q4_K:
+    case T_Q5_K: {
+        // dequant.rs:112-150 / 157-203
+        const bool q5 = w.type == T_Q5_K;
+        const uint8_t *blk = w.q + b * (q5 ? 176 : 144);
+        const float dv = h2f(rd16(blk)), mv = h2f(rd16(blk + 2));
+        const uint32_t grp = e >> 6, within = e & 63, l = within & 31, hi = within >> 5;
+        const uint32_t sub = 2 * grp + hi;
+        uint32_t sc, m;
+        scale_min_k4(sub, blk + 4, sc, m);
+        const uint8_t byte = blk[(q5 ? 48 : 16) + 32 * grp + l];
+        uint32_t q = hi ? (byte >> 4) : (byte & 15);
+        if (q5) q += ((blk[16 + l] >> sub) & 1) ? 16 : 0;
+        const float d1 = __fmul_rn(dv, (float)sc);
+        const float m1 = __fmul_rn(mv, (float)m);
+        return __fsub_rn(__fmul_rn(d1, (float)q), m1);
+    }
+    case T_Q6_K: {
+        // dequant.rs:205-258
+        const uint8_t *blk = w.q + b * Q6_QBYTES;
+        const float dv = h2f(w.d[b]);
+        const uint32_t half = e >> 7, within = e & 127, quarter = within >> 5, l = within & 31;
+        const uint8_t qlb = blk[64 * half + l + 32 * (quarter & 1)];
+        const uint32_t lo = quarter < 2 ? (qlb & 15) : (qlb >> 4);
+        const uint32_t hi2 = (blk[128 + 32 * half + l] >> (2 * quarter)) & 3;
+        const int q = (int)(lo | (hi2 << 4)) - 32;
+        const float s = (float)(int8_t)blk[192 + 8 * half + (l >> 4) + 2 * quarter];
+        return __fmul_rn(__fmul_rn(dv, s), (float)q);
+    }
+    case T_Q4_0: {
+        // dequant.rs:77-99
+        const uint8_t *blk = w.q + b * 18;
+        const int x = e < 16 ? (int)(blk[2 + e] & 15) - 8 : (int)(blk[2 + e - 16] >> 4) - 8;
+        return __fmul_rn((float)x, h2f(rd16(blk)));
+    }
+    case T_F16:
+        return h2f(reinterpret_cast<const uint16_t *>(w.q)[b]);
+    case T_F32:
+        return reinterpret_cast<const float *>(w.q)[b];
+    default:
+        return 0.0f;
+    }
+}
+
+__global__ void k_dequant(WeightView w, float *__restrict__ out) {
+    const uint32_t be = (uint32_t)block_elems(w.type);
+    const uint64_t n = (uint64_t)w.n_out * w.n_in;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        out[i] = deq_elem(w, i / be, (uint32_t)(i % be));
+}
+
+// rows_dev[r] selects a row; out is [n_rows * n_in] (embedding lookup,
+// ops.rs:11-26 on the dequantized table, done one row at a time)
+__global__ void k_dequant_rows(WeightView w, const uint32_t *__restrict__ rows, uint32_t n_rows,
+                               float *__restrict__ out) {
+    const uint32_t be = (uint32_t)block_elems(w.type);
+    const uint64_t n = (uint64_t)n_rows * w.n_in;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        uint32_t r = (uint32_t)(i / w.n_in), c = (uint32_t)(i % w.n_in);
+        uint32_t row = rows[r];
+        if (row >= w.n_out) row = w.n_out - 1;  // ids are validated on the host
+        uint64_t e = (uint64_t)row * w.n_in + c;
+        out[i] = deq_elem(w, e / be, (uint32_t)(e % be));
+    }
+}
+
+hipError_t launch_dequant(WeightView w, float *out, hipStream_t s) {
+    uint64_t n = (uint64_t)w.n_out * w.n_in;
+    hipLaunchKernelGGL(k_dequant, dim3(grid_for(n, 256)), dim3(256), 0, s, w, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_rows(WeightView w, const uint32_t *rows_dev, uint32_t n_rows, float *out,
+                               hipStream_t s) {
+    uint64_t n = (uint64_t)n_rows * w.n_in;
+    hipLaunchKernelGGL(k_dequant_rows, dim3(grid_for(n, 256)), dim3(256), 0, s, w, rows_dev,
+                       n_rows, out);
+    return hipGetLastError();
+}
+
+}  // namespace lrs

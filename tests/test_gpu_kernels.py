@@ -1,0 +1,270 @@
+"""GPU parity of the kernel-level C ABI against the CPU oracle.
+
+Bars: dequant bit-exact; matvec within 1e-4 relative
+L2 of dequant + sequential f32 dot (measured values are ~1e-7).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
+KQ = [Q8_0, Q4_K, Q5_K, Q6_K]
+THREADS = min(16, os.cpu_count() or 1)
+MATVEC_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def ctx(lrs):
+    c = lrs.Context()
+    yield c
+    c.close()
+
+
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def f16b(v):
+    h = int(np.array([v], np.float16).view(np.uint16)[0])
+    return [h & 0xFF, h >> 8]
+
+
+def random_blocks(orc, t, n, seed):
+    rng = np.random.default_rng(seed)
+    ts = orc.TYPE_SIZE[t]
+    raw = rng.integers(0, 256, size=ts * n, dtype=np.uint8)
+    for b in range(n):
+        o = b * ts
+        if t in (Q8_0, Q4_0):
+            raw[o:o + 2] = f16b(rng.uniform(-2, 2))
+        elif t in (Q4_K, Q5_K):
+            raw[o:o + 2] = f16b(rng.uniform(1e-4, 1e-1))
+            raw[o + 2:o + 4] = f16b(rng.uniform(1e-4, 1e-1))
+        elif t == Q6_K:
+            raw[o + 208:o + 210] = f16b(rng.uniform(-1e-1, 1e-1))
+    return raw
+
+
+# --------------------------------------------------------------------------
+# dequant: bit-exact
+# --------------------------------------------------------------------------
+def test_f16_widening_exhaustive(lrs, orc, ctx):
+    codes = np.arange(65536, dtype=np.uint16)
+    got = lrs.dequant_to_f32(ctx, F16, codes.view(np.uint8))
+    ref = orc.dequant(F16, codes.view(np.uint8))
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K, F32])
+def test_dequant_bit_exact_random_blocks(lrs, orc, ctx, t):
+    if t == F32:
+        raw = np.random.default_rng(1).standard_normal(4096).astype(np.float32).view(np.uint8)
+    else:
+        raw = random_blocks(orc, t, 2048, 10 + t)
+    got = lrs.dequant_to_f32(ctx, t, raw)
+    ref = orc.dequant(t, raw)
+    assert got.shape == ref.shape
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", KQ)
+@pytest.mark.parametrize("mode", [0, 1])
+def test_dequant_bit_exact_synthetic_blocks(lrs, orc, ctx, t, mode):
+    raw = orc.gen_blocks(t, 1234 + t, 4096, mode=mode)
+    got = lrs.dequant_to_f32(ctx, t, raw)
+    assert np.array_equal(got.view(np.uint32), orc.dequant(t, raw).view(np.uint32))
+
+
+def test_dequant_reference_known_answers(lrs, ctx):
+    # dequant.rs:297-319, 366-394, 410-464 through the GPU
+    out = lrs.dequant_to_f32(ctx, Q8_0, bytes(f16b(1.0) + [1, 0xFF] + [0] * 30))
+    assert out[0] == 1.0 and out[1] == -1.0 and np.all(out[2:] == 0)
+    out = lrs.dequant_to_f32(ctx, Q8_0, bytes(f16b(2.0) + [3] + [0] * 31))
+    assert out[0] == 6.0
+    out = lrs.dequant_to_f32(ctx, Q4_K, bytes(f16b(1.0) + f16b(1.0) + [8, 4] + [0] * 10 + [0x22] * 128))
+    assert np.all(out[:32] == 16) and np.all(out[32:64] == 8) and np.all(out[64:] == 0)
+    out = lrs.dequant_to_f32(ctx, Q6_K, bytes([0] * 192 + [1, 0] * 8 + f16b(1.0)))
+    for base in (0, 128):
+        for l in range(32):
+            for off in (0, 32, 64, 96):
+                assert out[base + l + off] == (-32.0 if l < 16 else 0.0)
+
+
+def test_q5_k_gguf_py_golden_block_on_gpu(lrs, ctx):
+    fx = json.load(open(os.path.join(HERE, "golden", "q5_k_gguf_py_block.json")))
+    out = lrs.dequant_to_f32(ctx, Q5_K, bytes(fx["raw"]))
+    for i, v in fx["spots"]:
+        assert abs(out[i] - v) < fx["spot_tol"]
+    assert abs(out.astype(np.float64).sum() - fx["sum"]) < fx["sum_tol"]
+
+
+def test_dequant_rejects_bad_sizes(lrs, ctx):
+    for t, bad in ((Q8_0, 33), (Q4_K, 143), (Q5_K, 175), (Q6_K, 209)):
+        with pytest.raises(lrs.ModelError):
+            lrs.dequant_to_f32(ctx, t, bytes(bad))
+
+
+# --------------------------------------------------------------------------
+# weights: upload / download / synthetic generator
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("t", KQ)
+def test_upload_download_round_trip(lrs, orc, ctx, t):
+    n_in = 512 if t != Q8_0 else 96
+    raw = random_blocks(orc, t, 7 * n_in // orc.BLOCK[t], 5)
+    w = lrs.Weight.upload(ctx, t, raw, n_in, 7)
+    assert w.gguf_bytes == raw.nbytes
+    assert np.array_equal(w.download(), raw)
+
+
+@pytest.mark.parametrize("t", KQ)
+@pytest.mark.parametrize("mode", [0, 1])
+def test_device_generator_matches_host_generator(lrs, orc, ctx, t, mode):
+    n_in, n_out = 1024, 33
+    w = lrs.Weight.generate(ctx, t, 99 + t, n_in, n_out, mode=mode)
+    ref = orc.gen_weight(t, 99 + t, n_out, n_in, mode=mode)
+    assert np.array_equal(w.download(), ref)
+
+
+def test_upload_rejects_bad_shapes(lrs, orc, ctx):
+    raw = orc.gen_weight(Q4_K, 1, 4, 512)
+    with pytest.raises(lrs.ModelError):
+        lrs.Weight.upload(ctx, Q4_K, raw, 500, 4)  # n_in not a multiple of 256
+    with pytest.raises(lrs.ModelError):
+        lrs.Weight.upload(ctx, Q4_K, raw[:-1], 512, 4)  # wrong byte count
+    with pytest.raises(lrs.ModelError):
+        lrs.Weight.upload(ctx, 3, raw, 512, 4)  # Q4_1: not supported
+
+
+# --------------------------------------------------------------------------
+# matvec parity
+# --------------------------------------------------------------------------
+def ref_pattern_weights(t, n_in, n_out):
+    """The reference's deterministic kernel-test weights (integration.rs:1115-1394)."""
+    ts = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}[t]
+    nb = n_in // (32 if t == Q8_0 else 256)
+    i = np.arange(n_out * nb * ts, dtype=np.int64)
+    if t == Q8_0:
+        w = ((i * 37) % 251).astype(np.uint8)
+        w[i % 34 == 0] = 0x00
+        w[i % 34 == 1] = 0x3C
+        return w
+    if t == Q6_K:
+        w = ((i * 89 + i // 5) % 251).astype(np.uint8).reshape(-1, 210)
+        w[:, 192:208] = np.array([((j * 7 % 40) - 20) for j in range(16)], np.int8).view(np.uint8)
+        w[:, 208:210] = f16b(0.0091)
+        return w.reshape(-1)
+    w = ((i * 101 + i // 7) % 251).astype(np.uint8).reshape(-1, ts)
+    w[:, 0:2] = f16b(0.0123)
+    w[:, 2:4] = f16b(0.0045)
+    return w.reshape(-1)
+
+
+@pytest.mark.parametrize("t,n_in,n_out", [
+    (Q4_K, 512, 16), (Q4_K, 4096, 16), (Q4_K, 5120, 16),
+    (Q5_K, 512, 16), (Q5_K, 4096, 16), (Q5_K, 5120, 16),
+    (Q6_K, 512, 16),
+    (Q8_0, 4864, 64), (Q8_0, 5120, 64), (Q8_0, 13824, 64),
+])
+def test_matvec_reference_kernel_cases(lrs, orc, ctx, t, n_in, n_out):
+    w = ref_pattern_weights(t, n_in, n_out)
+    x = ((np.arange(n_in) % 29) - 14.0).astype(np.float32) * np.float32(0.031)
+    got = lrs.Weight.upload(ctx, t, w, n_in, n_out).matvec(x)
+    ref = orc.matvec(t, w, n_in, n_out, x)
+    assert rel_l2(got, ref) < MATVEC_TOL
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5  # the reference's own bar
+
+
+GEOMS = [(l, r, wv) for l in (16, 32, 64) for r in (1, 2, 4) for wv in (1, 2, 4)]
+
+
+@pytest.mark.parametrize("t", KQ)
+def test_matvec_every_geometry_ragged(lrs, orc, ctx, t):
+    n_in = 1056 if t == Q8_0 else 1280  # unit count not a multiple of any lane count
+    n_out = 37
+    w = orc.gen_weight(t, 7, n_out, n_in, mode=1)
+    x = orc.gen_normal(8, n_in)
+    ref = orc.matvec(t, w, n_in, n_out, x)
+    W = lrs.Weight.upload(ctx, t, w, n_in, n_out)
+    try:
+        for g in GEOMS:
+            lrs.set_matvec_geom(*g)
+            got = W.matvec(x)
+            assert rel_l2(got, ref) < MATVEC_TOL, (g, rel_l2(got, ref))
+    finally:
+        lrs.set_matvec_geom(0, 0, 0)
+
+
+@pytest.mark.parametrize("t", KQ)
+def test_matvec_one_hot_selects_dequantized_column(lrs, orc, ctx, t):
+    n_in, n_out = 512, 24
+    w = orc.gen_weight(t, 3, n_out, n_in)
+    deq = orc.dequant(t, w).reshape(n_out, n_in)
+    W = lrs.Weight.upload(ctx, t, w, n_in, n_out)
+    for col in (0, 33, 255, 256 + 77, n_in - 1):
+        x = np.zeros(n_in, np.float32)
+        x[col] = 1.0
+        assert np.array_equal(W.matvec(x), deq[:, col])
+
+
+@pytest.mark.parametrize("t", KQ)
+def test_matvec_columns_equal_single_calls(lrs, orc, ctx, t):
+    """integration.rs:1520-1577: a batched call equals per-column calls exactly."""
+    n_in, n_out = 1024, 16
+    w = orc.gen_weight(t, 4, n_out, n_in)
+    W = lrs.Weight.upload(ctx, t, w, n_in, n_out)
+    xs = np.stack([orc.gen_normal(20 + c, n_in) * (1 + c) for c in range(5)])
+    yb = W.matvec(xs)
+    for c in range(5):
+        assert np.array_equal(yb[c], W.matvec(xs[c]))
+
+
+def test_matvec_zero_and_single_row(lrs, orc, ctx):
+    for t in KQ:
+        n_in = 256
+        w = orc.gen_weight(t, 5, 1, n_in)
+        x = orc.gen_normal(6, n_in)
+        assert rel_l2(lrs.Weight.upload(ctx, t, w, n_in, 1).matvec(x),
+                      orc.matvec(t, w, n_in, 1, x)) < MATVEC_TOL
+    # all-zero quants: Q4_K gives -dmin * sum_j m_j * sum(x in j)
+    raw = orc.gen_weight(Q4_K, 5, 8, 512).reshape(-1, 144)
+    raw[:, 16:] = 0
+    raw = raw.reshape(-1)
+    x = orc.gen_normal(7, 512)
+    assert rel_l2(lrs.Weight.upload(ctx, Q4_K, raw, 512, 8).matvec(x),
+                  orc.matvec(Q4_K, raw, 512, 8, x)) < MATVEC_TOL
+
+
+def test_matvec_rejects_unsupported(lrs, ctx):
+    w = lrs.Weight.upload(ctx, F32, np.zeros(64, np.float32).view(np.uint8), 4, 4)
+    with pytest.raises(lrs.ModelError):
+        w.matvec(np.zeros(4, np.float32))
+    w2 = lrs.Weight.generate(ctx, Q4_K, 1, 256, 4)
+    with pytest.raises(lrs.ModelError):
+        w2.matvec(np.zeros(255, np.float32))
+
+
+# BASELINE configs 1 and 2 at full size, BASELINE distributions
+CFG1 = [("q8_0", Q8_0, 4096, 4096)]
+CFG2 = [("attn_q", Q4_K, 5120, 5120), ("attn_k", Q4_K, 5120, 1024),
+        ("attn_v", Q6_K, 5120, 1024), ("attn_output", Q4_K, 5120, 5120),
+        ("ffn_gate", Q4_K, 5120, 13824), ("ffn_up", Q4_K, 5120, 13824),
+        ("ffn_down", Q6_K, 13824, 5120)]
+
+
+@pytest.mark.parametrize("name,t,n_in,n_out", CFG1 + CFG2)
+def test_matvec_baseline_config_shapes(lrs, orc, ctx, name, t, n_in, n_out):
+    seed = 1000 + n_in + n_out + t
+    W = lrs.Weight.generate(ctx, t, seed, n_in, n_out)
+    host = orc.gen_weight(t, seed, n_out, n_in)
+    x = orc.gen_normal(1234, n_in)
+    got = W.matvec(x)
+    ref = orc.matvec(t, host, n_in, n_out, x, threads=THREADS)
+    assert rel_l2(got, ref) < MATVEC_TOL, rel_l2(got, ref)
