@@ -113,8 +113,8 @@ int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y,
 int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
                    uint32_t cols);
 
-/* Matvec launch geometry override: lanes_per_row in {16,32,64}, rows per
- * lane group in {1,2,4}, waves per workgroup in {1,2,4}; all 0 = automatic.
+/* Matvec launch geometry override: lanes_per_row in {8,16,32,64}, rows per
+ * lane group in {1,2,4}, waves per workgroup in {2,4,8}; all 0 = automatic.
  * Replaces the LLAMA_RS_MATVEC_GEOM knob (resident_forward.rs:164-176); the
  * LRS_MATVEC_GEOM="lpr,rows,waves" environment variable sets the initial value. */
 int lrs_matvec_set_geom(int lanes_per_row, int rows, int waves);
@@ -127,6 +127,76 @@ int lrs_copy_d2h(lrs_ctx *ctx, void *dst, const void *src_dev, size_t bytes);
 /* HIP events on the context stream: start, then stop returns elapsed ms. */
 int lrs_timer_start(lrs_ctx *ctx);
 int lrs_timer_stop(lrs_ctx *ctx, float *ms);
+
+/* ------------------------------------------------------------------------ */
+/* model level: llama_model::GpuResidentDecode                              */
+/* (crates/llama-model/src/gpu.rs:379-455) as implemented by                 */
+/* llama_vulkan::ResidentForward (resident_forward.rs:5223-5282)             */
+/* ------------------------------------------------------------------------ */
+/* The LlamaConfig fields the dense forward uses (config.rs:51-187). */
+typedef struct {
+    uint32_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, vocab;
+    uint32_t rope_dim; /* RoPE on the first rope_dim dims of a head (adjacent pairs) */
+    uint32_t ctx;      /* KV-cache positions (--ctx, args.rs:38-42) */
+    float rms_eps, freq_base;
+} lrs_config;
+
+/* One decoder layer (LayerWeights, weights.rs; GpuRawWeights, gpu.rs:128-248).
+ * Weights are resident handles from lrs_weight_upload/generate on the same
+ * context and must outlive the model; norm/bias vectors are host f32 and are
+ * copied.  Biases (Qwen2 q/k/v) may be NULL. */
+typedef struct {
+    const lrs_weight *attn_q, *attn_k, *attn_v, *attn_output;
+    const lrs_weight *ffn_gate, *ffn_up, *ffn_down;
+    const float *attn_norm, *ffn_norm; /* [n_embd] */
+    const float *bq, *bk, *bv;         /* [n_head*head_dim], [n_head_kv*head_dim] x2 */
+} lrs_layer_weights;
+
+/* ResidentForward::new (resident_forward.rs:1302-1311): builds the f16 KV
+ * cache and captures the per-token forward as HIP graphs.  token_embd may be
+ * any dequantizable type (the row of each token is dequantized on the GPU,
+ * TokenEmbd::linha gpu.rs:297-304); matvec weights Q8_0/Q4_K/Q5_K/Q6_K. */
+int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weights *layers,
+                     const lrs_weight *token_embd, const float *output_norm,
+                     const lrs_weight *output, lrs_model **out);
+void lrs_model_destroy(lrs_model *m);
+/* GpuResidentDecode::decode: token at position pos (KV written at slot pos,
+ * attends 0..pos), logits [vocab] into caller memory; the cache length
+ * becomes pos+1.  LRS_E_CTX_OVERFLOW when pos >= ctx. */
+int lrs_decode(lrs_model *m, uint32_t token, uint32_t pos, float *logits);
+/* GpuResidentDecode::decode_batch: tokens at pos0..pos0+n-1, logits of the
+ * last one (gpu.rs:392-400). */
+int lrs_decode_batch(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0,
+                     float *logits);
+/* GpuResidentDecode::batch_size (tokens per decode_batch block). */
+uint32_t lrs_batch_size(const lrs_model *m);
+/* GpuResidentDecode::reset: cache length back to 0. */
+void lrs_reset(lrs_model *m);
+/* Current cache length (ResidentState::len). */
+uint32_t lrs_model_len(const lrs_model *m);
+/* decode + greedy sampling on the device (Sampler::sample with temperature 0,
+ * llama-sampling/src/sampler.rs:25-27, = ops::argmax ops.rs:1035-1045):
+ * writes the next token id instead of the logits. */
+int lrs_decode_greedy(lrs_model *m, uint32_t token, uint32_t pos, uint32_t *next);
+/* The greedy loop of gerar_streaming_residente (gpu.rs:609-666) without a
+ * tokenizer: prompt at positions pos0.., then n_gen greedy tokens generated
+ * on the device with no host round trip per token (out_tokens[n_gen]). */
+int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0,
+                        uint32_t n_gen, uint32_t *out_tokens);
+/* Per-op timing of the decode plan (the LLAMA_RS_PROFILE timestamps of
+ * resident_forward.rs:3141-3149, 4556-4745): launches `op` for layers
+ * 0,1,2,.. in turn `iters` times on the model stream, outside the graph, and
+ * returns the mean duration per launch (HIP events) and the GGUF / KV bytes
+ * one launch reads.  Attention reads the current cache length. */
+#define LRS_OP_QKV 0u
+#define LRS_OP_ATTN 1u
+#define LRS_OP_O 2u
+#define LRS_OP_GATEUP 3u
+#define LRS_OP_DOWN 4u
+#define LRS_OP_HEAD 5u
+int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, size_t *bytes);
+/* GGUF bytes of every weight matrix one decoded token streams. */
+size_t lrs_model_bytes_per_token(const lrs_model *m);
 
 #ifdef __cplusplus
 }

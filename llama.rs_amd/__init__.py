@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 
 import numpy as np
 
@@ -100,6 +101,11 @@ class Context:
         h = C.c_void_p()
         check(lib.lrs_ctx_create(device, C.byref(h)))
         self.h = h
+        # children must be released before the context (C-ABI contract):
+        # models first (they reference weights), then weights and buffers
+        self._models = weakref.WeakSet()
+        self._weights = weakref.WeakSet()
+        self._bufs = weakref.WeakSet()
 
     def sync(self) -> None:
         check(lib.lrs_ctx_sync(self.h))
@@ -122,8 +128,17 @@ class Context:
 
     def close(self) -> None:
         if getattr(self, "h", None):
+            for group in (self._models, self._weights, self._bufs):
+                for child in list(group):
+                    child.close() if hasattr(child, "close") else child.free()
             lib.lrs_ctx_destroy(self.h)
             self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def __enter__(self):
         return self
@@ -138,6 +153,7 @@ class DeviceBuffer:
         p = C.c_void_p()
         check(lib.lrs_dev_alloc(ctx.h, nbytes, C.byref(p)))
         self.ptr = p.value
+        ctx._bufs.add(self)
 
     def upload(self, a: np.ndarray) -> None:
         a = np.ascontiguousarray(a)
@@ -151,9 +167,15 @@ class DeviceBuffer:
         return out
 
     def free(self) -> None:
-        if self.ptr:
+        if self.ptr and self.ctx.h:
             check(lib.lrs_dev_free(self.ctx.h, self.ptr))
-            self.ptr = None
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class Weight:
@@ -161,6 +183,7 @@ class Weight:
 
     def __init__(self, ctx: Context, handle, t: int, n_in: int, n_out: int):
         self.ctx, self.h, self.type, self.n_in, self.n_out = ctx, handle, t, n_in, n_out
+        ctx._weights.add(self)
 
     @classmethod
     def upload(cls, ctx: Context, t: int, data, n_in: int, n_out: int) -> "Weight":
@@ -203,9 +226,9 @@ class Weight:
         check(lib.lrs_matvec_dev(self.ctx.h, self.h, x.ptr, y.ptr, cols))
 
     def free(self) -> None:
-        if getattr(self, "h", None):
+        if getattr(self, "h", None) and self.ctx.h:
             lib.lrs_weight_free(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "../../include/lrs.h"
+#include "mv_args.h"
 
 namespace lrs {
 
@@ -89,6 +90,8 @@ hipError_t launch_dequant(WeightView w, float *out, hipStream_t s);
 hipError_t launch_dequant_rows(WeightView w, const uint32_t *rows_dev, uint32_t n_rows,
                                float *out, hipStream_t s);
 int set_matvec_geom(int lpr, int r, int waves);
+MvGeom choose_geom(uint32_t t, uint32_t n_in, uint32_t rows, bool pairs);
+hipError_t launch_mv(const MvArgs &args, MvGeom gm, uint32_t type, hipStream_t s);
 hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols,
                          const float *bias, hipStream_t s);
 

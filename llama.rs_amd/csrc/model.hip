@@ -1,0 +1,650 @@
+// model.hip — the resident batch-1 decode of a dense Llama/Qwen2 model
+// (llama_model::GpuResidentDecode, crates/llama-model/src/gpu.rs:379-455, as
+// implemented by llama_vulkan::ResidentForward::{decode, decode_batch, reset},
+// resident_forward.rs:5223-5282), restating Model::forward
+// (crates/llama-model/src/model.rs:99-266) as a fixed sequence of fused
+// launches captured once in a HIP graph:
+//
+//   embed            x = dequant(token_embd[token])              (ops.rs:11-26)
+//   per layer
+//     qkv            rmsnorm(x)*attn_norm -> q,k,v (+bias) -> RoPE(q,k) ->
+//                    q to f32, k/v appended to the f16 cache at pos
+//     attention      split-K GQA over positions 0..pos            (attention.rs)
+//     o              x += W_o attn
+//     gate/up        rmsnorm(x)*ffn_norm -> silu(gate)*up          (ops.rs:983-988)
+//     down           x += W_down act
+//   head             rmsnorm(x)*output_norm -> logits            (model.rs:254-265)
+//   [argmax]         greedy token, written back as the next step's token
+//
+// The step's token and position live in device memory, so the same graph is
+// replayed for every token; a greedy generation loop runs as back-to-back
+// graph launches with no host round trip.
+#include "lrs_internal.h"
+#include "quant_dev.h"
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace lrs {
+uint32_t attn_splits(uint32_t ctx);
+hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *out,
+                            float *part, uint32_t *cnt, const uint32_t *step, uint32_t n_head,
+                            uint32_t n_kv, uint32_t head_dim, uint32_t ctx, uint32_t S,
+                            hipStream_t s);
+
+// x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304)
+__global__ void k_embed(WeightView w, const uint32_t *__restrict__ step, float *__restrict__ x) {
+    const uint32_t be = (uint32_t)block_elems(w.type);
+    uint32_t tok = step[0];
+    if (tok >= w.n_out) tok = w.n_out - 1;  // ids are validated on the host
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < w.n_in; i += gridDim.x * blockDim.x) {
+        const uint64_t e = (uint64_t)tok * w.n_in + i;
+        x[i] = deq_elem(w, e / be, (uint32_t)(e % be));
+    }
+}
+
+// greedy argmax (ops.rs:1035-1045: first index of the maximum), then the
+// next step: step = {token, pos + 1}; the token is also appended to out[]
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logits, uint32_t n,
+                                                 uint32_t *__restrict__ step,
+                                                 uint32_t *__restrict__ out, uint32_t out_cap) {
+    __shared__ float bv[16];
+    __shared__ uint32_t bi[16];
+    float best = -INFINITY;
+    uint32_t idx = 0xFFFFFFFFu;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = logits[i];
+        if (v > best) {  // strictly greater: keeps the first index per thread
+            best = v;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const uint32_t oi = __shfl_xor(idx, o, 64);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = best;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = bv[0];
+        idx = bi[0];
+        for (uint32_t w = 1; w < blockDim.x / 64; w++)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        if (idx == 0xFFFFFFFFu) idx = 0;  // all -inf / NaN: like argmax, index 0
+        const uint32_t k = step[2];
+        if (out && k < out_cap) out[k] = idx;
+        step[0] = idx;
+        step[1] = step[1] + 1;
+        step[2] = k + 1;
+    }
+}
+
+}  // namespace lrs
+
+using namespace lrs;
+
+struct DevLayer {
+    const lrs_weight *q, *k, *v, *o, *gate, *up, *down;
+    float *attn_norm, *ffn_norm, *bq, *bk, *bv;
+    _Float16 *kc, *vc;
+};
+
+struct lrs_model {
+    lrs_ctx *ctx;
+    lrs_config cfg;
+    std::vector<DevLayer> layers;
+    const lrs_weight *embd, *output;
+    float *output_norm, *freq;
+    // activations
+    float *x, *qbuf, *att, *act, *logits, *part;
+    uint32_t *cnt, *step, *gen;  // step = {token, pos, n_generated}
+    uint32_t gen_cap;
+    uint32_t S;                  // attention splits
+    _Float16 *kv;                // all layers' caches
+    uint32_t *step_host;         // pinned
+    float *logits_host;          // pinned
+    hipGraphExec_t g_logits = nullptr, g_greedy = nullptr;
+    uint32_t len = 0;
+    size_t gguf_bytes_per_token = 0;
+    std::vector<void *> allocs;
+};
+
+namespace {
+
+int dev_alloc(lrs_model *m, size_t bytes, void **p) {
+    hipError_t e = hipMalloc(p, bytes ? bytes : 4);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(model)");
+    m->allocs.push_back(*p);
+    return LRS_OK;
+}
+
+int upload_vec(lrs_model *m, const float *host, size_t n, float **dev) {
+    if (!host) {
+        *dev = nullptr;
+        return LRS_OK;
+    }
+    int rc = dev_alloc(m, n * sizeof(float), (void **)dev);
+    if (rc) return rc;
+    LRS_HIP(hipMemcpy(*dev, host, n * sizeof(float), hipMemcpyHostToDevice));
+    return LRS_OK;
+}
+
+bool is_mv_type(uint32_t t) { return t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+
+int check_w(const lrs_weight *w, const char *name, uint32_t n_in, uint32_t n_out, bool mv) {
+    if (!w) return fail(LRS_E_ARG, std::string("missing weight ") + name);
+    if (w->v.n_in != n_in || w->v.n_out != n_out)
+        return fail(LRS_E_ARG, std::string(name) + " is " + std::to_string(w->v.n_out) + "x" +
+                                   std::to_string(w->v.n_in) + ", expected " +
+                                   std::to_string(n_out) + "x" + std::to_string(n_in));
+    if (mv && !is_mv_type(w->v.type))
+        return fail(LRS_E_UNSUPPORTED, std::string(name) + ": matvec needs Q8_0/Q4_K/Q5_K/Q6_K");
+    return LRS_OK;
+}
+
+MvSeg seg_of(const lrs_weight *w, uint32_t epi) {
+    MvSeg s = {};
+    s.q0 = s.q1 = w->v.q;
+    s.d0 = s.d1 = w->v.d;
+    s.rows = w->v.n_out;
+    s.epi = epi;
+    return s;
+}
+
+// ---- one fused op of the per-token plan, enqueued on the model stream ----
+hipError_t op_embed(lrs_model *m) {
+    hipLaunchKernelGGL(k_embed, dim3((m->cfg.n_embd + 255) / 256), dim3(256), 0, m->ctx->stream,
+                       m->embd->v, m->step, m->x);
+    return hipGetLastError();
+}
+
+// q, k, v: rmsnorm + matvec + bias + RoPE + f16 KV append.  Segments that
+// share a weight type go in one launch (all three for Q8_0 / Q4_K-only
+// models; q+k then v for the Q4_K_M mix).
+hipError_t op_qkv(lrs_model *m, uint32_t l) {
+    const lrs_config &c = m->cfg;
+    const DevLayer &L = m->layers[l];
+    const uint32_t kvd = c.n_head_kv * c.head_dim, qd = c.n_head * c.head_dim;
+    MvArgs a = {};
+    a.n_in = c.n_embd;
+    a.x = m->x;
+    a.norm_w = L.attn_norm;
+    a.eps = c.rms_eps;
+    a.cols = 1;
+    a.step = m->step;
+    a.freq = m->freq;
+    a.head_dim = c.head_dim;
+    a.rope_dim = c.rope_dim;
+    a.ctx = c.ctx;
+    MvSeg sq = seg_of(L.q, EPI_STORE);
+    sq.rope = 1;
+    sq.bias = L.bq;
+    sq.out = m->qbuf;
+    MvSeg sk = seg_of(L.k, EPI_KV);
+    sk.rope = 1;
+    sk.bias = L.bk;
+    sk.kv = L.kc;
+    MvSeg sv = seg_of(L.v, EPI_KV);
+    sv.bias = L.bv;
+    sv.kv = L.vc;
+    const lrs_weight *ws[3] = {L.q, L.k, L.v};
+    const MvSeg segs[3] = {sq, sk, sv};
+    bool done[3] = {false, false, false};
+    for (int i = 0; i < 3; i++) {
+        if (done[i]) continue;
+        const uint32_t t = ws[i]->v.type;
+        a.n_seg = 0;
+        a.nb = ws[i]->v.nb;
+        uint32_t rows = 0;
+        for (int j = i; j < 3; j++) {
+            if (!done[j] && ws[j]->v.type == t) {
+                a.seg[a.n_seg++] = segs[j];
+                rows += ws[j]->v.n_out;
+                done[j] = true;
+            }
+        }
+        hipError_t e = launch_mv(a, choose_geom(t, c.n_embd, rows, true), t, m->ctx->stream);
+        if (e != hipSuccess) return e;
+    }
+    (void)qd;
+    (void)kvd;
+    return hipSuccess;
+}
+
+hipError_t op_attn(lrs_model *m, uint32_t l) {
+    const lrs_config &c = m->cfg;
+    const DevLayer &L = m->layers[l];
+    return launch_attention(m->qbuf, L.kc, L.vc, m->att, m->part, m->cnt, m->step, c.n_head,
+                            c.n_head_kv, c.head_dim, c.ctx, m->S, m->ctx->stream);
+}
+
+// x += W_o att
+hipError_t op_o(lrs_model *m, uint32_t l) {
+    const lrs_config &c = m->cfg;
+    const DevLayer &L = m->layers[l];
+    const uint32_t qd = c.n_head * c.head_dim;
+    MvArgs o = {};
+    o.n_seg = 1;
+    o.seg[0] = seg_of(L.o, EPI_ACCUM);
+    o.seg[0].out = m->x;
+    o.n_in = qd;
+    o.nb = L.o->v.nb;
+    o.x = m->att;
+    o.cols = 1;
+    return launch_mv(o, choose_geom(L.o->v.type, qd, c.n_embd, false), L.o->v.type, m->ctx->stream);
+}
+
+// act = silu(gate h) * (up h), h = rmsnorm(x) * ffn_norm; gate row j and up
+// row j are the two rows of one lane group (dual segment)
+hipError_t op_gateup(lrs_model *m, uint32_t l) {
+    const lrs_config &c = m->cfg;
+    const DevLayer &L = m->layers[l];
+    MvArgs f = {};
+    f.n_seg = 1;
+    MvSeg sg = seg_of(L.gate, EPI_SWIGLU);
+    sg.q1 = L.up->v.q;
+    sg.d1 = L.up->v.d;
+    sg.dual = 1;
+    sg.rows = 2 * c.n_ff;
+    sg.out = m->act;
+    f.seg[0] = sg;
+    f.n_in = c.n_embd;
+    f.nb = L.gate->v.nb;
+    f.x = m->x;
+    f.norm_w = L.ffn_norm;
+    f.eps = c.rms_eps;
+    f.cols = 1;
+    return launch_mv(f, choose_geom(L.gate->v.type, c.n_embd, 2 * c.n_ff, true), L.gate->v.type,
+                     m->ctx->stream);
+}
+
+// x += W_down act
+hipError_t op_down(lrs_model *m, uint32_t l) {
+    const lrs_config &c = m->cfg;
+    const DevLayer &L = m->layers[l];
+    MvArgs dn = {};
+    dn.n_seg = 1;
+    dn.seg[0] = seg_of(L.down, EPI_ACCUM);
+    dn.seg[0].out = m->x;
+    dn.n_in = c.n_ff;
+    dn.nb = L.down->v.nb;
+    dn.x = m->act;
+    dn.cols = 1;
+    return launch_mv(dn, choose_geom(L.down->v.type, c.n_ff, c.n_embd, false), L.down->v.type,
+                     m->ctx->stream);
+}
+
+// logits = W_out (rmsnorm(x) * output_norm)
+hipError_t op_head(lrs_model *m) {
+    const lrs_config &c = m->cfg;
+    MvArgs h = {};
+    h.n_seg = 1;
+    h.seg[0] = seg_of(m->output, EPI_STORE);
+    h.seg[0].out = m->logits;
+    h.n_in = c.n_embd;
+    h.nb = m->output->v.nb;
+    h.x = m->x;
+    h.norm_w = m->output_norm;
+    h.eps = c.rms_eps;
+    h.cols = 1;
+    return launch_mv(h, choose_geom(m->output->v.type, c.n_embd, c.vocab, false), m->output->v.type,
+                     m->ctx->stream);
+}
+
+hipError_t op_argmax(lrs_model *m) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, m->ctx->stream, m->logits, m->cfg.vocab,
+                       m->step, m->gen, m->gen_cap);
+    return hipGetLastError();
+}
+
+// enqueue one token's forward on the model stream
+hipError_t enqueue_forward(lrs_model *m, bool greedy) {
+    hipError_t e;
+    if ((e = op_embed(m)) != hipSuccess) return e;
+    for (uint32_t l = 0; l < m->cfg.n_layer; l++) {
+        if ((e = op_qkv(m, l)) != hipSuccess || (e = op_attn(m, l)) != hipSuccess ||
+            (e = op_o(m, l)) != hipSuccess || (e = op_gateup(m, l)) != hipSuccess ||
+            (e = op_down(m, l)) != hipSuccess)
+            return e;
+    }
+    if ((e = op_head(m)) != hipSuccess) return e;
+    if (greedy && (e = op_argmax(m)) != hipSuccess) return e;
+    return hipSuccess;
+}
+
+int capture(lrs_model *m, bool greedy, hipGraphExec_t *out) {
+    hipStream_t s = m->ctx->stream;
+    hipGraph_t g = nullptr;
+    LRS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    hipError_t e = enqueue_forward(m, greedy);
+    hipError_t e2 = hipStreamEndCapture(s, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return hip_fail(e, "forward capture");
+    }
+    if (e2 != hipSuccess) return hip_fail(e2, "hipStreamEndCapture");
+    e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    return LRS_OK;
+}
+
+size_t wbytes(const lrs_weight *w) { return lrs_weight_gguf_bytes(w); }
+
+}  // namespace
+
+extern "C" {
+
+int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weights *layers,
+                     const lrs_weight *token_embd, const float *output_norm,
+                     const lrs_weight *output, lrs_model **out) {
+    if (!ctx || !cfg || !layers || !token_embd || !output_norm || !output || !out)
+        return fail(LRS_E_ARG, "null argument");
+    const lrs_config c = *cfg;
+    if (c.n_layer == 0 || c.n_embd == 0 || c.n_head == 0 || c.n_head_kv == 0 || c.vocab == 0 ||
+        c.ctx == 0 || c.n_ff == 0)
+        return fail(LRS_E_ARG, "empty dimension in config");
+    if (c.n_head % c.n_head_kv) return fail(LRS_E_ARG, "n_head must be a multiple of n_head_kv");
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
+        return fail(LRS_E_UNSUPPORTED, "head_dim must be 64, 128 or 256");
+    if (c.rope_dim > c.head_dim || (c.rope_dim & 1)) return fail(LRS_E_ARG, "bad rope_dim");
+    if (c.n_head / c.n_head_kv > 8) return fail(LRS_E_UNSUPPORTED, "n_head / n_head_kv > 8");
+    if (c.n_embd % 256 || c.n_ff % 256 || (c.n_head * c.head_dim) % 256)
+        return fail(LRS_E_UNSUPPORTED, "n_embd, n_ff and n_head*head_dim must be multiples of 256");
+    const uint32_t qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+    int rc;
+    for (uint32_t l = 0; l < c.n_layer; l++) {
+        const lrs_layer_weights &L = layers[l];
+        if ((rc = check_w(L.attn_q, "attn_q", c.n_embd, qd, true)) ||
+            (rc = check_w(L.attn_k, "attn_k", c.n_embd, kvd, true)) ||
+            (rc = check_w(L.attn_v, "attn_v", c.n_embd, kvd, true)) ||
+            (rc = check_w(L.attn_output, "attn_output", qd, c.n_embd, true)) ||
+            (rc = check_w(L.ffn_gate, "ffn_gate", c.n_embd, c.n_ff, true)) ||
+            (rc = check_w(L.ffn_up, "ffn_up", c.n_embd, c.n_ff, true)) ||
+            (rc = check_w(L.ffn_down, "ffn_down", c.n_ff, c.n_embd, true)))
+            return rc;
+        if (L.ffn_gate->v.type != L.ffn_up->v.type)
+            return fail(LRS_E_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
+        if (!L.attn_norm || !L.ffn_norm) return fail(LRS_E_ARG, "missing norm weights");
+        if (L.attn_q->ctx != ctx || L.ffn_down->ctx != ctx)
+            return fail(LRS_E_ARG, "weights belong to another context");
+    }
+    if ((rc = check_w(token_embd, "token_embd", c.n_embd, c.vocab, false))) return rc;
+    if ((rc = check_w(output, "output", c.n_embd, c.vocab, true))) return rc;
+    if (token_embd->v.type == T_Q4_0 || block_elems(token_embd->v.type) < 0)
+        return fail(LRS_E_UNSUPPORTED, "token_embd type");
+
+    LRS_HIP(hipSetDevice(ctx->device));
+    lrs_model *m = new lrs_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->embd = token_embd;
+    m->output = output;
+    m->layers.resize(c.n_layer);
+    auto bail = [&](int code) {
+        lrs_model_destroy(m);
+        return code;
+    };
+    // attention splits: at most 128 positions per split at full context
+    m->S = attn_splits(c.ctx);
+    const size_t kv_layer = (size_t)kvd * c.ctx;
+    if ((rc = dev_alloc(m, kv_layer * 2 * c.n_layer * sizeof(_Float16), (void **)&m->kv))) return bail(rc);
+    if (hipMemset(m->kv, 0, kv_layer * 2 * c.n_layer * sizeof(_Float16)) != hipSuccess)
+        return bail(fail(LRS_E_HIP, "kv memset"));
+    for (uint32_t l = 0; l < c.n_layer; l++) {
+        const lrs_layer_weights &L = layers[l];
+        DevLayer &D = m->layers[l];
+        D.q = L.attn_q;
+        D.k = L.attn_k;
+        D.v = L.attn_v;
+        D.o = L.attn_output;
+        D.gate = L.ffn_gate;
+        D.up = L.ffn_up;
+        D.down = L.ffn_down;
+        D.kc = m->kv + kv_layer * 2 * l;
+        D.vc = D.kc + kv_layer;
+        if ((rc = upload_vec(m, L.attn_norm, c.n_embd, &D.attn_norm)) ||
+            (rc = upload_vec(m, L.ffn_norm, c.n_embd, &D.ffn_norm)) ||
+            (rc = upload_vec(m, L.bq, qd, &D.bq)) || (rc = upload_vec(m, L.bk, kvd, &D.bk)) ||
+            (rc = upload_vec(m, L.bv, kvd, &D.bv)))
+            return bail(rc);
+        m->gguf_bytes_per_token += wbytes(L.attn_q) + wbytes(L.attn_k) + wbytes(L.attn_v) +
+                                   wbytes(L.attn_output) + wbytes(L.ffn_gate) + wbytes(L.ffn_up) +
+                                   wbytes(L.ffn_down);
+    }
+    m->gguf_bytes_per_token += wbytes(output);
+    if ((rc = upload_vec(m, output_norm, c.n_embd, &m->output_norm))) return bail(rc);
+    // RoPE table freq[i] = base^(-2i/rope_dim), f32 powf (model.rs:339-343)
+    std::vector<float> fr(c.rope_dim / 2 + 1, 0.f);
+    for (uint32_t i = 0; i < c.rope_dim / 2; i++) {
+        float ex = -2.0f * (float)i;
+        ex = ex / (float)c.rope_dim;
+        fr[i] = powf(c.freq_base, ex);
+    }
+    if ((rc = upload_vec(m, fr.data(), fr.size(), &m->freq))) return bail(rc);
+    m->gen_cap = 1u << 16;
+    if ((rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
+        (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->qbuf)) ||
+        (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->att)) ||
+        (rc = dev_alloc(m, c.n_ff * sizeof(float), (void **)&m->act)) ||
+        (rc = dev_alloc(m, c.vocab * sizeof(float), (void **)&m->logits)) ||
+        (rc = dev_alloc(m, (size_t)c.n_head * m->S * (c.head_dim + 4) * sizeof(float),
+                        (void **)&m->part)) ||
+        (rc = dev_alloc(m, c.n_head_kv * sizeof(uint32_t), (void **)&m->cnt)) ||
+        (rc = dev_alloc(m, 4 * sizeof(uint32_t), (void **)&m->step)) ||
+        (rc = dev_alloc(m, m->gen_cap * sizeof(uint32_t), (void **)&m->gen)))
+        return bail(rc);
+    if (hipMemset(m->cnt, 0, c.n_head_kv * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess)
+        return bail(fail(LRS_E_HIP, "memset"));
+    if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
+            hipSuccess ||
+        hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=
+            hipSuccess)
+        return bail(fail(LRS_E_OOM, "pinned host buffers"));
+    if ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy)))
+        return bail(rc);
+    *out = m;
+    return LRS_OK;
+}
+
+void lrs_model_destroy(lrs_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->g_logits) (void)hipGraphExecDestroy(m->g_logits);
+    if (m->g_greedy) (void)hipGraphExecDestroy(m->g_greedy);
+    for (void *p : m->allocs) (void)hipFree(p);
+    if (m->step_host) (void)hipHostFree(m->step_host);
+    if (m->logits_host) (void)hipHostFree(m->logits_host);
+    delete m;
+}
+
+static int check_step(lrs_model *m, uint32_t token, uint32_t pos) {
+    if (token >= m->cfg.vocab)
+        return fail(LRS_E_ARG, "token " + std::to_string(token) + " outside the vocabulary");
+    if (pos >= m->cfg.ctx)
+        return fail(LRS_E_CTX_OVERFLOW, "position " + std::to_string(pos) + " beyond context " +
+                                            std::to_string(m->cfg.ctx));
+    return LRS_OK;
+}
+
+// enqueues n tokens at pos0.. (logits graph) without waiting; every token's
+// {token, pos} goes through its own pinned slot, and the stream is drained
+// whenever the slots run out
+static constexpr uint32_t STEP_SLOTS = 1024;
+static int enqueue_tokens(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0) {
+    for (uint32_t i = 0; i < n; i++) {
+        int rc = check_step(m, tokens[i], pos0 + i);
+        if (rc) return rc;
+    }
+    LRS_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    LRS_HIP(hipStreamSynchronize(s));  // slots of an earlier call are free
+    for (uint32_t i = 0; i < n; i++) {
+        const uint32_t slot = i % STEP_SLOTS;
+        if (i > 0 && slot == 0) LRS_HIP(hipStreamSynchronize(s));
+        uint32_t *sh = m->step_host + 4 * slot;
+        sh[0] = tokens[i];
+        sh[1] = pos0 + i;
+        sh[2] = 0;
+        LRS_HIP(hipMemcpyAsync(m->step, sh, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+        LRS_HIP(hipGraphLaunch(m->g_logits, s));
+    }
+    return LRS_OK;
+}
+
+int lrs_decode(lrs_model *m, uint32_t token, uint32_t pos, float *logits) {
+    if (!m || !logits) return fail(LRS_E_ARG, "null argument");
+    int rc = check_step(m, token, pos);
+    if (rc) return rc;
+    LRS_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    m->step_host[0] = token;
+    m->step_host[1] = pos;
+    m->step_host[2] = 0;
+    LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    LRS_HIP(hipGraphLaunch(m->g_logits, s));
+    LRS_HIP(hipMemcpyAsync(m->logits_host, m->logits, m->cfg.vocab * sizeof(float),
+                           hipMemcpyDeviceToHost, s));
+    LRS_HIP(hipStreamSynchronize(s));
+    memcpy(logits, m->logits_host, m->cfg.vocab * sizeof(float));
+    m->len = pos + 1;
+    return LRS_OK;
+}
+
+uint32_t lrs_batch_size(const lrs_model *m) { return m ? 1u : 0u; }
+
+int lrs_decode_batch(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0, float *logits) {
+    if (!m || !tokens || !logits || n == 0) return fail(LRS_E_ARG, "null argument / empty batch");
+    // GpuResidentDecode::decode_batch default (gpu.rs:392-400): token by
+    // token, the logits of the last one are returned
+    int rc = enqueue_tokens(m, tokens, n, pos0);
+    if (rc) return rc;
+    hipStream_t s = m->ctx->stream;
+    LRS_HIP(hipMemcpyAsync(m->logits_host, m->logits, m->cfg.vocab * sizeof(float),
+                           hipMemcpyDeviceToHost, s));
+    LRS_HIP(hipStreamSynchronize(s));
+    memcpy(logits, m->logits_host, m->cfg.vocab * sizeof(float));
+    m->len = pos0 + n;
+    return LRS_OK;
+}
+
+void lrs_reset(lrs_model *m) {
+    if (m) m->len = 0;
+}
+
+uint32_t lrs_model_len(const lrs_model *m) { return m ? m->len : 0; }
+
+int lrs_decode_greedy(lrs_model *m, uint32_t token, uint32_t pos, uint32_t *next) {
+    if (!m || !next) return fail(LRS_E_ARG, "null argument");
+    int rc = check_step(m, token, pos);
+    if (rc) return rc;
+    LRS_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    m->step_host[0] = token;
+    m->step_host[1] = pos;
+    m->step_host[2] = 0;
+    LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    LRS_HIP(hipGraphLaunch(m->g_greedy, s));
+    LRS_HIP(hipMemcpyAsync(m->step_host + 4, m->step, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    LRS_HIP(hipStreamSynchronize(s));
+    *next = m->step_host[4];
+    m->len = pos + 1;
+    return LRS_OK;
+}
+
+int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0,
+                        uint32_t n_gen, uint32_t *out_tokens) {
+    if (!m || !prompt || !out_tokens || n_prompt == 0 || n_gen == 0)
+        return fail(LRS_E_ARG, "null argument / empty prompt or generation");
+    // the last generated token is not fed back, so it needs no cache slot
+    if ((size_t)pos0 + n_prompt + n_gen - 1 > m->cfg.ctx)
+        return fail(LRS_E_CTX_OVERFLOW, "prompt + generation exceed the context");
+    if (n_gen > m->gen_cap) return fail(LRS_E_ARG, "too many tokens for one call");
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= m->cfg.vocab) return fail(LRS_E_ARG, "prompt token outside the vocabulary");
+    LRS_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    // prefill: tokens 0..n_prompt-2, then the last prompt token starts the
+    // greedy chain (its argmax is the first generated token)
+    int rc = LRS_OK;
+    if (n_prompt > 1 && (rc = enqueue_tokens(m, prompt, n_prompt - 1, pos0))) return rc;
+    LRS_HIP(hipStreamSynchronize(s));
+    m->step_host[0] = prompt[n_prompt - 1];
+    m->step_host[1] = pos0 + n_prompt - 1;
+    m->step_host[2] = 0;
+    LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    for (uint32_t i = 0; i < n_gen; i++) LRS_HIP(hipGraphLaunch(m->g_greedy, s));
+    LRS_HIP(hipMemcpyAsync(out_tokens, m->gen, n_gen * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    LRS_HIP(hipStreamSynchronize(s));
+    m->len = pos0 + n_prompt + n_gen - 1;
+    return LRS_OK;
+}
+
+int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, size_t *bytes) {
+    if (!m || !avg_us || iters == 0) return fail(LRS_E_ARG, "null argument");
+    const lrs_config &c = m->cfg;
+    if (op > LRS_OP_HEAD) return fail(LRS_E_ARG, "unknown op");
+    LRS_HIP(hipSetDevice(m->ctx->device));
+    hipStream_t s = m->ctx->stream;
+    const bool per_layer = op != LRS_OP_HEAD;
+    size_t b = 0;
+    const uint32_t kvd = c.n_head_kv * c.head_dim;
+    const uint32_t L = m->len ? m->len : 1;  // attention reads this many positions
+    if (per_layer) {
+        const DevLayer &D = m->layers[0];
+        switch (op) {
+        case LRS_OP_QKV: b = wbytes(D.q) + wbytes(D.k) + wbytes(D.v); break;
+        case LRS_OP_ATTN: b = (size_t)L * kvd * 2 * sizeof(_Float16); break;
+        case LRS_OP_O: b = wbytes(D.o); break;
+        case LRS_OP_GATEUP: b = wbytes(D.gate) + wbytes(D.up); break;
+        case LRS_OP_DOWN: b = wbytes(D.down); break;
+        }
+    } else {
+        b = wbytes(m->output);
+    }
+    // the step buffer must hold a valid position: the last decoded one
+    m->step_host[0] = 0;
+    m->step_host[1] = L - 1;
+    m->step_host[2] = 0;
+    LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    auto one = [&](uint32_t i) -> hipError_t {
+        const uint32_t l = i % c.n_layer;
+        switch (op) {
+        case LRS_OP_QKV: return op_qkv(m, l);
+        case LRS_OP_ATTN: return op_attn(m, l);
+        case LRS_OP_O: return op_o(m, l);
+        case LRS_OP_GATEUP: return op_gateup(m, l);
+        case LRS_OP_DOWN: return op_down(m, l);
+        default: return op_head(m);
+        }
+    };
+    for (uint32_t i = 0; i < c.n_layer && i < iters; i++) LRS_HIP(one(i));  // warm
+    LRS_HIP(hipEventRecord(m->ctx->ev0, s));
+    for (uint32_t i = 0; i < iters; i++) LRS_HIP(one(i));
+    LRS_HIP(hipEventRecord(m->ctx->ev1, s));
+    LRS_HIP(hipEventSynchronize(m->ctx->ev1));
+    float ms = 0.f;
+    LRS_HIP(hipEventElapsedTime(&ms, m->ctx->ev0, m->ctx->ev1));
+    *avg_us = ms * 1000.f / (float)iters;
+    if (bytes) *bytes = b;
+    return LRS_OK;
+}
+
+size_t lrs_model_bytes_per_token(const lrs_model *m) { return m ? m->gguf_bytes_per_token : 0; }
+
+}  // extern "C"

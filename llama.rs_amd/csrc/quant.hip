@@ -5,18 +5,9 @@
 // 58-258) element by element with the same f32 operation order; the library
 // is compiled with -ffp-contract=off, so d1*q - m1 rounds twice as in Rust.
 #include "lrs_internal.h"
+#include "quant_dev.h"
 
 namespace lrs {
-
-__device__ __forceinline__ float h2f(uint16_t h) {
-    _Float16 v;
-    __builtin_memcpy(&v, &h, 2);
-    return (float)v;
-}
-
-__device__ __forceinline__ uint16_t rd16(const uint8_t *p) {
-    return (uint16_t)(p[0] | ((uint16_t)p[1] << 8));
-}
 
 // ---------------------------------------------------------------------------
 // GGUF byte offset of byte `i` of the device q-part of a block
@@ -211,70 +202,6 @@ hipError_t launch_generate(WeightView w, uint8_t *q, uint16_t *d, uint64_t seed,
 // ---------------------------------------------------------------------------
 // dequant (bit-exact with dequant.rs)
 // ---------------------------------------------------------------------------
-// K-quant 6-bit (scale, min) of sub-block j: dequant.rs:101-110
-__device__ __forceinline__ void scale_min_k4(uint32_t j, const uint8_t *s, uint32_t &sc,
-                                             uint32_t &m) {
-    if (j < 4) {
-        sc = s[j] & 63;
-        m = s[j + 4] & 63;
-    } else {
-        sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
-        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-    }
-}
-
-// element e (0..255) of block b of a resident weight
-__device__ __forceinline__ float deq_elem(const WeightView &w, uint64_t b, uint32_t e) {
-    switch (w.type) {
-    case T_Q8_0: {
-        // dequant.rs:58-76
-        const uint8_t *qs = w.q + b * Q8_QBYTES;
-        return __fmul_rn((float)(int8_t)qs[e], h2f(w.d[b]));
-    }
-    case T_Q4_K:
-    case T_Q5_K: {
-        // dequant.rs:112-150 / 157-203
-        const bool q5 = w.type == T_Q5_K;
-        const uint8_t *blk = w.q + b * (q5 ? 176 : 144);
-        const float dv = h2f(rd16(blk)), mv = h2f(rd16(blk + 2));
-        const uint32_t grp = e >> 6, within = e & 63, l = within & 31, hi = within >> 5;
-        const uint32_t sub = 2 * grp + hi;
-        uint32_t sc, m;
-        scale_min_k4(sub, blk + 4, sc, m);
-        const uint8_t byte = blk[(q5 ? 48 : 16) + 32 * grp + l];
-        uint32_t q = hi ? (byte >> 4) : (byte & 15);
-        if (q5) q += ((blk[16 + l] >> sub) & 1) ? 16 : 0;
-        const float d1 = __fmul_rn(dv, (float)sc);
-        const float m1 = __fmul_rn(mv, (float)m);
-        return __fsub_rn(__fmul_rn(d1, (float)q), m1);
-    }
-    case T_Q6_K: {
-        // dequant.rs:205-258
-        const uint8_t *blk = w.q + b * Q6_QBYTES;
-        const float dv = h2f(w.d[b]);
-        const uint32_t half = e >> 7, within = e & 127, quarter = within >> 5, l = within & 31;
-        const uint8_t qlb = blk[64 * half + l + 32 * (quarter & 1)];
-        const uint32_t lo = quarter < 2 ? (qlb & 15) : (qlb >> 4);
-        const uint32_t hi2 = (blk[128 + 32 * half + l] >> (2 * quarter)) & 3;
-        const int q = (int)(lo | (hi2 << 4)) - 32;
-        const float s = (float)(int8_t)blk[192 + 8 * half + (l >> 4) + 2 * quarter];
-        return __fmul_rn(__fmul_rn(dv, s), (float)q);
-    }
-    case T_Q4_0: {
-        // dequant.rs:77-99
-        const uint8_t *blk = w.q + b * 18;
-        const int x = e < 16 ? (int)(blk[2 + e] & 15) - 8 : (int)(blk[2 + e - 16] >> 4) - 8;
-        return __fmul_rn((float)x, h2f(rd16(blk)));
-    }
-    case T_F16:
-        return h2f(reinterpret_cast<const uint16_t *>(w.q)[b]);
-    case T_F32:
-        return reinterpret_cast<const float *>(w.q)[b];
-    default:
-        return 0.0f;
-    }
-}
-
 __global__ void k_dequant(WeightView w, float *__restrict__ out) {
     const uint32_t be = (uint32_t)block_elems(w.type);
     const uint64_t n = (uint64_t)w.n_out * w.n_in;

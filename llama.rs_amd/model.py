@@ -1,0 +1,205 @@
+"""ResidentForward — host mirror of llama_model::GpuResidentDecode
+(crates/llama-model/src/gpu.rs:379-455) over liblrs.so's model entry points.
+
+Methods keep the reference's names and meaning: ``decode(token, pos)`` returns
+the logits of one token at absolute position ``pos`` (the KV cache then holds
+``pos + 1`` positions), ``decode_batch(tokens, pos0)`` the logits of the last
+of a block, ``batch_size()``, ``reset()``.  ``decode_greedy`` and
+``generate_greedy`` keep the argmax on the device (the temperature-0 path of
+gerar_streaming_residente, gpu.rs:609-666).  Failures raise ModelError.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import Context, ModelError, Weight, check, lib, Q4_K, Q6_K
+
+_u32p = C.POINTER(C.c_uint32)
+_f32p = C.POINTER(C.c_float)
+
+
+class LrsConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in
+                ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "vocab",
+                 "rope_dim", "ctx")] + [("rms_eps", C.c_float), ("freq_base", C.c_float)]
+
+
+class LrsLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in
+                ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down",
+                 "attn_norm", "ffn_norm", "bq", "bk", "bv")]
+
+
+def _bind():
+    vp = C.c_void_p
+    sig = {
+        "lrs_model_create": (C.c_int, [vp, C.POINTER(LrsConfig), vp, vp, vp, vp, C.POINTER(vp)]),
+        "lrs_model_destroy": (None, [vp]),
+        "lrs_decode": (C.c_int, [vp, C.c_uint32, C.c_uint32, vp]),
+        "lrs_decode_batch": (C.c_int, [vp, vp, C.c_uint32, C.c_uint32, vp]),
+        "lrs_batch_size": (C.c_uint32, [vp]),
+        "lrs_reset": (None, [vp]),
+        "lrs_model_len": (C.c_uint32, [vp]),
+        "lrs_decode_greedy": (C.c_int, [vp, C.c_uint32, C.c_uint32, _u32p]),
+        "lrs_generate_greedy": (C.c_int, [vp, vp, C.c_uint32, C.c_uint32, C.c_uint32, vp]),
+        "lrs_model_profile": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.POINTER(C.c_float),
+                                        C.POINTER(C.c_size_t)]),
+        "lrs_model_bytes_per_token": (C.c_size_t, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+
+
+_bind()
+
+CONFIG_KEYS = ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "vocab",
+               "rope_dim", "ctx", "rms_eps", "freq_base")
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+class ResidentForward:
+    """The whole model resident on one GPU; one HIP graph per token."""
+
+    def __init__(self, ctx: Context, cfg: dict, layers: list, token_embd: Weight,
+                 output_norm, output: Weight):
+        self.ctx, self.cfg = ctx, dict(cfg)
+        c = LrsConfig(*[cfg[k] for k in CONFIG_KEYS])
+        self._keep = [token_embd, output]
+        arr = (LrsLayer * cfg["n_layer"])()
+        for i, L in enumerate(layers):
+            vecs = {k: _f32(L.get(k)) for k in ("attn_norm", "ffn_norm", "bq", "bk", "bv")}
+            self._keep.append(vecs)
+            self._keep.extend(L[k] for k in ("attn_q", "attn_k", "attn_v", "attn_output",
+                                             "ffn_gate", "ffn_up", "ffn_down"))
+            for k in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+                      "ffn_down"):
+                setattr(arr[i], k, L[k].h.value if isinstance(L[k].h, C.c_void_p) else L[k].h)
+            for k, v in vecs.items():
+                setattr(arr[i], k, None if v is None else v.ctypes.data)
+        onorm = _f32(output_norm)
+        self._keep.append(onorm)
+        h = C.c_void_p()
+
+        def wh(w):
+            return w.h.value if isinstance(w.h, C.c_void_p) else w.h
+
+        check(lib.lrs_model_create(ctx.h, C.byref(c), C.cast(arr, C.c_void_p), wh(token_embd),
+                                   onorm.ctypes.data, wh(output), C.byref(h)))
+        self.h = h
+        self.vocab = cfg["vocab"]
+        ctx._models.add(self)
+
+    # --- GpuResidentDecode -------------------------------------------------
+    def decode(self, token: int, pos: int) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        check(lib.lrs_decode(self.h, int(token), int(pos), out.ctypes.data))
+        return out
+
+    def decode_batch(self, tokens, pos0: int) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.empty(self.vocab, np.float32)
+        check(lib.lrs_decode_batch(self.h, t.ctypes.data, t.size, int(pos0), out.ctypes.data))
+        return out
+
+    def batch_size(self) -> int:
+        return int(lib.lrs_batch_size(self.h))
+
+    def reset(self) -> None:
+        lib.lrs_reset(self.h)
+
+    def __len__(self) -> int:
+        return int(lib.lrs_model_len(self.h))
+
+    # --- device-side greedy ------------------------------------------------
+    def decode_greedy(self, token: int, pos: int) -> int:
+        nxt = C.c_uint32()
+        check(lib.lrs_decode_greedy(self.h, int(token), int(pos), C.byref(nxt)))
+        return int(nxt.value)
+
+    def generate_greedy(self, prompt, n_gen: int, pos0: int = 0) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(n_gen, np.uint32)
+        check(lib.lrs_generate_greedy(self.h, p.ctypes.data, p.size, int(pos0), int(n_gen),
+                                      out.ctypes.data))
+        return out
+
+    OPS = {"qkv": 0, "attn": 1, "o": 2, "gateup": 3, "down": 4, "head": 5}
+
+    def profile(self, op: str, iters: int):
+        """(mean us per launch, bytes per launch) of one fused op, outside the graph."""
+        us, b = C.c_float(), C.c_size_t()
+        check(lib.lrs_model_profile(self.h, self.OPS[op], int(iters), C.byref(us), C.byref(b)))
+        return float(us.value), int(b.value)
+
+    @property
+    def bytes_per_token(self) -> int:
+        return int(lib.lrs_model_bytes_per_token(self.h))
+
+    def close(self) -> None:
+        if getattr(self, "h", None) and self.ctx.h:
+            lib.lrs_model_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+# synthetic random-init models generated on the device (no host copy)
+# ---------------------------------------------------------------------------
+QWEN25_32B = dict(n_layer=64, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_ff=27648,
+                  vocab=152064, rope_dim=128, ctx=4096, rms_eps=1e-6, freq_base=1e6)
+# Q4_K_M mix used for the benchmark: q,k,o,gate,up Q4_K; v,down Q6_K; head Q6_K
+Q4_K_M_MIX = dict(attn_q=Q4_K, attn_k=Q4_K, attn_v=Q6_K, attn_output=Q4_K, ffn_gate=Q4_K,
+                  ffn_up=Q4_K, ffn_down=Q6_K, output=Q6_K, token_embd=Q4_K)
+
+
+def layer_shapes(cfg):
+    E, qd, kvd, ff = cfg["n_embd"], cfg["n_head"] * cfg["head_dim"], \
+        cfg["n_head_kv"] * cfg["head_dim"], cfg["n_ff"]
+    return dict(attn_q=(E, qd), attn_k=(E, kvd), attn_v=(E, kvd), attn_output=(qd, E),
+                ffn_gate=(E, ff), ffn_up=(E, ff), ffn_down=(ff, E))
+
+
+def synthetic_model(ctx: Context, cfg: dict, seed: int = 1, mix: dict | None = None,
+                    mode: int = 0, d_lo: float = 1e-3, d_hi: float = 1e-2,
+                    biases: bool = True):
+    """Random-init model of the given shape with weights generated on the GPU
+    (seeded GGUF blocks), norm weights ~U[0.9, 1.1] and small q/k/v biases."""
+    mix = dict(Q4_K_M_MIX, **(mix or {}))
+    rng = np.random.default_rng(seed)
+    shapes = layer_shapes(cfg)
+    layers = []
+    for l in range(cfg["n_layer"]):
+        L = {}
+        for i, (name, (n_in, n_out)) in enumerate(shapes.items()):
+            L[name] = Weight.generate(ctx, mix[name], seed * 1000003 + l * 64 + i, n_in, n_out,
+                                      mode=mode, d_lo=d_lo, d_hi=d_hi)
+        L["attn_norm"] = rng.uniform(0.9, 1.1, cfg["n_embd"]).astype(np.float32)
+        L["ffn_norm"] = rng.uniform(0.9, 1.1, cfg["n_embd"]).astype(np.float32)
+        if biases:
+            qd, kvd = shapes["attn_q"][1], shapes["attn_k"][1]
+            L["bq"] = rng.uniform(-0.1, 0.1, qd).astype(np.float32)
+            L["bk"] = rng.uniform(-0.1, 0.1, kvd).astype(np.float32)
+            L["bv"] = rng.uniform(-0.1, 0.1, kvd).astype(np.float32)
+        layers.append(L)
+    emb = Weight.generate(ctx, mix["token_embd"], seed * 7 + 1, cfg["n_embd"], cfg["vocab"],
+                          mode=mode, d_lo=d_lo, d_hi=d_hi)
+    out = Weight.generate(ctx, mix["output"], seed * 7 + 2, cfg["n_embd"], cfg["vocab"],
+                          mode=mode, d_lo=d_lo, d_hi=d_hi)
+    onorm = rng.uniform(0.9, 1.1, cfg["n_embd"]).astype(np.float32)
+    return ResidentForward(ctx, cfg, layers, emb, onorm, out)
+
+
+__all__ = ["ResidentForward", "synthetic_model", "QWEN25_32B", "Q4_K_M_MIX", "layer_shapes",
+           "ModelError"]

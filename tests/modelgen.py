@@ -1,0 +1,84 @@
+"""Seeded random-init models built on the host with the oracle's block
+generator, so that the CPU oracle and the GPU see byte-identical weights."""
+import numpy as np
+
+F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
+
+TINY = dict(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, vocab=512,
+            rope_dim=64, ctx=96, rms_eps=1e-6, freq_base=10000.0)
+# GQA with 5 query heads per KV head and head_dim 128, like the 32B shape
+GQA5 = dict(n_layer=2, n_embd=1280, n_head=10, n_head_kv=2, head_dim=128, n_ff=1024,
+            vocab=1000, rope_dim=128, ctx=160, rms_eps=1e-6, freq_base=1e6)
+
+Q4_K_M = dict(attn_q=Q4_K, attn_k=Q4_K, attn_v=Q6_K, attn_output=Q4_K, ffn_gate=Q4_K,
+              ffn_up=Q4_K, ffn_down=Q6_K, output=Q6_K, token_embd=Q4_K)
+ALL_Q8_0 = {k: Q8_0 for k in Q4_K_M}
+Q5_K_M = dict(Q4_K_M, attn_q=Q5_K, attn_k=Q5_K, attn_output=Q5_K, ffn_gate=Q5_K, ffn_up=Q5_K)
+
+
+def shapes(cfg):
+    E, qd, kvd, ff = cfg["n_embd"], cfg["n_head"] * cfg["head_dim"], \
+        cfg["n_head_kv"] * cfg["head_dim"], cfg["n_ff"]
+    return dict(attn_q=(E, qd), attn_k=(E, kvd), attn_v=(E, kvd), attn_output=(qd, E),
+                ffn_gate=(E, ff), ffn_up=(E, ff), ffn_down=(ff, E))
+
+
+def host_model(orc, cfg, seed=1, mix=None, mode=1, d_lo=2e-4, d_hi=2e-3, biases=True):
+    """weights: name -> (type, array) in the oracle's naming (blk.{l}.{name})."""
+    mix = dict(Q4_K_M, **(mix or {}))
+    w = {}
+    for l in range(cfg["n_layer"]):
+        for i, (name, (n_in, n_out)) in enumerate(shapes(cfg).items()):
+            t = mix[name]
+            w[f"blk.{l}.{name}"] = (t, orc.gen_weight(t, seed * 1000 + l * 16 + i, n_out, n_in,
+                                                     mode=mode, d_lo=d_lo, d_hi=d_hi))
+        w[f"blk.{l}.attn_norm"] = (F32, orc.gen_uniform(seed * 77 + 4 * l, cfg["n_embd"], 0.9, 1.1))
+        w[f"blk.{l}.ffn_norm"] = (F32, orc.gen_uniform(seed * 77 + 4 * l + 1, cfg["n_embd"], 0.9, 1.1))
+        if biases:
+            sh = shapes(cfg)
+            w[f"blk.{l}.bq"] = (F32, orc.gen_uniform(seed * 91 + 4 * l, sh["attn_q"][1], -0.1, 0.1))
+            w[f"blk.{l}.bk"] = (F32, orc.gen_uniform(seed * 91 + 4 * l + 1, sh["attn_k"][1], -0.1, 0.1))
+            w[f"blk.{l}.bv"] = (F32, orc.gen_uniform(seed * 91 + 4 * l + 2, sh["attn_v"][1], -0.1, 0.1))
+    w["token_embd"] = (mix["token_embd"], orc.gen_weight(mix["token_embd"], seed * 5 + 1,
+                                                          cfg["vocab"], cfg["n_embd"], mode=mode,
+                                                          d_lo=d_lo * 20, d_hi=d_hi * 20))
+    w["output"] = (mix["output"], orc.gen_weight(mix["output"], seed * 5 + 2, cfg["vocab"],
+                                                  cfg["n_embd"], mode=mode, d_lo=d_lo, d_hi=d_hi))
+    w["output_norm"] = (F32, orc.gen_uniform(seed * 5 + 3, cfg["n_embd"], 0.9, 1.1))
+    return w
+
+
+def gpu_model(lrs, ctx, cfg, w):
+    """Uploads a host model through the C ABI (the drop-in path)."""
+    from llama_rs_amd.model import ResidentForward
+
+    layers = []
+    for l in range(cfg["n_layer"]):
+        L = {}
+        for name, (n_in, n_out) in shapes(cfg).items():
+            t, arr = w[f"blk.{l}.{name}"]
+            L[name] = lrs.Weight.upload(ctx, t, arr, n_in, n_out)
+        for name in ("attn_norm", "ffn_norm", "bq", "bk", "bv"):
+            if f"blk.{l}.{name}" in w:
+                L[name] = w[f"blk.{l}.{name}"][1]
+        layers.append(L)
+    te, ta = w["token_embd"]
+    emb = lrs.Weight.upload(ctx, te, ta, cfg["n_embd"], cfg["vocab"])
+    ot, oa = w["output"]
+    out = lrs.Weight.upload(ctx, ot, oa, cfg["n_embd"], cfg["vocab"])
+    return ResidentForward(ctx, cfg, layers, emb, w["output_norm"][1], out)
+
+
+def oracle_greedy(model, prompt, n_gen):
+    """Model::generate with greedy sampling: forward(prompt), then one token
+    at a time (generate.rs:13-43)."""
+    toks = []
+    logits = model.forward(np.asarray(prompt, np.uint32))
+    nxt = int(np.argmax(logits))  # first index of the max, like ops::argmax
+    for _ in range(n_gen):
+        toks.append(nxt)
+        if len(toks) == n_gen:
+            break
+        logits = model.forward(np.asarray([nxt], np.uint32))
+        nxt = int(np.argmax(logits))
+    return toks

@@ -36,7 +36,9 @@ def kquant_scales(s12: np.ndarray):
 
 
 def dequant(t: int, data: np.ndarray) -> np.ndarray:
-    data = np.asarray(data, dtype=np.uint8)
+    data = np.ascontiguousarray(data)
+    if data.dtype != np.uint8:
+        data = data.view(np.uint8)
     ts = TYPE_SIZE[t]
     assert data.size % ts == 0
     b = data.reshape(-1, ts)

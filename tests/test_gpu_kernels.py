@@ -182,7 +182,7 @@ def test_matvec_reference_kernel_cases(lrs, orc, ctx, t, n_in, n_out):
     assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5  # the reference's own bar
 
 
-GEOMS = [(l, r, wv) for l in (16, 32, 64) for r in (1, 2, 4) for wv in (1, 2, 4)]
+GEOMS = [(l, r, wv) for l in (8, 16, 32, 64) for r in (1, 2, 4) for wv in (2, 4, 8)]
 
 
 @pytest.mark.parametrize("t", KQ)
@@ -243,7 +243,7 @@ def test_matvec_zero_and_single_row(lrs, orc, ctx):
 
 
 def test_matvec_rejects_unsupported(lrs, ctx):
-    w = lrs.Weight.upload(ctx, F32, np.zeros(64, np.float32).view(np.uint8), 4, 4)
+    w = lrs.Weight.upload(ctx, F32, np.zeros(16, np.float32).view(np.uint8), 4, 4)
     with pytest.raises(lrs.ModelError):
         w.matvec(np.zeros(4, np.float32))
     w2 = lrs.Weight.generate(ctx, Q4_K, 1, 256, 4)

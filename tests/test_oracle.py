@@ -340,3 +340,38 @@ def test_delta_net_known_answers(orc):
     assert np.abs(out * 2 - v2).max() < 1e-6
     out, st = orc.delta_net_step(st, k1, k1, np.zeros(d), 0.0, 0.0)
     assert np.abs(out * 2 - v1 * 0.5).max() < 1e-5
+
+
+# --------------------------------------------------------------------------
+# dense forward (model.rs:99-266) vs a float64 numpy restatement
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_forward_matches_float64_restatement(orc, kv_f16):
+    import modelgen
+
+    cfg = dict(modelgen.TINY, n_layer=2, ctx=16)
+    w = modelgen.host_model(orc, cfg, seed=3)
+    toks = [5, 17, 300, 2, 99]
+    m = orc.Model(cfg, w, kv_f16=kv_f16)
+    got = m.forward(toks)
+    ref = npref.rms_forward64(cfg, w, toks, kv_f16=kv_f16)[-1]
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel < 1e-4, rel
+    assert len(m) == 5
+    # one token at a time gives the same logits bit for bit (same per-row folds)
+    m2 = orc.Model(cfg, w, kv_f16=kv_f16)
+    for t in toks:
+        last = m2.forward([t])
+    assert np.array_equal(last, got)
+
+
+def test_forward_context_overflow_and_bad_token(orc):
+    import modelgen
+
+    cfg = dict(modelgen.TINY, n_layer=1, ctx=4)
+    m = orc.Model(cfg, modelgen.host_model(orc, cfg, seed=4))
+    m.forward([1, 2, 3])
+    with pytest.raises(ValueError):
+        m.forward([4, 5])  # 3 + 2 > ctx: attention.rs:36-40
+    with pytest.raises(ValueError):
+        m.forward([cfg["vocab"]])
