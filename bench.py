@@ -1,18 +1,30 @@
 """bench.py — batch-1 quantized decode hot path on one MI355X.
 
 Workloads:
-  layer   config 2: one Qwen2.5-14B-shaped decoder layer matvec set (q,k,v,o,
-          gate,up in Q4_K / v,down in Q6_K), batch 1, f32 activations.
-          A step is one pass over the 7 matvecs; weights rotate over enough
-          copies (> 2x the 256 MB Infinity Cache) that every byte comes from HBM.
-Prints one JSON line (driver contract) with a roofline object for the dominant
-kernel (Q4_K matvec) and the CPU oracle timed on a bounded sample.
+  decode  config 3 (default): Qwen2.5-32B-shaped dense decoder, random-init
+          Q4_K_M (q,k,o,gate,up Q4_K; v,down,output Q6_K; token_embd Q4_K),
+          whole model resident on the GPU.  A 512-token prompt is consumed,
+          then a step is one greedy decode token (one HIP-graph replay of the
+          full forward, argmax on the device).  W warmup tokens are decoded
+          at positions 511.., then the cache is rewound and K timed tokens are
+          decoded at the same positions 511..511+K-1 (attention length
+          512..511+K, the config's 128 tokens after a 512-token prompt).
+  layer   config 2: one Qwen2.5-14B-shaped layer matvec set, weights rotated
+          over 4 copies so every byte comes from HBM; a step is 7 matvecs.
+  pmc     profiling helper for the rocprofv3 counter passes: a plain copy
+          kernel of known size (calibration) and the dominant decode kernel
+          on a 4-layer model of the 32B shape.
+
+One JSON line (driver contract) with a roofline object for the dominant
+kernel, measured with HIP events on the model's stream, and the CPU oracle
+timed on a bounded sample of the same workload.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -23,14 +35,17 @@ sys.path.insert(0, REPO)
 sys.path.insert(0, os.path.join(REPO, "tests"))
 
 HBM_PEAK_GBS = 8000.0
+METRIC = "batch-1 decode tok/s Q4_K_M 32B-shape; quant matvec HBM GB/s vs peak"
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
-
-CFG2 = [("attn_q", Q4_K, 5120, 5120), ("attn_k", Q4_K, 5120, 1024),
-        ("attn_v", Q6_K, 5120, 1024), ("attn_output", Q4_K, 5120, 5120),
-        ("ffn_gate", Q4_K, 5120, 13824), ("ffn_up", Q4_K, 5120, 13824),
-        ("ffn_down", Q6_K, 13824, 5120)]
 TS = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 BS = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+OP_NAMES = {"qkv": "fused RMSNorm + q/k/v matvec + bias + RoPE + f16 KV append",
+            "attn": "split-K GQA attention over the f16 KV cache (+ combine)",
+            "o": "attn_output matvec + residual add",
+            "gateup": "fused RMSNorm + ffn_gate/ffn_up Q4_K matvec + SwiGLU",
+            "down": "ffn_down Q6_K matvec + residual add",
+            "head": "final RMSNorm + output head Q6_K matvec"}
+PROMPT = 512
 
 
 def gguf_bytes(t, n_in, n_out):
@@ -41,16 +56,130 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def cfg32(n_layer=None):
+    from llama_rs_amd.model import QWEN25_32B
+
+    c = dict(QWEN25_32B)
+    if n_layer:
+        c["n_layer"] = n_layer
+    return c
+
+
+def op_profile(m, n_layer):
+    """Average duration of every fused op (HIP events on the model's stream;
+    per-layer ops rotate over all layers so weights stream from HBM)."""
+    ops = {}
+    for op in ("qkv", "attn", "o", "gateup", "down", "head"):
+        iters = 2 * n_layer if op != "head" else 8
+        us, b = m.profile(op, iters)
+        mult = n_layer if op != "head" else 1
+        ops[op] = dict(us=us, bytes=b, per_token_us=us * mult, gbs=b / us / 1e3 if us else 0.0)
+    return ops
+
+
+def read_traffic(op):
+    """HBM bytes per launch of `op` from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
+    calibration), or None when no summary covers it."""
+    path = os.path.join(REPO, "profiles", "pmc_decode_32b_q4km.md")
+    try:
+        txt = open(path).read()
+    except OSError:
+        return None
+    mt = re.search(r"^traffic_bytes_per_launch\[%s\]\s*=\s*(\d+)" % re.escape(op), txt, re.M)
+    return int(mt.group(1)) if mt else None
+
+
+def bench_decode(lrs, ctx, steps, warmup):
+    from llama_rs_amd.model import synthetic_model
+
+    cfg = cfg32()
+    if PROMPT + max(steps, warmup) > cfg["ctx"]:
+        raise SystemExit(f"--steps/--warmup must keep {PROMPT} + tokens within ctx {cfg['ctx']}")
+    t0 = time.perf_counter()
+    m = synthetic_model(ctx, cfg, seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
+    ctx.sync()
+    log(f"[bench] 32B-shape Q4_K_M model resident in {time.perf_counter() - t0:.1f} s, "
+        f"{m.bytes_per_token / 1e9:.3f} GB of GGUF weights per token")
+    rng = np.random.default_rng(1234)
+    prompt = rng.integers(0, cfg["vocab"], PROMPT).astype(np.uint32)
+    t0 = time.perf_counter()
+    m.decode_batch(prompt[:-1], 0)
+    log(f"[bench] prompt {PROMPT - 1} tokens in {time.perf_counter() - t0:.2f} s")
+    last = prompt[-1:]
+    if warmup:
+        m.generate_greedy(last, warmup, pos0=PROMPT - 1)
+    ctx.sync()
+    # timed: K greedy tokens at positions 511..511+K-1 (the warmup tokens'
+    # cache entries are overwritten in order)
+    ctx.timer_start()
+    w0 = time.perf_counter()
+    toks = m.generate_greedy(last, steps, pos0=PROMPT - 1)
+    ctx.sync()
+    wall = time.perf_counter() - w0
+    ev_ms = ctx.timer_stop()
+    ms_tok = wall * 1e3 / steps
+    log(f"[bench] {steps} tokens: wall {wall * 1e3:.1f} ms, events {ev_ms:.1f} ms "
+        f"-> {steps / wall:.1f} tok/s; first tokens {toks[:6].tolist()}")
+    # per-token algorithmic bytes: GGUF weights + f16 K/V read at each length
+    kvd = cfg["n_head_kv"] * cfg["head_dim"]
+    kv_bytes = np.mean([L * kvd * 2 * 2 * cfg["n_layer"]
+                        for L in range(PROMPT, PROMPT + steps)])
+    tok_bytes = m.bytes_per_token + kv_bytes
+    ops = op_profile(m, cfg["n_layer"])
+    for k, v in ops.items():
+        log(f"[bench]   {k:7s} {v['us']:8.2f} us/launch {v['gbs']:7.0f} GB/s  "
+            f"{v['per_token_us'] / 1e3:.3f} ms/token")
+    m.close()
+    return dict(cfg=cfg, ms_tok=ms_tok, ev_ms_tok=ev_ms / steps, tok_bytes=tok_bytes,
+                kv_bytes=kv_bytes, w_bytes=m.bytes_per_token, ops=ops)
+
+
+def cpu_baseline_decode(threads):
+    """The oracle (C restatement of Model::forward: per-row dequant + sequential
+    f32 dot, rows in chunks of 32 over `threads`) on a bounded sample of the
+    32B-shaped workload: one decoder layer of the full shape timed over
+    repeated tokens, plus 1/8 of the Q6_K output head's rows; scaled to one
+    token = 64 layers + the whole head."""
+    import modelgen
+    import oracle
+
+    lc = cfg32(1)
+    lc.update(vocab=256, ctx=1024)
+    w = modelgen.host_model(oracle, lc, seed=3, mode=0, d_lo=1e-3, d_hi=1e-2)
+    om = oracle.Model(lc, w, kv_f16=True, threads=threads)
+    om.forward_partial([1], 1)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 8.0 and n < 1000:
+        om.forward_partial([(n * 7 + 3) % 256], 1)
+        n += 1
+    t_layer = (time.perf_counter() - t0) / n
+    om.close()
+    rows = 152064 // 8
+    hw = oracle.gen_weight(Q6_K, 5, rows, 5120)
+    x = oracle.gen_normal(1, 5120)
+    oracle.matvec(Q6_K, hw, 5120, rows, x, threads=threads)
+    nh, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 4.0:
+        oracle.matvec(Q6_K, hw, 5120, rows, x, threads=threads)
+        nh += 1
+    t_head = (time.perf_counter() - t0) / nh * 8
+    s_tok = 64 * t_layer + t_head
+    return {"value": round(1.0 / s_tok, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle Model::forward restatement: {n} single-token passes through one "
+                      f"32B-shape Q4_K_M layer ({t_layer * 1e3:.1f} ms each, positions 1..{n}) "
+                      f"+ {nh} matvecs over 1/8 of the Q6_K output head; per token = 64 layers "
+                      f"+ 8x the head slice = {s_tok:.2f} s"}
+
+
 def bench_layer(lrs, ctx, steps, warmup):
-    copies = 4  # 4 x 174.4 MB = 698 MB of distinct weights per rotation
-    mats = []
-    for c in range(copies):
-        mats.append([lrs.Weight.generate(ctx, t, 100 * c + i, n_in, n_out)
-                     for i, (_, t, n_in, n_out) in enumerate(CFG2)])
-    set_bytes = sum(gguf_bytes(t, n_in, n_out) for _, t, n_in, n_out in CFG2)
-    act_bytes = sum(4 * (n_in + n_out) for _, t, n_in, n_out in CFG2)
-    xbuf = ctx.alloc(4 * 13824)
-    ybuf = ctx.alloc(4 * 13824)
+    cfg2 = [(Q4_K, 5120, 5120), (Q4_K, 5120, 1024), (Q6_K, 5120, 1024), (Q4_K, 5120, 5120),
+            (Q4_K, 5120, 13824), (Q4_K, 5120, 13824), (Q6_K, 13824, 5120)]
+    copies = 4  # 4 x 174.4 MB of distinct weights per rotation (> the 256 MB MALL)
+    mats = [[lrs.Weight.generate(ctx, t, 100 * c + i, n_in, n_out)
+             for i, (t, n_in, n_out) in enumerate(cfg2)] for c in range(copies)]
+    set_bytes = sum(gguf_bytes(t, n_in, n_out) + 4 * (n_in + n_out) for t, n_in, n_out in cfg2)
+    xbuf, ybuf = ctx.alloc(4 * 13824), ctx.alloc(4 * 13824)
     xbuf.upload(np.random.default_rng(7).standard_normal(13824).astype(np.float32))
 
     def step(s):
@@ -63,98 +192,108 @@ def bench_layer(lrs, ctx, steps, warmup):
     ctx.timer_start()
     for s in range(steps):
         step(s)
-    ms = ctx.timer_stop()
-    per_set_ms = ms / steps
+    ms = ctx.timer_stop() / steps
+    return dict(ms=ms, bytes=set_bytes, gbs=set_bytes / (ms * 1e-3) / 1e9)
 
-    # dominant kernel alone: Q4_K ffn_gate/up 13824x5120 over 16 rotating copies
-    gates = [lrs.Weight.generate(ctx, Q4_K, 5000 + c, 5120, 13824) for c in range(16)]
-    n_launch = 16 * 20
-    for w in gates:
-        w.matvec_dev(xbuf, ybuf)
+
+def run_pmc(lrs, ctx):
+    """Kernels for the counter passes: the copy calibration (an F32 tensor's
+    identity dequant: 4 B read + 4 B written per element, grid-stride) and the
+    dominant decode op rotating over 4 layers of the 32B shape."""
+    from llama_rs_amd.model import synthetic_model
+
+    n = 128 << 20  # 512 MiB read + 512 MiB written
+    src = lrs.Weight.upload(ctx, F32, np.zeros(n, np.float32), n, 1)
+    dst = ctx.alloc(4 * n)
+    for _ in range(3):
+        src.dequant_dev(dst)
     ctx.sync()
-    ctx.timer_start()
-    for i in range(n_launch):
-        gates[i % 16].matvec_dev(xbuf, ybuf)
-    k_ms = ctx.timer_stop() / n_launch
-    k_bytes = gguf_bytes(Q4_K, 5120, 13824) + 4 * (5120 + 13824)
-    return {
-        "per_set_ms": per_set_ms,
-        "set_bytes": set_bytes + act_bytes,
-        "gbs": (set_bytes + act_bytes) / (per_set_ms * 1e-3) / 1e9,
-        "kernel": "k_matvec<Q4_K> 13824x5120",
-        "kernel_us": k_ms * 1e3,
-        "kernel_bytes": k_bytes,
-        "kernel_gbs": k_bytes / (k_ms * 1e-3) / 1e9,
-    }
-
-
-def cpu_baseline_layer():
-    """Oracle (C restatement of dequant + sequential f32 dot) on the ffn_gate
-    matrix, all host threads; scaled to GB/s of GGUF bytes."""
-    import oracle
-
-    threads = min(16, os.cpu_count() or 1)
-    t, n_in, n_out = Q4_K, 5120, 13824
-    w = oracle.gen_weight(t, 1, n_out, n_in)
-    x = oracle.gen_normal(2, n_in)
-    oracle.matvec(t, w, n_in, n_out, x, threads=threads)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < 10.0:
-        oracle.matvec(t, w, n_in, n_out, x, threads=threads)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    b = gguf_bytes(t, n_in, n_out) + 4 * (n_in + n_out)
-    return {"value": round(b / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} x Q4_K ffn_gate 13824x5120 matvec (dequant + sequential f32 dot "
-                      f"per row, rows in chunks of 32 over {threads} threads), ~10 s"}
+    log(f"[pmc] copy calibration: {3} launches of {4 * n} B read + {4 * n} B written")
+    m = synthetic_model(ctx, cfg32(4), seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
+    m.decode_batch(np.arange(8, dtype=np.uint32), 0)
+    for op in ("gateup", "down", "head"):
+        us, b = m.profile(op, 8 if op != "head" else 2)
+        log(f"[pmc] {op}: {us:.2f} us/launch, {b} algorithmic weight bytes")
+    m.close()
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="layer", choices=["layer"])
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--workload", default="decode", choices=["decode", "layer", "pmc"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     a = ap.parse_args()
     if a.gpus != 1:
-        print("bench.py measures one GPU: the decode path keeps the whole model resident on a "
-              "single MI355X and nothing crosses GPUs (see DESIGN.md, 'Sharding').",
+        print(f"bench.py measures one GPU only (asked for {a.gpus}): the decode path keeps the "
+              "whole model resident on a single MI355X and nothing crosses GPUs.",
               file=sys.stderr)
         sys.exit(2)
+    if a.steps < 1:
+        raise SystemExit("--steps must be >= 1")
     from pkgload import load_product
 
     lrs = load_product()
     ctx = lrs.Context()
     log(f"[bench] workload={a.workload} steps={a.steps} warmup={a.warmup}")
-    r = bench_layer(lrs, ctx, a.steps, a.warmup)
-    log(f"[bench] layer set {r['per_set_ms']*1e3:.1f} us ({r['gbs']:.0f} GB/s); "
-        f"{r['kernel']} {r['kernel_us']:.2f} us ({r['kernel_gbs']:.0f} GB/s)")
-    cpu = None if a.no_cpu else cpu_baseline_layer()
+    if a.workload == "pmc":
+        run_pmc(lrs, ctx)
+        ctx.close()
+        return
+    threads = min(16, os.cpu_count() or 1)
+    if a.workload == "layer":
+        r = bench_layer(lrs, ctx, a.steps, a.warmup)
+        out = {"metric": "quant matvec HBM GB/s, Qwen2.5-14B layer matvec set (batch-1 decode)",
+               "value": round(r["gbs"], 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+               "warmup": a.warmup, "ms_per_step": round(r["ms"], 5), "higher_is_better": True,
+               "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+               "data": "synthetic (seeded GGUF blocks, BASELINE distributions)",
+               "config": {"workload": "config2-qwen2.5-14b-layer-matvec-set", "batch": 1,
+                          "copies_rotated": 4}}
+        print(json.dumps(out), flush=True)
+        ctx.close()
+        return
+
+    r = bench_decode(lrs, ctx, a.steps, a.warmup)
+    ops = r["ops"]
+    dom = max(ops, key=lambda k: ops[k]["per_token_us"])
+    d = ops[dom]
+    ctx.close()
+    cpu = None if a.no_cpu else cpu_baseline_decode(threads)
+    tok_s = 1e3 / r["ms_tok"]
+    eff_gbs = r["tok_bytes"] / (r["ms_tok"] * 1e-3) / 1e9
+    cfg = r["cfg"]
     out = {
-        "metric": "quant matvec HBM GB/s, Qwen2.5-14B layer matvec set (batch-1 decode)",
-        "value": round(r["gbs"], 2),
-        "unit": "GB/s",
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(r["per_set_ms"], 5),
+        "ms_per_step": round(r["ms_tok"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 (Q4_K/Q6_K weights)",
-        "data": "synthetic (seeded GGUF blocks, BASELINE distributions)",
-        "config": {"workload": "qwen2.5-14b-layer-matvec-set", "batch": 1, "n_embd": 5120,
-                   "n_ff": 13824, "weights": "q,k,o,gate,up Q4_K; v,down Q6_K",
-                   "copies_rotated": 4},
-        "roofline": {"bound": "hbm", "achieved": round(r["kernel_gbs"], 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": r["kernel"], "kernel_us": round(r["kernel_us"], 3)},
+        "dtype": "f32",
+        "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU, BASELINE "
+                "distributions; prompt token ids uniform random, seed 1234)",
+        "config": {"workload": "config3-qwen2.5-32b-shape-q4_k_m-greedy-decode",
+                   "prompt": PROMPT, "decode_tokens": a.steps, "n_layer": cfg["n_layer"],
+                   "n_embd": cfg["n_embd"], "n_head": cfg["n_head"],
+                   "n_head_kv": cfg["n_head_kv"], "n_ff": cfg["n_ff"], "vocab": cfg["vocab"],
+                   "kv": "f16", "ctx": cfg["ctx"],
+                   "weights": "q,k,o,gate,up,token_embd Q4_K; v,down,output Q6_K",
+                   "bytes_per_token": int(r["tok_bytes"]),
+                   "token_roofline_frac": round(eff_gbs / HBM_PEAK_GBS, 4),
+                   "effective_gbs": round(eff_gbs, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(dom), "kernel": OP_NAMES[dom], "op": dom,
+                     "kernel_us": round(d["us"], 3), "bytes_per_launch": d["bytes"]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
-    ctx.close()
 
 
 if __name__ == "__main__":

@@ -155,7 +155,9 @@ typedef struct {
 /* ResidentForward::new (resident_forward.rs:1302-1311): builds the f16 KV
  * cache and captures the per-token forward as HIP graphs.  token_embd may be
  * any dequantizable type (the row of each token is dequantized on the GPU,
- * TokenEmbd::linha gpu.rs:297-304); matvec weights Q8_0/Q4_K/Q5_K/Q6_K. */
+ * TokenEmbd::linha gpu.rs:297-304); matvec weights Q8_0/Q4_K/Q5_K/Q6_K.
+ * With the environment variable LRS_GRAPH=0 no graph is captured and every
+ * token issues the same kernel launches directly (for tracing tools). */
 int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weights *layers,
                      const lrs_weight *token_embd, const float *output_norm,
                      const lrs_weight *output, lrs_model **out);
@@ -186,8 +188,9 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
 /* Per-op timing of the decode plan (the LLAMA_RS_PROFILE timestamps of
  * resident_forward.rs:3141-3149, 4556-4745): launches `op` for layers
  * 0,1,2,.. in turn `iters` times on the model stream, outside the graph, and
- * returns the mean duration per launch (HIP events) and the GGUF / KV bytes
- * one launch reads.  Attention reads the current cache length. */
+ * returns the mean duration per launch (HIP events) and the algorithmic bytes
+ * of one launch: GGUF weight bytes, f16 K/V read or appended and the f32
+ * vectors read or written once.  Attention reads the current cache length. */
 #define LRS_OP_QKV 0u
 #define LRS_OP_ATTN 1u
 #define LRS_OP_O 2u

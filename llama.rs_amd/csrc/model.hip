@@ -23,6 +23,7 @@
 #include "quant_dev.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -342,6 +343,13 @@ int capture(lrs_model *m, bool greedy, hipGraphExec_t *out) {
     return LRS_OK;
 }
 
+// one token's forward: the captured graph, or the same launches directly
+hipError_t run_forward(lrs_model *m, bool greedy) {
+    hipGraphExec_t g = greedy ? m->g_greedy : m->g_logits;
+    if (g) return hipGraphLaunch(g, m->ctx->stream);
+    return enqueue_forward(m, greedy);
+}
+
 size_t wbytes(const lrs_weight *w) { return lrs_weight_gguf_bytes(w); }
 
 }  // namespace
@@ -455,7 +463,12 @@ int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weight
         hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=
             hipSuccess)
         return bail(fail(LRS_E_OOM, "pinned host buffers"));
-    if ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy)))
+    // LRS_GRAPH=0 replays the same launches directly on the stream instead
+    // (for tools that cannot trace kernels inside graph launches)
+    const char *ge = getenv("LRS_GRAPH");
+    const bool graphs = !(ge && ge[0] == '0');
+    if (graphs &&
+        ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy))))
         return bail(rc);
     *out = m;
     return LRS_OK;
@@ -502,7 +515,7 @@ static int enqueue_tokens(lrs_model *m, const uint32_t *tokens, uint32_t n, uint
         sh[1] = pos0 + i;
         sh[2] = 0;
         LRS_HIP(hipMemcpyAsync(m->step, sh, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
-        LRS_HIP(hipGraphLaunch(m->g_logits, s));
+        LRS_HIP(run_forward(m, false));
     }
     return LRS_OK;
 }
@@ -517,7 +530,7 @@ int lrs_decode(lrs_model *m, uint32_t token, uint32_t pos, float *logits) {
     m->step_host[1] = pos;
     m->step_host[2] = 0;
     LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
-    LRS_HIP(hipGraphLaunch(m->g_logits, s));
+    LRS_HIP(run_forward(m, false));
     LRS_HIP(hipMemcpyAsync(m->logits_host, m->logits, m->cfg.vocab * sizeof(float),
                            hipMemcpyDeviceToHost, s));
     LRS_HIP(hipStreamSynchronize(s));
@@ -559,7 +572,7 @@ int lrs_decode_greedy(lrs_model *m, uint32_t token, uint32_t pos, uint32_t *next
     m->step_host[1] = pos;
     m->step_host[2] = 0;
     LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
-    LRS_HIP(hipGraphLaunch(m->g_greedy, s));
+    LRS_HIP(run_forward(m, true));
     LRS_HIP(hipMemcpyAsync(m->step_host + 4, m->step, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     LRS_HIP(hipStreamSynchronize(s));
     *next = m->step_host[4];
@@ -588,7 +601,7 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
     m->step_host[1] = pos0 + n_prompt - 1;
     m->step_host[2] = 0;
     LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
-    for (uint32_t i = 0; i < n_gen; i++) LRS_HIP(hipGraphLaunch(m->g_greedy, s));
+    for (uint32_t i = 0; i < n_gen; i++) LRS_HIP(run_forward(m, true));
     LRS_HIP(hipMemcpyAsync(out_tokens, m->gen, n_gen * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     LRS_HIP(hipStreamSynchronize(s));
     m->len = pos0 + n_prompt + n_gen - 1;
@@ -605,17 +618,23 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
     size_t b = 0;
     const uint32_t kvd = c.n_head_kv * c.head_dim;
     const uint32_t L = m->len ? m->len : 1;  // attention reads this many positions
+    // algorithmic bytes: GGUF weight bytes + f16 K/V + f32 vectors read or
+    // written once (scratch such as attention partials is not counted)
+    const size_t E4 = (size_t)c.n_embd * 4, qd4 = (size_t)c.n_head * c.head_dim * 4;
     if (per_layer) {
         const DevLayer &D = m->layers[0];
         switch (op) {
-        case LRS_OP_QKV: b = wbytes(D.q) + wbytes(D.k) + wbytes(D.v); break;
-        case LRS_OP_ATTN: b = (size_t)L * kvd * 2 * sizeof(_Float16); break;
-        case LRS_OP_O: b = wbytes(D.o); break;
-        case LRS_OP_GATEUP: b = wbytes(D.gate) + wbytes(D.up); break;
-        case LRS_OP_DOWN: b = wbytes(D.down); break;
+        case LRS_OP_QKV:
+            b = wbytes(D.q) + wbytes(D.k) + wbytes(D.v) + 2 * E4 + qd4 + (size_t)kvd * 2 * 2 +
+                (D.bq ? qd4 + (size_t)kvd * 8 : 0);
+            break;
+        case LRS_OP_ATTN: b = (size_t)L * kvd * 2 * sizeof(_Float16) + 2 * qd4; break;
+        case LRS_OP_O: b = wbytes(D.o) + qd4 + 2 * E4; break;
+        case LRS_OP_GATEUP: b = wbytes(D.gate) + wbytes(D.up) + 2 * E4 + (size_t)c.n_ff * 4; break;
+        case LRS_OP_DOWN: b = wbytes(D.down) + (size_t)c.n_ff * 4 + 2 * E4; break;
         }
     } else {
-        b = wbytes(m->output);
+        b = wbytes(m->output) + 2 * E4 + (size_t)c.vocab * 4;
     }
     // the step buffer must hold a valid position: the last decoded one
     m->step_host[0] = 0;
