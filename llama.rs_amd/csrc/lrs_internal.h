@@ -91,7 +91,14 @@ hipError_t launch_dequant_rows(WeightView w, const uint32_t *rows_dev, uint32_t 
                                float *out, hipStream_t s);
 int set_matvec_geom(int lpr, int r, int waves);
 MvGeom choose_geom(uint32_t t, uint32_t n_in, uint32_t rows, bool pairs);
-hipError_t launch_mv(const MvArgs &args, MvGeom gm, uint32_t type, hipStream_t s);
+hipError_t launch_mv(const MvArgs &args, MvGeom gm, uint32_t type, hipStream_t s,
+                     uint32_t *blocks_out = nullptr);
+// two weight types in one launch (Q4_K q/k + Q6_K v); hipErrorNotSupported otherwise
+hipError_t launch_mv2(const MvArgs &args, uint32_t t0, MvGeom g0, uint32_t t1, MvGeom g1,
+                      hipStream_t s);
+// reduces the per-block argmax keys of a launch with MvArgs::amax into step / out
+hipError_t launch_argmax_finish(const unsigned long long *keys, uint32_t n, uint32_t *step,
+                                uint32_t *out, uint32_t out_cap, hipStream_t s);
 hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols,
                          const float *bias, hipStream_t s);
 

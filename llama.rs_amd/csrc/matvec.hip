@@ -311,10 +311,22 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // ---------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------
+// orderable 64-bit argmax key of logit v at row r: larger value wins, ties go
+// to the smaller row (the first max, ops.rs:1035-1045); NaN never wins
+__device__ __forceinline__ unsigned long long amax_key(float v, uint32_t r) {
+    if (v != v) return 0ull;
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)o << 32) | (0xFFFFFFFFu - r);
+}
+
+// Segments [s_lo, s_hi) of `a` are processed by blocks of this shape; the
+// block's global index selects the segment.
 template <uint32_t T, int LPR, int R, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void k_mv(MvArgs a) {
+__device__ __forceinline__ void mv_body(const MvArgs &a, uint32_t s_lo, uint32_t s_hi) {
     extern __shared__ float lds[];
     __shared__ float red[WAVES];
+    __shared__ unsigned long long kred[WAVES];
     constexpr uint32_t UE = unit_elems<T>();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t li = lane % LPR, g = lane / LPR;
@@ -323,10 +335,10 @@ __global__ __launch_bounds__(64 * WAVES) void k_mv(MvArgs a) {
     constexpr uint32_t EPB = T == T_Q8_0 ? 32u : 256u;  // elements per quant block
 
     // segment of this block (uniform)
-    uint32_t si = 0;
+    uint32_t si = s_lo;
 #pragma unroll
     for (int s = 1; s < MV_MAX_SEG; s++)
-        if (s < (int)a.n_seg && blockIdx.x >= a.seg[s].block0) si = s;
+        if ((uint32_t)s > s_lo && (uint32_t)s < s_hi && blockIdx.x >= a.seg[s].block0) si = s;
     const MvSeg &sg = a.seg[si];
     const uint32_t rows = sg.rows;
     const uint32_t row0 = (blockIdx.x - sg.block0) * RPB + wave * RPW + g * R;
@@ -433,6 +445,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_mv(MvArgs a) {
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = group_sum<LPR>(acc[r]);
 
+        unsigned long long key = 0ull;  // greedy: this lane's best (logit, row)
         if (li == 0) {
             const uint32_t pos = a.step ? a.step[1] : 0u;
             float v[R];
@@ -489,9 +502,51 @@ __global__ __launch_bounds__(64 * WAVES) void k_mv(MvArgs a) {
                     if (lr < rows) out[lr] = v[r];
                 }
             }
+            if (a.amax) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t lr = row0 + r;
+                    if (lr < rows) {
+                        const unsigned long long k = amax_key(v[r], lr);
+                        key = k > key ? k : key;
+                    }
+                }
+            }
+        }
+        if (a.amax) {
+            // per-block argmax of the logits; k_argmax_finish reduces the blocks
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const unsigned long long k = __shfl_xor(key, o, 64);
+                key = k > key ? k : key;
+            }
+            if (lane == 0) kred[wave] = key;
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                unsigned long long b = kred[0];
+#pragma unroll
+                for (int w = 1; w < WAVES; w++) b = kred[w] > b ? kred[w] : b;
+                a.amax[blockIdx.x] = b;
+            }
         }
         __syncthreads();  // LDS and red[] are reused by the next column
     }
+}
+
+template <uint32_t T, int LPR, int R, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_mv(MvArgs a) {
+    mv_body<T, LPR, R, WAVES>(a, 0, a.n_seg);
+}
+
+// two weight types in one launch: segments [0, n_seg0) of type T0 (blocks of
+// shape L0 x R0), then [n_seg0, n_seg) of type T1 (L1 x R1); the activation
+// and its norm are shared (q/k Q4_K with v Q6_K in the Q4_K_M mix)
+template <uint32_t T0, int L0, int R0, uint32_t T1, int L1, int R1, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_mv2(MvArgs a) {
+    if (blockIdx.x < a.seg[a.n_seg0].block0)
+        mv_body<T0, L0, R0, WAVES>(a, 0, a.n_seg0);
+    else
+        mv_body<T1, L1, R1, WAVES>(a, a.n_seg0, a.n_seg);
 }
 
 // ---------------------------------------------------------------------------
@@ -569,7 +624,8 @@ MvGeom choose_geom(uint32_t t, uint32_t n_in, uint32_t rows, bool pairs) {
     return gm;
 }
 
-hipError_t launch_mv(const MvArgs &args_in, MvGeom gm, uint32_t type, hipStream_t s) {
+hipError_t launch_mv(const MvArgs &args_in, MvGeom gm, uint32_t type, hipStream_t s,
+                     uint32_t *blocks_out) {
     MvArgs a = args_in;
     const uint32_t rpb = (uint32_t)(gm.waves * (64 / gm.lpr) * gm.r);
     uint32_t blocks = 0;
@@ -589,7 +645,73 @@ hipError_t launch_mv(const MvArgs &args_in, MvGeom gm, uint32_t type, hipStream_
     case T_Q8_0: fn = pick_lpr<T_Q8_0>(gm.lpr, gm.r, gm.waves); break;
     default: return hipErrorInvalidValue;
     }
+    if (a.amax && (a.cols != 1 || blocks > a.amax_cap)) return hipErrorInvalidValue;
+    if (blocks_out) *blocks_out = blocks;
     hipLaunchKernelGGL(fn, dim3(blocks), dim3(64 * gm.waves), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int L0, int L1>
+static KFn pick_q4k_q6k() {
+    return k_mv2<T_Q4_K, L0, 2, T_Q6_K, L1, 1, 4>;
+}
+
+// Segments [0, n_seg0) of type t0 (row pairs: RoPE) and [n_seg0, n_seg) of
+// type t1 in one launch.  Instantiated for Q4_K + Q6_K (the Q4_K_M q/k + v);
+// hipErrorNotSupported for other pairs (the caller launches them apart).
+hipError_t launch_mv2(const MvArgs &args_in, uint32_t t0, MvGeom g0, uint32_t t1, MvGeom g1,
+                      hipStream_t s) {
+    if (t0 != T_Q4_K || t1 != T_Q6_K || g0.r != 2 || g1.r != 1 || g0.waves != 4 ||
+        g1.waves != 4 || (g0.lpr != 32 && g0.lpr != 64) || (g1.lpr != 32 && g1.lpr != 64) ||
+        args_in.n_seg0 == 0 || args_in.n_seg0 >= args_in.n_seg)
+        return hipErrorNotSupported;
+    MvArgs a = args_in;
+    uint32_t blocks = 0;
+    for (uint32_t i = 0; i < a.n_seg; i++) {
+        const MvGeom &g = i < a.n_seg0 ? g0 : g1;
+        const uint32_t rpb = (uint32_t)(g.waves * (64 / g.lpr) * g.r);
+        a.seg[i].block0 = blocks;
+        blocks += (a.seg[i].rows + rpb - 1) / rpb;
+    }
+    if (a.n_in % 128 || a.amax) return hipErrorInvalidValue;
+    a.tile = a.n_in <= MV_TILE ? a.n_in : MV_TILE;
+    // LDS of the wider layout (Q4_K pads every 64 elements, Q6_K every 128)
+    const size_t lds = ((size_t)a.tile + 4 * (a.tile / 64) + a.tile / 16) * sizeof(float);
+    KFn fn = g0.lpr == 32 ? (g1.lpr == 32 ? pick_q4k_q6k<32, 32>() : pick_q4k_q6k<32, 64>())
+                          : (g1.lpr == 32 ? pick_q4k_q6k<64, 32>() : pick_q4k_q6k<64, 64>());
+    hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(1024) void k_argmax_finish(const unsigned long long *__restrict__ keys,
+                                                        uint32_t n, uint32_t *__restrict__ step,
+                                                        uint32_t *__restrict__ out,
+                                                        uint32_t out_cap) {
+    __shared__ unsigned long long kb[16];
+    unsigned long long best = 0ull;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long k = __shfl_xor(best, o, 64);
+        best = k > best ? k : best;
+    }
+    if ((threadIdx.x & 63) == 0) kb[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / 64; w++) best = kb[w] > best ? kb[w] : best;
+        // no key (every logit NaN): index 0, like a first-max scan that never moves
+        const uint32_t idx = best ? 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull) : 0u;
+        const uint32_t k = step[2];
+        if (out && k < out_cap) out[k] = idx;
+        step[0] = idx;
+        step[1] = step[1] + 1;
+        step[2] = k + 1;
+    }
+}
+
+hipError_t launch_argmax_finish(const unsigned long long *keys, uint32_t n, uint32_t *step,
+                                uint32_t *out, uint32_t out_cap, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(1024), 0, s, keys, n, step, out, out_cap);
     return hipGetLastError();
 }
 

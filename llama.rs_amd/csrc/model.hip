@@ -46,53 +46,6 @@ __global__ void k_embed(WeightView w, const uint32_t *__restrict__ step, float *
     }
 }
 
-// greedy argmax (ops.rs:1035-1045: first index of the maximum), then the
-// next step: step = {token, pos + 1}; the token is also appended to out[]
-__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ logits, uint32_t n,
-                                                 uint32_t *__restrict__ step,
-                                                 uint32_t *__restrict__ out, uint32_t out_cap) {
-    __shared__ float bv[16];
-    __shared__ uint32_t bi[16];
-    float best = -INFINITY;
-    uint32_t idx = 0xFFFFFFFFu;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = logits[i];
-        if (v > best) {  // strictly greater: keeps the first index per thread
-            best = v;
-            idx = i;
-        }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const uint32_t oi = __shfl_xor(idx, o, 64);
-        if (ov > best || (ov == best && oi < idx)) {
-            best = ov;
-            idx = oi;
-        }
-    }
-    if ((threadIdx.x & 63) == 0) {
-        bv[threadIdx.x >> 6] = best;
-        bi[threadIdx.x >> 6] = idx;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        best = bv[0];
-        idx = bi[0];
-        for (uint32_t w = 1; w < blockDim.x / 64; w++)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
-                best = bv[w];
-                idx = bi[w];
-            }
-        if (idx == 0xFFFFFFFFu) idx = 0;  // all -inf / NaN: like argmax, index 0
-        const uint32_t k = step[2];
-        if (out && k < out_cap) out[k] = idx;
-        step[0] = idx;
-        step[1] = step[1] + 1;
-        step[2] = k + 1;
-    }
-}
-
 }  // namespace lrs
 
 using namespace lrs;
@@ -113,6 +66,10 @@ struct lrs_model {
     float *x, *qbuf, *att, *act, *logits, *part;
     uint32_t *cnt, *step, *gen;  // step = {token, pos, n_generated}
     uint32_t gen_cap;
+    // greedy: per-workgroup argmax keys of the head (ops.rs:1035-1045: the
+    // first index of the maximum), reduced into step / gen by k_argmax_finish
+    unsigned long long *amax;
+    uint32_t head_blocks = 0;
     uint32_t S;                  // attention splits
     _Float16 *kv;                // all layers' caches
     uint32_t *step_host;         // pinned
@@ -203,6 +160,20 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
     sv.kv = L.vc;
     const lrs_weight *ws[3] = {L.q, L.k, L.v};
     const MvSeg segs[3] = {sq, sk, sv};
+    if (L.q->v.type == L.k->v.type && L.v->v.type != L.q->v.type) {
+        // q, k of one type and v of another in a single launch (Q4_K_M: Q4_K + Q6_K)
+        a.n_seg = 3;
+        a.n_seg0 = 2;
+        a.nb = L.q->v.nb;
+        a.seg[0] = sq;
+        a.seg[1] = sk;
+        a.seg[2] = sv;
+        const MvGeom g0 = choose_geom(L.q->v.type, c.n_embd, L.q->v.n_out + L.k->v.n_out, true);
+        const MvGeom g1 = choose_geom(L.v->v.type, c.n_embd, L.v->v.n_out, false);
+        hipError_t e = launch_mv2(a, L.q->v.type, g0, L.v->v.type, g1, m->ctx->stream);
+        if (e != hipErrorNotSupported) return e;
+        a.n_seg0 = 0;
+    }
     bool done[3] = {false, false, false};
     for (int i = 0; i < 3; i++) {
         if (done[i]) continue;
@@ -288,8 +259,9 @@ hipError_t op_down(lrs_model *m, uint32_t l) {
                      m->ctx->stream);
 }
 
-// logits = W_out (rmsnorm(x) * output_norm)
-hipError_t op_head(lrs_model *m) {
+// logits = W_out (rmsnorm(x) * output_norm); greedy: each workgroup also
+// leaves the argmax key of its rows, reduced by op_argmax
+hipError_t op_head(lrs_model *m, bool greedy) {
     const lrs_config &c = m->cfg;
     MvArgs h = {};
     h.n_seg = 1;
@@ -301,14 +273,17 @@ hipError_t op_head(lrs_model *m) {
     h.norm_w = m->output_norm;
     h.eps = c.rms_eps;
     h.cols = 1;
+    if (greedy) {
+        h.amax = m->amax;
+        h.amax_cap = c.vocab;
+    }
     return launch_mv(h, choose_geom(m->output->v.type, c.n_embd, c.vocab, false), m->output->v.type,
-                     m->ctx->stream);
+                     m->ctx->stream, &m->head_blocks);
 }
 
 hipError_t op_argmax(lrs_model *m) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, m->ctx->stream, m->logits, m->cfg.vocab,
-                       m->step, m->gen, m->gen_cap);
-    return hipGetLastError();
+    return launch_argmax_finish(m->amax, m->head_blocks, m->step, m->gen, m->gen_cap,
+                                m->ctx->stream);
 }
 
 // enqueue one token's forward on the model stream
@@ -321,7 +296,7 @@ hipError_t enqueue_forward(lrs_model *m, bool greedy) {
             (e = op_down(m, l)) != hipSuccess)
             return e;
     }
-    if ((e = op_head(m)) != hipSuccess) return e;
+    if ((e = op_head(m, greedy)) != hipSuccess) return e;
     if (greedy && (e = op_argmax(m)) != hipSuccess) return e;
     return hipSuccess;
 }
@@ -453,7 +428,8 @@ int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weight
                         (void **)&m->part)) ||
         (rc = dev_alloc(m, c.n_head_kv * sizeof(uint32_t), (void **)&m->cnt)) ||
         (rc = dev_alloc(m, 4 * sizeof(uint32_t), (void **)&m->step)) ||
-        (rc = dev_alloc(m, m->gen_cap * sizeof(uint32_t), (void **)&m->gen)))
+        (rc = dev_alloc(m, m->gen_cap * sizeof(uint32_t), (void **)&m->gen)) ||
+        (rc = dev_alloc(m, (size_t)c.vocab * sizeof(unsigned long long), (void **)&m->amax)))
         return bail(rc);
     if (hipMemset(m->cnt, 0, c.n_head_kv * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess)
@@ -649,7 +625,7 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
         case LRS_OP_O: return op_o(m, l);
         case LRS_OP_GATEUP: return op_gateup(m, l);
         case LRS_OP_DOWN: return op_down(m, l);
-        default: return op_head(m);
+        default: return op_head(m, false);
         }
     };
     for (uint32_t i = 0; i < c.n_layer && i < iters; i++) LRS_HIP(one(i));  // warm

@@ -41,6 +41,9 @@ struct MvArgs {
     const float *freq;         // RoPE frequency table [rope_dim/2]
     uint32_t head_dim, rope_dim, ctx;
     uint32_t tile;             // K-tile staged in LDS (set by launch_mv)
+    uint32_t n_seg0;           // two-type launches: segments of the first type
+    unsigned long long *amax;  // [blocks] per-block argmax keys of the output, or null
+    uint32_t amax_cap;         // entries of amax
 };
 
 struct MvGeom {
