@@ -196,6 +196,33 @@ def bench_layer(lrs, ctx, steps, warmup):
     return dict(ms=ms, bytes=set_bytes, gbs=set_bytes / (ms * 1e-3) / 1e9)
 
 
+def bench_gemm(lrs, ctx, steps, warmup, m, precision):
+    """Config 5: M tokens x 5120 activations against Q4_K gate/up 13824x5120 and
+    Q6_K down 5120x13824 (the config-2 FFN), on the matrix cores."""
+    shapes = [("ffn_gate", Q4_K, 5120, 13824), ("ffn_up", Q4_K, 5120, 13824),
+              ("ffn_down", Q6_K, 13824, 5120)]
+    ws = [lrs.Weight.generate(ctx, t, 500 + i, n_in, n_out) for i, (_, t, n_in, n_out) in
+          enumerate(shapes)]
+    rng = np.random.default_rng(5)
+    a_big = ctx.alloc(4 * m * 13824)
+    y_big = ctx.alloc(4 * m * 13824)
+    a_big.upload(rng.standard_normal(m * 13824).astype(np.float32))
+    per = {}
+    for (name, t, n_in, n_out), w in zip(shapes, ws):
+        for _ in range(warmup):
+            w.gemm_dev(a_big, y_big, m, precision)
+        ctx.sync()
+        ctx.timer_start()
+        for _ in range(steps):
+            w.gemm_dev(a_big, y_big, m, precision)
+        us = ctx.timer_stop() * 1e3 / steps
+        flops = 2.0 * m * n_in * n_out
+        per[name] = dict(us=us, tflops=flops / us / 1e6)
+    tot_us = sum(v["us"] for v in per.values())
+    tot_flop = sum(2.0 * m * n_in * n_out for _, _, n_in, n_out in shapes)
+    return dict(per=per, us=tot_us, tflops=tot_flop / tot_us / 1e6, flop=tot_flop)
+
+
 def run_pmc(lrs, ctx):
     """Kernels for the counter passes: the copy calibration (an F32 tensor's
     identity dequant: 4 B read + 4 B written per element, grid-stride) and the
@@ -222,7 +249,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "layer", "pmc"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "layer", "gemm", "pmc"])
+    ap.add_argument("--m", type=int, default=512, help="gemm: prompt tokens (config 5: 128/512/2048)")
+    ap.add_argument("--precision", type=int, default=1, choices=[1, 3],
+                    help="gemm: 1 = bf16 operands, 3 = bf16 hi/lo split")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -242,6 +272,26 @@ def main():
         ctx.close()
         return
     threads = min(16, os.cpu_count() or 1)
+    if a.workload == "gemm":
+        r = bench_gemm(lrs, ctx, a.steps, a.warmup, a.m, a.precision)
+        for k, v in r["per"].items():
+            log(f"[bench]   {k:9s} {v['us']:9.1f} us {v['tflops']:8.1f} TFLOP/s")
+        peak = 2500.0  # MI355X dense bf16 MFMA
+        out = {"metric": "prefill dequant-GEMM TFLOP/s (config 5 FFN set, MFMA)",
+               "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1,
+               "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(r["us"] / 1e3, 5),
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+               "dtype": "bf16" if a.precision == 1 else "bf16x3",
+               "data": "synthetic (seeded GGUF blocks, x ~ N(0,1))",
+               "config": {"workload": "config5-prefill-gemm-ffn", "m": a.m,
+                          "weights": "gate/up Q4_K 13824x5120, down Q6_K 5120x13824",
+                          "flop_per_step": r["flop"]},
+               "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": peak,
+                            "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
+                            "traffic": None}}
+        print(json.dumps(out), flush=True)
+        ctx.close()
+        return
     if a.workload == "layer":
         r = bench_layer(lrs, ctx, a.steps, a.warmup)
         out = {"metric": "quant matvec HBM GB/s, Qwen2.5-14B layer matvec set (batch-1 decode)",

@@ -113,6 +113,18 @@ int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y,
 int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
                    uint32_t cols);
 
+/* Batched prefill GEMM on the matrix cores: y [m * n_out] = a [m * n_in] W^T,
+ * device f32 buffers, enqueued on the context stream (async).  Replaces the
+ * prefill matmul matmul::dispatch_mul_mm_q4k / shaders/mul_mm.comp
+ * (crates/llama-vulkan/src/matmul.rs:433-465), which quantizes a to int8:
+ * here a and dequant(W) go to v_mfma_f32_32x32x16_bf16 as bf16 with f32
+ * accumulation.  precision 1: each operand rounded to bf16 once;
+ * precision 3: each split into bf16 hi + lo and three products summed
+ * (~2^-16 relative, for prefill that must match the f32 forward).
+ * Weights: Q4_K, Q6_K; n_in a multiple of 64. */
+int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y_dev, uint32_t m,
+                 int precision);
+
 /* Matvec launch geometry override: lanes_per_row in {8,16,32,64}, rows per
  * lane group in {1,2,4}, waves per workgroup in {2,4,8}; all 0 = automatic.
  * Replaces the LLAMA_RS_MATVEC_GEOM knob (resident_forward.rs:164-176); the

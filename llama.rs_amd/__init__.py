@@ -63,6 +63,7 @@ def _load() -> C.CDLL:
         "lrs_weight_dequant_dev": (i32, [vp, vp, vp]),
         "lrs_matvec_f32": (i32, [vp, vp, vp, vp, u32]),
         "lrs_matvec_dev": (i32, [vp, vp, vp, vp, u32]),
+        "lrs_gemm_dev": (i32, [vp, vp, vp, vp, u32, i32]),
         "lrs_dev_alloc": (i32, [vp, sz, pvp]),
         "lrs_dev_free": (i32, [vp, vp]),
         "lrs_copy_h2d": (i32, [vp, vp, vp, sz]),
@@ -224,6 +225,24 @@ class Weight:
 
     def matvec_dev(self, x: DeviceBuffer, y: DeviceBuffer, cols: int = 1) -> None:
         check(lib.lrs_matvec_dev(self.ctx.h, self.h, x.ptr, y.ptr, cols))
+
+    def gemm_dev(self, a: DeviceBuffer, y: DeviceBuffer, m: int, precision: int = 1) -> None:
+        """Y[m][n_out] = A[m][n_in] W^T on the matrix cores (async, device buffers)."""
+        check(lib.lrs_gemm_dev(self.ctx.h, self.h, a.ptr, y.ptr, m, precision))
+
+    def gemm(self, a: np.ndarray, precision: int = 1) -> np.ndarray:
+        """Host wrapper of gemm_dev: a [m, n_in] f32 -> [m, n_out] f32."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        m = a.shape[0]
+        ab, yb = self.ctx.alloc(a.nbytes), self.ctx.alloc(4 * m * self.n_out)
+        try:
+            ab.upload(a)
+            self.gemm_dev(ab, yb, m, precision)
+            self.ctx.sync()
+            return yb.download(np.float32, m * self.n_out).reshape(m, self.n_out)
+        finally:
+            ab.free()
+            yb.free()
 
     def free(self) -> None:
         if getattr(self, "h", None) and self.ctx.h:

@@ -325,6 +325,18 @@ int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y, 
     return LRS_OK;
 }
 
+int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y_dev, uint32_t m,
+                 int precision) {
+    if (!ctx || !w || !a_dev || !y_dev) return fail(LRS_E_ARG, "null argument");
+    if (m == 0) return fail(LRS_E_ARG, "m must be >= 1");
+    if (precision != 1 && precision != 3) return fail(LRS_E_ARG, "precision must be 1 or 3");
+    if (w->v.type != T_Q4_K && w->v.type != T_Q6_K)
+        return fail(LRS_E_UNSUPPORTED, "the GEMM supports Q4_K and Q6_K weights");
+    SETDEV(ctx);
+    LRS_HIP(launch_gemm(w->v, a_dev, y_dev, m, w->v.n_out, precision, ctx->stream));
+    return LRS_OK;
+}
+
 int lrs_matvec_set_geom(int lanes_per_row, int rows, int waves) {
     if (set_matvec_geom(lanes_per_row, rows, waves) != 0)
         return fail(LRS_E_ARG, "geometry must be lanes_per_row in {16,32,64}, rows in {1,2,4}, "

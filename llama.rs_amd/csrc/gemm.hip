@@ -1,0 +1,204 @@
+// gemm.hip — dequantize x GEMM for batched prefill on the gfx950 matrix cores.
+//
+// Y[m][n] = sum_k A[m][k] * W[n][k]: A = M tokens x K activations (f32 in
+// HBM), W = a resident N x K GGUF weight (Q4_K or Q6_K).  Replaces the
+// reference's prefill GEMM (shaders/mul_mm.comp, dispatched by
+// matmul::dispatch_mul_mm_q4k, crates/llama-vulkan/src/matmul.rs:433-465),
+// which quantizes A to int8; here both operands go to the MFMA units as bf16
+// (v_mfma_f32_32x32x16_bf16, f32 accumulate):
+//   PREC 1  A and dequant(W) rounded to bf16 once
+//   PREC 3  both split into bf16 hi + lo, three products (hi*hi + hi*lo +
+//           lo*hi): ~2^-16 relative per product, for prefill whose logits must
+//           match the f32 reference
+//
+// Tiling.  A 256-thread workgroup owns a 128 (tokens) x 128 (weight rows)
+// output tile; each of its 4 wavefronts a 64 x 64 quarter = 2 x 2 MFMA tiles
+// of 32 x 32.  K advances 64 at a time (one Q4_K qs group / a quarter of a
+// Q6_K super-block): every thread stages 32 activations (f32 -> bf16) and
+// dequantizes 32 weights of one row (bit-exact f32 dequant as in dequant.rs,
+// then bf16) into LDS, then each wavefront issues 4 K16 steps x 4 tiles of
+// MFMA.  LDS rows are padded to 72 bf16 so the 32 lanes that read 32
+// different rows at one K offset hit distinct banks.
+#include "lrs_internal.h"
+#include "quant_dev.h"
+
+namespace lrs {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+
+constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 64;
+constexpr int GM_LD = GM_BK + 8;  // padded LDS row (bf16 elements)
+
+struct GemmArgs {
+    const float *a;      // [M][K]
+    float *y;            // [M][ldy]
+    const uint8_t *q;    // weight q-part (device layout)
+    const uint16_t *d;   // Q6_K d array
+    uint32_t M, N, K, nb, ldy;
+};
+
+// 32 consecutive weights of row n starting at element e (e % 32 == 0), f32
+// values exactly as ggml_cpu::dequant (dequant.rs:101-258)
+template <uint32_t T>
+__device__ __forceinline__ void deq32(const GemmArgs &g, uint32_t n, uint32_t e, float (&w)[32]) {
+    const size_t blk = (size_t)n * g.nb + (e >> 8);
+    const uint32_t o = e & 255;  // offset inside the super-block
+    if constexpr (T == T_Q4_K) {
+        const uint8_t *b = g.q + blk * 144;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(b);
+        const uint32_t j = o >> 6, hi = (o >> 5) & 1;  // qs group, high nibbles
+        const uint4 q0 = *reinterpret_cast<const uint4 *>(b + 16 + 32 * j);
+        const uint4 q1 = *reinterpret_cast<const uint4 *>(b + 16 + 32 * j + 16);
+        const uint8_t *sb = reinterpret_cast<const uint8_t *>(&hd) + 4;
+        uint32_t sc, m;
+        scale_min_k4(2 * j + hi, sb, sc, m);
+        const float dv = h2f((uint16_t)(hd.x & 0xFFFF)), mv = h2f((uint16_t)(hd.x >> 16));
+        const float d1 = __fmul_rn(dv, (float)sc), m1 = __fmul_rn(mv, (float)m);
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xFF;
+            const uint32_t q = hi ? (byte >> 4) : (byte & 15);
+            w[i] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
+        }
+    } else {  // T_Q6_K: device layout [ql 128 | qh 64 | scales 16] + d array
+        const uint8_t *b = g.q + blk * Q6_QBYTES;
+        const float dv = h2f(g.d[blk]);
+        const uint32_t h = o >> 7, quarter = (o >> 5) & 3;  // elements 128h + 32 quarter + l
+        const uint8_t *ql = b + 64 * h + 32 * (quarter & 1);
+        const uint8_t *qh = b + 128 + 32 * h;
+        const uint4 l0 = *reinterpret_cast<const uint4 *>(ql), l1 = *reinterpret_cast<const uint4 *>(ql + 16);
+        const uint4 h0 = *reinterpret_cast<const uint4 *>(qh), h1 = *reinterpret_cast<const uint4 *>(qh + 16);
+        const int8_t s0 = (int8_t)b[192 + 8 * h + 2 * quarter], s1 = (int8_t)b[192 + 8 * h + 1 + 2 * quarter];
+        const float ds0 = __fmul_rn(dv, (float)s0), ds1 = __fmul_rn(dv, (float)s1);
+        const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+        const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xFF;
+            const uint32_t hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xFF;
+            const uint32_t lo = quarter < 2 ? (lb & 15) : (lb >> 4);
+            const int q = (int)(lo | (((hb >> (2 * quarter)) & 3) << 4)) - 32;
+            w[i] = __fmul_rn(i < 16 ? ds0 : ds1, (float)q);
+        }
+    }
+}
+
+__device__ __forceinline__ __bf16 to_bf16(float v) { return (__bf16)v; }
+
+// stores 32 values as bf16 (hi) and, for PREC 3, the bf16 remainders (lo)
+template <int PREC>
+__device__ __forceinline__ void put32(__bf16 *hi, __bf16 *lo, const float (&v)[32]) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        bf16x8 h, l;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float x = v[8 * c + i];
+            h[i] = to_bf16(x);
+            if constexpr (PREC == 3) l[i] = to_bf16(x - (float)h[i]);
+        }
+        *reinterpret_cast<bf16x8 *>(hi + 8 * c) = h;
+        if constexpr (PREC == 3) *reinterpret_cast<bf16x8 *>(lo + 8 * c) = l;
+    }
+}
+
+template <uint32_t T, int PREC>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+    constexpr int NS = PREC == 3 ? 2 : 1;  // hi (+ lo) planes
+    __shared__ __attribute__((aligned(16))) __bf16 As[NS][GM_BM * GM_LD];
+    __shared__ __attribute__((aligned(16))) __bf16 Ws[NS][GM_BN * GM_LD];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t m0 = blockIdx.y * GM_BM, n0 = blockIdx.x * GM_BN;
+    const uint32_t wm = wave >> 1, wn = wave & 1;  // wave's 64 x 64 quarter
+    // staging roles: thread t handles row t/2, half t%2 (32 of the 64 K)
+    const uint32_t sr = tid >> 1, sh = (tid & 1) * 32;
+    const uint32_t am = min(m0 + sr, g.M - 1), wr = min(n0 + sr, g.N - 1);
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    for (uint32_t k0 = 0; k0 < g.K; k0 += GM_BK) {
+        {
+            float v[32];
+            const float4 *ap = reinterpret_cast<const float4 *>(g.a + (size_t)am * g.K + k0 + sh);
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const float4 t = ap[c];
+                v[4 * c] = t.x;
+                v[4 * c + 1] = t.y;
+                v[4 * c + 2] = t.z;
+                v[4 * c + 3] = t.w;
+            }
+            put32<PREC>(&As[0][sr * GM_LD + sh], &As[NS - 1][sr * GM_LD + sh], v);
+            deq32<T>(g, wr, k0 + sh, v);
+            put32<PREC>(&Ws[0][sr * GM_LD + sh], &Ws[NS - 1][sr * GM_LD + sh], v);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < GM_BK / 16; ks++) {
+            const uint32_t kk = 16 * ks + 8 * (lane >> 5);
+            bf16x8 a[NS][2], b[NS][2];
+#pragma unroll
+            for (int p = 0; p < NS; p++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    a[p][t] = *reinterpret_cast<const bf16x8 *>(&As[p][(64 * wm + 32 * t + (lane & 31)) * GM_LD + kk]);
+                    b[p][t] = *reinterpret_cast<const bf16x8 *>(&Ws[p][(64 * wn + 32 * t + (lane & 31)) * GM_LD + kk]);
+                }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    if constexpr (PREC == 3) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0][j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1][j], acc[i][j], 0, 0, 0);
+                    }
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+    }
+    // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t n = n0 + 64 * wn + 32 * j + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < g.M && n < g.N) g.y[(size_t)m * g.ldy + n] = acc[i][j][r];
+            }
+        }
+}
+
+hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint32_t ldy, int prec,
+                       hipStream_t s) {
+    if (M == 0 || w.n_in % GM_BK) return hipErrorInvalidValue;
+    GemmArgs g;
+    g.a = a;
+    g.y = y;
+    g.q = w.q;
+    g.d = w.d;
+    g.M = M;
+    g.N = w.n_out;
+    g.K = w.n_in;
+    g.nb = w.nb;
+    g.ldy = ldy;
+    dim3 grid((w.n_out + GM_BN - 1) / GM_BN, (M + GM_BM - 1) / GM_BM);
+    void (*fn)(GemmArgs) = nullptr;
+    if (w.type == T_Q4_K) fn = prec == 3 ? k_gemm<T_Q4_K, 3> : k_gemm<T_Q4_K, 1>;
+    else if (w.type == T_Q6_K) fn = prec == 3 ? k_gemm<T_Q6_K, 3> : k_gemm<T_Q6_K, 1>;
+    else return hipErrorNotSupported;
+    hipLaunchKernelGGL(fn, grid, dim3(256), 0, s, g);
+    return hipGetLastError();
+}
+
+}  // namespace lrs

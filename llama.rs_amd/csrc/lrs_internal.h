@@ -101,6 +101,9 @@ hipError_t launch_argmax_finish(const unsigned long long *keys, uint32_t n, uint
                                 uint32_t *out, uint32_t out_cap, hipStream_t s);
 hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols,
                          const float *bias, hipStream_t s);
+// Y[M][ldy] = A[M][K] W^T on the matrix cores (prec 1: bf16, 3: bf16 hi/lo split)
+hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint32_t ldy, int prec,
+                       hipStream_t s);
 
 }  // namespace lrs
 

@@ -1,0 +1,70 @@
+"""GPU parity of the batched-prefill dequant-GEMM (lrs_gemm_dev) against the
+CPU oracle's dequant (bit-exact dequant.rs restatement) and float64 products.
+
+precision 1 (bf16 operands, f32 accumulation) is checked
+against the exact product of the same bf16-rounded operands (tolerance 1e-5
+relative L2: only the f32 summation order differs); precision 3 (bf16 hi/lo
+split) against the f32 operands themselves (tolerance 1e-4, the north-star
+GEMM bar).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+Q4_K, Q6_K = 12, 14
+
+
+@pytest.fixture(scope="module")
+def ctx(lrs):
+    c = lrs.Context()
+    yield c
+    c.close()
+
+
+def bf16(x):
+    """Round float32 to the nearest bfloat16 (ties to even), as float32."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+    return b.astype(np.uint32).view(np.float32)
+
+
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("m,n,k", [(1, 200, 512), (7, 128, 256), (130, 300, 768), (256, 256, 1024)])
+def test_gemm_matches_oracle(lrs, orc, ctx, t, m, n, k):
+    w = orc.gen_weight(t, 31 + m + n, n, k, mode=1)
+    deq = orc.dequant(t, w).reshape(n, k)
+    a = np.random.default_rng(m * 7 + n).standard_normal((m, k)).astype(np.float32)
+    W = lrs.Weight.upload(ctx, t, w, k, n)
+    y1 = W.gemm(a, precision=1)
+    ref1 = bf16(a).astype(np.float64) @ bf16(deq).astype(np.float64).T
+    assert rel_l2(y1, ref1) < 1e-5
+    y3 = W.gemm(a, precision=3)
+    ref = a.astype(np.float64) @ deq.astype(np.float64).T
+    assert rel_l2(y3, ref) < 1e-4
+    # plain bf16 is ~2^-9 per operand: far from f32, which is why prefill uses 3
+    assert rel_l2(y1, ref) < 1e-2
+
+
+def test_gemm_row_of_one_hot_activations_is_a_weight_column(lrs, orc, ctx):
+    """a = identity rows: y[i] = column i of W (exact for values that bf16
+    represents, which the hi/lo split reaches to 2^-16)."""
+    k, n = 256, 64
+    w = orc.gen_weight(Q4_K, 5, n, k, mode=1)
+    deq = orc.dequant(Q4_K, w).reshape(n, k)
+    a = np.eye(k, dtype=np.float32)[:40]
+    y = lrs.Weight.upload(ctx, Q4_K, w, k, n).gemm(a, precision=3)
+    assert np.allclose(y, deq[:, :40].T, rtol=2e-5, atol=0)
+
+
+def test_gemm_rejects_bad_arguments(lrs, orc, ctx):
+    w = lrs.Weight.upload(ctx, 8, orc.gen_weight(8, 1, 4, 64), 64, 4)  # Q8_0
+    with pytest.raises(lrs.ModelError):
+        w.gemm(np.zeros((2, 64), np.float32))
+    w4 = lrs.Weight.upload(ctx, Q4_K, orc.gen_weight(Q4_K, 1, 4, 256), 256, 4)
+    with pytest.raises(lrs.ModelError):
+        w4.gemm(np.zeros((2, 256), np.float32), precision=2)
