@@ -105,7 +105,15 @@ def bench_decode(lrs, ctx, steps, warmup):
     prompt = rng.integers(0, cfg["vocab"], PROMPT).astype(np.uint32)
     t0 = time.perf_counter()
     m.decode_batch(prompt[:-1], 0)
-    log(f"[bench] prompt {PROMPT - 1} tokens in {time.perf_counter() - t0:.2f} s")
+    log(f"[bench] prompt {PROMPT - 1} tokens in {time.perf_counter() - t0:.2f} s (first call)")
+    # the same prompt again, buffers allocated: the batched-prompt rate
+    # (logits of the last token copied back included)
+    m.reset()
+    t0 = time.perf_counter()
+    m.decode_batch(prompt[:-1], 0)
+    prefill_s = time.perf_counter() - t0
+    log(f"[bench] prompt {PROMPT - 1} tokens in {prefill_s:.3f} s -> "
+        f"{(PROMPT - 1) / prefill_s:.0f} tok/s (batch_size {m.batch_size()})")
     last = prompt[-1:]
     if warmup:
         m.generate_greedy(last, warmup, pos0=PROMPT - 1)
@@ -132,6 +140,7 @@ def bench_decode(lrs, ctx, steps, warmup):
             f"{v['per_token_us'] / 1e3:.3f} ms/token")
     m.close()
     return dict(cfg=cfg, ms_tok=ms_tok, ev_ms_tok=ev_ms / steps, tok_bytes=tok_bytes,
+                prefill_tok_s=(PROMPT - 1) / prefill_s,
                 kv_bytes=kv_bytes, w_bytes=m.bytes_per_token, ops=ops)
 
 
@@ -336,7 +345,8 @@ def main():
                    "weights": "q,k,o,gate,up,token_embd Q4_K; v,down,output Q6_K",
                    "bytes_per_token": int(r["tok_bytes"]),
                    "token_roofline_frac": round(eff_gbs / HBM_PEAK_GBS, 4),
-                   "effective_gbs": round(eff_gbs, 1)},
+                   "effective_gbs": round(eff_gbs, 1),
+                   "prompt_tok_s": round(r["prefill_tok_s"], 1)},
         "roofline": {"bound": "hbm", "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(dom), "kernel": OP_NAMES[dom], "op": dom,

@@ -36,6 +36,7 @@ struct GemmArgs {
     const uint8_t *q;    // weight q-part (device layout)
     const uint16_t *d;   // Q6_K d array
     uint32_t M, N, K, nb, ldy;
+    uint32_t accum;      // 1: y += A W^T (residual add), 0: y = A W^T
 };
 
 // 32 consecutive weights of row n starting at element e (e % 32 == 0), f32
@@ -174,13 +175,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < g.M && n < g.N) g.y[(size_t)m * g.ldy + n] = acc[i][j][r];
+                if (m < g.M && n < g.N) {
+                    float *o = g.y + (size_t)m * g.ldy + n;
+                    *o = g.accum ? *o + acc[i][j][r] : acc[i][j][r];
+                }
             }
         }
 }
 
 hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint32_t ldy, int prec,
-                       hipStream_t s) {
+                       hipStream_t s, bool accum) {
     if (M == 0 || w.n_in % GM_BK) return hipErrorInvalidValue;
     GemmArgs g;
     g.a = a;
@@ -192,6 +196,7 @@ hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint3
     g.K = w.n_in;
     g.nb = w.nb;
     g.ldy = ldy;
+    g.accum = accum ? 1u : 0u;
     dim3 grid((w.n_out + GM_BN - 1) / GM_BN, (M + GM_BM - 1) / GM_BM);
     void (*fn)(GemmArgs) = nullptr;
     if (w.type == T_Q4_K) fn = prec == 3 ? k_gemm<T_Q4_K, 3> : k_gemm<T_Q4_K, 1>;

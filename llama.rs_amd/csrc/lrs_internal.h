@@ -103,7 +103,19 @@ hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols,
                          const float *bias, hipStream_t s);
 // Y[M][ldy] = A[M][K] W^T on the matrix cores (prec 1: bf16, 3: bf16 hi/lo split)
 hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint32_t ldy, int prec,
-                       hipStream_t s);
+                       hipStream_t s, bool accum = false);
+// batched prompt block (prefill.hip)
+hipError_t launch_rmsnorm_rows(const float *X, const float *w, float eps, uint32_t E, uint32_t n,
+                               float *Y, hipStream_t s);
+hipError_t launch_qkv_post(const float *qt, const float *kt, const float *vt, const float *bq,
+                           const float *bk, const float *bv, const float *freq, float *q,
+                           _Float16 *kc, _Float16 *vc, uint32_t n, uint32_t pos0, uint32_t qd,
+                           uint32_t kvd, uint32_t hd, uint32_t rope_dim, uint32_t ctx,
+                           hipStream_t s);
+hipError_t launch_attn_prefill(const float *q, const _Float16 *kc, const _Float16 *vc, float *out,
+                               uint32_t n, uint32_t pos0, uint32_t n_head, uint32_t n_kv,
+                               uint32_t hd, uint32_t ctx, hipStream_t s);
+hipError_t launch_swiglu_rows(float *G, const float *U, size_t n, hipStream_t s);
 
 }  // namespace lrs
 

@@ -70,6 +70,12 @@ struct lrs_model {
     // first index of the maximum), reduced into step / gen by k_argmax_finish
     unsigned long long *amax;
     uint32_t head_blocks = 0;
+    // batched prompt blocks (allocated at the first block): residual,
+    // normalised rows, q/k/v GEMM outputs, q after RoPE, attention output,
+    // gate / up, token ids
+    uint32_t pb_cap = 0;
+    float *pX = nullptr, *pXN, *pQt, *pKt, *pVt, *pQ, *pATT, *pG, *pU;
+    uint32_t *ptok;
     uint32_t S;                  // attention splits
     _Float16 *kv;                // all layers' caches
     uint32_t *step_host;         // pinned
@@ -471,10 +477,101 @@ static int check_step(lrs_model *m, uint32_t token, uint32_t pos) {
     return LRS_OK;
 }
 
+// ---- batched prompt blocks on the matrix cores --------------------------
+// Tokens per block of the batched prompt path (batch_size()).
+static constexpr uint32_t PREFILL_BLOCK = 512;
+
+// every matmul weight has a GEMM kernel and the attention shape is supported
+static bool prefill_capable(const lrs_model *m) {
+    auto ok = [](const lrs_weight *w) {
+        return (w->v.type == T_Q4_K || w->v.type == T_Q6_K) && w->v.n_in % 64 == 0;
+    };
+    const lrs_config &c = m->cfg;
+    if ((c.head_dim != 64 && c.head_dim != 128) || c.n_head / c.n_head_kv > 8 || c.n_embd % 4)
+        return false;
+    for (const DevLayer &L : m->layers)
+        if (!ok(L.q) || !ok(L.k) || !ok(L.v) || !ok(L.o) || !ok(L.gate) || !ok(L.up) ||
+            !ok(L.down))
+            return false;
+    return true;
+}
+
+static int ensure_prefill(lrs_model *m) {
+    if (m->pb_cap) return LRS_OK;
+    const lrs_config &c = m->cfg;
+    const size_t B = PREFILL_BLOCK, qd = (size_t)c.n_head * c.head_dim,
+                 kvd = (size_t)c.n_head_kv * c.head_dim;
+    int rc;
+    if ((rc = dev_alloc(m, B * c.n_embd * 4, (void **)&m->pX)) ||
+        (rc = dev_alloc(m, B * c.n_embd * 4, (void **)&m->pXN)) ||
+        (rc = dev_alloc(m, B * qd * 4, (void **)&m->pQt)) ||
+        (rc = dev_alloc(m, B * kvd * 4, (void **)&m->pKt)) ||
+        (rc = dev_alloc(m, B * kvd * 4, (void **)&m->pVt)) ||
+        (rc = dev_alloc(m, B * qd * 4, (void **)&m->pQ)) ||
+        (rc = dev_alloc(m, B * qd * 4, (void **)&m->pATT)) ||
+        (rc = dev_alloc(m, B * c.n_ff * 4, (void **)&m->pG)) ||
+        (rc = dev_alloc(m, B * c.n_ff * 4, (void **)&m->pU)) ||
+        (rc = dev_alloc(m, B * 4, (void **)&m->ptok)))
+        return rc;
+    m->pb_cap = PREFILL_BLOCK;
+    return LRS_OK;
+}
+
+// one block of nb tokens at positions pos0.. through every layer (the
+// forward of model.rs:99-266 with the matmuls as GEMMs, operands split into
+// bf16 hi + lo); leaves the residual rows in pX
+static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint32_t pos0) {
+    const lrs_config &c = m->cfg;
+    hipStream_t s = m->ctx->stream;
+    const uint32_t qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim, E = c.n_embd;
+    constexpr int P = 3;
+    LRS_HIP(hipMemcpyAsync(m->ptok, tokens, nb * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    LRS_HIP(launch_dequant_rows(m->embd->v, m->ptok, nb, m->pX, s));
+    for (uint32_t l = 0; l < c.n_layer; l++) {
+        const DevLayer &L = m->layers[l];
+        LRS_HIP(launch_rmsnorm_rows(m->pX, L.attn_norm, c.rms_eps, E, nb, m->pXN, s));
+        LRS_HIP(launch_gemm(L.q->v, m->pXN, m->pQt, nb, qd, P, s));
+        LRS_HIP(launch_gemm(L.k->v, m->pXN, m->pKt, nb, kvd, P, s));
+        LRS_HIP(launch_gemm(L.v->v, m->pXN, m->pVt, nb, kvd, P, s));
+        LRS_HIP(launch_qkv_post(m->pQt, m->pKt, m->pVt, L.bq, L.bk, L.bv, m->freq, m->pQ, L.kc,
+                                L.vc, nb, pos0, qd, kvd, c.head_dim, c.rope_dim, c.ctx, s));
+        LRS_HIP(launch_attn_prefill(m->pQ, L.kc, L.vc, m->pATT, nb, pos0, c.n_head, c.n_head_kv,
+                                    c.head_dim, c.ctx, s));
+        LRS_HIP(launch_gemm(L.o->v, m->pATT, m->pX, nb, E, P, s, true));
+        LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, m->pXN, s));
+        LRS_HIP(launch_gemm(L.gate->v, m->pXN, m->pG, nb, c.n_ff, P, s));
+        LRS_HIP(launch_gemm(L.up->v, m->pXN, m->pU, nb, c.n_ff, P, s));
+        LRS_HIP(launch_swiglu_rows(m->pG, m->pU, (size_t)nb * c.n_ff, s));
+        LRS_HIP(launch_gemm(L.down->v, m->pG, m->pX, nb, E, P, s, true));
+    }
+    return LRS_OK;
+}
+
+// the prompt in blocks of at most PREFILL_BLOCK tokens; with head, the logits
+// of the last token land in m->logits
+static int prefill(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0, bool head) {
+    int rc = ensure_prefill(m);
+    if (rc) return rc;
+    hipStream_t s = m->ctx->stream;
+    uint32_t nb = 0;
+    for (uint32_t i = 0; i < n; i += nb) {
+        nb = min(m->pb_cap, n - i);
+        if ((rc = prefill_block(m, tokens + i, nb, pos0 + i))) return rc;
+        // the host token ids of this block must stay valid until it is read
+        LRS_HIP(hipStreamSynchronize(s));
+    }
+    if (!head) return LRS_OK;
+    LRS_HIP(hipMemcpyAsync(m->x, m->pX + (size_t)(nb - 1) * m->cfg.n_embd,
+                           m->cfg.n_embd * sizeof(float), hipMemcpyDeviceToDevice, s));
+    LRS_HIP(op_head(m, false));
+    return LRS_OK;
+}
+
 // enqueues n tokens at pos0.. (logits graph) without waiting; every token's
 // {token, pos} goes through its own pinned slot, and the stream is drained
 // whenever the slots run out
 static constexpr uint32_t STEP_SLOTS = 1024;
+
 static int enqueue_tokens(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0) {
     for (uint32_t i = 0; i < n; i++) {
         int rc = check_step(m, tokens[i], pos0 + i);
@@ -515,14 +612,26 @@ int lrs_decode(lrs_model *m, uint32_t token, uint32_t pos, float *logits) {
     return LRS_OK;
 }
 
-uint32_t lrs_batch_size(const lrs_model *m) { return m ? 1u : 0u; }
+uint32_t lrs_batch_size(const lrs_model *m) {
+    if (!m) return 0u;
+    return prefill_capable(m) ? PREFILL_BLOCK : 1u;
+}
 
 int lrs_decode_batch(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0, float *logits) {
     if (!m || !tokens || !logits || n == 0) return fail(LRS_E_ARG, "null argument / empty batch");
-    // GpuResidentDecode::decode_batch default (gpu.rs:392-400): token by
-    // token, the logits of the last one are returned
-    int rc = enqueue_tokens(m, tokens, n, pos0);
-    if (rc) return rc;
+    // GpuResidentDecode::decode_batch (gpu.rs:392-400): the logits of the last
+    // token; several tokens go through the matrix-core GEMMs in blocks when
+    // every weight has one, else token by token
+    int rc;
+    if (n > 1 && prefill_capable(m)) {
+        for (uint32_t i = 0; i < n; i++)
+            if ((rc = check_step(m, tokens[i], pos0 + i))) return rc;
+        LRS_HIP(hipSetDevice(m->ctx->device));
+        LRS_HIP(hipStreamSynchronize(m->ctx->stream));
+        if ((rc = prefill(m, tokens, n, pos0, true))) return rc;
+    } else if ((rc = enqueue_tokens(m, tokens, n, pos0))) {
+        return rc;
+    }
     hipStream_t s = m->ctx->stream;
     LRS_HIP(hipMemcpyAsync(m->logits_host, m->logits, m->cfg.vocab * sizeof(float),
                            hipMemcpyDeviceToHost, s));
@@ -571,7 +680,11 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
     // prefill: tokens 0..n_prompt-2, then the last prompt token starts the
     // greedy chain (its argmax is the first generated token)
     int rc = LRS_OK;
-    if (n_prompt > 1 && (rc = enqueue_tokens(m, prompt, n_prompt - 1, pos0))) return rc;
+    if (n_prompt > 2 && prefill_capable(m)) {
+        if ((rc = prefill(m, prompt, n_prompt - 1, pos0, false))) return rc;
+    } else if (n_prompt > 1 && (rc = enqueue_tokens(m, prompt, n_prompt - 1, pos0))) {
+        return rc;
+    }
     LRS_HIP(hipStreamSynchronize(s));
     m->step_host[0] = prompt[n_prompt - 1];
     m->step_host[1] = pos0 + n_prompt - 1;

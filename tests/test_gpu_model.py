@@ -63,7 +63,12 @@ def test_decode_logits_and_greedy_match_oracle(lrs, orc, ctx, name, cfg, mix, mo
     assert got == want
 
 
-def test_decode_batch_equals_token_loop_and_reset_is_deterministic(lrs, orc, ctx):
+def test_decode_batch_matches_token_loop_and_reset_is_deterministic(lrs, orc, ctx):
+    """decode_batch runs the prompt through the matrix-core GEMMs (operands
+    split into bf16 hi + lo) instead of the matvecs.  The two differ by f32
+    summation order, which the f16 K/V cache turns into an occasional 1-ulp
+    f16 difference (2^-11 relative): both stay within the oracle bar, with the
+    same argmax."""
     cfg = modelgen.TINY
     w = modelgen.host_model(orc, cfg, seed=12)
     gm = modelgen.gpu_model(lrs, ctx, cfg, w)
@@ -72,12 +77,103 @@ def test_decode_batch_equals_token_loop_and_reset_is_deterministic(lrs, orc, ctx
         last = gm.decode(t, p)
     gm.reset()
     b = gm.decode_batch(toks, 0)
-    assert np.array_equal(b, last)
-    assert gm.batch_size() >= 1 and len(gm) == len(toks)
+    o = orc.Model(cfg, w, kv_f16=True, threads=8).forward(toks)
+    assert rel_l2(b, o) < LOGIT_TOL and rel_l2(last, o) < LOGIT_TOL
+    assert rel_l2(b, last) < LOGIT_TOL
+    assert int(np.argmax(b)) == int(np.argmax(last)) == int(np.argmax(o))
+    assert gm.batch_size() == 512 and len(gm) == len(toks)
+    gm.reset()
+    assert np.array_equal(gm.decode_batch(toks, 0), b)  # deterministic
     # greedy on device equals argmax of host logits
     gm.reset()
     gm.decode_batch(toks[:-1], 0)
     assert gm.decode_greedy(toks[-1], len(toks) - 1) == int(np.argmax(last))
+
+
+# Random-init models with the wide "mode 1" block scales amplify f16 K/V
+# rounding: for some seeds and lengths even the oracle with an f16 cache and
+# the oracle with an f32 cache differ by more than 1e-3.  The batched-prompt
+# cases therefore use the BASELINE weight distributions (mode 0), where the
+# logits track the oracle to ~1e-5 and a 1e-3 miss would be a real defect.
+PREFILL_CASES = [
+    # crosses the 512-token block boundary
+    ("tiny-q4km-600", dict(modelgen.TINY, ctx=640), 600, 21),
+    ("gqa5-q4km-150", modelgen.GQA5, 150, 21),
+    ("gqa5-q4km-40", modelgen.GQA5, 40, 23),
+]
+
+
+@pytest.mark.parametrize("name,cfg,n,seed", PREFILL_CASES, ids=[c[0] for c in PREFILL_CASES])
+def test_batched_prompt_matches_oracle(lrs, orc, ctx, name, cfg, n, seed):
+    """The batched prompt (GEMM + batched RMSNorm / RoPE / causal attention)
+    against Model::forward over the same prompt, then decode steps that read
+    the cache it wrote, then 32 greedy steps after a batched prompt."""
+    w = modelgen.host_model(orc, cfg, seed=seed, mode=0, d_lo=1e-3, d_hi=1e-2)
+    gm = modelgen.gpu_model(lrs, ctx, cfg, w)
+    assert gm.batch_size() == 512
+    om = orc.Model(cfg, w, kv_f16=True, threads=8)
+    prompt = np.random.default_rng(9).integers(0, cfg["vocab"], n).tolist()
+    g = gm.decode_batch(prompt, 0)
+    o = om.forward(prompt)
+    print(f"{name}: prompt logits rel L2 {rel_l2(g, o):.2e}")
+    assert rel_l2(g, o) < LOGIT_TOL, rel_l2(g, o)
+    assert int(np.argmax(g)) == int(np.argmax(o))
+    for i, t in enumerate([7, 2, 5]):
+        g = gm.decode(t, n + i)
+        o = om.forward([t])
+        assert rel_l2(g, o) < LOGIT_TOL, (i, rel_l2(g, o))
+        assert int(np.argmax(g)) == int(np.argmax(o))
+    # a prompt split over two calls (the second block attends to the first)
+    gm.reset()
+    k = n // 3
+    gm.decode_batch(prompt[:k], 0)
+    g2 = gm.decode_batch(prompt[k:], k)
+    om2 = orc.Model(cfg, w, kv_f16=True, threads=8)
+    o2 = om2.forward(prompt)
+    assert rel_l2(g2, o2) < LOGIT_TOL
+    assert int(np.argmax(g2)) == int(np.argmax(o2))
+    # greedy generation after a batched prompt
+    gm.reset()
+    short = prompt[:20]
+    om3 = orc.Model(cfg, w, kv_f16=True, threads=8)
+    assert gm.generate_greedy(short, 32).tolist() == modelgen.oracle_greedy(om3, short, 32)
+
+
+def test_prefill_in_blocks_matches_token_by_token(lrs, orc, ctx):
+    """integration.rs:1916-1995: 2 * batch_size() + 3 tokens, whole blocks
+    through decode_batch and the rest through decode, against decode() token
+    by token; max |difference| / max |logit| < 1e-3 and the same argmax."""
+    cfg = dict(modelgen.TINY, ctx=1100)
+    w = modelgen.host_model(orc, cfg, seed=24, mode=0, d_lo=1e-3, d_hi=1e-2)
+    gm = modelgen.gpu_model(lrs, ctx, cfg, w)
+    nb = gm.batch_size()
+    seq = np.random.default_rng(4).integers(0, cfg["vocab"], 2 * nb + 3).tolist()
+    for pos, t in enumerate(seq):
+        ref = gm.decode(t, pos)
+    gm.reset()
+    pos = 0
+    while len(seq) - pos >= nb:
+        got = gm.decode_batch(seq[pos:pos + nb], pos)
+        pos += nb
+    for t in seq[pos:]:
+        got = gm.decode(t, pos)
+        pos += 1
+    max_rel = float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-6))
+    print(f"prefill {len(seq)} tokens in blocks of {nb}: max rel {max_rel:.2e}")
+    assert max_rel < 1e-3
+    assert int(np.argmax(got)) == int(np.argmax(ref))
+
+
+def test_token_path_models_report_batch_size_one(lrs, orc, ctx):
+    cfg = modelgen.TINY
+    w = modelgen.host_model(orc, cfg, seed=15, mix=modelgen.ALL_Q8_0)
+    gm = modelgen.gpu_model(lrs, ctx, cfg, w)
+    assert gm.batch_size() == 1
+    toks = [1, 2, 3, 4]
+    for p, t in enumerate(toks):
+        last = gm.decode(t, p)
+    gm.reset()
+    assert np.array_equal(gm.decode_batch(toks, 0), last)
 
 
 def test_errors(lrs, orc, ctx):
