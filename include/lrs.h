@@ -105,8 +105,9 @@ int lrs_weight_dequant_dev(lrs_ctx *ctx, const lrs_weight *w, float *out_dev);
 /* y = W x for `cols` columns: x [cols*n_in] host f32, y [cols*n_out] host f32.
  * GpuMatmul::matvec_q8_0 (crates/llama-model/src/gpu.rs:1057-1065) generalised
  * to every resident type, and matmul::dispatch_{q8_0,q4_k,q5_k,q6_k}_matvec
- * (crates/llama-vulkan/src/matmul.rs:36-430).  Activations stay f32 (no int8
- * activation quantization).  Blocking. */
+ * (crates/llama-vulkan/src/matmul.rs:36-430).  The activation keeps 22
+ * significant bits per 32-element block (three exact int8 digits on the
+ * matrix cores; the reference rounds it to 8 bits).  Blocking. */
 int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y,
                    uint32_t cols);
 /* Same on device buffers, enqueued on the context stream (async). */
@@ -125,11 +126,11 @@ int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float 
 int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y_dev, uint32_t m,
                  int precision);
 
-/* Matvec launch geometry override: lanes_per_row in {8,16,32,64}, rows per
- * lane group in {1,2,4}, waves per workgroup in {2,4,8}; all 0 = automatic.
- * Replaces the LLAMA_RS_MATVEC_GEOM knob (resident_forward.rs:164-176); the
- * LRS_MATVEC_GEOM="lpr,rows,waves" environment variable sets the initial value. */
-int lrs_matvec_set_geom(int lanes_per_row, int rows, int waves);
+/* Matvec launch shape override: tiles of 16 rows per wavefront, tile groups
+ * per workgroup, K-slices per workgroup; one of the instantiated shapes
+ * (1,1,4) (1,2,4) (1,4,1) (2,2,1) (2,2,2) (1,2,6), or all 0 = automatic.
+ * Replaces the LLAMA_RS_MATVEC_GEOM knob (resident_forward.rs:164-176). */
+int lrs_matvec_set_geom(int tiles_per_wave, int tile_groups, int k_slices);
 
 /* device memory + timing helpers for callers that keep buffers resident */
 int lrs_dev_alloc(lrs_ctx *ctx, size_t bytes, void **dptr);

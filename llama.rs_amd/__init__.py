@@ -292,9 +292,14 @@ class GpuMatmul:
         return self._weight(t, w_bytes, n_in, n_out).matvec(np.asarray(x, np.float32))
 
 
-def set_matvec_geom(lanes_per_row: int = 0, rows: int = 0, waves: int = 0) -> None:
+# launch shapes of the plain matvec (tiles per wavefront, tile groups and
+# K-slices per workgroup) that the library instantiates
+MATVEC_GEOMS = [(1, 1, 4), (1, 2, 4), (1, 4, 1), (2, 2, 1), (2, 2, 2), (1, 2, 6)]
+
+
+def set_matvec_geom(tiles_per_wave: int = 0, tile_groups: int = 0, k_slices: int = 0) -> None:
     """Tuning knob (LLAMA_RS_MATVEC_GEOM, resident_forward.rs:164-176); 0s = automatic."""
-    check(lib.lrs_matvec_set_geom(lanes_per_row, rows, waves))
+    check(lib.lrs_matvec_set_geom(tiles_per_wave, tile_groups, k_slices))
 
 
 def version() -> str:

@@ -46,18 +46,13 @@ static int alloc_weight(lrs_ctx *ctx, uint32_t t, uint32_t n_in, uint32_t n_out,
     w->v.n_in = n_in;
     w->v.n_out = n_out;
     w->v.nb = n_in / (uint32_t)block_elems(t);
-    const size_t nblk = (size_t)w->v.nb * n_out;
-    w->q_alloc = nblk * q_bytes_per_block(t);
-    w->d_alloc = has_d_array(t) ? nblk * 2 : 0;
+    w->q_alloc = weight_dev_bytes(t, n_in, n_out);
     hipError_t e = hipMalloc(&w->q, w->q_alloc);
-    if (e == hipSuccess && w->d_alloc) e = hipMalloc(&w->d, w->d_alloc);
     if (e != hipSuccess) {
-        if (w->q) (void)hipFree(w->q);
         delete w;
         return hip_fail(e, "hipMalloc(weight)");
     }
     w->v.q = w->q;
-    w->v.d = w->d;
     *out = w;
     return LRS_OK;
 }
@@ -185,14 +180,15 @@ int lrs_weight_upload(lrs_ctx *ctx, uint32_t t, const void *bytes, size_t len, u
     rc = alloc_weight(ctx, t, n_in, n_out, &w);
     if (rc) return rc;
     hipError_t e;
-    if (!has_d_array(t)) {
+    if (!is_tiled(t)) {
         e = hipMemcpyAsync(w->q, bytes, len, hipMemcpyHostToDevice, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     } else {
+        // GGUF bytes to a staging buffer, then repacked into the tiled layout
         uint8_t *tmp = nullptr;
         e = hipMalloc(&tmp, len);
         if (e == hipSuccess) e = hipMemcpyAsync(tmp, bytes, len, hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess) e = launch_repack_from_gguf(tmp, w->v, w->q, w->d, ctx->stream);
+        if (e == hipSuccess) e = launch_repack_from_gguf(tmp, w->v, w->q, ctx->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
         if (tmp) (void)hipFree(tmp);
     }
@@ -215,7 +211,7 @@ int lrs_weight_generate(lrs_ctx *ctx, uint32_t t, uint64_t seed, int mode, float
     lrs_weight *w = nullptr;
     rc = alloc_weight(ctx, t, n_in, n_out, &w);
     if (rc) return rc;
-    hipError_t e = launch_generate(w->v, w->q, w->d, seed, mode, d_lo, d_hi, ctx->stream);
+    hipError_t e = launch_generate(w->v, w->q, seed, mode, d_lo, d_hi, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         lrs_weight_free(w);
@@ -234,7 +230,7 @@ int lrs_weight_download(lrs_ctx *ctx, const lrs_weight *w, void *dst, size_t len
     if (!ctx || !w || !dst) return fail(LRS_E_ARG, "null argument");
     if (len != lrs_weight_gguf_bytes(w)) return fail(LRS_E_ARG, "download size mismatch");
     SETDEV(ctx);
-    if (!has_d_array(w->v.type)) {
+    if (!is_tiled(w->v.type)) {
         LRS_HIP(hipMemcpyAsync(dst, w->q, len, hipMemcpyDeviceToHost, ctx->stream));
         LRS_HIP(hipStreamSynchronize(ctx->stream));
         return LRS_OK;
@@ -254,7 +250,6 @@ void lrs_weight_free(lrs_weight *w) {
     (void)hipSetDevice(w->ctx->device);
     (void)hipStreamSynchronize(w->ctx->stream);
     if (w->q) (void)hipFree(w->q);
-    if (w->d) (void)hipFree(w->d);
     delete w;
 }
 
@@ -303,7 +298,9 @@ int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float 
     int rc = matvec_check(w, cols);
     if (rc) return rc;
     SETDEV(ctx);
-    LRS_HIP(launch_matvec(w->v, x_dev, y_dev, cols, nullptr, ctx->stream));
+    void *pack = nullptr;
+    LRS_HIP(scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack));
+    LRS_HIP(launch_matvec(w->v, x_dev, y_dev, cols, pack, ctx->stream));
     return LRS_OK;
 }
 
@@ -314,12 +311,15 @@ int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y, 
     SETDEV(ctx);
     const size_t xb = (size_t)cols * w->v.n_in * sizeof(float);
     const size_t yb = (size_t)cols * w->v.n_out * sizeof(float);
+    const size_t pb = xpack_bytes(pack_blocks(w->v.type, w->v.n_in));
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
     void *buf = nullptr;
-    LRS_HIP(scratch(ctx, xb + yb + 256, &buf));
+    LRS_HIP(scratch(ctx, up(xb) + up(yb) + pb, &buf));
     float *xd = (float *)buf;
-    float *yd = (float *)((char *)buf + ((xb + 255) & ~(size_t)255));
+    float *yd = (float *)((char *)buf + up(xb));
+    void *pack = (char *)buf + up(xb) + up(yb);
     LRS_HIP(hipMemcpyAsync(xd, x, xb, hipMemcpyHostToDevice, ctx->stream));
-    LRS_HIP(launch_matvec(w->v, xd, yd, cols, nullptr, ctx->stream));
+    LRS_HIP(launch_matvec(w->v, xd, yd, cols, pack, ctx->stream));
     LRS_HIP(hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));
     LRS_HIP(hipStreamSynchronize(ctx->stream));
     return LRS_OK;
@@ -337,10 +337,10 @@ int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y
     return LRS_OK;
 }
 
-int lrs_matvec_set_geom(int lanes_per_row, int rows, int waves) {
-    if (set_matvec_geom(lanes_per_row, rows, waves) != 0)
-        return fail(LRS_E_ARG, "geometry must be lanes_per_row in {16,32,64}, rows in {1,2,4}, "
-                               "waves in {1,2,4} (or all 0)");
+int lrs_matvec_set_geom(int tiles_per_wave, int tile_groups, int k_slices) {
+    if (set_matvec_geom(tiles_per_wave, tile_groups, k_slices) != 0)
+        return fail(LRS_E_ARG, "unsupported matvec launch shape (tiles_per_wave, tile_groups, "
+                               "k_slices); all 0 restores the automatic choice");
     return LRS_OK;
 }
 

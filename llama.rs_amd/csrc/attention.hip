@@ -19,15 +19,15 @@
 // (on this multi-XCD part a per-workgroup "last one combines" handshake needs
 // an L2 writeback + invalidate per workgroup, which costs more than a launch).
 #include "lrs_internal.h"
+#include "pack_dev.h"
 
 namespace lrs {
 
 struct AttnArgs {
     const float *q;          // [n_head * HD], RoPE applied
     const _Float16 *kc, *vc; // this layer's caches
-    float *out;              // [n_head * HD]
+    XPack out;               // pack of the [n_head * HD] output (o-projection input)
     float *part;             // [n_head][S][HD + 4] split partials (acc, m, l, pad)
-    uint32_t *cnt;           // [n_head_kv] arrival counters (left at 0)
     const uint32_t *step;    // [token, pos]: attends positions 0..pos
     uint32_t n_head, n_kv, ctx, S, chunk_max;
     float scale;
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a) {
         num3 = fmaf(w[t + 3], pr[(size_t)(t + 3) * PR + d], num3);
     }
     for (; t < a.S; t++) num0 = fmaf(w[t], pr[(size_t)t * PR + d], num0);
-    a.out[(size_t)h * HD + d] = ((num0 + num1) + (num2 + num3)) / tot;
+    pack_half(((num0 + num1) + (num2 + num3)) / tot, (h * HD + d) >> 5, a.out);
 }
 
 size_t attn_lds_bytes(uint32_t head_dim, uint32_t chunk_max) {
@@ -246,17 +246,15 @@ uint32_t attn_splits(uint32_t ctx) {
     return S;
 }
 
-hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *out,
-                            float *part, uint32_t *cnt, const uint32_t *step, uint32_t n_head,
-                            uint32_t n_kv, uint32_t head_dim, uint32_t ctx, uint32_t S,
-                            hipStream_t s) {
+hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, XPack out,
+                            float *part, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
+                            uint32_t head_dim, uint32_t ctx, uint32_t S, hipStream_t s) {
     AttnArgs a;
     a.q = q;
     a.kc = kc;
     a.vc = vc;
     a.out = out;
     a.part = part;
-    a.cnt = cnt;
     a.step = step;
     a.n_head = n_head;
     a.n_kv = n_kv;

@@ -33,24 +33,26 @@ constexpr int GM_LD = GM_BK + 8;  // padded LDS row (bf16 elements)
 struct GemmArgs {
     const float *a;      // [M][K]
     float *y;            // [M][ldy]
-    const uint8_t *q;    // weight q-part (device layout)
-    const uint16_t *d;   // Q6_K d array
-    uint32_t M, N, K, nb, ldy;
+    const uint8_t *q;    // weight, tiled layout (tiled.h)
+    uint32_t M, N, K, units, ldy;
     uint32_t accum;      // 1: y += A W^T (residual add), 0: y = A W^T
 };
 
+__device__ __forceinline__ uint4 ldq16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
 // 32 consecutive weights of row n starting at element e (e % 32 == 0), f32
-// values exactly as ggml_cpu::dequant (dequant.rs:101-258)
+// values exactly as ggml_cpu::dequant (dequant.rs:101-258); the GGUF bytes
+// come from the row's pieces of the tiled chunk of super-block e / 256
 template <uint32_t T>
 __device__ __forceinline__ void deq32(const GemmArgs &g, uint32_t n, uint32_t e, float (&w)[32]) {
-    const size_t blk = (size_t)n * g.nb + (e >> 8);
-    const uint32_t o = e & 255;  // offset inside the super-block
+    const uint32_t o = e & 255, r = n & 15;  // offset inside the super-block, row in the tile
+    const uint8_t *c = g.q + ((size_t)(n >> 4) * g.units + (e >> 8)) * tchunk_bytes(T);
     if constexpr (T == T_Q4_K) {
-        const uint8_t *b = g.q + blk * 144;
-        const uint4 hd = *reinterpret_cast<const uint4 *>(b);
+        const uint4 hd = ldq16(c + 16 * r);
         const uint32_t j = o >> 6, hi = (o >> 5) & 1;  // qs group, high nibbles
-        const uint4 q0 = *reinterpret_cast<const uint4 *>(b + 16 + 32 * j);
-        const uint4 q1 = *reinterpret_cast<const uint4 *>(b + 16 + 32 * j + 16);
+        // qs bytes 32j..32j+31 = pieces (g, r) with g = 2(j&1), 2(j&1)+1 of half j>>1
+        const uint8_t *qp = c + 256 + 1024 * (j >> 1) + 16 * (16 * (2 * (j & 1)) + r);
+        const uint4 q0 = ldq16(qp), q1 = ldq16(qp + 256);
         const uint8_t *sb = reinterpret_cast<const uint8_t *>(&hd) + 4;
         uint32_t sc, m;
         scale_min_k4(2 * j + hi, sb, sc, m);
@@ -63,15 +65,15 @@ __device__ __forceinline__ void deq32(const GemmArgs &g, uint32_t n, uint32_t e,
             const uint32_t q = hi ? (byte >> 4) : (byte & 15);
             w[i] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
         }
-    } else {  // T_Q6_K: device layout [ql 128 | qh 64 | scales 16] + d array
-        const uint8_t *b = g.q + blk * Q6_QBYTES;
-        const float dv = h2f(g.d[blk]);
+    } else {  // T_Q6_K
+        const float dv = h2f(*reinterpret_cast<const uint16_t *>(c + 3328 + 2 * r));
         const uint32_t h = o >> 7, quarter = (o >> 5) & 3;  // elements 128h + 32 quarter + l
-        const uint8_t *ql = b + 64 * h + 32 * (quarter & 1);
-        const uint8_t *qh = b + 128 + 32 * h;
-        const uint4 l0 = *reinterpret_cast<const uint4 *>(ql), l1 = *reinterpret_cast<const uint4 *>(ql + 16);
-        const uint4 h0 = *reinterpret_cast<const uint4 *>(qh), h1 = *reinterpret_cast<const uint4 *>(qh + 16);
-        const int8_t s0 = (int8_t)b[192 + 8 * h + 2 * quarter], s1 = (int8_t)b[192 + 8 * h + 1 + 2 * quarter];
+        // ql[64h + 32(quarter&1) + l] and qh[32h + l]: pieces g = 2h (l < 16), 2h+1 (l >= 16)
+        const uint8_t *ql = c + 256 + 1024 * (quarter & 1) + 16 * (16 * (2 * h) + r);
+        const uint8_t *qh = c + 2304 + 16 * (16 * (2 * h) + r);
+        const uint4 l0 = ldq16(ql), l1 = ldq16(ql + 256);
+        const uint4 h0 = ldq16(qh), h1 = ldq16(qh + 256);
+        const int8_t s0 = (int8_t)c[16 * r + 8 * h + 2 * quarter], s1 = (int8_t)c[16 * r + 8 * h + 1 + 2 * quarter];
         const float ds0 = __fmul_rn(dv, (float)s0), ds1 = __fmul_rn(dv, (float)s1);
         const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
         const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
@@ -190,11 +192,10 @@ hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint3
     g.a = a;
     g.y = y;
     g.q = w.q;
-    g.d = w.d;
     g.M = M;
     g.N = w.n_out;
     g.K = w.n_in;
-    g.nb = w.nb;
+    g.units = tunits(w.type, w.n_in);
     g.ldy = ldy;
     g.accum = accum ? 1u : 0u;
     dim3 grid((w.n_out + GM_BN - 1) / GM_BN, (M + GM_BM - 1) / GM_BM);

@@ -9,7 +9,8 @@
 #include <string>
 
 #include "../../include/lrs.h"
-#include "mv_args.h"
+#include "tiled.h"
+#include "mq_args.h"
 
 namespace lrs {
 
@@ -53,54 +54,50 @@ __host__ __device__ inline int64_t block_bytes(uint32_t t) {
 }
 
 // ---------------------------------------------------------------------------
-// Device layout of a resident weight (n_out rows x nb blocks per row):
-//   Q4_K  q = GGUF blocks as-is (144 B, 16-B aligned), d unused
-//   Q5_K  q = GGUF blocks as-is (176 B), d unused
-//   Q6_K  q = per block [ql 128 | qh 64 | scales 16] = 208 B (16-B aligned),
-//         d = f16 super-block scale array [n_out*nb]
-//   Q8_0  q = per block qs[32] (32 B), d = f16 scale array [n_out*nb]
-//   Q4_0 / F32 / F16: q = the raw GGUF bytes (dequant only, no matvec)
-// Every byte read by a matvec is a GGUF byte: no padding is streamed.
+// Device layout of a resident weight (n_out rows x nb GGUF blocks per row):
+//   Q4_K / Q5_K / Q6_K / Q8_0: the tiled layout of tiled.h (16-row tiles,
+//         one contiguous chunk per unit, GGUF bytes only)
+//   Q4_0 / F32 / F16: the raw GGUF bytes (dequant / embedding only)
 // ---------------------------------------------------------------------------
-constexpr uint32_t Q6_QBYTES = 208;
-constexpr uint32_t Q8_QBYTES = 32;
-
 struct WeightView {
     const uint8_t *q;
-    const uint16_t *d;
-    uint32_t type, n_in, n_out, nb;  // nb = blocks per row
+    uint32_t type, n_in, n_out, nb;  // nb = GGUF blocks per row
 };
 
-__host__ __device__ inline size_t q_bytes_per_block(uint32_t t) {
-    switch (t) {
-    case T_Q6_K: return Q6_QBYTES;
-    case T_Q8_0: return Q8_QBYTES;
-    default: return (size_t)block_bytes(t);
-    }
+// device bytes of a weight's allocation
+inline size_t weight_dev_bytes(uint32_t t, uint32_t n_in, uint32_t n_out) {
+    if (is_tiled(t)) return tbytes(t, n_in, n_out);
+    return (size_t)(n_in / block_elems(t)) * n_out * block_bytes(t);
 }
-__host__ __device__ inline bool has_d_array(uint32_t t) { return t == T_Q6_K || t == T_Q8_0; }
 
 // launch wrappers implemented in the .hip files (all enqueue on `s`)
 hipError_t launch_repack_from_gguf(const uint8_t *gguf_dev, WeightView w, uint8_t *q,
-                                   uint16_t *d, hipStream_t s);
+                                   hipStream_t s);
 hipError_t launch_repack_to_gguf(WeightView w, uint8_t *gguf_dev, hipStream_t s);
-hipError_t launch_generate(WeightView w, uint8_t *q, uint16_t *d, uint64_t seed, int mode,
-                           float d_lo, float d_hi, hipStream_t s);
+hipError_t launch_generate(WeightView w, uint8_t *q, uint64_t seed, int mode, float d_lo,
+                           float d_hi, hipStream_t s);
 hipError_t launch_dequant(WeightView w, float *out, hipStream_t s);
 hipError_t launch_dequant_rows(WeightView w, const uint32_t *rows_dev, uint32_t n_rows,
                                float *out, hipStream_t s);
-int set_matvec_geom(int lpr, int r, int waves);
-MvGeom choose_geom(uint32_t t, uint32_t n_in, uint32_t rows, bool pairs);
-hipError_t launch_mv(const MvArgs &args, MvGeom gm, uint32_t type, hipStream_t s,
-                     uint32_t *blocks_out = nullptr);
-// two weight types in one launch (Q4_K q/k + Q6_K v); hipErrorNotSupported otherwise
-hipError_t launch_mv2(const MvArgs &args, uint32_t t0, MvGeom g0, uint32_t t1, MvGeom g1,
-                      hipStream_t s);
-// reduces the per-block argmax keys of a launch with MvArgs::amax into step / out
+// matrix-core matvec (mq.hip)
+hipError_t launch_xpack(const float *x, const float *nw, uint32_t n, uint32_t nxb, XPack p,
+                        hipStream_t s);
+hipError_t launch_mq(const MqArgs &a, uint32_t t0, uint32_t t1, MqGeom g, int epi, hipStream_t s,
+                     uint32_t *wgs_out = nullptr, uint32_t *keys_per_wg = nullptr);
+bool mq_geom_supported(const MqGeom &g);
+MqGeom store_geom(uint32_t t, uint32_t n_in, uint32_t n_out);
+// plain-matvec launch shape override (tiles per wave, tile groups, K-slices; all 0 = automatic)
+int set_matvec_geom(int tpw, int tg, int ks);
+// 32-element pack blocks of a K-long input of a weight of type t (K padded to units)
+inline uint32_t pack_blocks(uint32_t t, uint32_t n_in) {
+    return is_tiled(t) ? tunits(t, n_in) * tunit_elems(t) / 32 : (n_in + 31) / 32;
+}
+// reduces argmax keys (amax_key) into step {token, pos, n} and out[n]
 hipError_t launch_argmax_finish(const unsigned long long *keys, uint32_t n, uint32_t *step,
                                 uint32_t *out, uint32_t out_cap, hipStream_t s);
-hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols,
-                         const float *bias, hipStream_t s);
+// y[c] = W x[c] for cols columns (packs x, then one matvec per column)
+hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
+                         hipStream_t s);
 // Y[M][ldy] = A[M][K] W^T on the matrix cores (prec 1: bf16, 3: bf16 hi/lo split)
 hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint32_t ldy, int prec,
                        hipStream_t s, bool accum = false);
@@ -129,6 +126,5 @@ struct lrs_weight {
     lrs_ctx *ctx;
     lrs::WeightView v;
     uint8_t *q;
-    uint16_t *d;
-    size_t q_alloc, d_alloc;
+    size_t q_alloc;
 };

@@ -16,10 +16,18 @@
 //   head             rmsnorm(x)*output_norm -> logits            (model.rs:254-265)
 //   [argmax]         greedy token, written back as the next step's token
 //
+// Every matvec reads its activation as a pack (mq_args.h) written by the op
+// before it: embed and down write the pack of x * attn_norm (or output_norm
+// before the head), o the pack of x * ffn_norm, gate/up the pack of the
+// SwiGLU output, attention the pack of its output.  RMSNorm is applied as
+// W (x * w) * s, with s = 1/sqrt(mean(x^2) + eps) reduced from x by the
+// consuming kernel itself.
+//
 // The step's token and position live in device memory, so the same graph is
 // replayed for every token; a greedy generation loop runs as back-to-back
 // graph launches with no host round trip.
 #include "lrs_internal.h"
+#include "pack_dev.h"
 #include "quant_dev.h"
 
 #include <cmath>
@@ -30,20 +38,23 @@
 
 namespace lrs {
 uint32_t attn_splits(uint32_t ctx);
-hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *out,
-                            float *part, uint32_t *cnt, const uint32_t *step, uint32_t n_head,
-                            uint32_t n_kv, uint32_t head_dim, uint32_t ctx, uint32_t S,
-                            hipStream_t s);
+hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, XPack out,
+                            float *part, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
+                            uint32_t head_dim, uint32_t ctx, uint32_t S, hipStream_t s);
 
-// x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304)
-__global__ void k_embed(WeightView w, const uint32_t *__restrict__ step, float *__restrict__ x) {
+// x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304),
+// and the pack of x * nw for the first layer's q/k/v
+__global__ __launch_bounds__(256) void k_embed(WeightView w, const uint32_t *__restrict__ step,
+                                               const float *__restrict__ nw, float *__restrict__ x,
+                                               XPack p) {
     const uint32_t be = (uint32_t)block_elems(w.type);
     uint32_t tok = step[0];
     if (tok >= w.n_out) tok = w.n_out - 1;  // ids are validated on the host
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < w.n_in; i += gridDim.x * blockDim.x) {
-        const uint64_t e = (uint64_t)tok * w.n_in + i;
-        x[i] = deq_elem(w, e / be, (uint32_t)(e % be));
-    }
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;  // n_in is a multiple of 256
+    const uint64_t e = (uint64_t)tok * w.n_in + i;
+    const float v = deq_elem(w, e / be, (uint32_t)(e % be));
+    x[i] = v;
+    pack_half(v * nw[i], i >> 5, p);
 }
 
 }  // namespace lrs
@@ -62,14 +73,17 @@ struct lrs_model {
     std::vector<DevLayer> layers;
     const lrs_weight *embd, *output;
     float *output_norm, *freq;
-    // activations
-    float *x, *qbuf, *att, *act, *logits, *part;
-    uint32_t *cnt, *step, *gen;  // step = {token, pos, n_generated}
+    // activations: residual, q after RoPE, logits, attention partials
+    float *x, *qbuf, *logits, *part;
+    // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
+    // SwiGLU output
+    XPack pk_n, pk_f, pk_a, pk_s;
+    uint32_t *step, *gen;  // step = {token, pos, n_generated}
     uint32_t gen_cap;
     // greedy: per-workgroup argmax keys of the head (ops.rs:1035-1045: the
     // first index of the maximum), reduced into step / gen by k_argmax_finish
     unsigned long long *amax;
-    uint32_t head_blocks = 0;
+    uint32_t head_keys = 0;
     // batched prompt blocks (allocated at the first block): residual,
     // normalised rows, q/k/v GEMM outputs, q after RoPE, attention output,
     // gate / up, token ids
@@ -119,176 +133,167 @@ int check_w(const lrs_weight *w, const char *name, uint32_t n_in, uint32_t n_out
     return LRS_OK;
 }
 
-MvSeg seg_of(const lrs_weight *w, uint32_t epi) {
-    MvSeg s = {};
-    s.q0 = s.q1 = w->v.q;
-    s.d0 = s.d1 = w->v.d;
-    s.rows = w->v.n_out;
-    s.epi = epi;
+MqSeg mseg(const lrs_weight *w, uint32_t rows) {
+    MqSeg s = {};
+    s.w = w->v.q;
+    s.rows = rows;
     return s;
 }
 
+// launch shapes of the decode ops (16-row tiles; see mq.hip)
+constexpr MqGeom G_QKV = {1, 1, 4, 2};    // 448 workgroups of 4 K-slices (32B shape)
+constexpr MqGeom G_O = {1, 2, 4, 2};      // 2 tiles (one 32-row pack block) x 4 K-slices
+constexpr MqGeom G_GATEUP = {2, 2, 1, 2}; // gate+up tile pairs, 2 per workgroup
+constexpr MqGeom G_DOWN = {1, 2, 6, 2};   // 2 tiles x 6 K-slices
+constexpr MqGeom G_HEAD = {1, 4, 1, 2};   // 4 tiles per workgroup, full K per wavefront
+
 // ---- one fused op of the per-token plan, enqueued on the model stream ----
 hipError_t op_embed(lrs_model *m) {
-    hipLaunchKernelGGL(k_embed, dim3((m->cfg.n_embd + 255) / 256), dim3(256), 0, m->ctx->stream,
-                       m->embd->v, m->step, m->x);
+    hipLaunchKernelGGL(k_embed, dim3(m->cfg.n_embd / 256), dim3(256), 0, m->ctx->stream,
+                       m->embd->v, m->step, m->layers[0].attn_norm, m->x, m->pk_n);
     return hipGetLastError();
 }
 
-// q, k, v: rmsnorm + matvec + bias + RoPE + f16 KV append.  Segments that
-// share a weight type go in one launch (all three for Q8_0 / Q4_K-only
-// models; q+k then v for the Q4_K_M mix).
+// q, k, v: rmsnorm + matvec + bias + RoPE + f16 KV append.  Segments of two
+// weight types share a launch (Q4_K q/k with Q6_K v in the Q4_K_M mix);
+// otherwise one launch per type.
 hipError_t op_qkv(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
-    const uint32_t kvd = c.n_head_kv * c.head_dim, qd = c.n_head * c.head_dim;
-    MvArgs a = {};
+    MqArgs a = {};
     a.n_in = c.n_embd;
-    a.x = m->x;
-    a.norm_w = L.attn_norm;
+    a.xin = m->pk_n;
+    a.xres = m->x;
     a.eps = c.rms_eps;
-    a.cols = 1;
     a.step = m->step;
     a.freq = m->freq;
     a.head_dim = c.head_dim;
     a.rope_dim = c.rope_dim;
     a.ctx = c.ctx;
-    MvSeg sq = seg_of(L.q, EPI_STORE);
-    sq.rope = 1;
+    MqSeg sq = mseg(L.q, L.q->v.n_out);
+    sq.kind = 0;
     sq.bias = L.bq;
     sq.out = m->qbuf;
-    MvSeg sk = seg_of(L.k, EPI_KV);
-    sk.rope = 1;
+    MqSeg sk = mseg(L.k, L.k->v.n_out);
+    sk.kind = 1;
     sk.bias = L.bk;
     sk.kv = L.kc;
-    MvSeg sv = seg_of(L.v, EPI_KV);
+    MqSeg sv = mseg(L.v, L.v->v.n_out);
+    sv.kind = 2;
     sv.bias = L.bv;
     sv.kv = L.vc;
     const lrs_weight *ws[3] = {L.q, L.k, L.v};
-    const MvSeg segs[3] = {sq, sk, sv};
-    if (L.q->v.type == L.k->v.type && L.v->v.type != L.q->v.type) {
-        // q, k of one type and v of another in a single launch (Q4_K_M: Q4_K + Q6_K)
+    const MqSeg segs[3] = {sq, sk, sv};
+    const uint32_t tq = L.q->v.type, tv = L.v->v.type;
+    if (L.k->v.type == tq && tv != tq) {
         a.n_seg = 3;
         a.n_seg0 = 2;
-        a.nb = L.q->v.nb;
         a.seg[0] = sq;
         a.seg[1] = sk;
         a.seg[2] = sv;
-        const MvGeom g0 = choose_geom(L.q->v.type, c.n_embd, L.q->v.n_out + L.k->v.n_out, true);
-        const MvGeom g1 = choose_geom(L.v->v.type, c.n_embd, L.v->v.n_out, false);
-        hipError_t e = launch_mv2(a, L.q->v.type, g0, L.v->v.type, g1, m->ctx->stream);
+        a.nxb = pack_blocks(tq, c.n_embd);
+        hipError_t e = launch_mq(a, tq, tv, G_QKV, MQ_QKV, m->ctx->stream);
         if (e != hipErrorNotSupported) return e;
-        a.n_seg0 = 0;
     }
     bool done[3] = {false, false, false};
     for (int i = 0; i < 3; i++) {
         if (done[i]) continue;
         const uint32_t t = ws[i]->v.type;
         a.n_seg = 0;
-        a.nb = ws[i]->v.nb;
-        uint32_t rows = 0;
         for (int j = i; j < 3; j++) {
             if (!done[j] && ws[j]->v.type == t) {
                 a.seg[a.n_seg++] = segs[j];
-                rows += ws[j]->v.n_out;
                 done[j] = true;
             }
         }
-        hipError_t e = launch_mv(a, choose_geom(t, c.n_embd, rows, true), t, m->ctx->stream);
+        a.n_seg0 = a.n_seg;
+        a.nxb = pack_blocks(t, c.n_embd);
+        hipError_t e = launch_mq(a, t, t, G_QKV, MQ_QKV, m->ctx->stream);
         if (e != hipSuccess) return e;
     }
-    (void)qd;
-    (void)kvd;
     return hipSuccess;
 }
 
 hipError_t op_attn(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
-    return launch_attention(m->qbuf, L.kc, L.vc, m->att, m->part, m->cnt, m->step, c.n_head,
-                            c.n_head_kv, c.head_dim, c.ctx, m->S, m->ctx->stream);
+    return launch_attention(m->qbuf, L.kc, L.vc, m->pk_a, m->part, m->step, c.n_head, c.n_head_kv,
+                            c.head_dim, c.ctx, m->S, m->ctx->stream);
 }
 
-// x += W_o att
+// x += W_o att; pack of x * ffn_norm for gate/up
 hipError_t op_o(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
-    const uint32_t qd = c.n_head * c.head_dim;
-    MvArgs o = {};
-    o.n_seg = 1;
-    o.seg[0] = seg_of(L.o, EPI_ACCUM);
-    o.seg[0].out = m->x;
-    o.n_in = qd;
-    o.nb = L.o->v.nb;
-    o.x = m->att;
-    o.cols = 1;
-    return launch_mv(o, choose_geom(L.o->v.type, qd, c.n_embd, false), L.o->v.type, m->ctx->stream);
+    MqArgs a = {};
+    a.n_seg = 1;
+    a.seg[0] = mseg(L.o, c.n_embd);
+    a.n_in = c.n_head * c.head_dim;
+    a.nxb = pack_blocks(L.o->v.type, a.n_in);
+    a.xin = m->pk_a;
+    a.x = m->x;
+    a.nw = L.ffn_norm;
+    a.xout = m->pk_f;
+    return launch_mq(a, L.o->v.type, L.o->v.type, G_O, MQ_RESID, m->ctx->stream);
 }
 
-// act = silu(gate h) * (up h), h = rmsnorm(x) * ffn_norm; gate row j and up
-// row j are the two rows of one lane group (dual segment)
+// act = silu(gate h) * (up h), h = rmsnorm(x) * ffn_norm; gate and up tiles
+// of the same outputs in one wavefront; pack of act for down
 hipError_t op_gateup(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
-    MvArgs f = {};
-    f.n_seg = 1;
-    MvSeg sg = seg_of(L.gate, EPI_SWIGLU);
-    sg.q1 = L.up->v.q;
-    sg.d1 = L.up->v.d;
-    sg.dual = 1;
-    sg.rows = 2 * c.n_ff;
-    sg.out = m->act;
-    f.seg[0] = sg;
-    f.n_in = c.n_embd;
-    f.nb = L.gate->v.nb;
-    f.x = m->x;
-    f.norm_w = L.ffn_norm;
-    f.eps = c.rms_eps;
-    f.cols = 1;
-    return launch_mv(f, choose_geom(L.gate->v.type, c.n_embd, 2 * c.n_ff, true), L.gate->v.type,
-                     m->ctx->stream);
+    MqArgs a = {};
+    a.n_seg = 1;
+    a.seg[0] = mseg(L.gate, c.n_ff);
+    a.seg[0].w2 = L.up->v.q;
+    a.n_in = c.n_embd;
+    a.nxb = pack_blocks(L.gate->v.type, c.n_embd);
+    a.xin = m->pk_f;
+    a.xres = m->x;
+    a.eps = c.rms_eps;
+    a.xout = m->pk_s;
+    return launch_mq(a, L.gate->v.type, L.gate->v.type, G_GATEUP, MQ_SWIGLU, m->ctx->stream);
 }
 
-// x += W_down act
+// x += W_down act; pack of x * (next layer's attn_norm, or output_norm)
 hipError_t op_down(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
-    MvArgs dn = {};
-    dn.n_seg = 1;
-    dn.seg[0] = seg_of(L.down, EPI_ACCUM);
-    dn.seg[0].out = m->x;
-    dn.n_in = c.n_ff;
-    dn.nb = L.down->v.nb;
-    dn.x = m->act;
-    dn.cols = 1;
-    return launch_mv(dn, choose_geom(L.down->v.type, c.n_ff, c.n_embd, false), L.down->v.type,
-                     m->ctx->stream);
+    MqArgs a = {};
+    a.n_seg = 1;
+    a.seg[0] = mseg(L.down, c.n_embd);
+    a.n_in = c.n_ff;
+    a.nxb = pack_blocks(L.down->v.type, c.n_ff);
+    a.xin = m->pk_s;
+    a.x = m->x;
+    a.nw = l + 1 < c.n_layer ? m->layers[l + 1].attn_norm : m->output_norm;
+    a.xout = m->pk_n;
+    return launch_mq(a, L.down->v.type, L.down->v.type, G_DOWN, MQ_RESID, m->ctx->stream);
 }
 
-// logits = W_out (rmsnorm(x) * output_norm); greedy: each workgroup also
-// leaves the argmax key of its rows, reduced by op_argmax
+// logits = W_out (rmsnorm(x) * output_norm); greedy: each wavefront of
+// outputs also leaves the argmax key of its rows, reduced by op_argmax
 hipError_t op_head(lrs_model *m, bool greedy) {
     const lrs_config &c = m->cfg;
-    MvArgs h = {};
-    h.n_seg = 1;
-    h.seg[0] = seg_of(m->output, EPI_STORE);
-    h.seg[0].out = m->logits;
-    h.n_in = c.n_embd;
-    h.nb = m->output->v.nb;
-    h.x = m->x;
-    h.norm_w = m->output_norm;
-    h.eps = c.rms_eps;
-    h.cols = 1;
-    if (greedy) {
-        h.amax = m->amax;
-        h.amax_cap = c.vocab;
-    }
-    return launch_mv(h, choose_geom(m->output->v.type, c.n_embd, c.vocab, false), m->output->v.type,
-                     m->ctx->stream, &m->head_blocks);
+    MqArgs a = {};
+    a.n_seg = 1;
+    a.seg[0] = mseg(m->output, c.vocab);
+    a.seg[0].out = m->logits;
+    a.n_in = c.n_embd;
+    a.nxb = pack_blocks(m->output->v.type, c.n_embd);
+    a.xin = m->pk_n;
+    a.xres = m->x;
+    a.eps = c.rms_eps;
+    if (greedy) a.amax = m->amax;
+    uint32_t wgs = 0, kpw = 0;
+    hipError_t e = launch_mq(a, m->output->v.type, m->output->v.type, G_HEAD, MQ_STORE,
+                             m->ctx->stream, &wgs, &kpw);
+    m->head_keys = wgs * kpw;
+    return e;
 }
 
 hipError_t op_argmax(lrs_model *m) {
-    return launch_argmax_finish(m->amax, m->head_blocks, m->step, m->gen, m->gen_cap,
+    return launch_argmax_finish(m->amax, m->head_keys, m->step, m->gen, m->gen_cap,
                                 m->ctx->stream);
 }
 
@@ -427,18 +432,27 @@ int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weight
     m->gen_cap = 1u << 16;
     if ((rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
         (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->qbuf)) ||
-        (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->att)) ||
-        (rc = dev_alloc(m, c.n_ff * sizeof(float), (void **)&m->act)) ||
         (rc = dev_alloc(m, c.vocab * sizeof(float), (void **)&m->logits)) ||
         (rc = dev_alloc(m, (size_t)c.n_head * m->S * (c.head_dim + 4) * sizeof(float),
                         (void **)&m->part)) ||
-        (rc = dev_alloc(m, c.n_head_kv * sizeof(uint32_t), (void **)&m->cnt)) ||
         (rc = dev_alloc(m, 4 * sizeof(uint32_t), (void **)&m->step)) ||
         (rc = dev_alloc(m, m->gen_cap * sizeof(uint32_t), (void **)&m->gen)) ||
         (rc = dev_alloc(m, (size_t)c.vocab * sizeof(unsigned long long), (void **)&m->amax)))
         return bail(rc);
-    if (hipMemset(m->cnt, 0, c.n_head_kv * sizeof(uint32_t)) != hipSuccess ||
-        hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess)
+    {
+        // activation packs (n_embd, n_ff and n_head*head_dim are multiples of 256)
+        void *p = nullptr;
+        const uint32_t ne = c.n_embd / 32, nq = qd / 32, nf = c.n_ff / 32;
+        if ((rc = dev_alloc(m, xpack_bytes(ne), &p))) return bail(rc);
+        m->pk_n = xpack_at(p, ne);
+        if ((rc = dev_alloc(m, xpack_bytes(ne), &p))) return bail(rc);
+        m->pk_f = xpack_at(p, ne);
+        if ((rc = dev_alloc(m, xpack_bytes(nq), &p))) return bail(rc);
+        m->pk_a = xpack_at(p, nq);
+        if ((rc = dev_alloc(m, xpack_bytes(nf), &p))) return bail(rc);
+        m->pk_s = xpack_at(p, nf);
+    }
+    if (hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess)
         return bail(fail(LRS_E_HIP, "memset"));
     if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
             hipSuccess ||
@@ -563,6 +577,7 @@ static int prefill(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t po
     if (!head) return LRS_OK;
     LRS_HIP(hipMemcpyAsync(m->x, m->pX + (size_t)(nb - 1) * m->cfg.n_embd,
                            m->cfg.n_embd * sizeof(float), hipMemcpyDeviceToDevice, s));
+    LRS_HIP(launch_xpack(m->x, m->output_norm, m->cfg.n_embd, m->cfg.n_embd / 32, m->pk_n, s));
     LRS_HIP(op_head(m, false));
     return LRS_OK;
 }

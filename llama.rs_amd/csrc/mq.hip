@@ -1,0 +1,657 @@
+// mq.hip — fused dequantize x matvec on the gfx950 matrix cores.
+//
+// Replaces shaders/q{8_0,4_k,5_k,6_k}_matvec.comp of llama.rs (dispatched by
+// matmul.rs:36-430 and build_plan resident_forward.rs:3678-3752).  The
+// reference quantizes the activation to int8 (one f32 scale per 32) and uses
+// dot4 instructions; here the activation is kept to 22 significant bits per
+// 32-element block (the pack of mq_args.h: three exact int8 digits), the
+// integer products run on v_mfma_i32_16x16x64_i8 with exact i32 sums per
+// quant sub-block, and only the per-sub-block scale arithmetic is f32.  The
+// result matches dequant + f32 dot (ops.rs:78-101) to ~1e-6 relative.
+//
+// Work decomposition (wave64).  Weights are in the tiled layout of tiled.h:
+// one contiguous chunk per (16-row tile, unit), lane n + 16 g reading piece
+// (g, n).  One MFMA multiplies the 16 rows of a tile (B operand, column n =
+// row n) by 16 "slots" of the activation (A operand, row m = slot): slot m
+// carries one digit of the activation restricted to one quant sub-block, so
+// output register i of lane (n, G) is the exact integer sum over sub-block
+// c(G) of quant * digit i.  The lane then applies d * scale (and the min /
+// offset term with the f32 block sums) in f32.
+//
+// Per type and unit (one K-quant super-block, or 64 Q8_0 elements):
+//   Q4_K / Q5_K  2 halves x 2 MFMAs (low nibbles, high nibbles); within a
+//                half lane group g holds qs bytes 16g..16g+15 = elements
+//                16(g&1).. of sub-blocks 2(g>>1) (low) and 2(g>>1)+1 (high)
+//   Q6_K         4 MFMAs (one per 32-element quarter of each half); lane group
+//                g = (half g>>1, is g&1) holds the 16-element run of each quarter
+//   Q8_0         1 MFMA; lane group g holds bytes 16(g&1).. of block g>>1
+//
+// A workgroup is TG tile groups x KS K-slices of wavefronts.  A tile group is
+// TPW tiles that share the activation (two consecutive tiles, or the gate
+// and up tiles of the same outputs).  The input pack is copied to LDS once
+// per workgroup (global_load_lds, no VGPR staging) while the first units of
+// every wavefront are already in flight; each wavefront streams its K-slice
+// with P units of loads in flight, then the K-slices are summed through LDS
+// and an epilogue writes the outputs (store, q/k/v with bias + RoPE + f16 KV
+// append, residual add, SwiGLU) and, for the residual and SwiGLU epilogues,
+// the pack of the next op's input.
+#include "lrs_internal.h"
+#include "mq_args.h"
+#include "pack_dev.h"
+
+#include <cmath>
+
+namespace lrs {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ float hf16(uint32_t h) {
+    _Float16 v;
+    const uint16_t b = (uint16_t)h;
+    __builtin_memcpy(&v, &b, 2);
+    return (float)v;
+}
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ v4i asv(uint4 u) {
+    v4i r = {(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+    return r;
+}
+__device__ __forceinline__ v4i mfma8(v4i a, v4i b) {
+    const v4i z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, z, 0, 0, 0);
+}
+// exact digit sums -> f32 (digit weights 65536, 256, 1)
+__device__ __forceinline__ float cfold(v4i c) {
+    return fmaf((float)c[0], 65536.f, fmaf((float)c[1], 256.f, (float)c[2]));
+}
+
+// ---------------------------------------------------------------------------
+// activation pack
+// ---------------------------------------------------------------------------
+// x-pack of x (times nw when given) for blocks [0, nxb); elements >= n pack
+// as zero (padding of the K dimension to whole units)
+__global__ __launch_bounds__(256) void k_xpack(const float *__restrict__ x,
+                                               const float *__restrict__ nw, uint32_t n,
+                                               uint32_t nxb, XPack p) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= 32 * nxb) return;  // whole half-waves leave together
+    float v = 0.f;
+    if (e < n) v = nw ? x[e] * nw[e] : x[e];
+    pack_half(v, e >> 5, p);
+}
+
+hipError_t launch_xpack(const float *x, const float *nw, uint32_t n, uint32_t nxb, XPack p,
+                        hipStream_t s) {
+    const uint32_t threads = 32 * nxb;
+    hipLaunchKernelGGL(k_xpack, dim3((threads + 255) / 256), dim3(256), 0, s, x, nw, n, nxb, p);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// per-type unit registers and loads (tiled layout, tiled.h)
+// ---------------------------------------------------------------------------
+template <uint32_t T>
+struct WReg;
+template <>
+struct WReg<T_Q4_K> {
+    uint4 hd, qa, qb;
+};
+template <>
+struct WReg<T_Q5_K> {
+    uint4 hd, qh, qa, qb;
+};
+template <>
+struct WReg<T_Q6_K> {
+    uint4 sc, la, lb, qh;
+    uint32_t d;
+};
+template <>
+struct WReg<T_Q8_0> {
+    uint4 qs;
+    uint32_t d;
+};
+
+// c = chunk of the unit; lane = n + 16 g
+template <uint32_t T>
+__device__ __forceinline__ void wload(WReg<T> &r, const uint8_t *__restrict__ c, uint32_t lane) {
+    const uint32_t n = lane & 15, g = lane >> 4;
+    if constexpr (T == T_Q4_K) {
+        r.hd = ld16(c + 16 * n);
+        r.qa = ld16(c + 256 + 16 * lane);
+        r.qb = ld16(c + 1280 + 16 * lane);
+    } else if constexpr (T == T_Q5_K) {
+        r.hd = ld16(c + 16 * n);
+        r.qh = ld16(c + 256 + 16 * (16 * (g & 1) + n));
+        r.qa = ld16(c + 768 + 16 * lane);
+        r.qb = ld16(c + 1792 + 16 * lane);
+    } else if constexpr (T == T_Q6_K) {
+        r.sc = ld16(c + 16 * n);
+        r.la = ld16(c + 256 + 16 * lane);
+        r.lb = ld16(c + 1280 + 16 * lane);
+        r.qh = ld16(c + 2304 + 16 * lane);
+        r.d = *reinterpret_cast<const uint16_t *>(c + 3328 + 2 * n);
+    } else {
+        r.qs = ld16(c + 16 * lane);
+        r.d = *reinterpret_cast<const uint16_t *>(c + 1024 + 4 * n + 2 * (g >> 1));
+    }
+}
+
+// LDS layout of the staged input pack: digits [nxb][96], 16 zero bytes, then
+// meta [nxb] float4
+struct LPack {
+    uint32_t zero, meta;  // byte offsets
+};
+
+// per-lane constants of the A-operand (slot) mapping
+template <uint32_t T>
+struct ALane {
+    uint32_t base, step;  // LDS byte offset of this lane's digits for unit 0, step per unit
+    uint32_t c;           // Q4_K/Q5_K: sub-block of this lane's C slots within a half
+};
+
+template <uint32_t T>
+__device__ __forceinline__ ALane<T> alane(uint32_t lane, const LPack &lp) {
+    const uint32_t m = lane & 15, g = lane >> 4;
+    ALane<T> a;
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        // slot m: nibble half s = m>>3, sub-block pair sigma = (m>>2)&1, digit m&3;
+        // block 4h + 2 sigma + s, elements 16 (g&1) ..
+        const uint32_t s = m >> 3, sg = (m >> 2) & 1, d = m & 3;
+        const bool act = d < 3 && sg == (g >> 1);
+        a.base = act ? (2 * sg + s) * 96 + 32 * d + 16 * (g & 1) : lp.zero;
+        a.step = act ? 2 * 384 : 0;  // per super-block (2 halves of 4 blocks)
+        a.c = 2 * (g & 1) + (g >> 1);
+    } else if constexpr (T == T_Q6_K) {
+        // slot m: run group m>>2 (= g of the weights), digit m&3;
+        // block 8S + 4 (g>>1) + quarter, elements 16 (g&1) ..
+        const bool act = (m >> 2) == g && (m & 3) < 3;
+        a.base = act ? 4 * (g >> 1) * 96 + 32 * (m & 3) + 16 * (g & 1) : lp.zero;
+        a.step = act ? 8 * 96 : 0;
+        a.c = 0;
+    } else {
+        const bool act = (m >> 2) == g && (m & 3) < 3;
+        a.base = act ? (g >> 1) * 96 + 32 * (m & 3) + 16 * (g & 1) : lp.zero;
+        a.step = act ? 2 * 96 : 0;
+        a.c = 0;
+    }
+    return a;
+}
+
+__device__ __forceinline__ v4i lds_a(const uint8_t *lds, uint32_t off) {
+    return asv(*reinterpret_cast<const uint4 *>(lds + off));
+}
+
+// one unit u of TPW tiles: acc += sum d*sc*(x.q), accm += sum dmin*m*sum(x)
+template <uint32_t T, int TPW>
+__device__ __forceinline__ void udot(const WReg<T> (&w)[TPW], uint32_t u, const uint8_t *lds,
+                                     const LPack &lp, const ALane<T> &al, uint32_t lane,
+                                     float (&acc)[TPW], float (&accm)[TPW]) {
+    const uint32_t g = lane >> 4;
+    const uint32_t M = 0x0F0F0F0Fu;
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        const uint32_t c8 = 8 * al.c;
+        float dsc[TPW][2], dmm[TPW][2];
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            // 6-bit scale / min of sub-blocks c and 4 + c (dequant.rs:101-110)
+            const uint4 h = w[t].hd;
+            const float d = hf16(h.x & 0xFFFFu), dm = hf16(h.x >> 16);
+            const uint32_t s0 = h.y >> c8, s4 = h.z >> c8, s8 = h.w >> c8;
+            const uint32_t sc0 = s0 & 63u, m0 = s4 & 63u;
+            const uint32_t sc1 = (s8 & 15u) | (((s0 >> 6) & 3u) << 4);
+            const uint32_t m1 = ((s8 >> 4) & 15u) | (((s4 >> 6) & 3u) << 4);
+            dsc[t][0] = d * (float)sc0;
+            dsc[t][1] = d * (float)sc1;
+            dmm[t][0] = dm * (float)m0;
+            dmm[t][1] = dm * (float)m1;
+        }
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const uint32_t hh = 2 * u + p;  // half index in the row
+            const v4i A = lds_a(lds, al.base + u * al.step + (al.step ? 384 * p : 0));
+            const float2 mt =
+                *reinterpret_cast<const float2 *>(lds + lp.meta + 16 * (4 * hh + al.c));
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+                const uint4 q = p ? w[t].qb : w[t].qa;
+                uint4 lo = make_uint4(q.x & M, q.y & M, q.z & M, q.w & M);
+                uint4 hi = make_uint4((q.x >> 4) & M, (q.y >> 4) & M, (q.z >> 4) & M, (q.w >> 4) & M);
+                if constexpr (T == T_Q5_K) {
+                    // fifth bit: bit 2j (low) / 2j+1 (high) of qh[l], j = 2p + (g>>1)
+                    // (dequant.rs:157-203)
+                    const uint32_t j2 = 2 * (2 * p + (g >> 1));
+                    const uint4 qh = w[t].qh;
+                    const uint32_t B1 = 0x01010101u;
+                    lo.x |= ((qh.x >> j2) & B1) << 4;
+                    lo.y |= ((qh.y >> j2) & B1) << 4;
+                    lo.z |= ((qh.z >> j2) & B1) << 4;
+                    lo.w |= ((qh.w >> j2) & B1) << 4;
+                    hi.x |= ((qh.x >> (j2 + 1)) & B1) << 4;
+                    hi.y |= ((qh.y >> (j2 + 1)) & B1) << 4;
+                    hi.z |= ((qh.z >> (j2 + 1)) & B1) << 4;
+                    hi.w |= ((qh.w >> (j2 + 1)) & B1) << 4;
+                }
+                const v4i C1 = mfma8(A, asv(lo));
+                const v4i C2 = mfma8(A, asv(hi));
+                const float cf = g >= 2 ? cfold(C2) : cfold(C1);
+                acc[t] = fmaf(dsc[t][p], mt.x * cf, acc[t]);
+                accm[t] = fmaf(dmm[t][p], mt.y, accm[t]);
+            }
+        }
+    } else if constexpr (T == T_Q6_K) {
+        // dequant.rs:205-258: q = (ql nibble | qh 2 bits << 4) - 32, run scale sc[8 half + 2 quarter + is]
+        const uint32_t bsel = 8 * (g & 1);
+        float dsc[TPW][4];
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            const float d = hf16(w[t].d);
+            const uint32_t lo = (g >> 1) ? w[t].sc.z : w[t].sc.x;
+            const uint32_t hi = (g >> 1) ? w[t].sc.w : w[t].sc.y;
+            dsc[t][0] = d * (float)(int)(int8_t)((lo >> bsel) & 255u);
+            dsc[t][1] = d * (float)(int)(int8_t)((lo >> (bsel + 16)) & 255u);
+            dsc[t][2] = d * (float)(int)(int8_t)((hi >> bsel) & 255u);
+            dsc[t][3] = d * (float)(int)(int8_t)((hi >> (bsel + 16)) & 255u);
+        }
+        const uint32_t mq0 = lp.meta + 16 * (8 * u + 4 * (g >> 1));
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const v4i A = lds_a(lds, al.base + u * al.step + (al.step ? 96 * q : 0));
+            const float4 mt = *reinterpret_cast<const float4 *>(lds + mq0 + 16 * q);
+            const float rs = (g & 1) ? mt.w : mt.z;
+            const float xo = fmaf(-32.f, rs, 0.f);
+#pragma unroll
+            for (int t = 0; t < TPW; t++) {
+                const uint4 ql = (q & 1) ? w[t].lb : w[t].la;
+                const uint4 qh = w[t].qh;
+                const uint32_t H = 0x30303030u;
+                uint4 b;
+                if (q == 0) {
+                    b = make_uint4((ql.x & M) | ((qh.x << 4) & H), (ql.y & M) | ((qh.y << 4) & H),
+                                   (ql.z & M) | ((qh.z << 4) & H), (ql.w & M) | ((qh.w << 4) & H));
+                } else if (q == 1) {
+                    b = make_uint4((ql.x & M) | ((qh.x << 2) & H), (ql.y & M) | ((qh.y << 2) & H),
+                                   (ql.z & M) | ((qh.z << 2) & H), (ql.w & M) | ((qh.w << 2) & H));
+                } else if (q == 2) {
+                    b = make_uint4(((ql.x >> 4) & M) | (qh.x & H), ((ql.y >> 4) & M) | (qh.y & H),
+                                   ((ql.z >> 4) & M) | (qh.z & H), ((ql.w >> 4) & M) | (qh.w & H));
+                } else {
+                    b = make_uint4(((ql.x >> 4) & M) | ((qh.x >> 2) & H), ((ql.y >> 4) & M) | ((qh.y >> 2) & H),
+                                   ((ql.z >> 4) & M) | ((qh.z >> 2) & H), ((ql.w >> 4) & M) | ((qh.w >> 2) & H));
+                }
+                const float cf = cfold(mfma8(A, asv(b)));
+                acc[t] = fmaf(dsc[t][q], fmaf(mt.x, cf, xo), acc[t]);
+            }
+        }
+    } else {
+        // Q8_0 (dequant.rs:58-76): q * d, one d per 32-element block
+        const v4i A = lds_a(lds, al.base + u * al.step);
+        const float xs = *reinterpret_cast<const float *>(lds + lp.meta + 16 * (2 * u + (g >> 1)));
+#pragma unroll
+        for (int t = 0; t < TPW; t++) {
+            const float cf = cfold(mfma8(A, asv(w[t].qs)));
+            acc[t] = fmaf(hf16(w[t].d), xs * cf, acc[t]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// the kernel
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    // ops.rs:978-988: silu(g) = g / (1 + exp(-g)), then * up
+    return (g / (1.0f + expf(-g))) * u;
+}
+
+// copies `bytes` (multiple of 16) from global memory to LDS, 16 B per lane
+__device__ __forceinline__ void copy_to_lds(const uint8_t *__restrict__ g, uint8_t *lds,
+                                            uint32_t bytes) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (uint32_t base = wave * 1024; base < bytes; base += nw * 1024) {
+        const uint32_t off = base + lane * 16;
+        if (off < bytes) __builtin_amdgcn_global_load_lds(g + off, (lds_void *)(lds + base), 16, 0, 0);
+    }
+}
+
+// body for the segments [s_lo, s_hi) of type T (one workgroup)
+template <uint32_t T, int TPW, int TG, int KS, int P, int EPI>
+__device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *lds, float *red) {
+    constexpr int W = TG * KS;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t tg = wave / KS, ks = wave % KS;
+    const MqSeg &sg = a.seg[si];
+    const bool pair = sg.w2 != nullptr;
+    const uint32_t units = tunits(T, a.n_in);
+    const size_t tstride = (size_t)units * tchunk_bytes(T);
+    // output tiles of this workgroup: TG tile groups of TPW tiles (pairs: one
+    // output tile per group, its gate and up weights)
+    const uint32_t otiles_wg = pair ? TG : TG * TPW;
+    const uint32_t tile0 = (blockIdx.x - sg.wg0) * otiles_wg;
+    const uint32_t ntiles = ttiles(sg.rows);
+    const uint8_t *wt[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        uint32_t tile = pair ? tile0 + tg : tile0 + tg * TPW + t;
+        if (tile >= ntiles) tile = ntiles - 1;  // duplicate reads, results dropped
+        wt[t] = (pair && t == 1 ? sg.w2 : sg.w) + (size_t)tile * tstride;
+    }
+    const uint32_t u_lo = ks * units / KS, u_hi = (ks + 1) * units / KS;
+
+    // prefetch the first P units of this wavefront
+    WReg<T> wr[P][TPW];
+#pragma unroll
+    for (int i = 0; i < P; i++)
+        if (u_lo + i < u_hi) {
+#pragma unroll
+            for (int t = 0; t < TPW; t++) wload<T>(wr[i][t], wt[t] + (size_t)(u_lo + i) * tchunk_bytes(T), lane);
+        }
+
+    // stage the input pack; fused RMSNorm: sum of squares of xres
+    LPack lp;
+    lp.zero = a.nxb * 96;
+    lp.meta = lp.zero + 16;
+    copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.dig), lds, a.nxb * 96);
+    copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.meta), lds + lp.meta, a.nxb * 16);
+    if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + lp.zero)[threadIdx.x] = 0u;
+    float ss = 0.f;
+    if (a.xres) {
+        for (uint32_t i = 4 * threadIdx.x; i < a.n_in; i += 4 * blockDim.x) {
+            const float4 v = *reinterpret_cast<const float4 *>(a.xres + i);
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    const ALane<T> al = alane<T>(lane, lp);
+    float acc[TPW], accm[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) acc[t] = accm[t] = 0.f;
+
+    for (uint32_t u0 = u_lo; u0 < u_hi; u0 += P) {
+#pragma unroll
+        for (int i = 0; i < P; i++) {
+            const uint32_t u = u0 + i;
+            if (u >= u_hi) break;
+            udot<T, TPW>(wr[i], u, lds, lp, al, lane, acc, accm);
+            if (u + P < u_hi) {
+#pragma unroll
+                for (int t = 0; t < TPW; t++) wload<T>(wr[i][t], wt[t] + (size_t)(u + P) * tchunk_bytes(T), lane);
+            }
+        }
+    }
+
+    // row sums: lanes n, n+16, n+32, n+48 hold sub-block classes of row n
+    float v[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        v[t] = acc[t] - accm[t];
+        v[t] += __shfl_xor(v[t], 16, 64);
+        v[t] += __shfl_xor(v[t], 32, 64);
+    }
+    // red layout: [W][TPW][16] partials, then [W] sums of squares
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane < 16) {
+#pragma unroll
+        for (int t = 0; t < TPW; t++) red[(wave * TPW + t) * 16 + lane] = v[t];
+    }
+    if (lane == 0) red[W * TPW * 16 + wave] = ss;
+    __syncthreads();
+
+    // ---- epilogue: thread i owns output i of the workgroup ----
+    float s = 1.0f;
+    if (a.xres) {
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) tot += red[W * TPW * 16 + w];
+        // ops.rs:56-66: 1 / sqrt(mean(x^2) + eps)
+        s = 1.0f / sqrtf(tot / (float)a.n_in + a.eps);
+    }
+    const uint32_t i = threadIdx.x;
+    const uint32_t nout = otiles_wg * 16;  // outputs of the workgroup
+    // threads past the outputs leave; pack epilogues keep whole half-waves
+    // (one 32-element block each), the argmax keeps whole wavefronts
+    constexpr bool PACK = EPI == MQ_RESID || EPI == MQ_SWIGLU;
+    const uint32_t lim = PACK ? ((nout + 31) & ~31u) : EPI == MQ_STORE ? ((nout + 63) & ~63u) : nout;
+    if (i >= lim) return;
+    // value of output i: sum of the KS K-slice partials of its tile group
+    auto partial = [&](uint32_t grp, uint32_t t, uint32_t n) {
+        float r = 0.f;
+#pragma unroll
+        for (int k = 0; k < KS; k++) r += red[((grp * KS + k) * TPW + t) * 16 + n];
+        return r;
+    };
+    const uint32_t row = tile0 * 16 + i;
+    const bool valid = i < nout && row < sg.rows;
+    const uint32_t ii = i < nout ? i : nout - 1;
+    if constexpr (EPI == MQ_SWIGLU) {
+        const uint32_t grp = ii >> 4, n = ii & 15;
+        const float gv = s * partial(grp, 0, n), uv = s * partial(grp, TPW - 1, n);
+        const float act = valid ? silu_mul(gv, uv) : 0.f;
+        pack_half(act, row >> 5, a.xout);
+        return;
+    }
+    const uint32_t grp = pair ? (ii >> 4) : (ii >> 4) / TPW;
+    const uint32_t tt = pair ? 0 : (ii >> 4) % TPW;
+    float y = s * partial(grp, tt, ii & 15);
+    if (sg.bias && valid) y = y + sg.bias[row];
+    if constexpr (EPI == MQ_STORE) {
+        if (valid) sg.out[row] = y;
+        if (a.amax) {
+            unsigned long long key = valid ? amax_key(y, row) : 0ull;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const unsigned long long k2 = __shfl_xor(key, o, 64);
+                key = k2 > key ? k2 : key;
+            }
+            // one key per wavefront of outputs, reduced by the finish kernel
+            if (lane == 0) a.amax[(size_t)blockIdx.x * ((otiles_wg * 16 + 63) / 64) + wave] = key;
+        }
+    } else if constexpr (EPI == MQ_QKV) {
+        const uint32_t pos = a.step[1];
+        // adjacent-pair RoPE (ops.rs:952-975) on q and k: theta = pos * freq[d/2]
+        const float yo = __shfl_xor(y, 1, 64);
+        const uint32_t dd = row % a.head_dim;
+        if (sg.kind < 2 && dd < a.rope_dim) {
+            const float th = (float)pos * a.freq[dd >> 1];
+            float sn, cs;
+            sincosf(th, &sn, &cs);
+            y = (row & 1) ? yo * sn + y * cs : y * cs - yo * sn;
+        }
+        if (valid) {
+            if (sg.kind == 0) {
+                sg.out[row] = y;
+            } else {
+                const uint32_t hh = row / a.head_dim;
+                sg.kv[((size_t)hh * a.ctx + pos) * a.head_dim + dd] = (_Float16)y;
+            }
+        }
+    } else {  // MQ_RESID
+        float xn = 0.f;
+        if (valid) {
+            xn = a.x[row] + y;
+            a.x[row] = xn;
+        }
+        const float pv = valid ? (a.nw ? xn * a.nw[row] : xn) : 0.f;
+        pack_half(pv, row >> 5, a.xout);
+    }
+}
+
+template <uint32_t T0, uint32_t T1, int TPW, int TG, int KS, int P, int EPI>
+__global__ __launch_bounds__(64 * TG * KS) void k_mq(MqArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float red[TG * KS * TPW * 16 + TG * KS];
+    uint32_t si = 0;
+#pragma unroll
+    for (int s = 1; s < MQ_MAX_SEG; s++)
+        if ((uint32_t)s < a.n_seg && blockIdx.x >= a.seg[s].wg0) si = s;
+    if (T0 == T1 || si < a.n_seg0)
+        mq_body<T0, TPW, TG, KS, P, EPI>(a, si, lds, red);
+    else
+        mq_body<T1, TPW, TG, KS, P, EPI>(a, si, lds, red);
+}
+
+// ---------------------------------------------------------------------------
+// launch
+// ---------------------------------------------------------------------------
+using MqFn = void (*)(MqArgs);
+
+template <uint32_t T0, uint32_t T1, int EPI>
+static MqFn pick(const MqGeom &g) {
+#define LRS_MQ_CASE(TPW, TG, KS, P)                                                   \
+    if (g.tpw == TPW && g.tg == TG && g.ks == KS && g.p == P) return k_mq<T0, T1, TPW, TG, KS, P, EPI>;
+    LRS_MQ_CASE(1, 1, 4, 2)
+    LRS_MQ_CASE(1, 2, 4, 2)
+    LRS_MQ_CASE(1, 4, 1, 2)
+    LRS_MQ_CASE(2, 2, 1, 2)
+    LRS_MQ_CASE(2, 2, 2, 2)
+    LRS_MQ_CASE(1, 2, 6, 2)
+#undef LRS_MQ_CASE
+    return nullptr;
+}
+
+template <int EPI>
+static MqFn pick_types(uint32_t t0, uint32_t t1, const MqGeom &g) {
+    if (t0 == t1) {
+        switch (t0) {
+        case T_Q4_K: return pick<T_Q4_K, T_Q4_K, EPI>(g);
+        case T_Q5_K: return pick<T_Q5_K, T_Q5_K, EPI>(g);
+        case T_Q6_K: return pick<T_Q6_K, T_Q6_K, EPI>(g);
+        case T_Q8_0: return pick<T_Q8_0, T_Q8_0, EPI>(g);
+        default: return nullptr;
+        }
+    }
+    if (EPI == MQ_QKV && t0 == T_Q4_K && t1 == T_Q6_K) return pick<T_Q4_K, T_Q6_K, EPI>(g);
+    return nullptr;
+}
+
+bool mq_geom_supported(const MqGeom &g) {
+    return pick<T_Q4_K, T_Q4_K, MQ_STORE>(g) != nullptr;
+}
+
+hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int epi, hipStream_t s,
+                     uint32_t *wgs_out, uint32_t *keys_per_wg) {
+    MqArgs a = in;
+    if (a.n_seg == 0 || a.n_seg > MQ_MAX_SEG) return hipErrorInvalidValue;
+    if (t0 == t1) a.n_seg0 = a.n_seg;
+    uint32_t wgs = 0;
+    for (uint32_t i = 0; i < a.n_seg; i++) {
+        const bool pair = a.seg[i].w2 != nullptr;
+        const uint32_t per = pair ? (uint32_t)g.tg : (uint32_t)(g.tg * g.tpw);
+        if (pair && g.tpw != 2) return hipErrorInvalidValue;
+        a.seg[i].wg0 = wgs;
+        wgs += (ttiles(a.seg[i].rows) + per - 1) / per;
+    }
+    // output packs need whole 32-row blocks per workgroup
+    if (epi == MQ_RESID || epi == MQ_SWIGLU) {
+        for (uint32_t i = 0; i < a.n_seg; i++) {
+            const uint32_t outs = 16 * (a.seg[i].w2 ? g.tg : g.tg * g.tpw);
+            if (outs % 32 || a.seg[i].rows % outs) return hipErrorInvalidValue;
+        }
+    }
+    MqFn fn = nullptr;
+    switch (epi) {
+    case MQ_STORE: fn = pick_types<MQ_STORE>(t0, t1, g); break;
+    case MQ_QKV: fn = pick_types<MQ_QKV>(t0, t1, g); break;
+    case MQ_RESID: fn = pick_types<MQ_RESID>(t0, t1, g); break;
+    case MQ_SWIGLU: fn = pick_types<MQ_SWIGLU>(t0, t1, g); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (!fn) return hipErrorNotSupported;
+    const size_t lds = (size_t)a.nxb * 96 + 16 + (size_t)a.nxb * 16;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    if (wgs_out) *wgs_out = wgs;
+    if (keys_per_wg) {
+        const uint32_t outs = (uint32_t)(g.tg * g.tpw) * 16;
+        *keys_per_wg = (outs + 63) / 64;
+    }
+    hipLaunchKernelGGL(fn, dim3(wgs), dim3(64 * g.tg * g.ks), lds, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace lrs
+
+namespace lrs {
+
+// reduces per-wavefront argmax keys into the next step {token, pos + 1, n}
+__global__ __launch_bounds__(1024) void k_argmax_finish(const unsigned long long *__restrict__ keys,
+                                                        uint32_t n, uint32_t *__restrict__ step,
+                                                        uint32_t *__restrict__ out,
+                                                        uint32_t out_cap) {
+    __shared__ unsigned long long kb[16];
+    unsigned long long best = 0ull;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) best = keys[i] > best ? keys[i] : best;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long k = __shfl_xor(best, o, 64);
+        best = k > best ? k : best;
+    }
+    if ((threadIdx.x & 63) == 0) kb[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / 64; w++) best = kb[w] > best ? kb[w] : best;
+        // no key (every logit NaN): index 0, like a first-max scan that never moves
+        const uint32_t idx = best ? 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull) : 0u;
+        const uint32_t k = step[2];
+        if (out && k < out_cap) out[k] = idx;
+        step[0] = idx;
+        step[1] = step[1] + 1;
+        step[2] = k + 1;
+    }
+}
+
+hipError_t launch_argmax_finish(const unsigned long long *keys, uint32_t n, uint32_t *step,
+                                uint32_t *out, uint32_t out_cap, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(1024), 0, s, keys, n, step, out, out_cap);
+    return hipGetLastError();
+}
+
+static MqGeom g_store_override = {0, 0, 0, 0};
+
+int set_matvec_geom(int tpw, int tg, int ks) {
+    if (tpw == 0 && tg == 0 && ks == 0) {
+        g_store_override = {0, 0, 0, 0};
+        return 0;
+    }
+    const MqGeom g = {tpw, tg, ks, 2};
+    if (!mq_geom_supported(g)) return -1;
+    g_store_override = g;
+    return 0;
+}
+
+// launch shape of a plain matvec (and the output head): enough wavefronts
+// to cover 256 CUs, K split inside the workgroup when rows are few
+MqGeom store_geom(uint32_t t, uint32_t n_in, uint32_t n_out) {
+    (void)t;
+    (void)n_in;
+    if (g_store_override.tpw) return g_store_override;
+    const uint32_t tiles = ttiles(n_out);
+    if (tiles >= 1024) return {1, 4, 1, 2};
+    if (tiles >= 256) return {1, 2, 4, 2};
+    return {1, 1, 4, 2};
+}
+
+hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
+                         hipStream_t s) {
+    if (!is_tiled(w.type)) return hipErrorInvalidValue;
+    const uint32_t nxb = pack_blocks(w.type, w.n_in);
+    const XPack xp = xpack_at(pack, nxb);
+    for (uint32_t c = 0; c < cols; c++) {
+        hipError_t e = launch_xpack(x + (size_t)c * w.n_in, nullptr, w.n_in, nxb, xp, s);
+        if (e != hipSuccess) return e;
+        MqArgs a = {};
+        a.n_seg = 1;
+        a.seg[0].w = w.q;
+        a.seg[0].rows = w.n_out;
+        a.seg[0].out = y + (size_t)c * w.n_out;
+        a.n_in = w.n_in;
+        a.nxb = nxb;
+        a.xin = xp;
+        e = launch_mq(a, w.type, w.type, store_geom(w.type, w.n_in, w.n_out), MQ_STORE, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace lrs

@@ -1,0 +1,77 @@
+// Arguments of the matrix-core matvec (mq.hip) shared with its callers.
+#pragma once
+
+#include <cstdint>
+
+namespace lrs {
+
+// Activation pack: a vector of n elements as three int8 digits per element
+// with one power-of-two scale per 32-element block:
+//   x[32b + i] ~= scale_b * (d0 * 65536 + d1 * 256 + d2),  |error| <= scale_b / 2
+// where scale_b = 2^(e - 21) and 2^(e-1) <= max |x| of the block < 2^e (22
+// significant bits against the block maximum).  Sums of the original f32
+// elements ride along for the K-quant min / Q6_K offset terms.
+//   dig  [nxb][3][32] int8: digit d of element i at 96 b + 32 d + i
+//   meta [nxb] float4 {scale, sum of the 32 elements, sum of 0..15, sum of 16..31}
+struct XPack {
+    int8_t *dig;
+    float *meta;
+};
+
+// bytes of a pack of nxb blocks (digits, then meta, both 16-aligned)
+inline size_t xpack_bytes(uint32_t nxb) { return (size_t)nxb * 96 + (size_t)nxb * 16; }
+inline XPack xpack_at(void *base, uint32_t nxb) {
+    XPack p;
+    p.dig = reinterpret_cast<int8_t *>(base);
+    p.meta = reinterpret_cast<float *>(reinterpret_cast<char *>(base) + (size_t)nxb * 96);
+    return p;
+}
+
+enum MqEpilogue : uint32_t {
+    MQ_STORE = 0,   // out[row] = s*v (+ bias[row]); optional per-workgroup argmax keys
+    MQ_QKV = 1,     // q: out f32; k, v: f16 cache append at pos; bias, adjacent-pair RoPE on q/k
+    MQ_RESID = 2,   // x[row] += v; writes the pack of x_new * nw (next op's input)
+    MQ_SWIGLU = 3,  // tile pairs (gate, up): a = silu(s g) * (s u); writes the pack of a
+};
+
+constexpr int MQ_MAX_SEG = 3;
+
+// One output segment: a tiled weight (or a gate/up pair) and where its rows go.
+struct MqSeg {
+    const uint8_t *w;   // tiled weight
+    const uint8_t *w2;  // second weight of a tile pair (SwiGLU up) or null
+    uint32_t rows;      // valid rows (output index range for pairs)
+    uint32_t wg0;       // first workgroup (set by the launcher)
+    uint32_t kind;      // MQ_QKV: 0 = q, 1 = k, 2 = v
+    const float *bias;  // [rows] or null
+    float *out;         // f32 destination (STORE, QKV q)
+    _Float16 *kv;       // MQ_QKV k / v: this layer's cache [kv_head][ctx][head_dim]
+};
+
+struct MqArgs {
+    MqSeg seg[MQ_MAX_SEG];
+    uint32_t n_seg, n_seg0;  // segments; the first n_seg0 are of the first type
+    uint32_t n_in;           // K (elements)
+    uint32_t nxb;            // 32-element blocks of the input pack (K padded to units)
+    XPack xin;               // input pack
+    const float *xres;       // fused RMSNorm: the f32 vector whose rms scales the result
+    float eps;
+    // MQ_RESID
+    float *x;                // residual [rows]
+    const float *nw;         // norm weight folded into the output pack (null: 1)
+    XPack xout;              // output pack (RESID / SWIGLU)
+    // MQ_QKV
+    const uint32_t *step;    // device {token, pos}
+    const float *freq;       // RoPE frequencies [rope_dim / 2]
+    uint32_t head_dim, rope_dim, ctx;
+    // greedy (MQ_STORE)
+    unsigned long long *amax;  // [workgroups] argmax keys of the rows, or null
+};
+
+// launch shape: TPW tiles per wavefront sharing the activation, TG tile
+// groups and KS K-slices of wavefronts per workgroup, P units in flight
+struct MqGeom {
+    int tpw, tg, ks, p;
+};
+
+}  // namespace lrs

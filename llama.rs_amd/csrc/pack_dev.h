@@ -1,0 +1,50 @@
+// Device helpers shared by the kernels that write activation packs
+// (mq_args.h) or greedy argmax keys.
+#pragma once
+
+#include "lrs_internal.h"
+
+namespace lrs {
+
+// Packs one 32-element block held one element per lane by the 32 lanes of a
+// half wavefront (lane i of the half = element i).  Writes the 3 digit bytes
+// of the element and, from lane 0 of the half, the block's meta.
+__device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p) {
+    const uint32_t i = threadIdx.x & 31;
+    float amax = fabsf(v);
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    float r16 = v;  // sum of this lane's 16-element run
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) r16 += __shfl_xor(r16, o, 64);
+    const float other = __shfl_xor(r16, 16, 64);
+    int e;
+    frexpf(amax, &e);
+    if (e < -100) e = -100;  // blocks this small pack as zero
+    const int X = __float2int_rn(v * ldexpf(1.0f, 21 - e));
+    const int d2 = (int)(int8_t)(X & 255);
+    const int X1 = (X - d2) >> 8;
+    const int d1 = (int)(int8_t)(X1 & 255);
+    const int d0 = (X1 - d1) >> 8;
+    int8_t *dg = p.dig + (size_t)blk * 96 + i;
+    dg[0] = (int8_t)d0;
+    dg[32] = (int8_t)d1;
+    dg[64] = (int8_t)d2;
+    if (i == 0) {
+        // r16 = sum of elements 0..15, other = sum of 16..31
+        *reinterpret_cast<float4 *>(p.meta + 4 * (size_t)blk) =
+            make_float4(ldexpf(1.0f, e - 21), r16 + other, r16, other);
+    }
+}
+
+// orderable 64-bit argmax key of value v at index r: the larger value wins,
+// ties go to the smaller index (the first max of ops.rs:1035-1045); NaN
+// never wins
+__device__ __forceinline__ unsigned long long amax_key(float v, uint32_t r) {
+    if (v != v) return 0ull;
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)o << 32) | (0xFFFFFFFFu - r);
+}
+
+}  // namespace lrs

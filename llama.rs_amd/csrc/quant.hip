@@ -9,52 +9,6 @@
 
 namespace lrs {
 
-// ---------------------------------------------------------------------------
-// GGUF byte offset of byte `i` of the device q-part of a block
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t q_to_gguf_off(uint32_t t, uint32_t i) {
-    return t == T_Q8_0 ? i + 2 : i;  // Q6_K q-part = GGUF bytes 0..207
-}
-
-// repack: one thread per q-part byte / per d entry
-__global__ void k_repack_from_gguf(const uint8_t *__restrict__ g, uint32_t t, uint64_t n_blocks,
-                                   uint8_t *__restrict__ q, uint16_t *__restrict__ d) {
-    const uint32_t qb = (uint32_t)q_bytes_per_block(t), gb = (uint32_t)block_bytes(t);
-    const uint64_t nq = n_blocks * qb;
-    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nq;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        uint64_t b = i / qb;
-        uint32_t o = (uint32_t)(i - b * qb);
-        q[i] = g[b * gb + q_to_gguf_off(t, o)];
-    }
-    if (d) {
-        const uint32_t doff = t == T_Q6_K ? 208 : 0;
-        for (uint64_t b = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < n_blocks;
-             b += (uint64_t)gridDim.x * blockDim.x)
-            d[b] = rd16(g + b * gb + doff);
-    }
-}
-
-__global__ void k_repack_to_gguf(const uint8_t *__restrict__ q, const uint16_t *__restrict__ d,
-                                 uint32_t t, uint64_t n_blocks, uint8_t *__restrict__ g) {
-    const uint32_t qb = (uint32_t)q_bytes_per_block(t), gb = (uint32_t)block_bytes(t);
-    const uint64_t nq = n_blocks * qb;
-    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nq;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        uint64_t b = i / qb;
-        uint32_t o = (uint32_t)(i - b * qb);
-        g[b * gb + q_to_gguf_off(t, o)] = q[i];
-    }
-    if (d) {
-        const uint32_t doff = t == T_Q6_K ? 208 : 0;
-        for (uint64_t b = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < n_blocks;
-             b += (uint64_t)gridDim.x * blockDim.x) {
-            g[b * gb + doff] = (uint8_t)(d[b] & 0xFF);
-            g[b * gb + doff + 1] = (uint8_t)(d[b] >> 8);
-        }
-    }
-}
-
 static unsigned grid_for(uint64_t n, unsigned bs) {
     uint64_t g = (n + bs - 1) / bs;
     if (g > 65536u * 4u) g = 65536u * 4u;
@@ -62,20 +16,46 @@ static unsigned grid_for(uint64_t n, unsigned bs) {
     return (unsigned)g;
 }
 
-hipError_t launch_repack_from_gguf(const uint8_t *gguf_dev, WeightView w, uint8_t *q, uint16_t *d,
-                                   hipStream_t s) {
-    uint64_t nblk = (uint64_t)w.n_out * w.nb;
-    uint64_t n = nblk * q_bytes_per_block(w.type);
-    hipLaunchKernelGGL(k_repack_from_gguf, dim3(grid_for(n, 256)), dim3(256), 0, s, gguf_dev,
-                       w.type, nblk, q, has_d_array(w.type) ? d : nullptr);
+// ---------------------------------------------------------------------------
+// GGUF row-major blocks <-> device layout (tiled.h for the matvec types, the
+// GGUF bytes as they are for the others).  One thread per device word; every
+// padding byte is written as zero.
+// ---------------------------------------------------------------------------
+__global__ void k_repack_from_gguf(const uint8_t *__restrict__ g, WeightView w, size_t dev_bytes,
+                                   uint8_t *__restrict__ q) {
+    const uint32_t bb = (uint32_t)block_bytes(w.type);
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < dev_bytes / 4;
+         i += (size_t)gridDim.x * blockDim.x) {
+        uint32_t v = 0;
+        for (int k = 0; k < 4; k++) {
+            uint32_t row, blk, o;
+            if (tinv(w.type, w.n_in, w.n_out, 4 * i + k, row, blk, o))
+                v |= (uint32_t)g[((size_t)row * w.nb + blk) * bb + o] << (8 * k);
+        }
+        reinterpret_cast<uint32_t *>(q)[i] = v;
+    }
+}
+
+__global__ void k_repack_to_gguf(WeightView w, size_t dev_bytes, uint8_t *__restrict__ g) {
+    const uint32_t bb = (uint32_t)block_bytes(w.type);
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < dev_bytes;
+         i += (size_t)gridDim.x * blockDim.x) {
+        uint32_t row, blk, o;
+        if (tinv(w.type, w.n_in, w.n_out, i, row, blk, o)) g[((size_t)row * w.nb + blk) * bb + o] = w.q[i];
+    }
+}
+
+hipError_t launch_repack_from_gguf(const uint8_t *gguf_dev, WeightView w, uint8_t *q, hipStream_t s) {
+    const size_t db = weight_dev_bytes(w.type, w.n_in, w.n_out);
+    if (!is_tiled(w.type)) return hipMemcpyAsync(q, gguf_dev, db, hipMemcpyDeviceToDevice, s);
+    hipLaunchKernelGGL(k_repack_from_gguf, dim3(grid_for(db / 4, 256)), dim3(256), 0, s, gguf_dev, w, db, q);
     return hipGetLastError();
 }
 
 hipError_t launch_repack_to_gguf(WeightView w, uint8_t *gguf_dev, hipStream_t s) {
-    uint64_t nblk = (uint64_t)w.n_out * w.nb;
-    uint64_t n = nblk * q_bytes_per_block(w.type);
-    hipLaunchKernelGGL(k_repack_to_gguf, dim3(grid_for(n, 256)), dim3(256), 0, s, w.q, w.d,
-                       w.type, nblk, gguf_dev);
+    const size_t db = weight_dev_bytes(w.type, w.n_in, w.n_out);
+    if (!is_tiled(w.type)) return hipMemcpyAsync(gguf_dev, w.q, db, hipMemcpyDeviceToDevice, s);
+    hipLaunchKernelGGL(k_repack_to_gguf, dim3(grid_for(db, 256)), dim3(256), 0, s, w, db, gguf_dev);
     return hipGetLastError();
 }
 
@@ -169,33 +149,29 @@ __device__ uint8_t gen_byte(uint32_t t, uint64_t seed, uint64_t blk, uint32_t o,
     }
 }
 
-__global__ void k_generate(uint32_t t, uint64_t n_blocks, uint64_t seed, int mode, float lo,
-                           float hi, uint8_t *__restrict__ q, uint16_t *__restrict__ d) {
-    const uint32_t qb = (uint32_t)q_bytes_per_block(t);
-    const uint64_t nw = n_blocks * qb / 4;  // q-part sizes are multiples of 4 bytes
-    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < nw;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-        uint64_t byte = i * 4;
-        uint64_t b = byte / qb;
-        uint32_t o = (uint32_t)(byte - b * qb);
+// synthetic weight straight into the device layout: one thread per device
+// word, each byte the generator byte of its GGUF (block, offset); the block
+// index is the GGUF row-major one (row * nb + block), as on the host
+__global__ void k_generate(WeightView w, size_t dev_bytes, uint64_t seed, int mode, float lo, float hi,
+                           uint8_t *__restrict__ q) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < dev_bytes / 4;
+         i += (size_t)gridDim.x * blockDim.x) {
         uint32_t v = 0;
-        for (int k = 0; k < 4; k++)
-            v |= (uint32_t)gen_byte(t, seed, b, q_to_gguf_off(t, o + k), mode, lo, hi) << (8 * k);
+        for (int k = 0; k < 4; k++) {
+            uint32_t row, blk, o;
+            if (tinv(w.type, w.n_in, w.n_out, 4 * i + k, row, blk, o))
+                v |= (uint32_t)gen_byte(w.type, seed, (uint64_t)row * w.nb + blk, o, mode, lo, hi) << (8 * k);
+        }
         reinterpret_cast<uint32_t *>(q)[i] = v;
-    }
-    if (d) {
-        for (uint64_t b = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < n_blocks;
-             b += (uint64_t)gridDim.x * blockDim.x)
-            d[b] = gen_d16(t, seed, b, mode, lo, hi, false);
     }
 }
 
-hipError_t launch_generate(WeightView w, uint8_t *q, uint16_t *d, uint64_t seed, int mode,
-                           float d_lo, float d_hi, hipStream_t s) {
-    uint64_t nblk = (uint64_t)w.n_out * w.nb;
-    uint64_t n = nblk * q_bytes_per_block(w.type) / 4;
-    hipLaunchKernelGGL(k_generate, dim3(grid_for(n, 256)), dim3(256), 0, s, w.type, nblk, seed,
-                       mode, d_lo, d_hi, q, has_d_array(w.type) ? d : nullptr);
+hipError_t launch_generate(WeightView w, uint8_t *q, uint64_t seed, int mode, float d_lo, float d_hi,
+                           hipStream_t s) {
+    if (!is_tiled(w.type)) return hipErrorInvalidValue;
+    const size_t db = weight_dev_bytes(w.type, w.n_in, w.n_out);
+    hipLaunchKernelGGL(k_generate, dim3(grid_for(db / 4, 256)), dim3(256), 0, s, w, db, seed, mode,
+                       d_lo, d_hi, q);
     return hipGetLastError();
 }
 

@@ -182,7 +182,6 @@ def test_matvec_reference_kernel_cases(lrs, orc, ctx, t, n_in, n_out):
     assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-5  # the reference's own bar
 
 
-GEOMS = [(l, r, wv) for l in (8, 16, 32, 64) for r in (1, 2, 4) for wv in (2, 4, 8)]
 
 
 @pytest.mark.parametrize("t", KQ)
@@ -194,7 +193,7 @@ def test_matvec_every_geometry_ragged(lrs, orc, ctx, t):
     ref = orc.matvec(t, w, n_in, n_out, x)
     W = lrs.Weight.upload(ctx, t, w, n_in, n_out)
     try:
-        for g in GEOMS:
+        for g in lrs.MATVEC_GEOMS:
             lrs.set_matvec_geom(*g)
             got = W.matvec(x)
             assert rel_l2(got, ref) < MATVEC_TOL, (g, rel_l2(got, ref))
