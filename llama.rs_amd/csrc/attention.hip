@@ -1,285 +1,216 @@
-// attention.hip — batch-1 causal GQA decode attention over the f16 KV cache,
-// split-K ("flash decode"): partials per (split, KV head), then a combine.
+// attention.hip — batch-1 causal GQA decode attention over the f16 KV cache.
 //
-// Math of attention.rs:76-166 (scores q.k * 1/sqrt(head_dim), softmax,
-// weighted sum of V, query head h reads KV head h / (n_head / n_head_kv)),
-// over the f16 cache the reference GPU path keeps (kv_pack.comp,
-// attention_split.comp + attn_reduce.comp): every split keeps (max, sum,
-// unnormalised accumulator) and the combine rescales them, which is the
-// online-softmax identity, exact up to f32 rounding.
+// Math of attention.rs:76-166: scores q.k * 1/sqrt(head_dim) over positions
+// 0..pos, softmax, weighted sum of V; query head h reads KV head
+// h / (n_head / n_head_kv).  The cache holds f16 K and V, as the reference
+// GPU path keeps them (kv_pack.comp).
 //
-// Cache layout (per layer): [n_head_kv][ctx][head_dim] f16, so a split's K
-// (and V) rows are one contiguous run.  Each workgroup copies its K and V run
-// straight into LDS with global_load_lds_dwordx4 (one HBM round trip, no
-// VGPR staging), then: scores with HD/8 lanes per position (each lane owns 8
-// dims as one 128-bit LDS read, the rep query heads of the KV head held in
-// registers), softmax per head, the V sum with 2 dims per lane, and the
-// partial (m, l, acc) to global memory.  The
-// partials are rescaled and summed by a second, one-workgroup-per-head kernel
-// (on this multi-XCD part a per-workgroup "last one combines" handshake needs
-// an L2 writeback + invalidate per workgroup, which costs more than a launch).
+// One workgroup of 16 wavefronts per query head, all positions, one launch,
+// in three phases over the positions 0..pos:
+//   scores   a "lane group" of HD/8 lanes owns one position at a time (8 dims
+//            = one 16-byte piece of the K row per lane; the 64 lane groups
+//            take positions g, g+64, ..., with the next positions' loads in
+//            flight); q is split into f16 hi + lo halves so v_dot2_f32_f16
+//            forms q.k from exact f16 products to 22 bits of q; scores to LDS
+//   softmax  max and sum over the LDS scores (one exp per position)
+//   values   the same lane groups accumulate p * V over their positions; the
+//            groups of a wavefront are summed with cross-lane adds, the 16
+//            wavefronts through LDS
+// and the output is written as the activation pack of the o-projection.
+// A single pass replaces the split + combine pair of the reference
+// (attention_split.comp + attn_reduce.comp): no second launch, no partials
+// in HBM.
 #include "lrs_internal.h"
 #include "pack_dev.h"
 
 namespace lrs {
 
+constexpr int ATT_THREADS = 1024;
+constexpr int ATT_WAVES = ATT_THREADS / 64;
+constexpr int ATT_DEPTH = 4;  // positions per lane group with K and V loads in flight
+
 struct AttnArgs {
-    const float *q;          // [n_head * HD], RoPE applied
-    const _Float16 *kc, *vc; // this layer's caches
-    XPack out;               // pack of the [n_head * HD] output (o-projection input)
-    float *part;             // [n_head][S][HD + 4] split partials (acc, m, l, pad)
-    const uint32_t *step;    // [token, pos]: attends positions 0..pos
-    uint32_t n_head, n_kv, ctx, S, chunk_max;
+    const float *q;           // [n_head * HD], RoPE applied
+    const _Float16 *kc, *vc;  // this layer's caches [n_kv][ctx][HD]
+    XPack out;                // pack of the [n_head * HD] output
+    const uint32_t *step;     // {token, pos}: attends positions 0..pos
+    uint32_t n_head, n_kv, ctx;
     float scale;
 };
 
-constexpr int ATT_THREADS = 256;
-constexpr int ATT_WAVES = ATT_THREADS / 64;
-constexpr int ATT_MAX_REP = 8;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ half2_t as_h2(uint32_t v) {
+    half2_t r;
+    __builtin_memcpy(&r, &v, 4);
+    return r;
+}
 
-// copies `bytes` (multiple of 16) from global to LDS, 1 KB per wave
-// instruction (each lane 16 B); lanes past the end are masked off
-__device__ __forceinline__ void copy_to_lds(const uint8_t *__restrict__ g, uint8_t *lds,
-                                            uint32_t bytes) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (uint32_t base = wave * 1024; base < bytes; base += ATT_WAVES * 1024) {
-        const uint32_t off = base + lane * 16;
-        if (off < bytes)
-            __builtin_amdgcn_global_load_lds(g + off, (lds_void *)(lds + base), 16, 0, 0);
+// block-wide reduction of one float (max or sum) through LDS
+template <bool MAX>
+__device__ __forceinline__ float block_reduce(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float t = __shfl_xor(v, o, 64);
+        v = MAX ? fmaxf(v, t) : v + t;
     }
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();  // red[] may still be read by an earlier reduction
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < ATT_WAVES; w++) r = MAX ? fmaxf(r, red[w]) : r + red[w];
+    return r;
 }
 
 template <int HD>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ float m_s[ATT_MAX_REP], l_s[ATT_MAX_REP];
-    constexpr int LPP = HD / 8;        // lanes per position in the score phase
-    constexpr int PPW = 64 / LPP;      // positions per wave and step
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kh = blockIdx.y, s = blockIdx.x;
-    const uint32_t rep = a.n_head / a.n_kv, h0 = kh * rep;
+    constexpr int LP = HD / 8;              // lanes per position
+    constexpr int NG = ATT_THREADS / LP;    // lane groups per workgroup
+    extern __shared__ float sc[];           // [ctx] scores, then probabilities
+    __shared__ float red[ATT_WAVES];
+    __shared__ float sacc[ATT_WAVES][HD];
+    const uint32_t tid = threadIdx.x, sub = tid % LP, grp = tid / LP;
+    const uint32_t lane = tid & 63, wave = tid >> 6;
+    const uint32_t h = blockIdx.x, kh = h / (a.n_head / a.n_kv);
     const uint32_t L = a.step[1] + 1;
-    const uint32_t chunk = (L + a.S - 1) / a.S;
-    const uint32_t p0 = min(s * chunk, L), p1 = min(p0 + chunk, L), n = p1 - p0;
+    const _Float16 *kb = a.kc + (size_t)kh * a.ctx * HD + 8 * sub;
+    const _Float16 *vb = a.vc + (size_t)kh * a.ctx * HD + 8 * sub;
 
-    _Float16 *ks = reinterpret_cast<_Float16 *>(smem);            // [chunk_max][HD]
-    _Float16 *vs = ks + (size_t)a.chunk_max * HD;                 // [chunk_max][HD]
-    float *sc = reinterpret_cast<float *>(vs + (size_t)a.chunk_max * HD);  // [rep][chunk_max]
-    float *red = sc + ATT_MAX_REP * a.chunk_max;                  // [WAVES][rep][HD]
-
-    // K and V runs of this split straight into LDS
-    const size_t row0 = (size_t)kh * a.ctx + p0;
-    copy_to_lds(reinterpret_cast<const uint8_t *>(a.kc + row0 * HD), reinterpret_cast<uint8_t *>(ks),
-                n * HD * 2);
-    copy_to_lds(reinterpret_cast<const uint8_t *>(a.vc + row0 * HD), reinterpret_cast<uint8_t *>(vs),
-                n * HD * 2);
-    // this lane's 8 dims of every query head of the group
-    const uint32_t sub = lane % LPP, pw = lane / LPP;
-    float qr[ATT_MAX_REP][8];
+    // K and V of the first ATT_DEPTH positions of every lane group in flight
+    // at once (all of them up to 64 * ATT_DEPTH positions)
+    uint4 kr[ATT_DEPTH], vr[ATT_DEPTH];
 #pragma unroll
-    for (int r = 0; r < ATT_MAX_REP; r++) {
-        if (r < (int)rep) {
-            const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)(h0 + r) * HD + 8 * sub);
-            const float4 x0 = qp[0], x1 = qp[1];
-            qr[r][0] = x0.x; qr[r][1] = x0.y; qr[r][2] = x0.z; qr[r][3] = x0.w;
-            qr[r][4] = x1.x; qr[r][5] = x1.y; qr[r][6] = x1.z; qr[r][7] = x1.w;
+    for (int i = 0; i < ATT_DEPTH; i++) {
+        const uint32_t p = grp + i * NG;
+        if (p < L) kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)p * HD);
+    }
+#pragma unroll
+    for (int i = 0; i < ATT_DEPTH; i++) {
+        const uint32_t p = grp + i * NG;
+        if (p < L) vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)p * HD);
+    }
+    // q / 2^e as f16 hi + lo pairs (dims 8 sub .. 8 sub + 7), 2^e >= max |q|
+    // of the head so both halves stay in f16 range; the score is rescaled
+    // by 2^e * scale (exact power of two, then the reference's 1/sqrt(HD))
+    half2_t qh[4], ql[4];
+    float sscale;
+    {
+        const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + 8 * sub);
+        const float4 x0 = qp[0], x1 = qp[1];
+        float qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float qm = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) qm = fmaxf(qm, fabsf(qv[i]));
+#pragma unroll
+        for (int o = LP / 2; o >= 1; o >>= 1) qm = fmaxf(qm, __shfl_xor(qm, o, 64));
+        int e;
+        frexpf(qm, &e);
+        e = e < -60 ? -60 : e;
+#pragma unroll
+        for (int i = 0; i < 8; i++) qv[i] = ldexpf(qv[i], -e);
+        sscale = ldexpf(1.0f, e);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const _Float16 h0 = (_Float16)qv[2 * i], h1 = (_Float16)qv[2 * i + 1];
+            qh[i] = half2_t{h0, h1};
+            ql[i] = half2_t{(_Float16)(qv[2 * i] - (float)h0), (_Float16)(qv[2 * i + 1] - (float)h1)};
         }
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
 
-    // scores: positions in steps of PPW per wave, LPP lanes per position
-    for (uint32_t pb = wave * PPW; pb < n; pb += ATT_WAVES * PPW) {
-        const uint32_t pp = pb + pw;
-        float acc[ATT_MAX_REP];
+    // ---- scores ----
+    float smax = -INFINITY;
+    for (uint32_t p0 = grp; p0 < L; p0 += ATT_DEPTH * NG) {
 #pragma unroll
-        for (int r = 0; r < ATT_MAX_REP; r++) acc[r] = 0.f;
-        if (pp < n) {
-            const uint4 raw = *reinterpret_cast<const uint4 *>(ks + (size_t)pp * HD + 8 * sub);
-            const _Float16 *kv = reinterpret_cast<const _Float16 *>(&raw);
+        for (int i = 0; i < ATT_DEPTH; i++) {
+            const uint32_t p = p0 + i * NG;
+            if (p < L) {  // uniform within the lane group
+                const uint4 k = kr[i];
+                const uint32_t pn = p + ATT_DEPTH * NG;
+                if (pn < L) kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)pn * HD);
+                const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
+                float s = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float kf = (float)kv[e];
+                for (int j = 0; j < 4; j++) {
+                    s = __builtin_amdgcn_fdot2(ql[j], as_h2(kw[j]), s, false);
+                    s = __builtin_amdgcn_fdot2(qh[j], as_h2(kw[j]), s, false);
+                }
 #pragma unroll
-                for (int r = 0; r < ATT_MAX_REP; r++)
-                    if (r < (int)rep) acc[r] = fmaf(qr[r][e], kf, acc[r]);
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < ATT_MAX_REP; r++) {
-            if (r < (int)rep) {
-                float v = acc[r];
-#pragma unroll
-                for (int o = LPP / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-                if (sub == 0 && pp < n) sc[r * a.chunk_max + pp] = v * a.scale;
-            }
-        }
-    }
-    __syncthreads();
-
-    // per head: max, exp, sum (one wavefront per head)
-    for (uint32_t r = wave; r < rep; r += ATT_WAVES) {
-        float m = -INFINITY;
-        for (uint32_t pp = lane; pp < n; pp += 64) m = fmaxf(m, sc[r * a.chunk_max + pp]);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        float l = 0.f;
-        for (uint32_t pp = lane; pp < n; pp += 64) {
-            const float e = expf(sc[r * a.chunk_max + pp] - m);
-            sc[r * a.chunk_max + pp] = e;
-            l += e;
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
-        if (lane == 0) {
-            m_s[r] = m;
-            l_s[r] = l;
-        }
-    }
-    __syncthreads();
-
-    // V: wave w sums positions w, w+WAVES, ...; lane owns HD/64 dims
-    constexpr int DPL = HD / 64;
-    float acc[ATT_MAX_REP][DPL];
-#pragma unroll
-    for (int r = 0; r < ATT_MAX_REP; r++)
-#pragma unroll
-        for (int k = 0; k < DPL; k++) acc[r][k] = 0.f;
-    for (uint32_t pp = wave; pp < n; pp += ATT_WAVES) {
-        float v[DPL];
-        const _Float16 *vr = vs + (size_t)pp * HD + DPL * lane;
-#pragma unroll
-        for (int k = 0; k < DPL; k++) v[k] = (float)vr[k];
-#pragma unroll
-        for (int r = 0; r < ATT_MAX_REP; r++) {
-            if (r < (int)rep) {
-                const float p = sc[r * a.chunk_max + pp];
-#pragma unroll
-                for (int k = 0; k < DPL; k++) acc[r][k] = fmaf(p, v[k], acc[r][k]);
+                for (int o = LP / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+                s = (s * sscale) * a.scale;  // attention.rs: (q.k) / sqrt(head_dim)
+                if (sub == 0) sc[p] = s;
+                smax = fmaxf(smax, s);
             }
         }
     }
+
+    // ---- softmax (attention.rs:120-140) ----
+    const float M = block_reduce<true>(smax, red);  // also orders the score stores
+    float lsum = 0.f;
+    for (uint32_t p = tid; p < L; p += ATT_THREADS) {
+        const float e = expf(sc[p] - M);
+        sc[p] = e;
+        lsum += e;
+    }
+    const float den = block_reduce<false>(lsum, red);  // also orders the exp stores
+
+    // ---- values ----
+    float acc[8];
 #pragma unroll
-    for (int r = 0; r < ATT_MAX_REP; r++)
-        if (r < (int)rep)
+    for (int e = 0; e < 8; e++) acc[e] = 0.f;
+    for (uint32_t p0 = grp; p0 < L; p0 += ATT_DEPTH * NG) {
 #pragma unroll
-            for (int k = 0; k < DPL; k++) red[((size_t)wave * rep + r) * HD + DPL * lane + k] = acc[r][k];
-    __syncthreads();
-    for (uint32_t i = tid; i < rep * HD; i += ATT_THREADS) {
-        const uint32_t r = i / HD, d = i % HD;
-        float v = 0.f;
+        for (int i = 0; i < ATT_DEPTH; i++) {
+            const uint32_t p = p0 + i * NG;
+            if (p < L) {
+                const uint4 v = vr[i];
+                const uint32_t pn = p + ATT_DEPTH * NG;
+                if (pn < L) vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)pn * HD);
+                const float pe = sc[p];
+                const _Float16 *vh = reinterpret_cast<const _Float16 *>(&v);
 #pragma unroll
-        for (int w = 0; w < ATT_WAVES; w++) v += red[((size_t)w * rep + r) * HD + d];
-        float *pr = a.part + ((size_t)(h0 + r) * a.S + s) * (HD + 4);
-        pr[d] = v;
-        if (d == 0) {
-            pr[HD] = m_s[r];
-            pr[HD + 1] = l_s[r];
+                for (int e = 0; e < 8; e++) acc[e] = fmaf(pe, (float)vh[e], acc[e]);
+            }
         }
     }
-
-}
-
-// combine of the split partials of one query head (attn_reduce.comp): one
-// workgroup per head, the kernel boundary after k_attn makes every split's
-// partial visible (no per-workgroup L2 writeback / invalidate)
-template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_combine(AttnArgs a) {
-    extern __shared__ float w[];  // [S] split weights
-    __shared__ float red[HD / 64];
-    __shared__ float Msh;
-    const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
-    constexpr uint32_t PR = HD + 4;
-    const float *pr = a.part + (size_t)h * a.S * PR;
-    float M = -INFINITY;
-    for (uint32_t t = d; t < a.S; t += HD) M = fmaxf(M, pr[(size_t)t * PR + HD]);
+    // lane groups of a wavefront hold the same dims: sum them, then the waves
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    if (lane == 0) red[wave] = M;
-    __syncthreads();
-    if (d == 0) {
-        float mm = red[0];
-        for (int i = 1; i < HD / 64; i++) mm = fmaxf(mm, red[i]);
-        Msh = mm;
-    }
-    __syncthreads();
-    M = Msh;
-    float den = 0.f;
-    for (uint32_t t = d; t < a.S; t += HD) {
-        const float mt = pr[(size_t)t * PR + HD];
-        const float wt = mt == -INFINITY ? 0.f : expf(mt - M);
-        w[t] = wt;
-        den = fmaf(wt, pr[(size_t)t * PR + HD + 1], den);
-    }
+    for (int o = LP; o < 64; o <<= 1)
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
-    __syncthreads();
-    if (lane == 0) red[wave] = den;
-    __syncthreads();
-    float tot = 0.f;
-    for (int i = 0; i < HD / 64; i++) tot += red[i];
-    // all S loads of this thread's column are independent
-    float num0 = 0.f, num1 = 0.f, num2 = 0.f, num3 = 0.f;
-    uint32_t t = 0;
-    for (; t + 4 <= a.S; t += 4) {
-        num0 = fmaf(w[t], pr[(size_t)t * PR + d], num0);
-        num1 = fmaf(w[t + 1], pr[(size_t)(t + 1) * PR + d], num1);
-        num2 = fmaf(w[t + 2], pr[(size_t)(t + 2) * PR + d], num2);
-        num3 = fmaf(w[t + 3], pr[(size_t)(t + 3) * PR + d], num3);
+        for (int e = 0; e < 8; e++) acc[e] += __shfl_xor(acc[e], o, 64);
+    if (lane < LP) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) sacc[wave][8 * lane + e] = acc[e];
     }
-    for (; t < a.S; t++) num0 = fmaf(w[t], pr[(size_t)t * PR + d], num0);
-    pack_half(((num0 + num1) + (num2 + num3)) / tot, (h * HD + d) >> 5, a.out);
-}
-
-size_t attn_lds_bytes(uint32_t head_dim, uint32_t chunk_max) {
-    const size_t kv = 2 * (size_t)chunk_max * head_dim * sizeof(_Float16);
-    return kv + sizeof(float) * ((size_t)ATT_MAX_REP * chunk_max + (size_t)ATT_WAVES * ATT_MAX_REP * head_dim);
-}
-
-// splits so that a split holds at most 128 positions at full context
-uint32_t attn_splits(uint32_t ctx) {
-    uint32_t S = (ctx + 127) / 128;
-    if (S < 8) S = 8;
-    if (S > ctx) S = ctx;
-    return S;
+    __syncthreads();
+    if (tid >= HD) return;  // whole half-waves remain for the pack (HD % 32 == 0)
+    float num = 0.f;
+#pragma unroll
+    for (int w = 0; w < ATT_WAVES; w++) num += sacc[w][tid];
+    pack_half(num / den, (h * HD + tid) >> 5, a.out);
 }
 
 hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, XPack out,
-                            float *part, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
-                            uint32_t head_dim, uint32_t ctx, uint32_t S, hipStream_t s) {
+                            const uint32_t *step, uint32_t n_head, uint32_t n_kv,
+                            uint32_t head_dim, uint32_t ctx, hipStream_t s) {
     AttnArgs a;
     a.q = q;
     a.kc = kc;
     a.vc = vc;
     a.out = out;
-    a.part = part;
     a.step = step;
     a.n_head = n_head;
     a.n_kv = n_kv;
     a.ctx = ctx;
-    a.S = S;
-    a.chunk_max = (ctx + S - 1) / S;
     a.scale = 1.0f / sqrtf((float)head_dim);
-    if (n_head / n_kv > (uint32_t)ATT_MAX_REP) return hipErrorInvalidValue;
-    const size_t lds = attn_lds_bytes(head_dim, a.chunk_max);
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
-    dim3 grid(S, n_kv);
-    const size_t wl = S * sizeof(float);
+    if (n_kv == 0 || n_head % n_kv) return hipErrorInvalidValue;
+    const size_t lds = (size_t)ctx * sizeof(float);  // scores of every position
+    if (lds > 128 * 1024) return hipErrorInvalidValue;
     switch (head_dim) {
-    case 64:
-        hipLaunchKernelGGL(k_attn<64>, grid, dim3(ATT_THREADS), lds, s, a);
-        hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), wl, s, a);
-        break;
-    case 128:
-        hipLaunchKernelGGL(k_attn<128>, grid, dim3(ATT_THREADS), lds, s, a);
-        hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_head), dim3(128), wl, s, a);
-        break;
-    case 256:
-        hipLaunchKernelGGL(k_attn<256>, grid, dim3(ATT_THREADS), lds, s, a);
-        hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_head), dim3(256), wl, s, a);
-        break;
+    case 64: hipLaunchKernelGGL(k_attn<64>, dim3(n_head), dim3(ATT_THREADS), lds, s, a); break;
+    case 128: hipLaunchKernelGGL(k_attn<128>, dim3(n_head), dim3(ATT_THREADS), lds, s, a); break;
+    case 256: hipLaunchKernelGGL(k_attn<256>, dim3(n_head), dim3(ATT_THREADS), lds, s, a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -37,10 +37,9 @@
 #include <vector>
 
 namespace lrs {
-uint32_t attn_splits(uint32_t ctx);
 hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, XPack out,
-                            float *part, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
-                            uint32_t head_dim, uint32_t ctx, uint32_t S, hipStream_t s);
+                            const uint32_t *step, uint32_t n_head, uint32_t n_kv,
+                            uint32_t head_dim, uint32_t ctx, hipStream_t s);
 
 // x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304),
 // and the pack of x * nw for the first layer's q/k/v
@@ -73,8 +72,8 @@ struct lrs_model {
     std::vector<DevLayer> layers;
     const lrs_weight *embd, *output;
     float *output_norm, *freq;
-    // activations: residual, q after RoPE, logits, attention partials
-    float *x, *qbuf, *logits, *part;
+    // activations: residual, q after RoPE, logits
+    float *x, *qbuf, *logits;
     // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
     // SwiGLU output
     XPack pk_n, pk_f, pk_a, pk_s;
@@ -90,7 +89,6 @@ struct lrs_model {
     uint32_t pb_cap = 0;
     float *pX = nullptr, *pXN, *pQt, *pKt, *pVt, *pQ, *pATT, *pG, *pU;
     uint32_t *ptok;
-    uint32_t S;                  // attention splits
     _Float16 *kv;                // all layers' caches
     uint32_t *step_host;         // pinned
     float *logits_host;          // pinned
@@ -141,11 +139,11 @@ MqSeg mseg(const lrs_weight *w, uint32_t rows) {
 }
 
 // launch shapes of the decode ops (16-row tiles; see mq.hip)
-constexpr MqGeom G_QKV = {1, 1, 4, 2};    // 448 workgroups of 4 K-slices (32B shape)
+constexpr MqGeom G_QKV = {1, 1, 4, 3};    // 448 workgroups of 4 K-slices (32B shape)
 constexpr MqGeom G_O = {1, 2, 4, 2};      // 2 tiles (one 32-row pack block) x 4 K-slices
-constexpr MqGeom G_GATEUP = {2, 2, 1, 2}; // gate+up tile pairs, 2 per workgroup
+constexpr MqGeom G_GATEUP = {2, 4, 2, 2}; // gate+up tile pairs, 4 per workgroup x 2 K-slices
 constexpr MqGeom G_DOWN = {1, 2, 6, 2};   // 2 tiles x 6 K-slices
-constexpr MqGeom G_HEAD = {1, 4, 1, 2};   // 4 tiles per workgroup, full K per wavefront
+constexpr MqGeom G_HEAD = {1, 2, 2, 2};   // 2 tiles per workgroup x 2 K-slices
 
 // ---- one fused op of the per-token plan, enqueued on the model stream ----
 hipError_t op_embed(lrs_model *m) {
@@ -217,8 +215,8 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
 hipError_t op_attn(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
-    return launch_attention(m->qbuf, L.kc, L.vc, m->pk_a, m->part, m->step, c.n_head, c.n_head_kv,
-                            c.head_dim, c.ctx, m->S, m->ctx->stream);
+    return launch_attention(m->qbuf, L.kc, L.vc, m->pk_a, m->step, c.n_head, c.n_head_kv,
+                            c.head_dim, c.ctx, m->ctx->stream);
 }
 
 // x += W_o att; pack of x * ffn_norm for gate/up
@@ -392,8 +390,6 @@ int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weight
         lrs_model_destroy(m);
         return code;
     };
-    // attention splits: at most 128 positions per split at full context
-    m->S = attn_splits(c.ctx);
     const size_t kv_layer = (size_t)kvd * c.ctx;
     if ((rc = dev_alloc(m, kv_layer * 2 * c.n_layer * sizeof(_Float16), (void **)&m->kv))) return bail(rc);
     if (hipMemset(m->kv, 0, kv_layer * 2 * c.n_layer * sizeof(_Float16)) != hipSuccess)
@@ -433,8 +429,6 @@ int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weight
     if ((rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
         (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->qbuf)) ||
         (rc = dev_alloc(m, c.vocab * sizeof(float), (void **)&m->logits)) ||
-        (rc = dev_alloc(m, (size_t)c.n_head * m->S * (c.head_dim + 4) * sizeof(float),
-                        (void **)&m->part)) ||
         (rc = dev_alloc(m, 4 * sizeof(uint32_t), (void **)&m->step)) ||
         (rc = dev_alloc(m, m->gen_cap * sizeof(uint32_t), (void **)&m->gen)) ||
         (rc = dev_alloc(m, (size_t)c.vocab * sizeof(unsigned long long), (void **)&m->amax)))

@@ -502,10 +502,10 @@ static MqFn pick(const MqGeom &g) {
 #define LRS_MQ_CASE(TPW, TG, KS, P)                                                   \
     if (g.tpw == TPW && g.tg == TG && g.ks == KS && g.p == P) return k_mq<T0, T1, TPW, TG, KS, P, EPI>;
     LRS_MQ_CASE(1, 1, 4, 2)
+    LRS_MQ_CASE(1, 1, 4, 3)
     LRS_MQ_CASE(1, 2, 4, 2)
-    LRS_MQ_CASE(1, 4, 1, 2)
-    LRS_MQ_CASE(2, 2, 1, 2)
-    LRS_MQ_CASE(2, 2, 2, 2)
+    LRS_MQ_CASE(1, 2, 2, 2)
+    LRS_MQ_CASE(2, 4, 2, 2)
     LRS_MQ_CASE(1, 2, 6, 2)
 #undef LRS_MQ_CASE
     return nullptr;
@@ -627,7 +627,7 @@ MqGeom store_geom(uint32_t t, uint32_t n_in, uint32_t n_out) {
     (void)n_in;
     if (g_store_override.tpw) return g_store_override;
     const uint32_t tiles = ttiles(n_out);
-    if (tiles >= 1024) return {1, 4, 1, 2};
+    if (tiles >= 1024) return {1, 2, 2, 2};
     if (tiles >= 256) return {1, 2, 4, 2};
     return {1, 1, 4, 2};
 }
