@@ -5,36 +5,38 @@
 // h / (n_head / n_head_kv).  The cache holds f16 K and V, as the reference
 // GPU path keeps them (kv_pack.comp).
 //
-// One workgroup of 16 wavefronts per query head, all positions, one launch,
-// in three phases over the positions 0..pos:
-//   scores   a "lane group" of HD/8 lanes owns one position at a time (8 dims
-//            = one 16-byte piece of the K row per lane; the 64 lane groups
-//            take positions g, g+64, ..., with the next positions' loads in
-//            flight); q is split into f16 hi + lo halves so v_dot2_f32_f16
-//            forms q.k from exact f16 products to 22 bits of q; scores to LDS
-//   softmax  max and sum over the LDS scores (one exp per position)
-//   values   the same lane groups accumulate p * V over their positions; the
-//            groups of a wavefront are summed with cross-lane adds, the 16
-//            wavefronts through LDS
-// and the output is written as the activation pack of the o-projection.
-// A single pass replaces the split + combine pair of the reference
-// (attention_split.comp + attn_reduce.comp): no second launch, no partials
-// in HBM.
+// Split over positions ("flash decode"): workgroup (split s, KV head kh)
+// takes positions [s*chunk, (s+1)*chunk) of 0..pos for all REP query heads
+// of the GQA group (K and V are read once for the group).  A "lane group" of
+// HD/8 lanes owns one position at a time (8 dims = one 16-byte piece of the K
+// and V rows per lane; lane group g takes positions g, g+NG, ..., with the
+// next positions' loads in flight):
+//   score    q is split into f16 hi + lo halves so v_dot2_f32_f16 forms q.k
+//            from exact f16 products to 22 bits of q; the row sum over the
+//            lane group is four DPP adds
+//   update   online softmax per lane group: running max m, sum l and
+//            accumulator e^(s - m) V, rescaled when the max moves
+// The lane groups' states are merged through LDS with the same rescaling
+// (out = sum_g e^(m_g - M) acc_g / sum_g e^(m_g - M) l_g) into each head's
+// (acc, m, l) partial of the split.  A second kernel, one workgroup per query
+// head, merges the splits the same way (the identity of attention_split.comp
+// + attn_reduce.comp) and writes the output as the activation pack of the
+// o-projection.  The split spreads the K/V stream over ~256 workgroups: one
+// CU streams only ~35 GB/s.
 #include "lrs_internal.h"
 #include "pack_dev.h"
 
 namespace lrs {
 
-constexpr int ATT_THREADS = 1024;
-constexpr int ATT_WAVES = ATT_THREADS / 64;
+constexpr int ATT_THREADS = 256;
 constexpr int ATT_DEPTH = 4;  // positions per lane group with K and V loads in flight
 
 struct AttnArgs {
     const float *q;           // [n_head * HD], RoPE applied
     const _Float16 *kc, *vc;  // this layer's caches [n_kv][ctx][HD]
-    XPack out;                // pack of the [n_head * HD] output
+    float *part;              // [n_head][splits][HD + 4]: acc[HD], m, l
     const uint32_t *step;     // {token, pos}: attends positions 0..pos
-    uint32_t n_head, n_kv, ctx;
+    uint32_t n_head, n_kv, ctx, splits;
     float scale;
 };
 
@@ -46,58 +48,55 @@ __device__ __forceinline__ half2_t as_h2(uint32_t v) {
     return r;
 }
 
-// block-wide reduction of one float (max or sum) through LDS
-template <bool MAX>
-__device__ __forceinline__ float block_reduce(float v, float *red) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float t = __shfl_xor(v, o, 64);
-        v = MAX ? fmaxf(v, t) : v + t;
-    }
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();  // red[] may still be read by an earlier reduction
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float r = red[0];
-#pragma unroll
-    for (int w = 1; w < ATT_WAVES; w++) r = MAX ? fmaxf(r, red[w]) : r + red[w];
-    return r;
+// sum over aligned groups of N lanes (N = 8, 16, 32) in every lane: DPP
+// within a row of 16 (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror), a lane shuffle across rows
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    if constexpr (N >= 16) v += dpp_f<0x140>(v);  // row_mirror
+    if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
+    return v;
 }
 
-template <int HD>
+template <int HD, int REP>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     constexpr int LP = HD / 8;              // lanes per position
     constexpr int NG = ATT_THREADS / LP;    // lane groups per workgroup
-    extern __shared__ float sc[];           // [ctx] scores, then probabilities
-    __shared__ float red[ATT_WAVES];
-    __shared__ float sacc[ATT_WAVES][HD];
+    __shared__ float sm[NG][REP], sl[NG][REP], sw[NG][REP];
+    __shared__ float sacc[NG][REP][HD];
     const uint32_t tid = threadIdx.x, sub = tid % LP, grp = tid / LP;
-    const uint32_t lane = tid & 63, wave = tid >> 6;
-    const uint32_t h = blockIdx.x, kh = h / (a.n_head / a.n_kv);
+    const uint32_t sp = blockIdx.x, kh = blockIdx.y, h0 = kh * REP;
     const uint32_t L = a.step[1] + 1;
-    const _Float16 *kb = a.kc + (size_t)kh * a.ctx * HD + 8 * sub;
-    const _Float16 *vb = a.vc + (size_t)kh * a.ctx * HD + 8 * sub;
+    const uint32_t chunk = (L + a.splits - 1) / a.splits;
+    const uint32_t p0 = min(sp * chunk, L), n = min(p0 + chunk, L) - p0;
+    const _Float16 *kb = a.kc + ((size_t)kh * a.ctx + p0) * HD + 8 * sub;
+    const _Float16 *vb = a.vc + ((size_t)kh * a.ctx + p0) * HD + 8 * sub;
 
     // K and V of the first ATT_DEPTH positions of every lane group in flight
-    // at once (all of them up to 64 * ATT_DEPTH positions)
     uint4 kr[ATT_DEPTH], vr[ATT_DEPTH];
 #pragma unroll
     for (int i = 0; i < ATT_DEPTH; i++) {
         const uint32_t p = grp + i * NG;
-        if (p < L) kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)p * HD);
-    }
-#pragma unroll
-    for (int i = 0; i < ATT_DEPTH; i++) {
-        const uint32_t p = grp + i * NG;
-        if (p < L) vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)p * HD);
+        if (p < n) {
+            kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)p * HD);
+            vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)p * HD);
+        }
     }
     // q / 2^e as f16 hi + lo pairs (dims 8 sub .. 8 sub + 7), 2^e >= max |q|
     // of the head so both halves stay in f16 range; the score is rescaled
     // by 2^e * scale (exact power of two, then the reference's 1/sqrt(HD))
-    half2_t qh[4], ql[4];
-    float sscale;
-    {
-        const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)h * HD + 8 * sub);
+    half2_t qh[REP][4], ql[REP][4];
+    float sscale[REP];
+#pragma unroll
+    for (int r = 0; r < REP; r++) {
+        const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)(h0 + r) * HD + 8 * sub);
         const float4 x0 = qp[0], x1 = qp[1];
         float qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         float qm = 0.f;
@@ -110,108 +109,193 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
         e = e < -60 ? -60 : e;
 #pragma unroll
         for (int i = 0; i < 8; i++) qv[i] = ldexpf(qv[i], -e);
-        sscale = ldexpf(1.0f, e);
+        sscale[r] = ldexpf(1.0f, e) * a.scale;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const _Float16 h0 = (_Float16)qv[2 * i], h1 = (_Float16)qv[2 * i + 1];
-            qh[i] = half2_t{h0, h1};
-            ql[i] = half2_t{(_Float16)(qv[2 * i] - (float)h0), (_Float16)(qv[2 * i + 1] - (float)h1)};
+            const _Float16 x0h = (_Float16)qv[2 * i], x1h = (_Float16)qv[2 * i + 1];
+            qh[r][i] = half2_t{x0h, x1h};
+            ql[r][i] = half2_t{(_Float16)(qv[2 * i] - (float)x0h), (_Float16)(qv[2 * i + 1] - (float)x1h)};
         }
     }
 
-    // ---- scores ----
-    float smax = -INFINITY;
-    for (uint32_t p0 = grp; p0 < L; p0 += ATT_DEPTH * NG) {
+    // online softmax over this lane group's positions (attention.rs:120-166)
+    float m[REP], l[REP], acc[REP][8];
+#pragma unroll
+    for (int r = 0; r < REP; r++) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
+    }
+    for (uint32_t q0 = grp; q0 < n; q0 += ATT_DEPTH * NG) {
 #pragma unroll
         for (int i = 0; i < ATT_DEPTH; i++) {
-            const uint32_t p = p0 + i * NG;
-            if (p < L) {  // uniform within the lane group
-                const uint4 k = kr[i];
+            const uint32_t p = q0 + i * NG;
+            if (p < n) {  // uniform within the lane group
+                const uint4 k = kr[i], v = vr[i];
                 const uint32_t pn = p + ATT_DEPTH * NG;
-                if (pn < L) kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)pn * HD);
-                const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
-                float s = 0.f;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    s = __builtin_amdgcn_fdot2(ql[j], as_h2(kw[j]), s, false);
-                    s = __builtin_amdgcn_fdot2(qh[j], as_h2(kw[j]), s, false);
+                if (pn < n) {
+                    kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)pn * HD);
+                    vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)pn * HD);
                 }
-#pragma unroll
-                for (int o = LP / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
-                s = (s * sscale) * a.scale;  // attention.rs: (q.k) / sqrt(head_dim)
-                if (sub == 0) sc[p] = s;
-                smax = fmaxf(smax, s);
-            }
-        }
-    }
-
-    // ---- softmax (attention.rs:120-140) ----
-    const float M = block_reduce<true>(smax, red);  // also orders the score stores
-    float lsum = 0.f;
-    for (uint32_t p = tid; p < L; p += ATT_THREADS) {
-        const float e = expf(sc[p] - M);
-        sc[p] = e;
-        lsum += e;
-    }
-    const float den = block_reduce<false>(lsum, red);  // also orders the exp stores
-
-    // ---- values ----
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) acc[e] = 0.f;
-    for (uint32_t p0 = grp; p0 < L; p0 += ATT_DEPTH * NG) {
-#pragma unroll
-        for (int i = 0; i < ATT_DEPTH; i++) {
-            const uint32_t p = p0 + i * NG;
-            if (p < L) {
-                const uint4 v = vr[i];
-                const uint32_t pn = p + ATT_DEPTH * NG;
-                if (pn < L) vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)pn * HD);
-                const float pe = sc[p];
+                const uint32_t kw[4] = {k.x, k.y, k.z, k.w};
                 const _Float16 *vh = reinterpret_cast<const _Float16 *>(&v);
+                float vf[8];
 #pragma unroll
-                for (int e = 0; e < 8; e++) acc[e] = fmaf(pe, (float)vh[e], acc[e]);
+                for (int e = 0; e < 8; e++) vf[e] = (float)vh[e];
+#pragma unroll
+                for (int r = 0; r < REP; r++) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        s = __builtin_amdgcn_fdot2(ql[r][j], as_h2(kw[j]), s, false);
+                        s = __builtin_amdgcn_fdot2(qh[r][j], as_h2(kw[j]), s, false);
+                    }
+                    s = group_sum<LP>(s) * sscale[r];  // attention.rs: (q.k) / sqrt(head_dim)
+                    const float mn = fmaxf(m[r], s);
+                    const float c = expf(m[r] - mn), pe = expf(s - mn);
+                    l[r] = fmaf(l[r], c, pe);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[r][e] = fmaf(pe, vf[e], acc[r][e] * c);
+                    m[r] = mn;
+                }
             }
         }
     }
-    // lane groups of a wavefront hold the same dims: sum them, then the waves
+    // merge the lane groups' states through LDS
+    if (sub == 0) {
 #pragma unroll
-    for (int o = LP; o < 64; o <<= 1)
+        for (int r = 0; r < REP; r++) {
+            sm[grp][r] = m[r];
+            sl[grp][r] = l[r];
+        }
+    }
 #pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] += __shfl_xor(acc[e], o, 64);
-    if (lane < LP) {
+    for (int r = 0; r < REP; r++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) sacc[wave][8 * lane + e] = acc[e];
+        for (int e = 0; e < 8; e++) sacc[grp][r][8 * sub + e] = acc[r][e];
+    __syncthreads();
+    if (tid < REP) {
+        // head r: split max M, weights e^(m_g - M) of the lane groups (0 for a
+        // group with no position) and the denominator sum_g w_g l_g
+        const uint32_t r = tid;
+        float M = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < NG; g++) M = fmaxf(M, sm[g][r]);
+        float den = 0.f;
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const float w = sm[g][r] == -INFINITY ? 0.f : expf(sm[g][r] - M);
+            sw[g][r] = w;
+            den = fmaf(w, sl[g][r], den);
+        }
+        float *pp = a.part + ((size_t)(h0 + r) * a.splits + sp) * (HD + 4);
+        pp[HD] = M;  // -inf: an empty split, no weight
+        pp[HD + 1] = den;
     }
     __syncthreads();
-    if (tid >= HD) return;  // whole half-waves remain for the pack (HD % 32 == 0)
-    float num = 0.f;
+    for (uint32_t i = tid; i < REP * HD; i += ATT_THREADS) {
+        const uint32_t r = i / HD, d = i % HD;
+        float num = 0.f;
 #pragma unroll
-    for (int w = 0; w < ATT_WAVES; w++) num += sacc[w][tid];
-    pack_half(num / den, (h * HD + tid) >> 5, a.out);
+        for (int g = 0; g < NG; g++) num = fmaf(sw[g][r], sacc[g][r][d], num);
+        a.part[((size_t)(h0 + r) * a.splits + sp) * (HD + 4) + d] = num;  // relative to the split max
+    }
 }
 
-hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, XPack out,
-                            const uint32_t *step, uint32_t n_head, uint32_t n_kv,
-                            uint32_t head_dim, uint32_t ctx, hipStream_t s) {
+typedef __attribute__((address_space(3))) void lds_void;
+
+// combine of the split partials of head blockIdx.x: the head's partial block
+// goes to LDS in one round trip (global_load_lds), then thread d owns dim d
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ part, uint32_t splits,
+                                                     XPack out) {
+    extern __shared__ __attribute__((aligned(16))) float pl[];  // [splits][HD + 4]
+    __shared__ float wsh[64], red[1];
+    constexpr uint32_t ST = HD + 4;
+    const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(part + (size_t)h * splits * ST);
+    const uint32_t bytes = splits * ST * 4;  // multiple of 16
+    for (uint32_t base = wave * 1024; base < bytes; base += HD * 16) {
+        const uint32_t off = base + lane * 16;
+        if (off < bytes)
+            __builtin_amdgcn_global_load_lds(src + off, (lds_void *)(reinterpret_cast<uint8_t *>(pl) + base), 16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // wave 0: M = max over the splits (splits <= 64), weights, denominator
+    if (wave == 0) {
+        const float ms = lane < splits ? pl[lane * ST + HD] : -INFINITY;
+        float M = ms;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        const float w = ms == -INFINITY ? 0.f : expf(ms - M);  // empty splits weigh 0
+        float den = lane < splits ? w * pl[lane * ST + HD + 1] : 0.f;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
+        if (lane < splits) wsh[lane] = w;
+        if (lane == 0) red[0] = den;
+    }
+    __syncthreads();
+    const float den = red[0];
+    float num = 0.f;
+    for (uint32_t s = 0; s < splits; s++) num = fmaf(wsh[s], pl[s * ST + d], num);
+    pack_half(num / den, (h * HD + d) >> 5, out);
+}
+
+// split count: about one workgroup per CU (256 = splits x KV heads)
+uint32_t attn_splits(uint32_t n_kv) {
+    const uint32_t S = 256 / n_kv;
+    return S < 1 ? 1 : S > 64 ? 64 : S;
+}
+
+using AttnFn = void (*)(AttnArgs);
+template <int HD>
+static AttnFn pick_rep(uint32_t rep) {
+    switch (rep) {
+    case 1: return k_attn<HD, 1>;
+    case 2: return k_attn<HD, 2>;
+    case 3: return k_attn<HD, 3>;
+    case 4: return k_attn<HD, 4>;
+    case 5: return k_attn<HD, 5>;
+    case 6: return k_attn<HD, 6>;
+    case 7: return k_attn<HD, 7>;
+    case 8: return k_attn<HD, 8>;
+    default: return nullptr;
+    }
+}
+
+hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *part,
+                            XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
+                            uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s) {
     AttnArgs a;
     a.q = q;
     a.kc = kc;
     a.vc = vc;
-    a.out = out;
+    a.part = part;
     a.step = step;
     a.n_head = n_head;
     a.n_kv = n_kv;
     a.ctx = ctx;
+    a.splits = splits;
     a.scale = 1.0f / sqrtf((float)head_dim);
-    if (n_kv == 0 || n_head % n_kv) return hipErrorInvalidValue;
-    const size_t lds = (size_t)ctx * sizeof(float);  // scores of every position
-    if (lds > 128 * 1024) return hipErrorInvalidValue;
+    if (n_kv == 0 || n_head % n_kv || splits == 0) return hipErrorInvalidValue;
+    const uint32_t rep = n_head / n_kv;
+    const dim3 grid(splits, n_kv);
+    AttnFn fn = nullptr;
     switch (head_dim) {
-    case 64: hipLaunchKernelGGL(k_attn<64>, dim3(n_head), dim3(ATT_THREADS), lds, s, a); break;
-    case 128: hipLaunchKernelGGL(k_attn<128>, dim3(n_head), dim3(ATT_THREADS), lds, s, a); break;
-    case 256: hipLaunchKernelGGL(k_attn<256>, dim3(n_head), dim3(ATT_THREADS), lds, s, a); break;
+    case 64: fn = pick_rep<64>(rep); break;
+    case 128: fn = pick_rep<128>(rep); break;
+    case 256: fn = pick_rep<256>(rep); break;
     default: return hipErrorInvalidValue;
+    }
+    if (!fn) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(fn, grid, dim3(ATT_THREADS), 0, s, a);
+    const size_t cl = (size_t)splits * (head_dim + 4) * sizeof(float);
+    switch (head_dim) {
+    case 64: hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), cl, s, part, splits, out); break;
+    case 128: hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_head), dim3(128), cl, s, part, splits, out); break;
+    default: hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_head), dim3(256), cl, s, part, splits, out); break;
     }
     return hipGetLastError();
 }

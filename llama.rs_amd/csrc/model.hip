@@ -37,9 +37,10 @@
 #include <vector>
 
 namespace lrs {
-hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, XPack out,
-                            const uint32_t *step, uint32_t n_head, uint32_t n_kv,
-                            uint32_t head_dim, uint32_t ctx, hipStream_t s);
+uint32_t attn_splits(uint32_t n_kv);
+hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *part,
+                            XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
+                            uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s);
 
 // x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304),
 // and the pack of x * nw for the first layer's q/k/v
@@ -72,8 +73,9 @@ struct lrs_model {
     std::vector<DevLayer> layers;
     const lrs_weight *embd, *output;
     float *output_norm, *freq;
-    // activations: residual, q after RoPE, logits
-    float *x, *qbuf, *logits;
+    // activations: residual, q after RoPE, logits, attention split partials
+    float *x, *qbuf, *logits, *pa;
+    uint32_t a_splits;
     // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
     // SwiGLU output
     XPack pk_n, pk_f, pk_a, pk_s;
@@ -215,8 +217,8 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
 hipError_t op_attn(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
-    return launch_attention(m->qbuf, L.kc, L.vc, m->pk_a, m->step, c.n_head, c.n_head_kv,
-                            c.head_dim, c.ctx, m->ctx->stream);
+    return launch_attention(m->qbuf, L.kc, L.vc, m->pa, m->pk_a, m->step, c.n_head, c.n_head_kv,
+                            c.head_dim, c.ctx, m->a_splits, m->ctx->stream);
 }
 
 // x += W_o att; pack of x * ffn_norm for gate/up
@@ -426,7 +428,10 @@ int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weight
     }
     if ((rc = upload_vec(m, fr.data(), fr.size(), &m->freq))) return bail(rc);
     m->gen_cap = 1u << 16;
-    if ((rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
+    m->a_splits = attn_splits(c.n_head_kv);
+    if ((rc = dev_alloc(m, (size_t)c.n_head * m->a_splits * (c.head_dim + 4) * sizeof(float),
+                        (void **)&m->pa)) ||
+        (rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
         (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->qbuf)) ||
         (rc = dev_alloc(m, c.vocab * sizeof(float), (void **)&m->logits)) ||
         (rc = dev_alloc(m, 4 * sizeof(uint32_t), (void **)&m->step)) ||

@@ -32,7 +32,7 @@ constexpr uint32_t TILE_ROWS = 16;
 __host__ __device__ inline bool is_tiled(uint32_t t) { return t == 8 || t == 12 || t == 13 || t == 14; }
 
 // bytes of one unit chunk (16 rows)
-__host__ __device__ inline uint32_t tchunk_bytes(uint32_t t) {
+__host__ __device__ constexpr uint32_t tchunk_bytes(uint32_t t) {
     switch (t) {
     case 12: return 2304;
     case 13: return 2816;
@@ -42,7 +42,7 @@ __host__ __device__ inline uint32_t tchunk_bytes(uint32_t t) {
     }
 }
 // elements of one unit
-__host__ __device__ inline uint32_t tunit_elems(uint32_t t) { return t == 8 ? 64u : 256u; }
+__host__ __device__ constexpr uint32_t tunit_elems(uint32_t t) { return t == 8 ? 64u : 256u; }
 
 // units per row (Q8_0: blocks rounded up to pairs)
 __host__ __device__ inline uint32_t tunits(uint32_t t, uint32_t n_in) {
