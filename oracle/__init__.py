@@ -91,6 +91,15 @@ def lib() -> C.CDLL:
         L.lrso_conv1d_step.argtypes = [f32p, f32p, f32p, C.c_uint32, C.c_uint32, f32p]
         L.lrso_delta_net_step.argtypes = [f32p, f32p, f32p, f32p, C.c_float, C.c_float,
                                           C.c_uint32, f32p]
+        L.lrso_hybrid_create.restype = C.c_void_p
+        L.lrso_hybrid_create.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                         C.c_void_p, C.c_int, C.c_int]
+        L.lrso_hybrid_forward.restype = C.c_int
+        L.lrso_hybrid_forward.argtypes = [C.c_void_p, u32p, C.c_uint32, f32p]
+        L.lrso_hybrid_len.restype = C.c_uint32
+        L.lrso_hybrid_len.argtypes = [C.c_void_p]
+        L.lrso_hybrid_reset.argtypes = [C.c_void_p]
+        L.lrso_hybrid_destroy.argtypes = [C.c_void_p]
         _lib = L
     return _lib
 
@@ -326,6 +335,79 @@ class Model:
     def close(self) -> None:
         if self._h:
             lib().lrso_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+# hybrid attention + gated delta-net model (qwen35)
+# ---------------------------------------------------------------------------
+class _HybridCfg(C.Structure):
+    _fields_ = [("base", _Cfg)] + [(n, C.c_uint32) for n in
+                                   ("full_attn_interval", "dn_k_heads", "dn_v_heads",
+                                    "dn_state", "dn_conv")]
+
+
+HYBRID_TENSORS = ("attn_norm", "post_norm", "ffn_gate", "ffn_up", "ffn_down",
+                  "attn_q", "attn_k", "attn_v", "attn_output", "q_norm", "k_norm",
+                  "ssm_qkv", "ssm_gate", "ssm_out", "ssm_alpha", "ssm_beta", "ssm_a", "ssm_dt",
+                  "ssm_conv", "ssm_norm")
+
+
+class _HybridLayer(C.Structure):
+    _fields_ = [(n, _Tensor) for n in HYBRID_TENSORS]
+
+
+class HybridModel:
+    """Oracle forward of the hybrid (full attention every
+    ``full_attn_interval``-th layer, gated delta-net elsewhere) model over a
+    weight dict produced by ``tests/modelgen.py``; arrays are borrowed."""
+
+    def __init__(self, cfg: dict, weights: dict, kv_f16: bool = True, threads: int = 1):
+        self.cfg = cfg
+        self._keep = weights
+        base = _Cfg(cfg["n_layer"], cfg["n_embd"], cfg["n_head"], cfg["n_head_kv"],
+                    cfg["head_dim"], cfg["n_ff"], cfg["vocab"], cfg["rope_dim"], cfg["ctx"],
+                    cfg["rms_eps"], cfg["freq_base"])
+        c = _HybridCfg(base, cfg["full_attn_interval"], cfg["dn_k_heads"], cfg["dn_v_heads"],
+                       cfg["dn_state"], cfg["dn_conv"])
+        layers = (_HybridLayer * cfg["n_layer"])()
+        for i in range(cfg["n_layer"]):
+            for n in HYBRID_TENSORS:
+                setattr(layers[i], n, _tensor(weights.get(f"blk.{i}.{n}")))
+        self._c, self._layers = c, layers
+        self._embd = _tensor(weights["token_embd"])
+        self._onorm = _tensor(weights["output_norm"])
+        self._out = _tensor(weights["output"])
+        h = lib().lrso_hybrid_create(C.byref(c), C.byref(self._embd), layers,
+                                     C.byref(self._onorm), C.byref(self._out),
+                                     1 if kv_f16 else 0, threads)
+        if not h:
+            raise ValueError("oracle hybrid model: bad shapes")
+        self._h = h
+
+    def forward(self, tokens) -> np.ndarray:
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        logits = np.zeros(self.cfg["vocab"], dtype=np.float32)
+        rc = lib().lrso_hybrid_forward(self._h, _u32(toks), toks.size, _f32(logits))
+        if rc != 0:
+            raise ValueError(f"oracle hybrid forward error {rc}")
+        return logits
+
+    def __len__(self) -> int:
+        return int(lib().lrso_hybrid_len(self._h))
+
+    def reset(self) -> None:
+        lib().lrso_hybrid_reset(self._h)
+
+    def close(self) -> None:
+        if self._h:
+            lib().lrso_hybrid_destroy(self._h)
             self._h = None
 
     def __del__(self):

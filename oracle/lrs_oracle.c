@@ -742,3 +742,273 @@ void lrso_delta_net_step(float *state, const float *q, const float *k,
     }
     free(delta);
 }
+
+/* ------------------------------------------------------------------------- */
+/* hybrid attention + gated delta-net model (qwen35).  No CPU forward exists  */
+/* in the reference (runner.rs:164): this follows the GPU plan's op order,    */
+/* resident_forward.rs:3826-4103 and plano_delta :2252-2470.                  */
+/* ------------------------------------------------------------------------- */
+struct lrso_hybrid {
+    lrso_hybrid_config c;
+    lrso_tensor embd, onorm, out;
+    lrso_hybrid_layer *layers;
+    float *freq;
+    float *kc, *vc;   /* [n_attn_layers][ctx][kv_dim] */
+    float *state;     /* [n_dn_layers][v_heads][d][d], state[j*d+i] = S[i][j] */
+    float *win;       /* [n_dn_layers][conv_dim][d_conv-1] */
+    uint32_t *slot;   /* layer -> index among the layers of its kind */
+    uint32_t n_attn, n_dn, len;
+    int kv_f16, n_threads;
+};
+
+static int hy_full(const lrso_hybrid_config *c, uint32_t l) {
+    /* LlamaConfig::eh_linear (config.rs:25-35) */
+    return (l + 1) % c->full_attn_interval == 0;
+}
+
+static uint32_t hy_conv_dim(const lrso_hybrid_config *c) {
+    return 2 * c->dn_k_heads * c->dn_state + c->dn_v_heads * c->dn_state;
+}
+
+lrso_hybrid *lrso_hybrid_create(const lrso_hybrid_config *cfg, const lrso_tensor *token_embd,
+                                const lrso_hybrid_layer *layers,
+                                const lrso_tensor *output_norm, const lrso_tensor *output,
+                                int kv_f16, int n_threads) {
+    const lrso_hybrid_config *c = cfg;
+    const lrso_config *b = &c->base;
+    if (!c->full_attn_interval || !c->dn_k_heads || !c->dn_v_heads || !c->dn_state ||
+        c->dn_conv < 1 || c->dn_v_heads % c->dn_k_heads || b->n_head % b->n_head_kv)
+        return NULL;
+    const uint32_t E = b->n_embd, HD = b->head_dim, QD = b->n_head * HD, KV = b->n_head_kv * HD;
+    const uint32_t d = c->dn_state, KD = c->dn_k_heads * d, VD = c->dn_v_heads * d;
+    const uint32_t CD = hy_conv_dim(c);
+    if (!tensor_ok(token_embd, E, b->vocab) || !tensor_ok(output, E, b->vocab) ||
+        !tensor_ok(output_norm, E, 1))
+        return NULL;
+    (void)KD;
+    for (uint32_t l = 0; l < b->n_layer; l++) {
+        const lrso_hybrid_layer *L = &layers[l];
+        if (!tensor_ok(&L->attn_norm, E, 1) || !tensor_ok(&L->post_norm, E, 1) ||
+            !tensor_ok(&L->ffn_gate, E, b->n_ff) || !tensor_ok(&L->ffn_up, E, b->n_ff) ||
+            !tensor_ok(&L->ffn_down, b->n_ff, E))
+            return NULL;
+        if (hy_full(c, l)) {
+            if (!tensor_ok(&L->attn_q, E, 2 * QD) || !tensor_ok(&L->attn_k, E, KV) ||
+                !tensor_ok(&L->attn_v, E, KV) || !tensor_ok(&L->attn_output, QD, E) ||
+                !tensor_ok(&L->q_norm, HD, 1) || !tensor_ok(&L->k_norm, HD, 1))
+                return NULL;
+        } else {
+            if (!tensor_ok(&L->ssm_qkv, E, CD) || !tensor_ok(&L->ssm_gate, E, VD) ||
+                !tensor_ok(&L->ssm_out, VD, E) || !tensor_ok(&L->ssm_alpha, E, c->dn_v_heads) ||
+                !tensor_ok(&L->ssm_beta, E, c->dn_v_heads) ||
+                !tensor_ok(&L->ssm_a, c->dn_v_heads, 1) || !tensor_ok(&L->ssm_dt, c->dn_v_heads, 1) ||
+                !tensor_ok(&L->ssm_conv, c->dn_conv, CD) || !tensor_ok(&L->ssm_norm, d, 1))
+                return NULL;
+        }
+    }
+    lrso_hybrid *m = (lrso_hybrid *)calloc(1, sizeof(lrso_hybrid));
+    m->c = *c;
+    m->embd = *token_embd; m->onorm = *output_norm; m->out = *output;
+    m->layers = (lrso_hybrid_layer *)malloc(sizeof(lrso_hybrid_layer) * b->n_layer);
+    memcpy(m->layers, layers, sizeof(lrso_hybrid_layer) * b->n_layer);
+    m->slot = (uint32_t *)malloc(sizeof(uint32_t) * b->n_layer);
+    for (uint32_t l = 0; l < b->n_layer; l++)
+        m->slot[l] = hy_full(c, l) ? m->n_attn++ : m->n_dn++;
+    /* freq[i] = 1 / base^(2i/rope_dim) (gpu.rs:540-547) */
+    m->freq = (float *)malloc(sizeof(float) * (b->rope_dim / 2 + 1));
+    for (uint32_t i = 0; i < b->rope_dim / 2; i++) {
+        float ex = (float)(2 * i) / (float)b->rope_dim;
+        m->freq[i] = 1.0f / powf(b->freq_base, ex);
+    }
+    m->kc = (float *)calloc((size_t)m->n_attn * b->ctx * KV + 1, sizeof(float));
+    m->vc = (float *)calloc((size_t)m->n_attn * b->ctx * KV + 1, sizeof(float));
+    m->state = (float *)calloc((size_t)m->n_dn * c->dn_v_heads * d * d + 1, sizeof(float));
+    m->win = (float *)calloc((size_t)m->n_dn * CD * (c->dn_conv - 1) + 1, sizeof(float));
+    m->kv_f16 = kv_f16;
+    m->n_threads = n_threads;
+    return m;
+}
+
+/* RMSNorm of one head in place, dn_norm.comp mode 2: x * (1/sqrt(mean(x^2)+eps)) * w */
+static void hy_head_rms(float *x, uint32_t dim, const float *w, float eps) {
+    float ss = -0.0f;
+    for (uint32_t i = 0; i < dim; i++) { float sq = x[i] * x[i]; ss = ss + sq; }
+    float s = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (uint32_t i = 0; i < dim; i++) { float v = x[i] * s; x[i] = v * w[i]; }
+}
+
+/* adjacent-pair RoPE of one head (rope.comp / ops.rs:952-975) */
+static void hy_rope_head(float *b, uint32_t rope_dim, const float *freq, uint32_t pos) {
+    for (uint32_t i = 0; i < rope_dim / 2; i++) {
+        float theta = (float)pos * freq[i];
+        float s = sinf(theta), c = cosf(theta);
+        float a = b[2 * i], bb = b[2 * i + 1];
+        float ac = a * c, bs = bb * s, as = a * s, bc = bb * c;
+        b[2 * i] = ac - bs;
+        b[2 * i + 1] = as + bc;
+    }
+}
+
+static float hy_silu(float v) { float den = 1.0f + expf(-v); return v / den; }
+
+/* one token through the full-attention mixer; o [n_embd] */
+static void hy_attn(lrso_hybrid *m, uint32_t l, const float *h, float *o) {
+    const lrso_config *b = &m->c.base;
+    const lrso_hybrid_layer *L = &m->layers[l];
+    const uint32_t E = b->n_embd, HD = b->head_dim, QD = b->n_head * HD, KV = b->n_head_kv * HD;
+    const uint32_t pos = m->len;
+    float *qg = (float *)malloc(sizeof(float) * 2 * QD);
+    float *q = (float *)malloc(sizeof(float) * QD);
+    float *k = (float *)malloc(sizeof(float) * KV);
+    float *v = (float *)malloc(sizeof(float) * KV);
+    float *att = (float *)malloc(sizeof(float) * QD);
+    float *qn = tensor_f32(&L->q_norm, HD), *kn = tensor_f32(&L->k_norm, HD);
+    lrso_matvec(L->attn_q.type, L->attn_q.bytes, L->attn_q.len, E, 2 * QD, h, qg, 1, m->n_threads);
+    lrso_matvec(L->attn_k.type, L->attn_k.bytes, L->attn_k.len, E, KV, h, k, 1, m->n_threads);
+    lrso_matvec(L->attn_v.type, L->attn_v.bytes, L->attn_v.len, E, KV, h, v, 1, m->n_threads);
+    /* QK-norm (dn_norm mode 2, Q heads 2*head_dim apart) then RoPE */
+    for (uint32_t hh = 0; hh < b->n_head; hh++) {
+        float *qh = qg + (size_t)hh * 2 * HD;
+        hy_head_rms(qh, HD, qn, b->rms_eps);
+        hy_rope_head(qh, b->rope_dim, m->freq, pos);
+        memcpy(q + (size_t)hh * HD, qh, sizeof(float) * HD);
+    }
+    for (uint32_t hh = 0; hh < b->n_head_kv; hh++) {
+        hy_head_rms(k + (size_t)hh * HD, HD, kn, b->rms_eps);
+        hy_rope_head(k + (size_t)hh * HD, b->rope_dim, m->freq, pos);
+    }
+    const size_t sl = (size_t)m->slot[l] * b->ctx * KV;
+    float *kl = m->kc + sl, *vl = m->vc + sl;
+    for (uint32_t i = 0; i < KV; i++) {
+        float kk = k[i], vv = v[i];
+        if (m->kv_f16) {
+            kk = lrso_f16_to_f32(lrso_f32_to_f16(kk));
+            vv = lrso_f16_to_f32(lrso_f32_to_f16(vv));
+        }
+        kl[(size_t)pos * KV + i] = kk;
+        vl[(size_t)pos * KV + i] = vv;
+    }
+    lrso_attention(q, kl, vl, 1, pos, b->n_head, b->n_head_kv, HD, att);
+    /* gate_quant.comp: att * sigmoid(gate), gate = second half of the head's Q rows */
+    for (uint32_t hh = 0; hh < b->n_head; hh++)
+        for (uint32_t i = 0; i < HD; i++) {
+            float g = qg[(size_t)hh * 2 * HD + HD + i];
+            att[(size_t)hh * HD + i] *= 1.0f / (1.0f + expf(-g));
+        }
+    lrso_matvec(L->attn_output.type, L->attn_output.bytes, L->attn_output.len, QD, E, att, o, 1,
+                m->n_threads);
+    free(qg); free(q); free(k); free(v); free(att); free(qn); free(kn);
+}
+
+/* one token through the gated delta-net mixer (plano_delta order); o [n_embd] */
+static void hy_delta(lrso_hybrid *m, uint32_t l, const float *h, float *o) {
+    const lrso_hybrid_config *c = &m->c;
+    const lrso_config *b = &c->base;
+    const lrso_hybrid_layer *L = &m->layers[l];
+    const uint32_t E = b->n_embd, d = c->dn_state, KD = c->dn_k_heads * d, VD = c->dn_v_heads * d;
+    const uint32_t CD = hy_conv_dim(c), NV = c->dn_v_heads;
+    float *qkv = (float *)malloc(sizeof(float) * CD);
+    float *cv = (float *)malloc(sizeof(float) * CD);
+    float *z = (float *)malloc(sizeof(float) * VD);
+    float *y = (float *)malloc(sizeof(float) * VD);
+    float *al = tensor_f32(&L->ssm_alpha, E * NV), *be = tensor_f32(&L->ssm_beta, E * NV);
+    float *sa = tensor_f32(&L->ssm_a, NV), *dt = tensor_f32(&L->ssm_dt, NV);
+    float *cw = tensor_f32(&L->ssm_conv, CD * c->dn_conv), *nw = tensor_f32(&L->ssm_norm, d);
+    lrso_matvec(L->ssm_qkv.type, L->ssm_qkv.bytes, L->ssm_qkv.len, E, CD, h, qkv, 1, m->n_threads);
+    lrso_matvec(L->ssm_gate.type, L->ssm_gate.bytes, L->ssm_gate.len, E, VD, h, z, 1, m->n_threads);
+    /* causal conv with state, then SiLU (dn_conv.comp; delta_net.rs:51-78) */
+    float *win = m->win + (size_t)m->slot[l] * CD * (c->dn_conv - 1);
+    lrso_conv1d_step(win, qkv, cw, CD, c->dn_conv, cv);
+    for (uint32_t i = 0; i < CD; i++) cv[i] = hy_silu(cv[i]);
+    /* L2 norm of q and k per key head (dn_l2_qk.comp, eps = rms_eps) */
+    lrso_l2_norm_rows(cv, 2 * c->dn_k_heads, d, b->rms_eps);
+    float *st = m->state + (size_t)m->slot[l] * NV * d * d;
+    for (uint32_t hh = 0; hh < NV; hh++) {
+        /* gates (dn_gates.comp): g = a * softplus(alpha.h + dt), beta = sigmoid(beta.h) */
+        float pa = -0.0f, pb = -0.0f;
+        for (uint32_t i = 0; i < E; i++) {
+            float p1 = al[(size_t)hh * E + i] * h[i], p2 = be[(size_t)hh * E + i] * h[i];
+            pa = pa + p1;
+            pb = pb + p2;
+        }
+        float g = sa[hh] * lrso_softplus(pa + dt[hh]);
+        float beta = 1.0f / (1.0f + expf(-pb));
+        /* value head hh reads key head hh % k_heads (delta_net.comp:75-85) */
+        const uint32_t kh = hh % c->dn_k_heads;
+        lrso_delta_net_step(st + (size_t)hh * d * d, cv + (size_t)kh * d, cv + KD + (size_t)kh * d,
+                            cv + 2 * KD + (size_t)hh * d, g, beta, d, y + (size_t)hh * d);
+        /* gated RMSNorm (dn_norm mode 1): (y * 1/sqrt(mean(y^2)+eps)) * (w * silu(z)) */
+        float *yh = y + (size_t)hh * d;
+        const float *zh = z + (size_t)hh * d;
+        float ss = -0.0f;
+        for (uint32_t i = 0; i < d; i++) { float sq = yh[i] * yh[i]; ss = ss + sq; }
+        float s = 1.0f / sqrtf(ss / (float)d + b->rms_eps);
+        for (uint32_t i = 0; i < d; i++) {
+            float vv = yh[i] * s;
+            float gz = nw[i] * hy_silu(zh[i]);
+            yh[i] = vv * gz;
+        }
+    }
+    lrso_matvec(L->ssm_out.type, L->ssm_out.bytes, L->ssm_out.len, VD, E, y, o, 1, m->n_threads);
+    free(qkv); free(cv); free(z); free(y); free(al); free(be); free(sa); free(dt); free(cw); free(nw);
+}
+
+int lrso_hybrid_forward(lrso_hybrid *m, const uint32_t *tokens, uint32_t n_tok, float *logits) {
+    const lrso_config *b = &m->c.base;
+    const uint32_t E = b->n_embd;
+    if (n_tok == 0) return -1;
+    if (m->len + n_tok > b->ctx) return -3;
+    for (uint32_t t = 0; t < n_tok; t++)
+        if (tokens[t] >= b->vocab) return -4;
+    size_t row_bytes = m->embd.len / b->vocab;
+    float *x = (float *)malloc(sizeof(float) * E);
+    float *h = (float *)malloc(sizeof(float) * E);
+    float *o = (float *)malloc(sizeof(float) * E);
+    float *g = (float *)malloc(sizeof(float) * b->n_ff);
+    float *u = (float *)malloc(sizeof(float) * b->n_ff);
+    for (uint32_t t = 0; t < n_tok; t++) {
+        lrso_dequant(m->embd.type, m->embd.bytes + (size_t)tokens[t] * row_bytes, row_bytes, x);
+        for (uint32_t l = 0; l < b->n_layer; l++) {
+            lrso_hybrid_layer *L = &m->layers[l];
+            float *an = tensor_f32(&L->attn_norm, E), *pn = tensor_f32(&L->post_norm, E);
+            lrso_rmsnorm_scale(x, an, 1, E, b->rms_eps, h);
+            if (hy_full(&m->c, l)) hy_attn(m, l, h, o);
+            else hy_delta(m, l, h, o);
+            for (uint32_t i = 0; i < E; i++) x[i] += o[i];
+            lrso_rmsnorm_scale(x, pn, 1, E, b->rms_eps, h);
+            lrso_matvec(L->ffn_gate.type, L->ffn_gate.bytes, L->ffn_gate.len, E, b->n_ff, h, g, 1,
+                        m->n_threads);
+            lrso_matvec(L->ffn_up.type, L->ffn_up.bytes, L->ffn_up.len, E, b->n_ff, h, u, 1,
+                        m->n_threads);
+            lrso_swiglu(g, u, b->n_ff, g);
+            lrso_matvec(L->ffn_down.type, L->ffn_down.bytes, L->ffn_down.len, b->n_ff, E, g, o, 1,
+                        m->n_threads);
+            for (uint32_t i = 0; i < E; i++) x[i] += o[i];
+            free(an); free(pn);
+        }
+        m->len++;
+    }
+    if (logits) {
+        float *on = tensor_f32(&m->onorm, E);
+        lrso_rmsnorm_scale(x, on, 1, E, b->rms_eps, h);
+        lrso_matvec(m->out.type, m->out.bytes, m->out.len, E, b->vocab, h, logits, 1, m->n_threads);
+        free(on);
+    }
+    free(x); free(h); free(o); free(g); free(u);
+    return 0;
+}
+
+uint32_t lrso_hybrid_len(const lrso_hybrid *m) { return m->len; }
+
+void lrso_hybrid_reset(lrso_hybrid *m) {
+    const lrso_hybrid_config *c = &m->c;
+    m->len = 0;
+    memset(m->state, 0, sizeof(float) * ((size_t)m->n_dn * c->dn_v_heads * c->dn_state * c->dn_state));
+    memset(m->win, 0, sizeof(float) * ((size_t)m->n_dn * hy_conv_dim(c) * (c->dn_conv - 1)));
+}
+
+void lrso_hybrid_destroy(lrso_hybrid *m) {
+    if (!m) return;
+    free(m->layers); free(m->slot); free(m->freq); free(m->kc); free(m->vc);
+    free(m->state); free(m->win); free(m);
+}

@@ -158,6 +158,45 @@ void lrso_delta_net_step(float *state, const float *q, const float *k,
                          float *out);
 float lrso_silu(float x);                           /* delta_net.rs:27-30 */
 
+/* ---- hybrid attention + gated delta-net model (qwen35) ----
+ * The reference has no CPU forward for this architecture (runner.rs:164); this
+ * restates the GPU plan's op order (resident_forward.rs:3826-4103 with
+ * plano_delta :2252-2470) with the CPU primitives of delta_net.rs and ops.rs
+ * and the shader formulas of dn_gates.comp, dn_norm.comp, dn_l2_qk.comp,
+ * dn_conv.comp, delta_net.comp and gate_quant.comp.  Model-level parity
+ * against the reference is unpinned (no reference logits exist); the
+ * structure is pinned by a float64 numpy restatement (tests/npref.py). */
+typedef struct {
+    lrso_config base;            /* full-attention layers use n_head, n_head_kv, head_dim */
+    uint32_t full_attn_interval; /* layer l is full attention iff (l+1) % interval == 0 */
+    uint32_t dn_k_heads, dn_v_heads, dn_state, dn_conv;
+} lrso_hybrid_config;
+typedef struct {
+    lrso_tensor attn_norm, post_norm, ffn_gate, ffn_up, ffn_down;
+    /* full attention: attn_q is [n_head * 2 * head_dim] rows, query then gate
+     * per head; q_norm / k_norm F32 [head_dim] */
+    lrso_tensor attn_q, attn_k, attn_v, attn_output, q_norm, k_norm;
+    /* delta net: ssm_qkv [conv_dim = 2*k_heads*state + v_heads*state] rows
+     * (q | k | v channels), ssm_gate (z) [v_heads*state], ssm_out [n_embd] */
+    lrso_tensor ssm_qkv, ssm_gate, ssm_out;
+    lrso_tensor ssm_alpha, ssm_beta; /* F32 [v_heads][n_embd] */
+    lrso_tensor ssm_a, ssm_dt;       /* F32 [v_heads] (ssm_a < 0) */
+    lrso_tensor ssm_conv;            /* F32 [conv_dim][dn_conv] */
+    lrso_tensor ssm_norm;            /* F32 [dn_state] */
+} lrso_hybrid_layer;
+typedef struct lrso_hybrid lrso_hybrid;
+lrso_hybrid *lrso_hybrid_create(const lrso_hybrid_config *cfg, const lrso_tensor *token_embd,
+                                const lrso_hybrid_layer *layers,
+                                const lrso_tensor *output_norm, const lrso_tensor *output,
+                                int kv_f16, int n_threads);
+/* tokens at positions len..len+n_tok-1, one at a time (the recurrence is
+ * sequential); last token's logits [vocab].  -3 on context overflow. */
+int lrso_hybrid_forward(lrso_hybrid *m, const uint32_t *tokens, uint32_t n_tok, float *logits);
+uint32_t lrso_hybrid_len(const lrso_hybrid *m);
+/* length 0, recurrent states and conv windows cleared */
+void lrso_hybrid_reset(lrso_hybrid *m);
+void lrso_hybrid_destroy(lrso_hybrid *m);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,3 +82,74 @@ def oracle_greedy(model, prompt, n_gen):
         logits = model.forward(np.asarray([nxt], np.uint32))
         nxt = int(np.argmax(logits))
     return toks
+
+
+# ---------------------------------------------------------------------------
+# hybrid attention + gated delta-net (qwen35-shaped) models
+# ---------------------------------------------------------------------------
+# layers 0-2 delta net, layer 3 full attention; 4 value heads over 2 key heads
+# (the modulo GQA mapping), partial RoPE
+HY_TINY = dict(n_layer=4, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, vocab=512,
+               rope_dim=32, ctx=64, rms_eps=1e-6, freq_base=1e7, full_attn_interval=4,
+               dn_k_heads=2, dn_v_heads=4, dn_state=64, dn_conv=4)
+# the config-4 head shapes (24/4 x 256 attention -> GQA 6, d_state 128) at a
+# small width
+HY_MID = dict(n_layer=4, n_embd=512, n_head=6, n_head_kv=1, head_dim=256, n_ff=768, vocab=1024,
+              rope_dim=64, ctx=64, rms_eps=1e-6, freq_base=1e7, full_attn_interval=2,
+              dn_k_heads=2, dn_v_heads=2, dn_state=128, dn_conv=4)
+
+HY_Q4_K_M = dict(Q4_K_M, ssm_qkv=Q4_K, ssm_gate=Q4_K, ssm_out=Q4_K)
+
+
+def hy_conv_dim(cfg):
+    return (2 * cfg["dn_k_heads"] + cfg["dn_v_heads"]) * cfg["dn_state"]
+
+
+def hy_is_full(cfg, l):
+    return (l + 1) % cfg["full_attn_interval"] == 0
+
+
+def hybrid_shapes(cfg, l):
+    """(n_in, n_out) of the quantized matrices of layer l."""
+    E, ff = cfg["n_embd"], cfg["n_ff"]
+    sh = dict(ffn_gate=(E, ff), ffn_up=(E, ff), ffn_down=(ff, E))
+    if hy_is_full(cfg, l):
+        qd, kvd = cfg["n_head"] * cfg["head_dim"], cfg["n_head_kv"] * cfg["head_dim"]
+        sh.update(attn_q=(E, 2 * qd), attn_k=(E, kvd), attn_v=(E, kvd), attn_output=(qd, E))
+    else:
+        vd = cfg["dn_v_heads"] * cfg["dn_state"]
+        sh.update(ssm_qkv=(E, hy_conv_dim(cfg)), ssm_gate=(E, vd), ssm_out=(vd, E))
+    return sh
+
+
+def hybrid_f32_shapes(cfg, l):
+    """element counts of the f32 vectors of layer l and their uniform ranges."""
+    E = cfg["n_embd"]
+    sh = dict(attn_norm=(E, 0.9, 1.1), post_norm=(E, 0.9, 1.1))
+    if hy_is_full(cfg, l):
+        sh.update(q_norm=(cfg["head_dim"], 0.9, 1.1), k_norm=(cfg["head_dim"], 0.9, 1.1))
+    else:
+        nv, r = cfg["dn_v_heads"], 1.7 / np.sqrt(E)
+        sh.update(ssm_alpha=(nv * E, -r, r), ssm_beta=(nv * E, -r, r), ssm_a=(nv, -1.0, -0.1),
+                  ssm_dt=(nv, -1.0, 1.0), ssm_conv=(hy_conv_dim(cfg) * cfg["dn_conv"], -0.5, 0.5),
+                  ssm_norm=(cfg["dn_state"], 0.9, 1.1))
+    return sh
+
+
+def hybrid_host_model(orc, cfg, seed=1, mix=None, mode=1, d_lo=2e-4, d_hi=2e-3):
+    mix = dict(HY_Q4_K_M, **(mix or {}))
+    w = {}
+    for l in range(cfg["n_layer"]):
+        for i, (name, (n_in, n_out)) in enumerate(sorted(hybrid_shapes(cfg, l).items())):
+            t = mix[name]
+            w[f"blk.{l}.{name}"] = (t, orc.gen_weight(t, seed * 1000 + l * 32 + i, n_out, n_in,
+                                                     mode=mode, d_lo=d_lo, d_hi=d_hi))
+        for i, (name, (n, lo, hi)) in enumerate(sorted(hybrid_f32_shapes(cfg, l).items())):
+            w[f"blk.{l}.{name}"] = (F32, orc.gen_uniform(seed * 77 + 32 * l + i, n, lo, hi))
+    w["token_embd"] = (mix["token_embd"], orc.gen_weight(mix["token_embd"], seed * 5 + 1,
+                                                          cfg["vocab"], cfg["n_embd"], mode=mode,
+                                                          d_lo=d_lo * 20, d_hi=d_hi * 20))
+    w["output"] = (mix["output"], orc.gen_weight(mix["output"], seed * 5 + 2, cfg["vocab"],
+                                                  cfg["n_embd"], mode=mode, d_lo=d_lo, d_hi=d_hi))
+    w["output_norm"] = (F32, orc.gen_uniform(seed * 5 + 3, cfg["n_embd"], 0.9, 1.1))
+    return w

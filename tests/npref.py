@@ -164,3 +164,106 @@ def rms_forward64(cfg: dict, weights: dict, tokens, kv_f16: bool):
         x = x + a @ W(p + "ffn_down", c["n_ff"], E).T
     h = norm(x, vec("output_norm"))
     return h @ W("output", E, c["vocab"]).T
+
+
+def hybrid_forward64(c, weights, tokens, kv_f16=True):
+    """float64 restatement of the hybrid (qwen35) decode, one token at a time:
+    full attention when (l+1) % full_attn_interval == 0 (config.rs:25-35),
+    else the gated delta net of plano_delta (resident_forward.rs:2252-2470).
+    Written from the formulas (delta rule as S <- a S + beta (v - a S k) k^T on
+    a row-major S[v][k] matrix) rather than from the oracle's loops.  Returns
+    the logits of every token [n_tok][vocab]."""
+    E, H, HKV, HD = c["n_embd"], c["n_head"], c["n_head_kv"], c["head_dim"]
+    NK, NV, D, W = c["dn_k_heads"], c["dn_v_heads"], c["dn_state"], c["dn_conv"]
+    eps = c["rms_eps"]
+
+    def mat(name, n_in, n_out):
+        t, arr = weights[name]
+        return dequant(t, arr).astype(np.float64).reshape(n_out, n_in)
+
+    def vec(name):
+        t, arr = weights[name]
+        return dequant(t, arr).astype(np.float64)
+
+    def rms(x, w):
+        return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w
+
+    def silu(v):
+        return v / (1.0 + np.exp(-v))
+
+    half = c["rope_dim"] // 2
+    inv_freq = 1.0 / np.float64(c["freq_base"]) ** (2.0 * np.arange(half) / c["rope_dim"])
+
+    def rope(heads, pos):  # heads [n, HD]; adjacent pairs of the first rope_dim dims
+        out = heads.copy()
+        th = pos * inv_freq
+        a, b = heads[:, 0:2 * half:2], heads[:, 1:2 * half:2]
+        out[:, 0:2 * half:2] = a * np.cos(th) - b * np.sin(th)
+        out[:, 1:2 * half:2] = a * np.sin(th) + b * np.cos(th)
+        return out
+
+    full = [(l + 1) % c["full_attn_interval"] == 0 for l in range(c["n_layer"])]
+    kcache = {l: [] for l in range(c["n_layer"]) if full[l]}
+    vcache = {l: [] for l in range(c["n_layer"]) if full[l]}
+    S = {l: np.zeros((NV, D, D)) for l in range(c["n_layer"]) if not full[l]}
+    CD = (2 * NK + NV) * D
+    hist = {l: np.zeros((W - 1, CD)) for l in range(c["n_layer"]) if not full[l]}
+    emb = mat("token_embd", E, c["vocab"])
+    logits = []
+    for pos, tok in enumerate(np.asarray(tokens)):
+        x = emb[tok].copy()
+        for l in range(c["n_layer"]):
+            p = f"blk.{l}."
+            h = rms(x, vec(p + "attn_norm"))
+            if full[l]:
+                qg = (mat(p + "attn_q", E, 2 * H * HD) @ h).reshape(H, 2, HD)
+                q, gate = qg[:, 0, :], qg[:, 1, :]
+                k = (mat(p + "attn_k", E, HKV * HD) @ h).reshape(HKV, HD)
+                v = (mat(p + "attn_v", E, HKV * HD) @ h).reshape(HKV, HD)
+                q = rope(rms(q, vec(p + "q_norm")), pos)
+                k = rope(rms(k, vec(p + "k_norm")), pos)
+                if kv_f16:
+                    k = k.astype(np.float32).astype(np.float16).astype(np.float64)
+                    v = v.astype(np.float32).astype(np.float16).astype(np.float64)
+                kcache[l].append(k)
+                vcache[l].append(v)
+                K, V = np.stack(kcache[l]), np.stack(vcache[l])  # [t, HKV, HD]
+                att = np.zeros((H, HD))
+                for hh in range(H):
+                    kh = hh // (H // HKV)
+                    s = K[:, kh, :] @ q[hh] / np.sqrt(HD)
+                    s = np.exp(s - s.max())
+                    att[hh] = (s / s.sum()) @ V[:, kh, :]
+                att = att / (1.0 + np.exp(-gate))
+                o = mat(p + "attn_output", H * HD, E) @ att.reshape(-1)
+            else:
+                qkv = mat(p + "ssm_qkv", E, CD) @ h
+                z = (mat(p + "ssm_gate", E, NV * D) @ h).reshape(NV, D)
+                ker = vec(p + "ssm_conv").reshape(CD, W)
+                win = np.vstack([hist[l], qkv[None, :]])  # oldest first, [W, CD]
+                conv = silu((win * ker.T).sum(0))
+                hist[l] = win[1:]
+                q = conv[:NK * D].reshape(NK, D)
+                k = conv[NK * D:2 * NK * D].reshape(NK, D)
+                v = conv[2 * NK * D:].reshape(NV, D)
+                q = q / np.sqrt((q * q).sum(-1, keepdims=True) + eps)
+                k = k / np.sqrt((k * k).sum(-1, keepdims=True) + eps)
+                alpha = vec(p + "ssm_alpha").reshape(NV, E) @ h
+                beta = 1.0 / (1.0 + np.exp(-(vec(p + "ssm_beta").reshape(NV, E) @ h)))
+                a = np.exp(vec(p + "ssm_a") * np.log1p(np.exp(alpha + vec(p + "ssm_dt"))))
+                y = np.zeros((NV, D))
+                for hh in range(NV):
+                    kk, qq = k[hh % NK], q[hh % NK]
+                    Sh = a[hh] * S[l][hh]                     # S[v, k]
+                    Sh = Sh + beta[hh] * np.outer(v[hh] - Sh @ kk, kk)
+                    S[l][hh] = Sh
+                    y[hh] = Sh @ qq / np.sqrt(D)
+                y = rms(y, vec(p + "ssm_norm")) * silu(z)
+                o = mat(p + "ssm_out", NV * D, E) @ y.reshape(-1)
+            x = x + o
+            h = rms(x, vec(p + "post_norm"))
+            g = mat(p + "ffn_gate", E, c["n_ff"]) @ h
+            u = mat(p + "ffn_up", E, c["n_ff"]) @ h
+            x = x + mat(p + "ffn_down", c["n_ff"], E) @ (silu(g) * u)
+        logits.append(mat("output", E, c["vocab"]) @ rms(x, vec("output_norm")))
+    return np.stack(logits)
