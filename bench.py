@@ -11,6 +11,13 @@ Workloads:
           512..511+K, the config's 128 tokens after a 512-token prompt).
   layer   config 2: one Qwen2.5-14B-shaped layer matvec set, weights rotated
           over 4 copies so every byte comes from HBM; a step is 7 matvecs.
+  hybrid  config 4: 27B-scale hybrid model (64 layers, gated full attention
+          every 4th: 24 q / 4 kv x 256; 48 gated delta-net layers of 16 heads
+          x 128x128 f32 state), random-init Q4_K_M; the 512-token prompt is
+          consumed token by token (the recurrence is sequential), then K greedy
+          tokens are timed at positions 511..  (warmup runs on a separate pass:
+          the recurrent state cannot be rewound, so the model is reset and the
+          prompt replayed before the timed tokens).
   pmc     profiling helper for the rocprofv3 counter passes: a plain copy
           kernel of known size (calibration) and the dominant decode kernel
           on a 4-layer model of the 32B shape.
@@ -144,6 +151,103 @@ def bench_decode(lrs, ctx, steps, warmup):
                 kv_bytes=kv_bytes, w_bytes=m.bytes_per_token, ops=ops)
 
 
+HY_OPS = ("dn_proj", "dn_step", "dn_out", "qkv", "qk_prep", "attn", "o", "gateup", "down",
+          "head")
+OP_NAMES.update({"dn_proj": "fused RMSNorm + delta-net qkv/z Q4_K matvec",
+                 "dn_step": "delta-net step: gates, conv, L2, delta rule, gated norm",
+                 "dn_out": "delta-net ssm_out matvec + residual add",
+                 "qk_prep": "QK-norm + RoPE + f16 KV append (gated attention layers)"})
+
+
+def bench_hybrid(lrs, ctx, steps, warmup):
+    from llama_rs_amd.model import QWEN35_27B, synthetic_hybrid_model
+
+    cfg = dict(QWEN35_27B)
+    if PROMPT + steps > cfg["ctx"]:
+        raise SystemExit(f"--steps must keep {PROMPT} + tokens within ctx {cfg['ctx']}")
+    t0 = time.perf_counter()
+    m = synthetic_hybrid_model(ctx, cfg, seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
+    ctx.sync()
+    log(f"[bench] 27B-scale hybrid Q4_K_M model resident in {time.perf_counter() - t0:.1f} s, "
+        f"{m.bytes_per_token / 1e9:.3f} GB of weights per token")
+    rng = np.random.default_rng(1234)
+    prompt = rng.integers(0, cfg["vocab"], PROMPT).astype(np.uint32)
+    t0 = time.perf_counter()
+    m.decode_batch(prompt[:-1], 0)
+    prefill_s = time.perf_counter() - t0
+    log(f"[bench] prompt {PROMPT - 1} tokens in {prefill_s:.2f} s (token by token)")
+    if warmup:
+        m.generate_greedy(prompt[-1:], warmup, pos0=PROMPT - 1)
+        m.reset()
+        m.decode_batch(prompt[:-1], 0)
+    ctx.sync()
+    ctx.timer_start()
+    w0 = time.perf_counter()
+    toks = m.generate_greedy(prompt[-1:], steps, pos0=PROMPT - 1)
+    ctx.sync()
+    wall = time.perf_counter() - w0
+    ev_ms = ctx.timer_stop()
+    log(f"[bench] {steps} tokens: wall {wall * 1e3:.1f} ms, events {ev_ms:.1f} ms "
+        f"-> {steps / wall:.1f} tok/s; first tokens {toks[:6].tolist()}")
+    n_attn = sum((l + 1) % cfg["full_attn_interval"] == 0 for l in range(cfg["n_layer"]))
+    n_dn = cfg["n_layer"] - n_attn
+    kvd = cfg["n_head_kv"] * cfg["head_dim"]
+    kv_bytes = np.mean([L * kvd * 2 * 2 * n_attn for L in range(PROMPT, PROMPT + steps)])
+    D, nv = cfg["dn_state"], cfg["dn_v_heads"]
+    cd = (2 * cfg["dn_k_heads"] + nv) * D
+    rec_bytes = n_dn * (nv * D * D * 4 * 2 + cd * 4 * cfg["dn_conv"])
+    tok_bytes = m.bytes_per_token + kv_bytes + rec_bytes
+    ops = {}
+    for op in HY_OPS:
+        mult = n_dn if op.startswith("dn_") else n_attn if op in ("qkv", "qk_prep", "attn",
+                                                                   "o") else \
+            1 if op == "head" else cfg["n_layer"]
+        us, b = m.profile(op, 2 * mult if op != "head" else 8)
+        ops[op] = dict(us=us, bytes=b, per_token_us=us * mult, gbs=b / us / 1e3 if us else 0.0)
+        log(f"[bench]   {op:8s} {us:8.2f} us/launch {ops[op]['gbs']:7.0f} GB/s  "
+            f"{us * mult / 1e3:.3f} ms/token")
+    m.close()
+    return dict(cfg=cfg, ms_tok=wall * 1e3 / steps, tok_bytes=tok_bytes, kv_bytes=kv_bytes,
+                rec_bytes=rec_bytes, w_bytes=m.bytes_per_token, ops=ops, prefill_s=prefill_s)
+
+
+def cpu_baseline_hybrid(threads):
+    """The oracle's hybrid forward on a bounded sample of config 4: one block of
+    4 layers of the full shape (3 delta-net + 1 gated attention) timed over
+    repeated tokens, plus 1/16 of the Q6_K output head's rows; scaled to one
+    token = 16 blocks + the whole head."""
+    import modelgen
+    import oracle
+    from llama_rs_amd.model import QWEN35_27B
+
+    lc = dict(QWEN35_27B, n_layer=4, vocab=256, ctx=1024)
+    w = modelgen.hybrid_host_model(oracle, lc, seed=3, mode=0, d_lo=1e-3, d_hi=1e-2)
+    om = oracle.HybridModel(lc, w, kv_f16=True, threads=threads)
+    om.forward([1])
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 8.0 and n < 500:
+        om.forward([(n * 7 + 3) % 256])
+        n += 1
+    t_block = (time.perf_counter() - t0) / n
+    om.close()
+    rows = 248320 // 16
+    hw = oracle.gen_weight(Q6_K, 5, rows, 5120)
+    x = oracle.gen_normal(1, 5120)
+    oracle.matvec(Q6_K, hw, 5120, rows, x, threads=threads)
+    nh, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 4.0:
+        oracle.matvec(Q6_K, hw, 5120, rows, x, threads=threads)
+        nh += 1
+    t_head = (time.perf_counter() - t0) / nh * 16
+    s_tok = 16 * t_block + t_head
+    return {"value": round(1.0 / s_tok, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle hybrid forward: {n} single-token passes through a 4-layer block "
+                      f"(3 delta-net + 1 gated attention) of the config-4 shape "
+                      f"({t_block * 1e3:.1f} ms each) + {nh} matvecs over 1/16 of the Q6_K "
+                      f"output head; per token = 16 blocks + 16x the head slice "
+                      f"= {s_tok:.2f} s"}
+
+
 def cpu_baseline_decode(threads):
     """The oracle (C restatement of Model::forward: per-row dequant + sequential
     f32 dot, rows in chunks of 32 over `threads`) on a bounded sample of the
@@ -258,7 +362,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "layer", "gemm", "pmc"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "hybrid", "layer", "gemm", "pmc"])
     ap.add_argument("--m", type=int, default=512, help="gemm: prompt tokens (config 5: 128/512/2048)")
     ap.add_argument("--precision", type=int, default=1, choices=[1, 3],
                     help="gemm: 1 = bf16 operands, 3 = bf16 hi/lo split")
@@ -312,6 +417,45 @@ def main():
                           "copies_rotated": 4}}
         print(json.dumps(out), flush=True)
         ctx.close()
+        return
+
+    if a.workload == "hybrid":
+        r = bench_hybrid(lrs, ctx, a.steps, a.warmup)
+        ops = r["ops"]
+        dom = max(ops, key=lambda k: ops[k]["per_token_us"])
+        d = ops[dom]
+        ctx.close()
+        cpu = None if a.no_cpu else cpu_baseline_hybrid(threads)
+        cfg = r["cfg"]
+        eff_gbs = r["tok_bytes"] / (r["ms_tok"] * 1e-3) / 1e9
+        out = {"metric": "batch-1 decode tok/s, hybrid attention + gated delta-net 27B-scale "
+                         "Q4_K_M (config 4)",
+               "value": round(1e3 / r["ms_tok"], 2), "unit": "tok/s", "n_gpus": 1,
+               "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(r["ms_tok"], 4),
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+               "dtype": "f32",
+               "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU, "
+                       "BASELINE distributions; f32 delta-net vectors seeded; prompt ids "
+                       "uniform random, seed 1234)",
+               "config": {"workload": "config4-hybrid-27b-scale-q4_k_m-greedy-decode",
+                          "prompt": PROMPT, "decode_tokens": a.steps,
+                          **{k: cfg[k] for k in ("n_layer", "n_embd", "n_head", "n_head_kv",
+                                                 "head_dim", "n_ff", "vocab",
+                                                 "full_attn_interval", "dn_k_heads",
+                                                 "dn_v_heads", "dn_state", "dn_conv",
+                                                 "rope_dim")},
+                          "weights": "q,k,o,gate,up,ssm_qkv,ssm_gate,ssm_out,token_embd Q4_K; "
+                                     "v,down,output Q6_K; alpha/beta/conv/norms f32",
+                          "bytes_per_token": int(r["tok_bytes"]),
+                          "token_roofline_frac": round(eff_gbs / HBM_PEAK_GBS, 4),
+                          "effective_gbs": round(eff_gbs, 1)},
+               "roofline": {"bound": "hbm", "achieved": round(d["gbs"], 1),
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": OP_NAMES[dom], "op": dom, "kernel_us": round(d["us"], 3),
+                            "bytes_per_launch": d["bytes"]},
+               "cpu_baseline": cpu}
+        print(json.dumps(out), flush=True)
         return
 
     r = bench_decode(lrs, ctx, a.steps, a.warmup)

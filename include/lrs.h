@@ -174,6 +174,49 @@ typedef struct {
 int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weights *layers,
                      const lrs_weight *token_embd, const float *output_norm,
                      const lrs_weight *output, lrs_model **out);
+
+/* Hybrid attention + gated delta-net model (qwen35; LlamaConfig::delta_net,
+ * config.rs:10-46, 126-141): layer l is gated full attention when
+ * (l + 1) % full_attn_interval == 0 and a gated delta net otherwise
+ * (LlamaConfig::eh_linear).  Replaces ResidentForward::new for this
+ * architecture (resident_forward.rs:1302-1311; plan of the layer loop
+ * :3826-4103 and plano_delta :2252-2470).  The full-attention layers use
+ * base.n_head / n_head_kv / head_dim and RoPE of the first base.rope_dim dims
+ * with freq[i] = 1 / freq_base^(2i/rope_dim) (gpu.rs:540-547).  Delta-net
+ * layers: dn_v_heads value heads of dn_state x dn_state f32 state reading key
+ * head h % dn_k_heads; conv over the last dn_conv inputs.  dn_state 64 or 128
+ * (the key and value head width, ssm.state_size). */
+typedef struct {
+    lrs_config base;
+    uint32_t full_attn_interval;
+    uint32_t dn_k_heads, dn_v_heads, dn_state, dn_conv;
+} lrs_hybrid_config;
+
+/* One hybrid layer.  Every layer: FFN weights, attn_norm (input norm) and
+ * post_norm (post_attention_norm, before the FFN).  Full-attention layers:
+ * attn_q has 2*n_head*head_dim rows (per head the query, then its output
+ * gate), q_norm / k_norm [head_dim] (per-head RMSNorm before RoPE).  Delta-net
+ * layers: ssm_qkv [conv_dim = (2*k_heads + v_heads)*dn_state rows: q | k | v
+ * channels], ssm_gate (z) [v_heads*dn_state], ssm_out [n_embd x v_heads*dn_state];
+ * host f32: ssm_alpha / ssm_beta [v_heads][n_embd], ssm_a (negative) and
+ * ssm_dt [v_heads], ssm_conv [conv_dim][dn_conv], ssm_norm [dn_state].
+ * Unused members of the other layer kind may be NULL. */
+typedef struct {
+    const lrs_weight *ffn_gate, *ffn_up, *ffn_down;
+    const float *attn_norm, *post_norm;
+    const lrs_weight *attn_q, *attn_k, *attn_v, *attn_output;
+    const float *q_norm, *k_norm;
+    const lrs_weight *ssm_qkv, *ssm_gate, *ssm_out;
+    const float *ssm_alpha, *ssm_beta, *ssm_a, *ssm_dt, *ssm_conv, *ssm_norm;
+} lrs_hybrid_layer;
+
+/* Builds a hybrid model: the same decode / decode_batch / greedy / reset
+ * entry points apply.  Its recurrent state cannot be rewound: every decode
+ * must continue at the current length (pos == lrs_model_len) and
+ * lrs_reset clears the states and conv windows; batch_size() is 1. */
+int lrs_hybrid_create(lrs_ctx *ctx, const lrs_hybrid_config *cfg, const lrs_hybrid_layer *layers,
+                      const lrs_weight *token_embd, const float *output_norm,
+                      const lrs_weight *output, lrs_model **out);
 void lrs_model_destroy(lrs_model *m);
 /* GpuResidentDecode::decode: token at position pos (KV written at slot pos,
  * attends 0..pos), logits [vocab] into caller memory; the cache length
@@ -210,6 +253,13 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
 #define LRS_OP_GATEUP 3u
 #define LRS_OP_DOWN 4u
 #define LRS_OP_HEAD 5u
+/* hybrid models: delta-net projections (qkv + z), the delta-net step, its
+ * output projection, and the QK-norm + RoPE of the attention layers;
+ * LRS_OP_QKV / ATTN / O then time the attention layers' ops */
+#define LRS_OP_DN_PROJ 6u
+#define LRS_OP_DN_STEP 7u
+#define LRS_OP_DN_OUT 8u
+#define LRS_OP_QK_PREP 9u
 int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, size_t *bytes);
 /* GGUF bytes of every weight matrix one decoded token streams. */
 size_t lrs_model_bytes_per_token(const lrs_model *m);

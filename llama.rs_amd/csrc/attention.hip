@@ -209,7 +209,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 // goes to LDS in one round trip (global_load_lds), then thread d owns dim d
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ part, uint32_t splits,
-                                                     XPack out) {
+                                                     const float *__restrict__ gate,
+                                                     uint32_t gstride, XPack out) {
     extern __shared__ __attribute__((aligned(16))) float pl[];  // [splits][HD + 4]
     __shared__ float wsh[64], red[1];
     constexpr uint32_t ST = HD + 4;
@@ -240,7 +241,10 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     const float den = red[0];
     float num = 0.f;
     for (uint32_t s = 0; s < splits; s++) num = fmaf(wsh[s], pl[s * ST + d], num);
-    pack_half(num / den, (h * HD + d) >> 5, out);
+    float o = num / den;
+    // gated attention (gate_quant.comp): o * sigmoid(gate of head h, dim d)
+    if (gate) o = o * (1.0f / (1.0f + expf(-gate[(size_t)h * gstride + d])));
+    pack_half(o, (h * HD + d) >> 5, out);
 }
 
 // split count: about one workgroup per CU (256 = splits x KV heads)
@@ -267,7 +271,8 @@ static AttnFn pick_rep(uint32_t rep) {
 
 hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *part,
                             XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
-                            uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s) {
+                            uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s,
+                            const float *gate, uint32_t gstride) {
     AttnArgs a;
     a.q = q;
     a.kc = kc;
@@ -293,9 +298,9 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
     hipLaunchKernelGGL(fn, grid, dim3(ATT_THREADS), 0, s, a);
     const size_t cl = (size_t)splits * (head_dim + 4) * sizeof(float);
     switch (head_dim) {
-    case 64: hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), cl, s, part, splits, out); break;
-    case 128: hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_head), dim3(128), cl, s, part, splits, out); break;
-    default: hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_head), dim3(256), cl, s, part, splits, out); break;
+    case 64: hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), cl, s, part, splits, gate, gstride, out); break;
+    case 128: hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_head), dim3(128), cl, s, part, splits, gate, gstride, out); break;
+    default: hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_head), dim3(256), cl, s, part, splits, gate, gstride, out); break;
     }
     return hipGetLastError();
 }

@@ -1,0 +1,301 @@
+// dn.hip — the two mixers of the hybrid (qwen35) decode that the dense model
+// does not have: the gated delta-net step and the QK-norm + RoPE of the gated
+// full-attention layers.
+//
+// Delta-net step (plano_delta, resident_forward.rs:2252-2470, with the math of
+// delta_net.rs:13-131 and shaders dn_gates / dn_conv / dn_l2_qk / delta_net /
+// dn_norm), one launch per layer and token.  Value head h owns a D x D f32
+// state S_h (row j = value dim j, contiguous over the key dim) and reads key
+// head h % k_heads (the modulo GQA of delta_net.comp:75-85):
+//
+//   gates   g = a_h * softplus(alpha_h . hn + dt_h), beta = sigmoid(beta_h . hn),
+//           hn = rmsnorm(x) * attn_norm (f32 rows, as dn_gates reads b_normed)
+//   conv    c = SiLU(sum_t w[t] x_{pos-W+1+t}) over the last W conv inputs
+//   L2      q <- q / sqrt(|q|^2 + eps), k <- k / sqrt(|k|^2 + eps)
+//   rule    S <- e^g S;  S_j <- S_j + beta (v_j - S_j . k) k;  o_j = S_j . q / sqrt(D)
+//   norm    y_j = o_j / sqrt(mean_j(o^2) + eps) * norm_w[j] * silu(z_j)
+//
+// The rows of a head are independent in the rule, so a head is split over
+// D/32 workgroups of 32 rows (one pack block each): the state streams from
+// 4 x more CUs than one workgroup per head would use.  Each workgroup
+// recomputes the head's gates, q and k (a few KB, L2-resident) and packs its
+// 32 y values without the head's RMS factor; the workgroup that finishes the
+// head last (an arrival counter, no waiting) sums the partial sums of squares
+// and multiplies the factor into the pack scales of the head's blocks (the
+// pack is linear in its scale and block sums).  The conv inputs live in a ring
+// of W slots indexed by position, so the slot being written (pos % W) is never
+// one being read: workgroups that share a key head need no ordering.
+#include "lrs_internal.h"
+#include "pack_dev.h"
+
+namespace lrs {
+
+
+template <int CTRL>
+__device__ __forceinline__ float dn_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// sum over each aligned group of 8 lanes, in every lane of the group
+__device__ __forceinline__ float sum8(float v) {
+    v += dn_dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dn_dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dn_dpp<0x141>(v);  // row_half_mirror
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float ld_coherent(const float *p) {
+    return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t *>(const_cast<float *>(p)), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT));
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
+    constexpr uint32_t R = D / 32;    // workgroups per head (32 rows each)
+    constexpr int PPL = D / 32;       // float4 pieces of a row per lane (8 lanes per row)
+    const uint32_t r = blockIdx.x, hh = blockIdx.y, tid = threadIdx.x;
+    const uint32_t lane = tid & 63, wave = tid >> 6;
+    const uint32_t rho = tid >> 3, lam = tid & 7;  // row of the lane group, lane in the group
+    const uint32_t j = 32 * r + rho;
+    const uint32_t kh = hh % a.k_heads;
+    const uint32_t KD = a.k_heads * D, CD = 2 * KD + a.v_heads * D;
+    __shared__ __attribute__((aligned(16))) float sq[D], sk[D];
+    __shared__ float sv[32], so[32], red[3][4], gb[2];
+    __shared__ uint32_t last;
+
+    // state row j in flight first: lane lam holds pieces 8c + lam
+    float4 st[PPL];
+    float4 *srow = reinterpret_cast<float4 *>(a.state + ((size_t)hh * D + j) * D);
+#pragma unroll
+    for (int c = 0; c < PPL; c++) st[c] = srow[8 * c + lam];
+
+    // gate projections of hn = rmsnorm(x) * attn_norm (dn_gates.comp)
+    {
+        float ss = 0.f, pa = 0.f, pb = 0.f;
+        const float *al = a.alpha + (size_t)hh * a.n_embd, *be = a.beta + (size_t)hh * a.n_embd;
+        for (uint32_t i = 4 * tid; i < a.n_embd; i += 1024) {
+            const float4 xv = *reinterpret_cast<const float4 *>(a.x + i);
+            const float4 wv = *reinterpret_cast<const float4 *>(a.attn_norm + i);
+            const float4 av = *reinterpret_cast<const float4 *>(al + i);
+            const float4 bv = *reinterpret_cast<const float4 *>(be + i);
+            ss += (xv.x * xv.x + xv.y * xv.y) + (xv.z * xv.z + xv.w * xv.w);
+            const float h0 = xv.x * wv.x, h1 = xv.y * wv.y, h2 = xv.z * wv.z, h3 = xv.w * wv.w;
+            pa += (av.x * h0 + av.y * h1) + (av.z * h2 + av.w * h3);
+            pb += (bv.x * h0 + bv.y * h1) + (bv.z * h2 + bv.w * h3);
+        }
+        ss = wave_sum(ss);
+        pa = wave_sum(pa);
+        pb = wave_sum(pb);
+        if (lane == 0) {
+            red[0][wave] = ss;
+            red[1][wave] = pa;
+            red[2][wave] = pb;
+        }
+    }
+
+    // causal conv + SiLU of q, k (key head kh) and this workgroup's v rows
+    // (dn_conv.comp); the current input goes to ring slot pos % W, written
+    // once per channel: q/k by workgroup 0 of value head kh, v by its owner
+    const uint32_t pos = a.step[1];
+    const uint32_t W = a.d_conv, wslot = pos % W;
+    const bool own_qk = r == 0 && hh < a.k_heads;
+    for (uint32_t c = tid; c < 2 * D + 32; c += 256) {
+        const uint32_t ch = c < D ? kh * D + c
+                            : c < 2 * D ? KD + kh * D + (c - D)
+                                        : 2 * KD + hh * D + 32 * r + (c - 2 * D);
+        const float xc = a.qkv[ch];
+        const float *w = a.conv_w + (size_t)ch * W;
+        float acc = 0.f;
+        for (uint32_t t = 0; t + 1 < W; t++)
+            acc += a.win[(size_t)((pos + 1 + t) % W) * CD + ch] * w[t];
+        acc += xc * w[W - 1];
+        const float v = acc / (1.0f + expf(-acc));
+        if (c < D) sq[c] = v;
+        else if (c < 2 * D) sk[c - D] = v;
+        else sv[c - 2 * D] = v;
+        if (c >= 2 * D || own_qk) a.win[(size_t)wslot * CD + ch] = xc;
+    }
+    __syncthreads();
+
+    if (tid == 0) {
+        const float ss = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        const float pa = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+        const float pb = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
+        const float s = 1.0f / sqrtf(ss / (float)a.n_embd + a.eps);
+        const float zz = pa * s + a.dt[hh];
+        const float sp = zz > 20.0f ? zz : log1pf(expf(zz));  // delta_net.rs:13-20
+        gb[0] = expf(a.a[hh] * sp);                          // decay e^g
+        gb[1] = 1.0f / (1.0f + expf(-(pb * s)));             // beta
+    }
+    // L2 norms of q and k (dn_l2_qk.comp); 1/sqrt(D) of the read-out folded into q
+    {
+        float qq = 0.f, kk = 0.f;
+        for (uint32_t c = tid; c < (uint32_t)D; c += 256) {
+            qq += sq[c] * sq[c];
+            kk += sk[c] * sk[c];
+        }
+        qq = wave_sum(qq);
+        kk = wave_sum(kk);
+        __syncthreads();  // red[] reuse after the gate reduction above
+        if (lane == 0) {
+            red[0][wave] = qq;
+            red[1][wave] = kk;
+        }
+    }
+    __syncthreads();
+    const float qq = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    const float kk = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    const float qs = 1.0f / sqrtf(qq + a.eps) * (1.0f / sqrtf((float)D));
+    const float ks = 1.0f / sqrtf(kk + a.eps);
+    const float decay = gb[0], beta = gb[1];
+
+    // delta rule on row j: 8 lanes per row
+    float4 kr[PPL], qr[PPL];
+#pragma unroll
+    for (int c = 0; c < PPL; c++) {
+        const float4 k4 = reinterpret_cast<const float4 *>(sk)[8 * c + lam];
+        const float4 q4 = reinterpret_cast<const float4 *>(sq)[8 * c + lam];
+        kr[c] = make_float4(k4.x * ks, k4.y * ks, k4.z * ks, k4.w * ks);
+        qr[c] = make_float4(q4.x * qs, q4.y * qs, q4.z * qs, q4.w * qs);
+    }
+    float pred = 0.f;
+#pragma unroll
+    for (int c = 0; c < PPL; c++) {
+        st[c].x *= decay;
+        st[c].y *= decay;
+        st[c].z *= decay;
+        st[c].w *= decay;
+        pred += (st[c].x * kr[c].x + st[c].y * kr[c].y) + (st[c].z * kr[c].z + st[c].w * kr[c].w);
+    }
+    pred = sum8(pred);
+    const float delta = (sv[rho] - pred) * beta;
+    float o = 0.f;
+#pragma unroll
+    for (int c = 0; c < PPL; c++) {
+        st[c].x = fmaf(delta, kr[c].x, st[c].x);
+        st[c].y = fmaf(delta, kr[c].y, st[c].y);
+        st[c].z = fmaf(delta, kr[c].z, st[c].z);
+        st[c].w = fmaf(delta, kr[c].w, st[c].w);
+        o += (st[c].x * qr[c].x + st[c].y * qr[c].y) + (st[c].z * qr[c].z + st[c].w * qr[c].w);
+        srow[8 * c + lam] = st[c];
+    }
+    o = sum8(o);
+    if (lam == 0) so[rho] = o;
+    __syncthreads();
+
+    // pack of o * norm_w * silu(z) for the 32 rows (dn_norm.comp mode 1 without
+    // the head's RMS factor) and this workgroup's share of sum(o^2)
+    if (tid < 32) {
+        const uint32_t jj = 32 * r + tid;
+        const float ov = so[tid];
+        const float zz = a.z[(size_t)hh * D + jj];
+        const float y = ov * (a.norm_w[jj] * (zz / (1.0f + expf(-zz))));
+        pack_half(y, (hh * D + jj) >> 5, a.out);
+        float p = ov * ov;
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) p += __shfl_xor(p, off, 64);
+        if (tid == 0) a.part[hh * R + r] = p;
+    }
+    // the last workgroup of the head to arrive applies 1/sqrt(mean(o^2) + eps)
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(&a.cnt[hh], 1u) == R - 1;
+    __syncthreads();
+    if (!last || wave != 0) return;
+    __threadfence();
+    float p = lane < R ? ld_coherent(a.part + hh * R + lane) : 0.f;
+    p = wave_sum(p);
+    const float f = 1.0f / sqrtf(p / (float)D + a.eps);
+    if (lane < R) {
+        float *m = a.out.meta + 4 * ((size_t)hh * R + lane);
+        const float m0 = ld_coherent(m), m1 = ld_coherent(m + 1), m2 = ld_coherent(m + 2),
+                    m3 = ld_coherent(m + 3);
+        *reinterpret_cast<float4 *>(m) = make_float4(m0 * f, m1 * f, m2 * f, m3 * f);
+    }
+    if (lane == 0) __hip_atomic_store(&a.cnt[hh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+hipError_t launch_dn_step(const DnArgs &a, uint32_t d_state, hipStream_t s) {
+    if (a.k_heads == 0 || a.v_heads % a.k_heads || a.d_conv == 0 || a.n_embd % 4)
+        return hipErrorInvalidValue;
+    switch (d_state) {
+    case 64: hipLaunchKernelGGL(k_dn_step<64>, dim3(2, a.v_heads), dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL(k_dn_step<128>, dim3(4, a.v_heads), dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// QK-norm + RoPE of the gated full-attention layer (resident_forward.rs:
+// 3885-3963: dn_norm mode 2 on Q heads 2*head_dim apart and on K, then
+// rope.comp), one workgroup per head: q heads (query half of the Q rows) to
+// the contiguous q buffer, k heads with their v rows to the f16 cache at pos
+template <int HD>
+__global__ __launch_bounds__(HD) void k_qk_prep(const float *__restrict__ qg, const float *__restrict__ kb,
+                                                const float *__restrict__ vb,
+                                                const float *__restrict__ q_norm,
+                                                const float *__restrict__ k_norm,
+                                                const float *__restrict__ freq,
+                                                const uint32_t *__restrict__ step, float *__restrict__ q,
+                                                _Float16 *__restrict__ kc, _Float16 *__restrict__ vc,
+                                                uint32_t n_head, uint32_t ctx, uint32_t rope_dim,
+                                                float eps) {
+    __shared__ float red[HD / 64];
+    const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
+    const bool isq = h < n_head;
+    const uint32_t kh = h - n_head;
+    const float x = isq ? qg[(size_t)h * 2 * HD + d] : kb[(size_t)kh * HD + d];
+    const float ss = wave_sum(x * x);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < HD / 64; w++) tot += red[w];
+    const float s = 1.0f / sqrtf(tot / (float)HD + eps);
+    float y = (x * s) * (isq ? q_norm[d] : k_norm[d]);
+    const uint32_t pos = step[1];
+    const float yo = __shfl_xor(y, 1, 64);
+    if (d < rope_dim) {
+        const float th = (float)pos * freq[d >> 1];
+        float sn, cs;
+        sincosf(th, &sn, &cs);
+        y = (d & 1) ? yo * sn + y * cs : y * cs - yo * sn;
+    }
+    if (isq) {
+        q[(size_t)h * HD + d] = y;
+    } else {
+        const size_t o = ((size_t)kh * ctx + pos) * HD + d;
+        kc[o] = (_Float16)y;
+        vc[o] = (_Float16)vb[(size_t)kh * HD + d];
+    }
+}
+
+hipError_t launch_qk_prep(const float *qg, const float *kb, const float *vb, const float *q_norm,
+                          const float *k_norm, const float *freq, const uint32_t *step, float *q,
+                          _Float16 *kc, _Float16 *vc, uint32_t n_head, uint32_t n_kv,
+                          uint32_t head_dim, uint32_t ctx, uint32_t rope_dim, float eps,
+                          hipStream_t s) {
+    const dim3 g(n_head + n_kv);
+    switch (head_dim) {
+    case 64:
+        hipLaunchKernelGGL(k_qk_prep<64>, g, dim3(64), 0, s, qg, kb, vb, q_norm, k_norm, freq, step, q,
+                           kc, vc, n_head, ctx, rope_dim, eps);
+        break;
+    case 128:
+        hipLaunchKernelGGL(k_qk_prep<128>, g, dim3(128), 0, s, qg, kb, vb, q_norm, k_norm, freq, step,
+                           q, kc, vc, n_head, ctx, rope_dim, eps);
+        break;
+    case 256:
+        hipLaunchKernelGGL(k_qk_prep<256>, g, dim3(256), 0, s, qg, kb, vb, q_norm, k_norm, freq, step,
+                           q, kc, vc, n_head, ctx, rope_dim, eps);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace lrs

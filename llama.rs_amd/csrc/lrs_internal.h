@@ -113,6 +113,31 @@ hipError_t launch_attn_prefill(const float *q, const _Float16 *kc, const _Float1
                                uint32_t n, uint32_t pos0, uint32_t n_head, uint32_t n_kv,
                                uint32_t hd, uint32_t ctx, hipStream_t s);
 hipError_t launch_swiglu_rows(float *G, const float *U, size_t n, hipStream_t s);
+// hybrid (qwen35) mixers (dn.hip)
+struct DnArgs {
+    const float *qkv;           // [conv_dim] conv input (RMSNorm already applied by the matvec)
+    const float *z;             // [v_heads * D] output gate
+    const float *x;             // [n_embd] residual (gate projections)
+    const float *attn_norm;     // [n_embd]
+    const float *alpha, *beta;  // [v_heads][n_embd]
+    const float *a, *dt;        // [v_heads]
+    const float *conv_w;        // [conv_dim][d_conv]
+    float *win;                 // [d_conv][conv_dim] ring of conv inputs
+    float *state;               // [v_heads][D][D]
+    const float *norm_w;        // [D]
+    float *part;                // [v_heads][D/32] partial sums of squares of o
+    uint32_t *cnt;              // [v_heads] arrival counters, zero between launches
+    XPack out;                  // pack of y [v_heads * D]
+    const uint32_t *step;       // {token, pos}
+    uint32_t n_embd, k_heads, v_heads, d_conv;
+    float eps;
+};
+hipError_t launch_dn_step(const DnArgs &a, uint32_t d_state, hipStream_t s);
+hipError_t launch_qk_prep(const float *qg, const float *kb, const float *vb, const float *q_norm,
+                          const float *k_norm, const float *freq, const uint32_t *step, float *q,
+                          _Float16 *kc, _Float16 *vc, uint32_t n_head, uint32_t n_kv,
+                          uint32_t head_dim, uint32_t ctx, uint32_t rope_dim, float eps,
+                          hipStream_t s);
 
 }  // namespace lrs
 

@@ -40,7 +40,8 @@ namespace lrs {
 uint32_t attn_splits(uint32_t n_kv);
 hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *part,
                             XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
-                            uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s);
+                            uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s,
+                            const float *gate = nullptr, uint32_t gstride = 0);
 
 // x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304),
 // and the pack of x * nw for the first layer's q/k/v
@@ -63,8 +64,15 @@ using namespace lrs;
 
 struct DevLayer {
     const lrs_weight *q, *k, *v, *o, *gate, *up, *down;
-    float *attn_norm, *ffn_norm, *bq, *bk, *bv;
+    float *attn_norm, *ffn_norm, *bq, *bk, *bv;  // ffn_norm: post_attention_norm (hybrid)
     _Float16 *kc, *vc;
+    // hybrid: gated delta-net mixer (dn) or gated attention with QK-norm
+    bool dn = false;
+    const lrs_weight *ssm_qkv = nullptr, *ssm_gate = nullptr, *ssm_out = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr;
+    float *alpha = nullptr, *beta = nullptr, *ssm_a = nullptr, *ssm_dt = nullptr;
+    float *conv = nullptr, *ssm_norm = nullptr;
+    float *win = nullptr, *state = nullptr;  // conv input ring [d_conv][conv_dim], S [v][D][D]
 };
 
 struct lrs_model {
@@ -98,6 +106,17 @@ struct lrs_model {
     uint32_t len = 0;
     size_t gguf_bytes_per_token = 0;
     std::vector<void *> allocs;
+    // hybrid (qwen35) model: config and per-token buffers: Q rows (query +
+    // gate per head), k, v, conv input, output gate, partial sums of squares
+    // and arrival counters of the delta-net step; recurrent memory (rings +
+    // states of every delta-net layer) cleared by reset
+    bool hybrid = false;
+    lrs_hybrid_config hc = {};
+    float *qg = nullptr, *kb = nullptr, *vb = nullptr, *dn_qkv = nullptr, *dn_z = nullptr,
+          *dn_part = nullptr;
+    uint32_t *dn_cnt = nullptr;
+    void *rec = nullptr;
+    size_t rec_bytes = 0;
 };
 
 namespace {
@@ -214,27 +233,137 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
     return hipSuccess;
 }
 
+// attention over the f16 cache; hybrid layers gate the output with
+// sigmoid(second half of each head's Q rows) before packing it
 hipError_t op_attn(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
+    const float *gate = m->hybrid ? m->qg + c.head_dim : nullptr;
     return launch_attention(m->qbuf, L.kc, L.vc, m->pa, m->pk_a, m->step, c.n_head, c.n_head_kv,
-                            c.head_dim, c.ctx, m->a_splits, m->ctx->stream);
+                            c.head_dim, c.ctx, m->a_splits, m->ctx->stream, gate,
+                            2 * c.head_dim);
 }
 
-// x += W_o att; pack of x * ffn_norm for gate/up
+// x += W_o att (or W_ssm_out y of a delta-net layer); pack of x * ffn_norm
+// (post_attention_norm) for gate/up
 hipError_t op_o(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
+    const lrs_weight *wo = L.dn ? L.ssm_out : L.o;
     MqArgs a = {};
     a.n_seg = 1;
-    a.seg[0] = mseg(L.o, c.n_embd);
-    a.n_in = c.n_head * c.head_dim;
-    a.nxb = pack_blocks(L.o->v.type, a.n_in);
+    a.seg[0] = mseg(wo, c.n_embd);
+    a.n_in = wo->v.n_in;
+    a.nxb = pack_blocks(wo->v.type, a.n_in);
     a.xin = m->pk_a;
     a.x = m->x;
     a.nw = L.ffn_norm;
     a.xout = m->pk_f;
-    return launch_mq(a, L.o->v.type, L.o->v.type, G_O, MQ_RESID, m->ctx->stream);
+    return launch_mq(a, wo->v.type, wo->v.type, G_O, MQ_RESID, m->ctx->stream);
+}
+
+// outs[i] = W_i (rmsnorm(x) * attn_norm) for n weights (f32 rows out): one
+// launch when they share a type or are Q4_K + Q6_K, else one per type
+hipError_t op_store(lrs_model *m, const lrs_weight *const *ws, float *const *outs, int n) {
+    const lrs_config &c = m->cfg;
+    MqArgs a = {};
+    a.n_in = c.n_embd;
+    a.xin = m->pk_n;
+    a.xres = m->x;
+    a.eps = c.rms_eps;
+    bool q4 = false, q6 = false, other = false;
+    for (int i = 0; i < n; i++) {
+        const uint32_t t = ws[i]->v.type;
+        q4 |= t == T_Q4_K;
+        q6 |= t == T_Q6_K;
+        other |= t != T_Q4_K && t != T_Q6_K;
+    }
+    if (q4 && q6 && !other) {
+        a.n_seg = 0;
+        for (int pass = 0; pass < 2; pass++)
+            for (int i = 0; i < n; i++)
+                if ((ws[i]->v.type == T_Q4_K) == (pass == 0)) {
+                    MqSeg sg = mseg(ws[i], ws[i]->v.n_out);
+                    sg.out = outs[i];
+                    a.seg[a.n_seg++] = sg;
+                }
+        a.n_seg0 = 0;
+        for (int i = 0; i < n; i++) a.n_seg0 += ws[i]->v.type == T_Q4_K;
+        a.nxb = pack_blocks(T_Q4_K, c.n_embd);
+        hipError_t e = launch_mq(a, T_Q4_K, T_Q6_K, G_QKV, MQ_STORE, m->ctx->stream);
+        if (e != hipErrorNotSupported) return e;
+    }
+    bool done[MQ_MAX_SEG] = {false, false, false};
+    for (int i = 0; i < n; i++) {
+        if (done[i]) continue;
+        const uint32_t t = ws[i]->v.type;
+        a.n_seg = 0;
+        for (int j = i; j < n; j++)
+            if (!done[j] && ws[j]->v.type == t) {
+                MqSeg sg = mseg(ws[j], ws[j]->v.n_out);
+                sg.out = outs[j];
+                a.seg[a.n_seg++] = sg;
+                done[j] = true;
+            }
+        a.n_seg0 = a.n_seg;
+        a.nxb = pack_blocks(t, c.n_embd);
+        hipError_t e = launch_mq(a, t, t, G_QKV, MQ_STORE, m->ctx->stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// hybrid attention layer: Q (query + gate rows), k, v projections
+hipError_t op_hattn_proj(lrs_model *m, uint32_t l) {
+    const DevLayer &L = m->layers[l];
+    const lrs_weight *ws[3] = {L.q, L.k, L.v};
+    float *outs[3] = {m->qg, m->kb, m->vb};
+    return op_store(m, ws, outs, 3);
+}
+
+// QK-norm + RoPE; q to qbuf, k / v to the f16 cache at pos
+hipError_t op_qk_prep(lrs_model *m, uint32_t l) {
+    const lrs_config &c = m->cfg;
+    const DevLayer &L = m->layers[l];
+    return launch_qk_prep(m->qg, m->kb, m->vb, L.q_norm, L.k_norm, m->freq, m->step, m->qbuf, L.kc,
+                          L.vc, c.n_head, c.n_head_kv, c.head_dim, c.ctx, c.rope_dim, c.rms_eps,
+                          m->ctx->stream);
+}
+
+// delta-net layer: conv input (q | k | v channels) and output gate z
+hipError_t op_dn_proj(lrs_model *m, uint32_t l) {
+    const DevLayer &L = m->layers[l];
+    const lrs_weight *ws[2] = {L.ssm_qkv, L.ssm_gate};
+    float *outs[2] = {m->dn_qkv, m->dn_z};
+    return op_store(m, ws, outs, 2);
+}
+
+// delta-net step: gates, conv, L2, delta rule, gated norm -> pack of y
+hipError_t op_dn_step(lrs_model *m, uint32_t l) {
+    const DevLayer &L = m->layers[l];
+    DnArgs a = {};
+    a.qkv = m->dn_qkv;
+    a.z = m->dn_z;
+    a.x = m->x;
+    a.attn_norm = L.attn_norm;
+    a.alpha = L.alpha;
+    a.beta = L.beta;
+    a.a = L.ssm_a;
+    a.dt = L.ssm_dt;
+    a.conv_w = L.conv;
+    a.win = L.win;
+    a.state = L.state;
+    a.norm_w = L.ssm_norm;
+    a.part = m->dn_part;
+    a.cnt = m->dn_cnt;
+    a.out = m->pk_a;
+    a.step = m->step;
+    a.n_embd = m->cfg.n_embd;
+    a.k_heads = m->hc.dn_k_heads;
+    a.v_heads = m->hc.dn_v_heads;
+    a.d_conv = m->hc.dn_conv;
+    a.eps = m->cfg.rms_eps;
+    return launch_dn_step(a, m->hc.dn_state, m->ctx->stream);
 }
 
 // act = silu(gate h) * (up h), h = rmsnorm(x) * ffn_norm; gate and up tiles
@@ -302,8 +431,17 @@ hipError_t enqueue_forward(lrs_model *m, bool greedy) {
     hipError_t e;
     if ((e = op_embed(m)) != hipSuccess) return e;
     for (uint32_t l = 0; l < m->cfg.n_layer; l++) {
-        if ((e = op_qkv(m, l)) != hipSuccess || (e = op_attn(m, l)) != hipSuccess ||
-            (e = op_o(m, l)) != hipSuccess || (e = op_gateup(m, l)) != hipSuccess ||
+        if (m->layers[l].dn) {
+            if ((e = op_dn_proj(m, l)) != hipSuccess || (e = op_dn_step(m, l)) != hipSuccess)
+                return e;
+        } else if (m->hybrid) {
+            if ((e = op_hattn_proj(m, l)) != hipSuccess || (e = op_qk_prep(m, l)) != hipSuccess ||
+                (e = op_attn(m, l)) != hipSuccess)
+                return e;
+        } else if ((e = op_qkv(m, l)) != hipSuccess || (e = op_attn(m, l)) != hipSuccess) {
+            return e;
+        }
+        if ((e = op_o(m, l)) != hipSuccess || (e = op_gateup(m, l)) != hipSuccess ||
             (e = op_down(m, l)) != hipSuccess)
             return e;
     }
@@ -337,6 +475,58 @@ hipError_t run_forward(lrs_model *m, bool greedy) {
 }
 
 size_t wbytes(const lrs_weight *w) { return lrs_weight_gguf_bytes(w); }
+
+// allocations shared by the dense and hybrid models, then the graph capture;
+// pack_a_elems: elements of the o-projection's input pack beyond n_head*head_dim
+int finish_model(lrs_model *m, const float *output_norm, const std::vector<float> &fr,
+                 uint32_t pack_a_elems) {
+    const lrs_config &c = m->cfg;
+    const uint32_t qd = c.n_head * c.head_dim;
+    int rc;
+    m->gguf_bytes_per_token += wbytes(m->output);
+    if ((rc = upload_vec(m, output_norm, c.n_embd, &m->output_norm))) return rc;
+    if ((rc = upload_vec(m, fr.data(), fr.size(), &m->freq))) return rc;
+    m->gen_cap = 1u << 16;
+    m->a_splits = attn_splits(c.n_head_kv);
+    if ((rc = dev_alloc(m, (size_t)c.n_head * m->a_splits * (c.head_dim + 4) * sizeof(float),
+                        (void **)&m->pa)) ||
+        (rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
+        (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->qbuf)) ||
+        (rc = dev_alloc(m, c.vocab * sizeof(float), (void **)&m->logits)) ||
+        (rc = dev_alloc(m, 4 * sizeof(uint32_t), (void **)&m->step)) ||
+        (rc = dev_alloc(m, m->gen_cap * sizeof(uint32_t), (void **)&m->gen)) ||
+        (rc = dev_alloc(m, (size_t)c.vocab * sizeof(unsigned long long), (void **)&m->amax)))
+        return rc;
+    {
+        // activation packs (n_embd, n_ff and the o-projection inputs are
+        // multiples of 256)
+        void *p = nullptr;
+        const uint32_t ne = c.n_embd / 32, nq = (qd > pack_a_elems ? qd : pack_a_elems) / 32,
+                       nf = c.n_ff / 32;
+        if ((rc = dev_alloc(m, xpack_bytes(ne), &p))) return rc;
+        m->pk_n = xpack_at(p, ne);
+        if ((rc = dev_alloc(m, xpack_bytes(ne), &p))) return rc;
+        m->pk_f = xpack_at(p, ne);
+        if ((rc = dev_alloc(m, xpack_bytes(nq), &p))) return rc;
+        m->pk_a = xpack_at(p, nq);
+        if ((rc = dev_alloc(m, xpack_bytes(nf), &p))) return rc;
+        m->pk_s = xpack_at(p, nf);
+    }
+    if (hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess) return fail(LRS_E_HIP, "memset");
+    if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
+            hipSuccess ||
+        hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=
+            hipSuccess)
+        return fail(LRS_E_OOM, "pinned host buffers");
+    // LRS_GRAPH=0 replays the same launches directly on the stream instead
+    // (for tools that cannot trace kernels inside graph launches)
+    const char *ge = getenv("LRS_GRAPH");
+    const bool graphs = !(ge && ge[0] == '0');
+    if (graphs &&
+        ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy))))
+        return rc;
+    return LRS_OK;
+}
 
 }  // namespace
 
@@ -417,8 +607,6 @@ int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weight
                                    wbytes(L.attn_output) + wbytes(L.ffn_gate) + wbytes(L.ffn_up) +
                                    wbytes(L.ffn_down);
     }
-    m->gguf_bytes_per_token += wbytes(output);
-    if ((rc = upload_vec(m, output_norm, c.n_embd, &m->output_norm))) return bail(rc);
     // RoPE table freq[i] = base^(-2i/rope_dim), f32 powf (model.rs:339-343)
     std::vector<float> fr(c.rope_dim / 2 + 1, 0.f);
     for (uint32_t i = 0; i < c.rope_dim / 2; i++) {
@@ -426,45 +614,153 @@ int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weight
         ex = ex / (float)c.rope_dim;
         fr[i] = powf(c.freq_base, ex);
     }
-    if ((rc = upload_vec(m, fr.data(), fr.size(), &m->freq))) return bail(rc);
-    m->gen_cap = 1u << 16;
-    m->a_splits = attn_splits(c.n_head_kv);
-    if ((rc = dev_alloc(m, (size_t)c.n_head * m->a_splits * (c.head_dim + 4) * sizeof(float),
-                        (void **)&m->pa)) ||
-        (rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
-        (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->qbuf)) ||
-        (rc = dev_alloc(m, c.vocab * sizeof(float), (void **)&m->logits)) ||
-        (rc = dev_alloc(m, 4 * sizeof(uint32_t), (void **)&m->step)) ||
-        (rc = dev_alloc(m, m->gen_cap * sizeof(uint32_t), (void **)&m->gen)) ||
-        (rc = dev_alloc(m, (size_t)c.vocab * sizeof(unsigned long long), (void **)&m->amax)))
-        return bail(rc);
-    {
-        // activation packs (n_embd, n_ff and n_head*head_dim are multiples of 256)
-        void *p = nullptr;
-        const uint32_t ne = c.n_embd / 32, nq = qd / 32, nf = c.n_ff / 32;
-        if ((rc = dev_alloc(m, xpack_bytes(ne), &p))) return bail(rc);
-        m->pk_n = xpack_at(p, ne);
-        if ((rc = dev_alloc(m, xpack_bytes(ne), &p))) return bail(rc);
-        m->pk_f = xpack_at(p, ne);
-        if ((rc = dev_alloc(m, xpack_bytes(nq), &p))) return bail(rc);
-        m->pk_a = xpack_at(p, nq);
-        if ((rc = dev_alloc(m, xpack_bytes(nf), &p))) return bail(rc);
-        m->pk_s = xpack_at(p, nf);
+    if ((rc = finish_model(m, output_norm, fr, 0))) return bail(rc);
+    *out = m;
+    return LRS_OK;
+}
+
+int lrs_hybrid_create(lrs_ctx *ctx, const lrs_hybrid_config *hcfg, const lrs_hybrid_layer *layers,
+                      const lrs_weight *token_embd, const float *output_norm,
+                      const lrs_weight *output, lrs_model **out) {
+    if (!ctx || !hcfg || !layers || !token_embd || !output_norm || !output || !out)
+        return fail(LRS_E_ARG, "null argument");
+    const lrs_hybrid_config hc = *hcfg;
+    const lrs_config c = hc.base;
+    if (c.n_layer == 0 || c.n_embd == 0 || c.n_head == 0 || c.n_head_kv == 0 || c.vocab == 0 ||
+        c.ctx == 0 || c.n_ff == 0 || hc.full_attn_interval == 0 || hc.dn_k_heads == 0 ||
+        hc.dn_v_heads == 0 || hc.dn_conv == 0)
+        return fail(LRS_E_ARG, "empty dimension in config");
+    if (c.n_head % c.n_head_kv) return fail(LRS_E_ARG, "n_head must be a multiple of n_head_kv");
+    if (hc.dn_v_heads % hc.dn_k_heads)
+        return fail(LRS_E_ARG, "dn_v_heads must be a multiple of dn_k_heads");
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
+        return fail(LRS_E_UNSUPPORTED, "head_dim must be 64, 128 or 256");
+    if (hc.dn_state != 64 && hc.dn_state != 128)
+        return fail(LRS_E_UNSUPPORTED, "dn_state must be 64 or 128");
+    if (hc.dn_conv > 8) return fail(LRS_E_UNSUPPORTED, "dn_conv above 8");
+    if (c.rope_dim > c.head_dim || (c.rope_dim & 1)) return fail(LRS_E_ARG, "bad rope_dim");
+    if (c.n_head / c.n_head_kv > 8) return fail(LRS_E_UNSUPPORTED, "n_head / n_head_kv > 8");
+    const uint32_t qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+    const uint32_t D = hc.dn_state, KD = hc.dn_k_heads * D, VD = hc.dn_v_heads * D;
+    const uint32_t CD = 2 * KD + VD;
+    if (c.n_embd % 256 || c.n_ff % 256 || qd % 256 || VD % 256)
+        return fail(LRS_E_UNSUPPORTED,
+                    "n_embd, n_ff, n_head*head_dim and dn_v_heads*dn_state must be multiples of 256");
+    int rc;
+    uint32_t n_attn = 0, n_dn = 0;
+    for (uint32_t l = 0; l < c.n_layer; l++) {
+        const lrs_hybrid_layer &L = layers[l];
+        const bool full = (l + 1) % hc.full_attn_interval == 0;  // config.rs:25-35
+        if ((rc = check_w(L.ffn_gate, "ffn_gate", c.n_embd, c.n_ff, true)) ||
+            (rc = check_w(L.ffn_up, "ffn_up", c.n_embd, c.n_ff, true)) ||
+            (rc = check_w(L.ffn_down, "ffn_down", c.n_ff, c.n_embd, true)))
+            return rc;
+        if (L.ffn_gate->v.type != L.ffn_up->v.type)
+            return fail(LRS_E_UNSUPPORTED, "ffn_gate and ffn_up must share a type");
+        if (!L.attn_norm || !L.post_norm) return fail(LRS_E_ARG, "missing norm weights");
+        if (L.ffn_down->ctx != ctx) return fail(LRS_E_ARG, "weights belong to another context");
+        if (full) {
+            if ((rc = check_w(L.attn_q, "attn_q", c.n_embd, 2 * qd, true)) ||
+                (rc = check_w(L.attn_k, "attn_k", c.n_embd, kvd, true)) ||
+                (rc = check_w(L.attn_v, "attn_v", c.n_embd, kvd, true)) ||
+                (rc = check_w(L.attn_output, "attn_output", qd, c.n_embd, true)))
+                return rc;
+            if (!L.q_norm || !L.k_norm) return fail(LRS_E_ARG, "missing q_norm / k_norm");
+            n_attn++;
+        } else {
+            if ((rc = check_w(L.ssm_qkv, "ssm_qkv", c.n_embd, CD, true)) ||
+                (rc = check_w(L.ssm_gate, "ssm_gate", c.n_embd, VD, true)) ||
+                (rc = check_w(L.ssm_out, "ssm_out", VD, c.n_embd, true)))
+                return rc;
+            if (!L.ssm_alpha || !L.ssm_beta || !L.ssm_a || !L.ssm_dt || !L.ssm_conv || !L.ssm_norm)
+                return fail(LRS_E_ARG, "missing delta-net vectors");
+            n_dn++;
+        }
     }
-    if (hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess)
-        return bail(fail(LRS_E_HIP, "memset"));
-    if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
-            hipSuccess ||
-        hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=
-            hipSuccess)
-        return bail(fail(LRS_E_OOM, "pinned host buffers"));
-    // LRS_GRAPH=0 replays the same launches directly on the stream instead
-    // (for tools that cannot trace kernels inside graph launches)
-    const char *ge = getenv("LRS_GRAPH");
-    const bool graphs = !(ge && ge[0] == '0');
-    if (graphs &&
-        ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy))))
+    if ((rc = check_w(token_embd, "token_embd", c.n_embd, c.vocab, false))) return rc;
+    if ((rc = check_w(output, "output", c.n_embd, c.vocab, true))) return rc;
+    if (token_embd->v.type == T_Q4_0 || block_elems(token_embd->v.type) < 0)
+        return fail(LRS_E_UNSUPPORTED, "token_embd type");
+
+    LRS_HIP(hipSetDevice(ctx->device));
+    lrs_model *m = new lrs_model();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->hybrid = true;
+    m->hc = hc;
+    m->embd = token_embd;
+    m->output = output;
+    m->layers.resize(c.n_layer);
+    auto bail = [&](int code) {
+        lrs_model_destroy(m);
+        return code;
+    };
+    const size_t kv_layer = (size_t)kvd * c.ctx;
+    const size_t win_f = (size_t)hc.dn_conv * CD, st_f = (size_t)hc.dn_v_heads * D * D;
+    m->rec_bytes = (win_f + st_f) * n_dn * sizeof(float);
+    if ((rc = dev_alloc(m, kv_layer * 2 * n_attn * sizeof(_Float16), (void **)&m->kv)) ||
+        (rc = dev_alloc(m, m->rec_bytes, &m->rec)) ||
+        (rc = dev_alloc(m, 2 * (size_t)qd * sizeof(float), (void **)&m->qg)) ||
+        (rc = dev_alloc(m, kvd * sizeof(float), (void **)&m->kb)) ||
+        (rc = dev_alloc(m, kvd * sizeof(float), (void **)&m->vb)) ||
+        (rc = dev_alloc(m, CD * sizeof(float), (void **)&m->dn_qkv)) ||
+        (rc = dev_alloc(m, VD * sizeof(float), (void **)&m->dn_z)) ||
+        (rc = dev_alloc(m, (size_t)hc.dn_v_heads * (D / 32) * sizeof(float), (void **)&m->dn_part)) ||
+        (rc = dev_alloc(m, hc.dn_v_heads * sizeof(uint32_t), (void **)&m->dn_cnt)))
         return bail(rc);
+    if (hipMemset(m->kv, 0, kv_layer * 2 * n_attn * sizeof(_Float16)) != hipSuccess ||
+        hipMemset(m->rec, 0, m->rec_bytes) != hipSuccess ||
+        hipMemset(m->dn_cnt, 0, hc.dn_v_heads * sizeof(uint32_t)) != hipSuccess)
+        return bail(fail(LRS_E_HIP, "memset"));
+    uint32_t ia = 0, id = 0;
+    for (uint32_t l = 0; l < c.n_layer; l++) {
+        const lrs_hybrid_layer &L = layers[l];
+        DevLayer &D_ = m->layers[l];
+        D_.gate = L.ffn_gate;
+        D_.up = L.ffn_up;
+        D_.down = L.ffn_down;
+        if ((rc = upload_vec(m, L.attn_norm, c.n_embd, &D_.attn_norm)) ||
+            (rc = upload_vec(m, L.post_norm, c.n_embd, &D_.ffn_norm)))
+            return bail(rc);
+        m->gguf_bytes_per_token += wbytes(L.ffn_gate) + wbytes(L.ffn_up) + wbytes(L.ffn_down);
+        if ((l + 1) % hc.full_attn_interval == 0) {
+            D_.q = L.attn_q;
+            D_.k = L.attn_k;
+            D_.v = L.attn_v;
+            D_.o = L.attn_output;
+            D_.kc = m->kv + kv_layer * 2 * ia++;
+            D_.vc = D_.kc + kv_layer;
+            if ((rc = upload_vec(m, L.q_norm, c.head_dim, &D_.q_norm)) ||
+                (rc = upload_vec(m, L.k_norm, c.head_dim, &D_.k_norm)))
+                return bail(rc);
+            m->gguf_bytes_per_token += wbytes(L.attn_q) + wbytes(L.attn_k) + wbytes(L.attn_v) +
+                                       wbytes(L.attn_output);
+        } else {
+            D_.dn = true;
+            D_.ssm_qkv = L.ssm_qkv;
+            D_.ssm_gate = L.ssm_gate;
+            D_.ssm_out = L.ssm_out;
+            float *r0 = reinterpret_cast<float *>(m->rec) + (win_f + st_f) * id++;
+            D_.win = r0;
+            D_.state = r0 + win_f;
+            if ((rc = upload_vec(m, L.ssm_alpha, (size_t)hc.dn_v_heads * c.n_embd, &D_.alpha)) ||
+                (rc = upload_vec(m, L.ssm_beta, (size_t)hc.dn_v_heads * c.n_embd, &D_.beta)) ||
+                (rc = upload_vec(m, L.ssm_a, hc.dn_v_heads, &D_.ssm_a)) ||
+                (rc = upload_vec(m, L.ssm_dt, hc.dn_v_heads, &D_.ssm_dt)) ||
+                (rc = upload_vec(m, L.ssm_conv, (size_t)CD * hc.dn_conv, &D_.conv)) ||
+                (rc = upload_vec(m, L.ssm_norm, D, &D_.ssm_norm)))
+                return bail(rc);
+            m->gguf_bytes_per_token += wbytes(L.ssm_qkv) + wbytes(L.ssm_gate) + wbytes(L.ssm_out) +
+                                       2 * (size_t)hc.dn_v_heads * c.n_embd * sizeof(float);
+        }
+    }
+    // freq[i] = 1 / base^(2i/rope_dim) (gpu.rs:540-547)
+    std::vector<float> fr(c.rope_dim / 2 + 1, 0.f);
+    for (uint32_t i = 0; i < c.rope_dim / 2; i++) {
+        const float ex = (float)(2 * i) / (float)c.rope_dim;
+        fr[i] = 1.0f / powf(c.freq_base, ex);
+    }
+    if ((rc = finish_model(m, output_norm, fr, VD))) return bail(rc);
     *out = m;
     return LRS_OK;
 }
@@ -479,6 +775,16 @@ void lrs_model_destroy(lrs_model *m) {
     if (m->step_host) (void)hipHostFree(m->step_host);
     if (m->logits_host) (void)hipHostFree(m->logits_host);
     delete m;
+}
+
+// a hybrid model's recurrent state only moves forward: pos0 must be the
+// current length
+static int check_continue(lrs_model *m, uint32_t pos0) {
+    if (m->hybrid && pos0 != m->len)
+        return fail(LRS_E_ARG, "hybrid model: position " + std::to_string(pos0) +
+                                   " must continue the sequence at " + std::to_string(m->len) +
+                                   " (the recurrent state cannot be rewound; reset first)");
+    return LRS_OK;
 }
 
 static int check_step(lrs_model *m, uint32_t token, uint32_t pos) {
@@ -500,6 +806,7 @@ static bool prefill_capable(const lrs_model *m) {
         return (w->v.type == T_Q4_K || w->v.type == T_Q6_K) && w->v.n_in % 64 == 0;
     };
     const lrs_config &c = m->cfg;
+    if (m->hybrid) return false;  // the recurrence runs token by token
     if ((c.head_dim != 64 && c.head_dim != 128) || c.n_head / c.n_head_kv > 8 || c.n_embd % 4)
         return false;
     for (const DevLayer &L : m->layers)
@@ -610,7 +917,7 @@ static int enqueue_tokens(lrs_model *m, const uint32_t *tokens, uint32_t n, uint
 int lrs_decode(lrs_model *m, uint32_t token, uint32_t pos, float *logits) {
     if (!m || !logits) return fail(LRS_E_ARG, "null argument");
     int rc = check_step(m, token, pos);
-    if (rc) return rc;
+    if (rc || (rc = check_continue(m, pos))) return rc;
     LRS_HIP(hipSetDevice(m->ctx->device));
     hipStream_t s = m->ctx->stream;
     m->step_host[0] = token;
@@ -636,7 +943,8 @@ int lrs_decode_batch(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t 
     // GpuResidentDecode::decode_batch (gpu.rs:392-400): the logits of the last
     // token; several tokens go through the matrix-core GEMMs in blocks when
     // every weight has one, else token by token
-    int rc;
+    int rc = check_continue(m, pos0);
+    if (rc) return rc;
     if (n > 1 && prefill_capable(m)) {
         for (uint32_t i = 0; i < n; i++)
             if ((rc = check_step(m, tokens[i], pos0 + i))) return rc;
@@ -656,7 +964,15 @@ int lrs_decode_batch(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t 
 }
 
 void lrs_reset(lrs_model *m) {
-    if (m) m->len = 0;
+    if (!m) return;
+    m->len = 0;
+    if (m->rec) {
+        // delta-net states and conv windows back to zero (the KV cache needs
+        // no clearing: attention reads positions 0..pos only)
+        (void)hipSetDevice(m->ctx->device);
+        (void)hipMemsetAsync(m->rec, 0, m->rec_bytes, m->ctx->stream);
+        (void)hipStreamSynchronize(m->ctx->stream);
+    }
 }
 
 uint32_t lrs_model_len(const lrs_model *m) { return m ? m->len : 0; }
@@ -664,7 +980,7 @@ uint32_t lrs_model_len(const lrs_model *m) { return m ? m->len : 0; }
 int lrs_decode_greedy(lrs_model *m, uint32_t token, uint32_t pos, uint32_t *next) {
     if (!m || !next) return fail(LRS_E_ARG, "null argument");
     int rc = check_step(m, token, pos);
-    if (rc) return rc;
+    if (rc || (rc = check_continue(m, pos))) return rc;
     LRS_HIP(hipSetDevice(m->ctx->device));
     hipStream_t s = m->ctx->stream;
     m->step_host[0] = token;
@@ -689,6 +1005,7 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
     if (n_gen > m->gen_cap) return fail(LRS_E_ARG, "too many tokens for one call");
     for (uint32_t i = 0; i < n_prompt; i++)
         if (prompt[i] >= m->cfg.vocab) return fail(LRS_E_ARG, "prompt token outside the vocabulary");
+    if (int rc0 = check_continue(m, pos0)) return rc0;
     LRS_HIP(hipSetDevice(m->ctx->device));
     hipStream_t s = m->ctx->stream;
     // prefill: tokens 0..n_prompt-2, then the last prompt token starts the
@@ -714,7 +1031,17 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
 int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, size_t *bytes) {
     if (!m || !avg_us || iters == 0) return fail(LRS_E_ARG, "null argument");
     const lrs_config &c = m->cfg;
-    if (op > LRS_OP_HEAD) return fail(LRS_E_ARG, "unknown op");
+    if (op > LRS_OP_QK_PREP) return fail(LRS_E_ARG, "unknown op");
+    const bool dn_op = op == LRS_OP_DN_PROJ || op == LRS_OP_DN_STEP || op == LRS_OP_DN_OUT;
+    const bool attn_op = op == LRS_OP_QKV || op == LRS_OP_ATTN || op == LRS_OP_O ||
+                         op == LRS_OP_QK_PREP;
+    if ((dn_op || op == LRS_OP_QK_PREP) && !m->hybrid)
+        return fail(LRS_E_ARG, "op needs a hybrid model");
+    // the layers the op runs on (all, or those of its mixer kind)
+    std::vector<uint32_t> ls;
+    for (uint32_t l = 0; l < c.n_layer; l++)
+        if ((!dn_op && !attn_op) || (dn_op == m->layers[l].dn)) ls.push_back(l);
+    if (ls.empty()) return fail(LRS_E_ARG, "no layer of this kind");
     LRS_HIP(hipSetDevice(m->ctx->device));
     hipStream_t s = m->ctx->stream;
     const bool per_layer = op != LRS_OP_HEAD;
@@ -724,13 +1051,29 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
     // algorithmic bytes: GGUF weight bytes + f16 K/V + f32 vectors read or
     // written once (scratch such as attention partials is not counted)
     const size_t E4 = (size_t)c.n_embd * 4, qd4 = (size_t)c.n_head * c.head_dim * 4;
+    const lrs_hybrid_config &hc = m->hc;
+    const size_t dnD = hc.dn_state, VD4 = (size_t)hc.dn_v_heads * dnD * 4,
+                 CD4 = (size_t)(2 * hc.dn_k_heads + hc.dn_v_heads) * dnD * 4;
     if (per_layer) {
-        const DevLayer &D = m->layers[0];
+        const DevLayer &D = m->layers[ls[0]];
         switch (op) {
         case LRS_OP_QKV:
-            b = wbytes(D.q) + wbytes(D.k) + wbytes(D.v) + 2 * E4 + qd4 + (size_t)kvd * 2 * 2 +
-                (D.bq ? qd4 + (size_t)kvd * 8 : 0);
+            if (m->hybrid)  // Q (query + gate) / k / v rows out as f32
+                b = wbytes(D.q) + wbytes(D.k) + wbytes(D.v) + 2 * E4 + 2 * qd4 + (size_t)kvd * 8;
+            else
+                b = wbytes(D.q) + wbytes(D.k) + wbytes(D.v) + 2 * E4 + qd4 + (size_t)kvd * 2 * 2 +
+                    (D.bq ? qd4 + (size_t)kvd * 8 : 0);
             break;
+        case LRS_OP_QK_PREP: b = 2 * qd4 + (size_t)kvd * 8 + qd4 + (size_t)kvd * 4; break;
+        case LRS_OP_DN_PROJ: b = wbytes(D.ssm_qkv) + wbytes(D.ssm_gate) + 2 * E4 + CD4 + VD4; break;
+        case LRS_OP_DN_STEP:
+            // state read + written, f32 gate rows, conv weights and window,
+            // inputs, the y pack (3.5 B per element)
+            b = 2 * (size_t)hc.dn_v_heads * dnD * dnD * 4 +
+                2 * (size_t)hc.dn_v_heads * E4 + CD4 * hc.dn_conv + CD4 * hc.dn_conv + CD4 +
+                VD4 + 2 * E4 + VD4 / 4 * 7 / 2;
+            break;
+        case LRS_OP_DN_OUT: b = wbytes(D.ssm_out) + VD4 + 2 * E4; break;
         case LRS_OP_ATTN: b = (size_t)L * kvd * 2 * sizeof(_Float16) + 2 * qd4; break;
         case LRS_OP_O: b = wbytes(D.o) + qd4 + 2 * E4; break;
         case LRS_OP_GATEUP: b = wbytes(D.gate) + wbytes(D.up) + 2 * E4 + (size_t)c.n_ff * 4; break;
@@ -745,17 +1088,20 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
     m->step_host[2] = 0;
     LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     auto one = [&](uint32_t i) -> hipError_t {
-        const uint32_t l = i % c.n_layer;
+        const uint32_t l = ls[i % ls.size()];
         switch (op) {
-        case LRS_OP_QKV: return op_qkv(m, l);
+        case LRS_OP_QKV: return m->hybrid ? op_hattn_proj(m, l) : op_qkv(m, l);
         case LRS_OP_ATTN: return op_attn(m, l);
-        case LRS_OP_O: return op_o(m, l);
+        case LRS_OP_O: case LRS_OP_DN_OUT: return op_o(m, l);
         case LRS_OP_GATEUP: return op_gateup(m, l);
         case LRS_OP_DOWN: return op_down(m, l);
+        case LRS_OP_QK_PREP: return op_qk_prep(m, l);
+        case LRS_OP_DN_PROJ: return op_dn_proj(m, l);
+        case LRS_OP_DN_STEP: return op_dn_step(m, l);
         default: return op_head(m, false);
         }
     };
-    for (uint32_t i = 0; i < c.n_layer && i < iters; i++) LRS_HIP(one(i));  // warm
+    for (uint32_t i = 0; i < ls.size() && i < iters; i++) LRS_HIP(one(i));  // warm
     LRS_HIP(hipEventRecord(m->ctx->ev0, s));
     for (uint32_t i = 0; i < iters; i++) LRS_HIP(one(i));
     LRS_HIP(hipEventRecord(m->ctx->ev1, s));

@@ -522,7 +522,8 @@ static MqFn pick_types(uint32_t t0, uint32_t t1, const MqGeom &g) {
         default: return nullptr;
         }
     }
-    if (EPI == MQ_QKV && t0 == T_Q4_K && t1 == T_Q6_K) return pick<T_Q4_K, T_Q6_K, EPI>(g);
+    if ((EPI == MQ_QKV || EPI == MQ_STORE) && t0 == T_Q4_K && t1 == T_Q6_K)
+        return pick<T_Q4_K, T_Q6_K, EPI>(g);
     return nullptr;
 }
 

@@ -32,10 +32,32 @@ class LrsLayer(C.Structure):
                  "attn_norm", "ffn_norm", "bq", "bk", "bv")]
 
 
+class LrsHybridConfig(C.Structure):
+    _fields_ = [("base", LrsConfig)] + [(n, C.c_uint32) for n in
+                                        ("full_attn_interval", "dn_k_heads", "dn_v_heads",
+                                         "dn_state", "dn_conv")]
+
+
+HYBRID_WEIGHTS = ("ffn_gate", "ffn_up", "ffn_down")
+HYBRID_LAYER_FIELDS = (("ffn_gate", "w"), ("ffn_up", "w"), ("ffn_down", "w"),
+                       ("attn_norm", "f"), ("post_norm", "f"),
+                       ("attn_q", "w"), ("attn_k", "w"), ("attn_v", "w"), ("attn_output", "w"),
+                       ("q_norm", "f"), ("k_norm", "f"),
+                       ("ssm_qkv", "w"), ("ssm_gate", "w"), ("ssm_out", "w"),
+                       ("ssm_alpha", "f"), ("ssm_beta", "f"), ("ssm_a", "f"), ("ssm_dt", "f"),
+                       ("ssm_conv", "f"), ("ssm_norm", "f"))
+
+
+class LrsHybridLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n, _ in HYBRID_LAYER_FIELDS]
+
+
 def _bind():
     vp = C.c_void_p
     sig = {
         "lrs_model_create": (C.c_int, [vp, C.POINTER(LrsConfig), vp, vp, vp, vp, C.POINTER(vp)]),
+        "lrs_hybrid_create": (C.c_int, [vp, C.POINTER(LrsHybridConfig), vp, vp, vp, vp,
+                                        C.POINTER(vp)]),
         "lrs_model_destroy": (None, [vp]),
         "lrs_decode": (C.c_int, [vp, C.c_uint32, C.c_uint32, vp]),
         "lrs_decode_batch": (C.c_int, [vp, vp, C.c_uint32, C.c_uint32, vp]),
@@ -130,7 +152,8 @@ class ResidentForward:
                                       out.ctypes.data))
         return out
 
-    OPS = {"qkv": 0, "attn": 1, "o": 2, "gateup": 3, "down": 4, "head": 5}
+    OPS = {"qkv": 0, "attn": 1, "o": 2, "gateup": 3, "down": 4, "head": 5,
+           "dn_proj": 6, "dn_step": 7, "dn_out": 8, "qk_prep": 9}
 
     def profile(self, op: str, iters: int):
         """(mean us per launch, bytes per launch) of one fused op, outside the graph."""
@@ -152,6 +175,46 @@ class ResidentForward:
             self.close()
         except Exception:
             pass
+
+
+def _wh(w):
+    return w.h.value if isinstance(w.h, C.c_void_p) else w.h
+
+
+class HybridForward(ResidentForward):
+    """Hybrid (qwen35) model: gated full attention every
+    ``full_attn_interval``-th layer, gated delta net elsewhere.  Same decode
+    interface; positions must continue the sequence (the recurrent state
+    cannot be rewound) and ``reset()`` clears it."""
+
+    def __init__(self, ctx: Context, cfg: dict, layers: list, token_embd: Weight,
+                 output_norm, output: Weight):
+        self.ctx, self.cfg = ctx, dict(cfg)
+        base = LrsConfig(*[cfg[k] for k in CONFIG_KEYS])
+        c = LrsHybridConfig(base, cfg["full_attn_interval"], cfg["dn_k_heads"],
+                            cfg["dn_v_heads"], cfg["dn_state"], cfg["dn_conv"])
+        self._keep = [token_embd, output]
+        arr = (LrsHybridLayer * cfg["n_layer"])()
+        for i, L in enumerate(layers):
+            for name, kind in HYBRID_LAYER_FIELDS:
+                v = L.get(name)
+                if v is None:
+                    continue
+                if kind == "w":
+                    self._keep.append(v)
+                    setattr(arr[i], name, _wh(v))
+                else:
+                    a = _f32(v)
+                    self._keep.append(a)
+                    setattr(arr[i], name, a.ctypes.data)
+        onorm = _f32(output_norm)
+        self._keep.append(onorm)
+        h = C.c_void_p()
+        check(lib.lrs_hybrid_create(ctx.h, C.byref(c), C.cast(arr, C.c_void_p), _wh(token_embd),
+                                    onorm.ctypes.data, _wh(output), C.byref(h)))
+        self.h = h
+        self.vocab = cfg["vocab"]
+        ctx._models.add(self)
 
 
 # ---------------------------------------------------------------------------
@@ -201,5 +264,65 @@ def synthetic_model(ctx: Context, cfg: dict, seed: int = 1, mix: dict | None = N
     return ResidentForward(ctx, cfg, layers, emb, onorm, out)
 
 
-__all__ = ["ResidentForward", "synthetic_model", "QWEN25_32B", "Q4_K_M_MIX", "layer_shapes",
-           "ModelError"]
+# config 4: 27B-scale hybrid: 64 layers, full attention every 4th (24 q / 4 kv
+# x 256, partial RoPE of 64 dims), 48 delta-net layers of 16 heads x 128
+QWEN35_27B = dict(n_layer=64, n_embd=5120, n_head=24, n_head_kv=4, head_dim=256, n_ff=17408,
+                  vocab=248320, rope_dim=64, ctx=4096, rms_eps=1e-6, freq_base=1e7,
+                  full_attn_interval=4, dn_k_heads=16, dn_v_heads=16, dn_state=128, dn_conv=4)
+HYBRID_MIX = dict(Q4_K_M_MIX, ssm_qkv=Q4_K, ssm_gate=Q4_K, ssm_out=Q4_K)
+
+
+def hybrid_layer_shapes(cfg, l):
+    """(n_in, n_out) of the quantized matrices of hybrid layer l."""
+    E, ff = cfg["n_embd"], cfg["n_ff"]
+    sh = dict(ffn_gate=(E, ff), ffn_up=(E, ff), ffn_down=(ff, E))
+    if (l + 1) % cfg["full_attn_interval"] == 0:
+        qd, kvd = cfg["n_head"] * cfg["head_dim"], cfg["n_head_kv"] * cfg["head_dim"]
+        sh.update(attn_q=(E, 2 * qd), attn_k=(E, kvd), attn_v=(E, kvd), attn_output=(qd, E))
+    else:
+        vd = cfg["dn_v_heads"] * cfg["dn_state"]
+        cd = (2 * cfg["dn_k_heads"] + cfg["dn_v_heads"]) * cfg["dn_state"]
+        sh.update(ssm_qkv=(E, cd), ssm_gate=(E, vd), ssm_out=(vd, E))
+    return sh
+
+
+def synthetic_hybrid_model(ctx: Context, cfg: dict, seed: int = 1, mix: dict | None = None,
+                           mode: int = 0, d_lo: float = 1e-3, d_hi: float = 1e-2):
+    """Random-init hybrid model with weights generated on the GPU; f32 vectors
+    drawn like the test models (norms ~U[0.9, 1.1], gate rows ~U[+-1.7/sqrt(E)],
+    ssm_a ~U[-1, -0.1], dt ~U[-1, 1], conv taps ~U[-0.5, 0.5])."""
+    mix = dict(HYBRID_MIX, **(mix or {}))
+    rng = np.random.default_rng(seed)
+    E = cfg["n_embd"]
+    layers = []
+    for l in range(cfg["n_layer"]):
+        L = {}
+        for i, (name, (n_in, n_out)) in enumerate(sorted(hybrid_layer_shapes(cfg, l).items())):
+            L[name] = Weight.generate(ctx, mix[name], seed * 1000003 + l * 64 + i, n_in, n_out,
+                                      mode=mode, d_lo=d_lo, d_hi=d_hi)
+        L["attn_norm"] = rng.uniform(0.9, 1.1, E).astype(np.float32)
+        L["post_norm"] = rng.uniform(0.9, 1.1, E).astype(np.float32)
+        if (l + 1) % cfg["full_attn_interval"] == 0:
+            L["q_norm"] = rng.uniform(0.9, 1.1, cfg["head_dim"]).astype(np.float32)
+            L["k_norm"] = rng.uniform(0.9, 1.1, cfg["head_dim"]).astype(np.float32)
+        else:
+            nv, r = cfg["dn_v_heads"], 1.7 / np.sqrt(E)
+            cd = (2 * cfg["dn_k_heads"] + nv) * cfg["dn_state"]
+            L["ssm_alpha"] = rng.uniform(-r, r, nv * E).astype(np.float32)
+            L["ssm_beta"] = rng.uniform(-r, r, nv * E).astype(np.float32)
+            L["ssm_a"] = rng.uniform(-1.0, -0.1, nv).astype(np.float32)
+            L["ssm_dt"] = rng.uniform(-1.0, 1.0, nv).astype(np.float32)
+            L["ssm_conv"] = rng.uniform(-0.5, 0.5, cd * cfg["dn_conv"]).astype(np.float32)
+            L["ssm_norm"] = rng.uniform(0.9, 1.1, cfg["dn_state"]).astype(np.float32)
+        layers.append(L)
+    emb = Weight.generate(ctx, mix["token_embd"], seed * 7 + 1, E, cfg["vocab"],
+                          mode=mode, d_lo=d_lo, d_hi=d_hi)
+    out = Weight.generate(ctx, mix["output"], seed * 7 + 2, E, cfg["vocab"],
+                          mode=mode, d_lo=d_lo, d_hi=d_hi)
+    onorm = rng.uniform(0.9, 1.1, E).astype(np.float32)
+    return HybridForward(ctx, cfg, layers, emb, onorm, out)
+
+
+__all__ = ["ResidentForward", "HybridForward", "synthetic_model", "synthetic_hybrid_model",
+           "QWEN25_32B", "QWEN35_27B", "Q4_K_M_MIX", "HYBRID_MIX", "layer_shapes",
+           "hybrid_layer_shapes", "ModelError"]

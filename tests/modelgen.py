@@ -153,3 +153,23 @@ def hybrid_host_model(orc, cfg, seed=1, mix=None, mode=1, d_lo=2e-4, d_hi=2e-3):
                                                   cfg["n_embd"], mode=mode, d_lo=d_lo, d_hi=d_hi))
     w["output_norm"] = (F32, orc.gen_uniform(seed * 5 + 3, cfg["n_embd"], 0.9, 1.1))
     return w
+
+
+def gpu_hybrid_model(lrs, ctx, cfg, w):
+    """Uploads a host hybrid model through the C ABI."""
+    from llama_rs_amd.model import HybridForward
+
+    layers = []
+    for l in range(cfg["n_layer"]):
+        L = {}
+        for name, (n_in, n_out) in hybrid_shapes(cfg, l).items():
+            t, arr = w[f"blk.{l}.{name}"]
+            L[name] = lrs.Weight.upload(ctx, t, arr, n_in, n_out)
+        for name in hybrid_f32_shapes(cfg, l):
+            L[name] = w[f"blk.{l}.{name}"][1]
+        layers.append(L)
+    te, ta = w["token_embd"]
+    emb = lrs.Weight.upload(ctx, te, ta, cfg["n_embd"], cfg["vocab"])
+    ot, oa = w["output"]
+    out = lrs.Weight.upload(ctx, ot, oa, cfg["n_embd"], cfg["vocab"])
+    return HybridForward(ctx, cfg, layers, emb, w["output_norm"][1], out)
