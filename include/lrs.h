@@ -128,7 +128,7 @@ int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y
 
 /* Matvec launch shape override: tiles of 16 rows per wavefront, tile groups
  * per workgroup, K-slices per workgroup; one of the instantiated shapes
- * (1,1,4) (1,2,4) (1,2,2) (2,4,2) (1,2,6), or all 0 = automatic.
+ * (1,1,4) (1,2,4) (1,2,2) (2,4,2) (2,2,4) (1,2,6), or all 0 = automatic.
  * Replaces the LLAMA_RS_MATVEC_GEOM knob (resident_forward.rs:164-176). */
 int lrs_matvec_set_geom(int tiles_per_wave, int tile_groups, int k_slices);
 

@@ -294,7 +294,7 @@ class GpuMatmul:
 
 # launch shapes of the plain matvec (tiles per wavefront, tile groups and
 # K-slices per workgroup) that the library instantiates
-MATVEC_GEOMS = [(1, 1, 4), (1, 2, 4), (1, 2, 2), (2, 4, 2), (1, 2, 6)]
+MATVEC_GEOMS = [(1, 1, 4), (1, 2, 4), (1, 2, 2), (2, 4, 2), (2, 2, 4), (1, 2, 6)]
 
 
 def set_matvec_geom(tiles_per_wave: int = 0, tile_groups: int = 0, k_slices: int = 0) -> None:

@@ -18,13 +18,14 @@
 // The rows of a head are independent in the rule, so a head is split over
 // D/32 workgroups of 32 rows (one pack block each): the state streams from
 // 4 x more CUs than one workgroup per head would use.  Each workgroup
-// recomputes the head's gates, q and k (a few KB, L2-resident) and packs its
-// 32 y values without the head's RMS factor; the workgroup that finishes the
-// head last (an arrival counter, no waiting) sums the partial sums of squares
-// and multiplies the factor into the pack scales of the head's blocks (the
-// pack is linear in its scale and block sums).  The conv inputs live in a ring
-// of W slots indexed by position, so the slot being written (pos % W) is never
-// one being read: workgroups that share a key head need no ordering.
+// recomputes the head's gates, q and k (a few KB, L2-resident), packs its 32
+// y values without the head's RMS factor and leaves its share of sum(o^2);
+// the consumer (the ssm_out matvec) sums the shares of each head and scales
+// the pack's block scales by the factor while it stages the pack (the pack is
+// linear in its scale and block sums), so no workgroup waits for another.
+// The conv inputs live in a ring of W slots indexed by position, so the slot
+// being written (pos % W) is never one being read: workgroups that share a
+// key head need no ordering.
 #include "lrs_internal.h"
 #include "pack_dev.h"
 
@@ -48,11 +49,6 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ float ld_coherent(const float *p) {
-    return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t *>(const_cast<float *>(p)), __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT));
-}
-
 template <int D>
 __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
     constexpr uint32_t R = D / 32;    // workgroups per head (32 rows each)
@@ -65,7 +61,6 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
     const uint32_t KD = a.k_heads * D, CD = 2 * KD + a.v_heads * D;
     __shared__ __attribute__((aligned(16))) float sq[D], sk[D];
     __shared__ float sv[32], so[32], red[3][4], gb[2];
-    __shared__ uint32_t last;
 
     // state row j in flight first: lane lam holds pieces 8c + lam
     float4 st[PPL];
@@ -73,19 +68,32 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
 #pragma unroll
     for (int c = 0; c < PPL; c++) st[c] = srow[8 * c + lam];
 
-    // gate projections of hn = rmsnorm(x) * attn_norm (dn_gates.comp)
+    // gate projections of hn = rmsnorm(x) * attn_norm (dn_gates.comp): every
+    // load of a thread's elements is issued before the first product
     {
-        float ss = 0.f, pa = 0.f, pb = 0.f;
+        constexpr int GI = 8;  // float4 per thread per row: n_embd <= 8192
         const float *al = a.alpha + (size_t)hh * a.n_embd, *be = a.beta + (size_t)hh * a.n_embd;
-        for (uint32_t i = 4 * tid; i < a.n_embd; i += 1024) {
-            const float4 xv = *reinterpret_cast<const float4 *>(a.x + i);
-            const float4 wv = *reinterpret_cast<const float4 *>(a.attn_norm + i);
-            const float4 av = *reinterpret_cast<const float4 *>(al + i);
-            const float4 bv = *reinterpret_cast<const float4 *>(be + i);
-            ss += (xv.x * xv.x + xv.y * xv.y) + (xv.z * xv.z + xv.w * xv.w);
-            const float h0 = xv.x * wv.x, h1 = xv.y * wv.y, h2 = xv.z * wv.z, h3 = xv.w * wv.w;
-            pa += (av.x * h0 + av.y * h1) + (av.z * h2 + av.w * h3);
-            pb += (bv.x * h0 + bv.y * h1) + (bv.z * h2 + bv.w * h3);
+        float4 xv[GI], wv[GI], av[GI], bv[GI];
+#pragma unroll
+        for (int g = 0; g < GI; g++) {
+            const uint32_t i = 4 * tid + 1024 * g;
+            if (i < a.n_embd) {
+                xv[g] = *reinterpret_cast<const float4 *>(a.x + i);
+                wv[g] = *reinterpret_cast<const float4 *>(a.attn_norm + i);
+                av[g] = *reinterpret_cast<const float4 *>(al + i);
+                bv[g] = *reinterpret_cast<const float4 *>(be + i);
+            }
+        }
+        float ss = 0.f, pa = 0.f, pb = 0.f;
+#pragma unroll
+        for (int g = 0; g < GI; g++) {
+            if (4 * tid + 1024 * g < a.n_embd) {
+                const float4 xq = xv[g], wq = wv[g], aq = av[g], bq = bv[g];
+                ss += (xq.x * xq.x + xq.y * xq.y) + (xq.z * xq.z + xq.w * xq.w);
+                const float h0 = xq.x * wq.x, h1 = xq.y * wq.y, h2 = xq.z * wq.z, h3 = xq.w * wq.w;
+                pa += (aq.x * h0 + aq.y * h1) + (aq.z * h2 + aq.w * h3);
+                pb += (bq.x * h0 + bq.y * h1) + (bq.z * h2 + bq.w * h3);
+            }
         }
         ss = wave_sum(ss);
         pa = wave_sum(pa);
@@ -99,25 +107,50 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
 
     // causal conv + SiLU of q, k (key head kh) and this workgroup's v rows
     // (dn_conv.comp); the current input goes to ring slot pos % W, written
-    // once per channel: q/k by workgroup 0 of value head kh, v by its owner
+    // once per channel: q/k by workgroup 0 of value head kh, v by its owner.
+    // Two channels per thread (2D + 32 <= 512), all loads issued first.
     const uint32_t pos = a.step[1];
     const uint32_t W = a.d_conv, wslot = pos % W;
     const bool own_qk = r == 0 && hh < a.k_heads;
-    for (uint32_t c = tid; c < 2 * D + 32; c += 256) {
-        const uint32_t ch = c < D ? kh * D + c
-                            : c < 2 * D ? KD + kh * D + (c - D)
-                                        : 2 * KD + hh * D + 32 * r + (c - 2 * D);
-        const float xc = a.qkv[ch];
-        const float *w = a.conv_w + (size_t)ch * W;
-        float acc = 0.f;
-        for (uint32_t t = 0; t + 1 < W; t++)
-            acc += a.win[(size_t)((pos + 1 + t) % W) * CD + ch] * w[t];
-        acc += xc * w[W - 1];
-        const float v = acc / (1.0f + expf(-acc));
-        if (c < D) sq[c] = v;
-        else if (c < 2 * D) sk[c - D] = v;
-        else sv[c - 2 * D] = v;
-        if (c >= 2 * D || own_qk) a.win[(size_t)wslot * CD + ch] = xc;
+    {
+        constexpr int WM = 8;  // d_conv <= 8
+        float xc[2], wt[2][WM], wn[2][WM];
+        uint32_t chs[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint32_t c = tid + 256 * u;
+            const uint32_t ch = c < D ? kh * D + c
+                                : c < 2 * D ? KD + kh * D + (c - D)
+                                            : 2 * KD + hh * D + 32 * r + (c - 2 * D);
+            chs[u] = ch;
+            if (c < 2 * D + 32) {
+                xc[u] = a.qkv[ch];
+#pragma unroll
+                for (int t = 0; t < WM; t++) {
+                    if ((uint32_t)t < W) wt[u][t] = a.conv_w[(size_t)ch * W + t];
+                    if ((uint32_t)t + 1 < W) wn[u][t] = a.win[(size_t)((pos + 1 + t) % W) * CD + ch];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint32_t c = tid + 256 * u;
+            if (c >= 2 * D + 32) continue;
+            float acc = 0.f;
+#pragma unroll
+            for (int t = 0; t < WM; t++)
+                if ((uint32_t)t + 1 < W) acc += wn[u][t] * wt[u][t];
+            float wl = wt[u][0];
+#pragma unroll
+            for (int t = 1; t < WM; t++)
+                if ((uint32_t)t == W - 1) wl = wt[u][t];
+            acc += xc[u] * wl;
+            const float v = acc / (1.0f + expf(-acc));
+            if (c < D) sq[c] = v;
+            else if (c < 2 * D) sk[c - D] = v;
+            else sv[c - 2 * D] = v;
+            if (c >= 2 * D || own_qk) a.win[(size_t)wslot * CD + chs[u]] = xc[u];
+        }
     }
     __syncthreads();
 
@@ -200,27 +233,11 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
         for (int off = 16; off >= 1; off >>= 1) p += __shfl_xor(p, off, 64);
         if (tid == 0) a.part[hh * R + r] = p;
     }
-    // the last workgroup of the head to arrive applies 1/sqrt(mean(o^2) + eps)
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = atomicAdd(&a.cnt[hh], 1u) == R - 1;
-    __syncthreads();
-    if (!last || wave != 0) return;
-    __threadfence();
-    float p = lane < R ? ld_coherent(a.part + hh * R + lane) : 0.f;
-    p = wave_sum(p);
-    const float f = 1.0f / sqrtf(p / (float)D + a.eps);
-    if (lane < R) {
-        float *m = a.out.meta + 4 * ((size_t)hh * R + lane);
-        const float m0 = ld_coherent(m), m1 = ld_coherent(m + 1), m2 = ld_coherent(m + 2),
-                    m3 = ld_coherent(m + 3);
-        *reinterpret_cast<float4 *>(m) = make_float4(m0 * f, m1 * f, m2 * f, m3 * f);
-    }
-    if (lane == 0) __hip_atomic_store(&a.cnt[hh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 hipError_t launch_dn_step(const DnArgs &a, uint32_t d_state, hipStream_t s) {
-    if (a.k_heads == 0 || a.v_heads % a.k_heads || a.d_conv == 0 || a.n_embd % 4)
+    if (a.k_heads == 0 || a.v_heads % a.k_heads || a.d_conv == 0 || a.d_conv > 8 ||
+        a.n_embd % 4 || a.n_embd > 8192)
         return hipErrorInvalidValue;
     switch (d_state) {
     case 64: hipLaunchKernelGGL(k_dn_step<64>, dim3(2, a.v_heads), dim3(256), 0, s, a); break;

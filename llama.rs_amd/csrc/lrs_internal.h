@@ -126,8 +126,7 @@ struct DnArgs {
     float *state;               // [v_heads][D][D]
     const float *norm_w;        // [D]
     float *part;                // [v_heads][D/32] partial sums of squares of o
-    uint32_t *cnt;              // [v_heads] arrival counters, zero between launches
-    XPack out;                  // pack of y [v_heads * D]
+    XPack out;                  // pack of y [v_heads * D] without the head's RMS factor
     const uint32_t *step;       // {token, pos}
     uint32_t n_embd, k_heads, v_heads, d_conv;
     float eps;

@@ -107,14 +107,13 @@ struct lrs_model {
     size_t gguf_bytes_per_token = 0;
     std::vector<void *> allocs;
     // hybrid (qwen35) model: config and per-token buffers: Q rows (query +
-    // gate per head), k, v, conv input, output gate, partial sums of squares
-    // and arrival counters of the delta-net step; recurrent memory (rings +
+    // gate per head), k, v, conv input, output gate, per-32-row sums of
+    // squares of the delta-net output; recurrent memory (rings +
     // states of every delta-net layer) cleared by reset
     bool hybrid = false;
     lrs_hybrid_config hc = {};
     float *qg = nullptr, *kb = nullptr, *vb = nullptr, *dn_qkv = nullptr, *dn_z = nullptr,
           *dn_part = nullptr;
-    uint32_t *dn_cnt = nullptr;
     void *rec = nullptr;
     size_t rec_bytes = 0;
 };
@@ -162,9 +161,19 @@ MqSeg mseg(const lrs_weight *w, uint32_t rows) {
 // launch shapes of the decode ops (16-row tiles; see mq.hip)
 constexpr MqGeom G_QKV = {1, 1, 4, 3};    // 448 workgroups of 4 K-slices (32B shape)
 constexpr MqGeom G_O = {1, 2, 4, 2};      // 2 tiles (one 32-row pack block) x 4 K-slices
-constexpr MqGeom G_GATEUP = {2, 4, 2, 2}; // gate+up tile pairs, 4 per workgroup x 2 K-slices
-constexpr MqGeom G_DOWN = {1, 2, 6, 2};   // 2 tiles x 6 K-slices
 constexpr MqGeom G_HEAD = {1, 2, 2, 2};   // 2 tiles per workgroup x 2 K-slices
+constexpr MqGeom G_STORE = {1, 2, 4, 2};  // hybrid q/k/v and delta-net projections
+
+// gate+up tile pairs: 4 per workgroup x 2 K-slices while that gives >= 400
+// workgroups (27648 rows: 432), else 2 per workgroup x 4 K-slices (17408
+// rows: 544 workgroups instead of 272 on 256 CUs)
+MqGeom gateup_geom(uint32_t n_ff) {
+    return ttiles(n_ff) / 4 >= 400 ? MqGeom{2, 4, 2, 2} : MqGeom{2, 2, 4, 2};
+}
+// down (n_embd rows): 2 tiles x 6 K-slices for long K (27648), 4 below
+MqGeom down_geom(uint32_t n_ff) {
+    return n_ff >= 24576 ? MqGeom{1, 2, 6, 2} : MqGeom{1, 2, 4, 2};
+}
 
 // ---- one fused op of the per-token plan, enqueued on the model stream ----
 hipError_t op_embed(lrs_model *m) {
@@ -259,6 +268,13 @@ hipError_t op_o(lrs_model *m, uint32_t l) {
     a.x = m->x;
     a.nw = L.ffn_norm;
     a.xout = m->pk_f;
+    if (L.dn) {
+        // the gated norm's per-head RMS factor, from the step's partial sums
+        a.gss = m->dn_part;
+        a.gblk = m->hc.dn_state / 32;
+        a.gn = (float)m->hc.dn_state;
+        a.eps = c.rms_eps;
+    }
     return launch_mq(a, wo->v.type, wo->v.type, G_O, MQ_RESID, m->ctx->stream);
 }
 
@@ -290,7 +306,7 @@ hipError_t op_store(lrs_model *m, const lrs_weight *const *ws, float *const *out
         a.n_seg0 = 0;
         for (int i = 0; i < n; i++) a.n_seg0 += ws[i]->v.type == T_Q4_K;
         a.nxb = pack_blocks(T_Q4_K, c.n_embd);
-        hipError_t e = launch_mq(a, T_Q4_K, T_Q6_K, G_QKV, MQ_STORE, m->ctx->stream);
+        hipError_t e = launch_mq(a, T_Q4_K, T_Q6_K, G_STORE, MQ_STORE, m->ctx->stream);
         if (e != hipErrorNotSupported) return e;
     }
     bool done[MQ_MAX_SEG] = {false, false, false};
@@ -307,7 +323,7 @@ hipError_t op_store(lrs_model *m, const lrs_weight *const *ws, float *const *out
             }
         a.n_seg0 = a.n_seg;
         a.nxb = pack_blocks(t, c.n_embd);
-        hipError_t e = launch_mq(a, t, t, G_QKV, MQ_STORE, m->ctx->stream);
+        hipError_t e = launch_mq(a, t, t, G_STORE, MQ_STORE, m->ctx->stream);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -355,7 +371,6 @@ hipError_t op_dn_step(lrs_model *m, uint32_t l) {
     a.state = L.state;
     a.norm_w = L.ssm_norm;
     a.part = m->dn_part;
-    a.cnt = m->dn_cnt;
     a.out = m->pk_a;
     a.step = m->step;
     a.n_embd = m->cfg.n_embd;
@@ -381,7 +396,8 @@ hipError_t op_gateup(lrs_model *m, uint32_t l) {
     a.xres = m->x;
     a.eps = c.rms_eps;
     a.xout = m->pk_s;
-    return launch_mq(a, L.gate->v.type, L.gate->v.type, G_GATEUP, MQ_SWIGLU, m->ctx->stream);
+    return launch_mq(a, L.gate->v.type, L.gate->v.type, gateup_geom(c.n_ff), MQ_SWIGLU,
+                     m->ctx->stream);
 }
 
 // x += W_down act; pack of x * (next layer's attn_norm, or output_norm)
@@ -397,7 +413,8 @@ hipError_t op_down(lrs_model *m, uint32_t l) {
     a.x = m->x;
     a.nw = l + 1 < c.n_layer ? m->layers[l + 1].attn_norm : m->output_norm;
     a.xout = m->pk_n;
-    return launch_mq(a, L.down->v.type, L.down->v.type, G_DOWN, MQ_RESID, m->ctx->stream);
+    return launch_mq(a, L.down->v.type, L.down->v.type, down_geom(c.n_ff), MQ_RESID,
+                     m->ctx->stream);
 }
 
 // logits = W_out (rmsnorm(x) * output_norm); greedy: each wavefront of
@@ -638,6 +655,7 @@ int lrs_hybrid_create(lrs_ctx *ctx, const lrs_hybrid_config *hcfg, const lrs_hyb
     if (hc.dn_state != 64 && hc.dn_state != 128)
         return fail(LRS_E_UNSUPPORTED, "dn_state must be 64 or 128");
     if (hc.dn_conv > 8) return fail(LRS_E_UNSUPPORTED, "dn_conv above 8");
+    if (c.n_embd > 8192) return fail(LRS_E_UNSUPPORTED, "hybrid n_embd above 8192");
     if (c.rope_dim > c.head_dim || (c.rope_dim & 1)) return fail(LRS_E_ARG, "bad rope_dim");
     if (c.n_head / c.n_head_kv > 8) return fail(LRS_E_UNSUPPORTED, "n_head / n_head_kv > 8");
     const uint32_t qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
@@ -705,12 +723,10 @@ int lrs_hybrid_create(lrs_ctx *ctx, const lrs_hybrid_config *hcfg, const lrs_hyb
         (rc = dev_alloc(m, kvd * sizeof(float), (void **)&m->vb)) ||
         (rc = dev_alloc(m, CD * sizeof(float), (void **)&m->dn_qkv)) ||
         (rc = dev_alloc(m, VD * sizeof(float), (void **)&m->dn_z)) ||
-        (rc = dev_alloc(m, (size_t)hc.dn_v_heads * (D / 32) * sizeof(float), (void **)&m->dn_part)) ||
-        (rc = dev_alloc(m, hc.dn_v_heads * sizeof(uint32_t), (void **)&m->dn_cnt)))
+        (rc = dev_alloc(m, (size_t)hc.dn_v_heads * (D / 32) * sizeof(float), (void **)&m->dn_part)))
         return bail(rc);
     if (hipMemset(m->kv, 0, kv_layer * 2 * n_attn * sizeof(_Float16)) != hipSuccess ||
-        hipMemset(m->rec, 0, m->rec_bytes) != hipSuccess ||
-        hipMemset(m->dn_cnt, 0, hc.dn_v_heads * sizeof(uint32_t)) != hipSuccess)
+        hipMemset(m->rec, 0, m->rec_bytes) != hipSuccess)
         return bail(fail(LRS_E_HIP, "memset"));
     uint32_t ia = 0, id = 0;
     for (uint32_t l = 0; l < c.n_layer; l++) {

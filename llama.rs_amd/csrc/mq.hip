@@ -362,6 +362,20 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (a.gss) {
+        // the producer packed each group without its RMS factor; the pack is
+        // linear in the block scale and sums, so the factor scales the meta
+        for (uint32_t b = threadIdx.x; b < a.nxb; b += blockDim.x) {
+            const uint32_t g = b / a.gblk;
+            float t = 0.f;
+            for (uint32_t r = 0; r < a.gblk; r++) t += a.gss[g * a.gblk + r];
+            const float f = 1.0f / sqrtf(t / a.gn + a.eps);
+            float4 *mb = reinterpret_cast<float4 *>(lds + lp.meta + 16 * b);
+            const float4 v = *mb;
+            *mb = make_float4(v.x * f, v.y * f, v.z * f, v.w * f);
+        }
+        __syncthreads();
+    }
 
     const ALane<T> al = alane<T>(lane, lp);
     float acc[TPW], accm[TPW];
@@ -506,6 +520,7 @@ static MqFn pick(const MqGeom &g) {
     LRS_MQ_CASE(1, 2, 4, 2)
     LRS_MQ_CASE(1, 2, 2, 2)
     LRS_MQ_CASE(2, 4, 2, 2)
+    LRS_MQ_CASE(2, 2, 4, 2)
     LRS_MQ_CASE(1, 2, 6, 2)
 #undef LRS_MQ_CASE
     return nullptr;

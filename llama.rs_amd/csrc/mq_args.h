@@ -66,6 +66,12 @@ struct MqArgs {
     uint32_t head_dim, rope_dim, ctx;
     // greedy (MQ_STORE)
     unsigned long long *amax;  // [workgroups] argmax keys of the rows, or null
+    // per-group RMS factor of the input (the delta net's gated norm): input
+    // block b belongs to group b / gblk and is scaled by
+    // 1 / sqrt(sum(gss[g*gblk .. g*gblk + gblk)) / gn + eps); null: none
+    const float *gss;
+    uint32_t gblk;
+    float gn;
 };
 
 // launch shape: TPW tiles per wavefront sharing the activation, TG tile
