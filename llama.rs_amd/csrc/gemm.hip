@@ -16,9 +16,9 @@
 // of 32 x 32.  K advances 64 at a time (one Q4_K qs group / a quarter of a
 // Q6_K super-block): every thread stages 32 activations (f32 -> bf16) and
 // dequantizes 32 weights of one row (bit-exact f32 dequant as in dequant.rs,
-// then bf16) into LDS, then each wavefront issues 4 K16 steps x 4 tiles of
-// MFMA.  LDS rows are padded to 72 bf16 so the 32 lanes that read 32
-// different rows at one K offset hit distinct banks.
+// then bf16) into a double-buffered LDS tile, and each wavefront issues 4 K16
+// steps x 4 tiles of MFMA.  LDS rows are padded to 72 bf16 so the 32 lanes
+// that read 32 different rows at one K offset hit distinct banks.
 #include "lrs_internal.h"
 #include "quant_dev.h"
 
@@ -40,50 +40,74 @@ struct GemmArgs {
 
 __device__ __forceinline__ uint4 ldq16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-// 32 consecutive weights of row n starting at element e (e % 32 == 0), f32
-// values exactly as ggml_cpu::dequant (dequant.rs:101-258); the GGUF bytes
-// come from the row's pieces of the tiled chunk of super-block e / 256
+// Raw GGUF bytes a thread needs for 32 consecutive weights of row n starting
+// at element e (e % 32 == 0): loaded one K-step ahead, dequantized after the
+// current step's matrix-core work has been issued
+template <uint32_t T> struct WRaw;
+template <> struct WRaw<T_Q4_K> { uint4 hd, q0, q1; };
+template <> struct WRaw<T_Q6_K> { uint4 l0, l1, h0, h1; uint32_t sc, d; };
+
 template <uint32_t T>
-__device__ __forceinline__ void deq32(const GemmArgs &g, uint32_t n, uint32_t e, float (&w)[32]) {
+__device__ __forceinline__ void wload(const GemmArgs &g, uint32_t n, uint32_t e, WRaw<T> &w) {
     const uint32_t o = e & 255, r = n & 15;  // offset inside the super-block, row in the tile
     const uint8_t *c = g.q + ((size_t)(n >> 4) * g.units + (e >> 8)) * tchunk_bytes(T);
     if constexpr (T == T_Q4_K) {
-        const uint4 hd = ldq16(c + 16 * r);
-        const uint32_t j = o >> 6, hi = (o >> 5) & 1;  // qs group, high nibbles
+        const uint32_t j = o >> 6;  // qs group
         // qs bytes 32j..32j+31 = pieces (g, r) with g = 2(j&1), 2(j&1)+1 of half j>>1
         const uint8_t *qp = c + 256 + 1024 * (j >> 1) + 16 * (16 * (2 * (j & 1)) + r);
-        const uint4 q0 = ldq16(qp), q1 = ldq16(qp + 256);
-        const uint8_t *sb = reinterpret_cast<const uint8_t *>(&hd) + 4;
-        uint32_t sc, m;
-        scale_min_k4(2 * j + hi, sb, sc, m);
-        const float dv = h2f((uint16_t)(hd.x & 0xFFFF)), mv = h2f((uint16_t)(hd.x >> 16));
-        const float d1 = __fmul_rn(dv, (float)sc), m1 = __fmul_rn(mv, (float)m);
-        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xFF;
-            const uint32_t q = hi ? (byte >> 4) : (byte & 15);
-            w[i] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
-        }
+        w.hd = ldq16(c + 16 * r);
+        w.q0 = ldq16(qp);
+        w.q1 = ldq16(qp + 256);
     } else {  // T_Q6_K
-        const float dv = h2f(*reinterpret_cast<const uint16_t *>(c + 3328 + 2 * r));
         const uint32_t h = o >> 7, quarter = (o >> 5) & 3;  // elements 128h + 32 quarter + l
         // ql[64h + 32(quarter&1) + l] and qh[32h + l]: pieces g = 2h (l < 16), 2h+1 (l >= 16)
         const uint8_t *ql = c + 256 + 1024 * (quarter & 1) + 16 * (16 * (2 * h) + r);
         const uint8_t *qh = c + 2304 + 16 * (16 * (2 * h) + r);
-        const uint4 l0 = ldq16(ql), l1 = ldq16(ql + 256);
-        const uint4 h0 = ldq16(qh), h1 = ldq16(qh + 256);
-        const int8_t s0 = (int8_t)c[16 * r + 8 * h + 2 * quarter], s1 = (int8_t)c[16 * r + 8 * h + 1 + 2 * quarter];
-        const float ds0 = __fmul_rn(dv, (float)s0), ds1 = __fmul_rn(dv, (float)s1);
-        const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-        const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        w.l0 = ldq16(ql);
+        w.l1 = ldq16(ql + 256);
+        w.h0 = ldq16(qh);
+        w.h1 = ldq16(qh + 256);
+        w.sc = *reinterpret_cast<const uint16_t *>(c + 16 * r + 8 * h + 2 * quarter);
+        w.d = *reinterpret_cast<const uint16_t *>(c + 3328 + 2 * r);
+    }
+}
+
+// the 32 weights in f32, exactly as ggml_cpu::dequant (dequant.rs:101-258)
+template <uint32_t T>
+__device__ __forceinline__ void wdeq(const WRaw<T> &w, uint32_t e, float (&v)[32]) {
+    const uint32_t o = e & 255;
+    if constexpr (T == T_Q4_K) {
+        const uint32_t j = o >> 6, hi = (o >> 5) & 1;  // qs group, high nibbles
+        // get_scale_min_k4 (dequant.rs:101-110): scale bytes 0-3, 4-7, 8-11 are
+        // header words y, z, w; sub-block jj reads byte jj & 3 of each
+        const uint32_t jj = 2 * j + hi, sh = 8 * (jj & 3);
+        const uint32_t by = (w.hd.y >> sh) & 0xFF, bz = (w.hd.z >> sh) & 0xFF,
+                       bw = (w.hd.w >> sh) & 0xFF;
+        const uint32_t sc = jj < 4 ? (by & 63) : ((bw & 0xF) | ((by >> 6) << 4));
+        const uint32_t m = jj < 4 ? (bz & 63) : ((bw >> 4) | ((bz >> 6) << 4));
+        const float dv = h2f((uint16_t)(w.hd.x & 0xFFFF)), mv = h2f((uint16_t)(w.hd.x >> 16));
+        const float d1 = __fmul_rn(dv, (float)sc), m1 = __fmul_rn(mv, (float)m);
+        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xFF;
+            const uint32_t q = hi ? (byte >> 4) : (byte & 15);
+            v[i] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
+        }
+    } else {  // T_Q6_K
+        const uint32_t quarter = (o >> 5) & 3;
+        const float dv = h2f((uint16_t)w.d);
+        const float ds0 = __fmul_rn(dv, (float)(int8_t)(w.sc & 0xFF));
+        const float ds1 = __fmul_rn(dv, (float)(int8_t)(w.sc >> 8));
+        const uint32_t lw[8] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w, w.l1.x, w.l1.y, w.l1.z, w.l1.w};
+        const uint32_t hw[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xFF;
             const uint32_t hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xFF;
             const uint32_t lo = quarter < 2 ? (lb & 15) : (lb >> 4);
             const int q = (int)(lo | (((hb >> (2 * quarter)) & 3) << 4)) - 32;
-            w[i] = __fmul_rn(i < 16 ? ds0 : ds1, (float)q);
+            v[i] = __fmul_rn(i < 16 ? ds0 : ds1, (float)q);
         }
     }
 }
@@ -107,17 +131,23 @@ __device__ __forceinline__ void put32(__bf16 *hi, __bf16 *lo, const float (&v)[3
     }
 }
 
+// Software pipeline over K: step k's operands sit in LDS buffer k & 1 while
+// step k+1's activations and raw weight bytes are in flight to registers;
+// the wavefronts issue step k's MFMAs, then convert / dequantize step k+1
+// into the other buffer (VALU work that overlaps the matrix cores), then one
+// barrier.
 template <uint32_t T, int PREC>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     constexpr int NS = PREC == 3 ? 2 : 1;  // hi (+ lo) planes
-    __shared__ __attribute__((aligned(16))) __bf16 As[NS][GM_BM * GM_LD];
-    __shared__ __attribute__((aligned(16))) __bf16 Ws[NS][GM_BN * GM_LD];
+    __shared__ __attribute__((aligned(16))) __bf16 As[2][NS][GM_BM * GM_LD];
+    __shared__ __attribute__((aligned(16))) __bf16 Ws[2][NS][GM_BN * GM_LD];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t m0 = blockIdx.y * GM_BM, n0 = blockIdx.x * GM_BN;
     const uint32_t wm = wave >> 1, wn = wave & 1;  // wave's 64 x 64 quarter
     // staging roles: thread t handles row t/2, half t%2 (32 of the 64 K)
     const uint32_t sr = tid >> 1, sh = (tid & 1) * 32;
     const uint32_t am = min(m0 + sr, g.M - 1), wr = min(n0 + sr, g.N - 1);
+    const float *arow = g.a + (size_t)am * g.K + sh;
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -127,23 +157,35 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    for (uint32_t k0 = 0; k0 < g.K; k0 += GM_BK) {
-        {
-            float v[32];
-            const float4 *ap = reinterpret_cast<const float4 *>(g.a + (size_t)am * g.K + k0 + sh);
+    float4 ar[8];
+    WRaw<T> wraw;
+    auto fetch = [&](uint32_t k0) {
+        const float4 *ap = reinterpret_cast<const float4 *>(arow + k0);
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const float4 t = ap[c];
-                v[4 * c] = t.x;
-                v[4 * c + 1] = t.y;
-                v[4 * c + 2] = t.z;
-                v[4 * c + 3] = t.w;
-            }
-            put32<PREC>(&As[0][sr * GM_LD + sh], &As[NS - 1][sr * GM_LD + sh], v);
-            deq32<T>(g, wr, k0 + sh, v);
-            put32<PREC>(&Ws[0][sr * GM_LD + sh], &Ws[NS - 1][sr * GM_LD + sh], v);
+        for (int c = 0; c < 8; c++) ar[c] = ap[c];
+        wload<T>(g, wr, k0 + sh, wraw);
+    };
+    auto stage = [&](int buf, uint32_t k0) {
+        float v[32];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            v[4 * c] = ar[c].x;
+            v[4 * c + 1] = ar[c].y;
+            v[4 * c + 2] = ar[c].z;
+            v[4 * c + 3] = ar[c].w;
         }
-        __syncthreads();
+        put32<PREC>(&As[buf][0][sr * GM_LD + sh], &As[buf][NS - 1][sr * GM_LD + sh], v);
+        wdeq<T>(wraw, k0 + sh, v);
+        put32<PREC>(&Ws[buf][0][sr * GM_LD + sh], &Ws[buf][NS - 1][sr * GM_LD + sh], v);
+    };
+
+    const uint32_t nk = g.K / GM_BK;
+    fetch(0);
+    stage(0, 0);
+    __syncthreads();
+    for (uint32_t k = 0; k < nk; k++) {
+        const int cur = k & 1;
+        if (k + 1 < nk) fetch((k + 1) * GM_BK);
 #pragma unroll
         for (int ks = 0; ks < GM_BK / 16; ks++) {
             const uint32_t kk = 16 * ks + 8 * (lane >> 5);
@@ -152,8 +194,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
             for (int p = 0; p < NS; p++)
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
-                    a[p][t] = *reinterpret_cast<const bf16x8 *>(&As[p][(64 * wm + 32 * t + (lane & 31)) * GM_LD + kk]);
-                    b[p][t] = *reinterpret_cast<const bf16x8 *>(&Ws[p][(64 * wn + 32 * t + (lane & 31)) * GM_LD + kk]);
+                    a[p][t] = *reinterpret_cast<const bf16x8 *>(&As[cur][p][(64 * wm + 32 * t + (lane & 31)) * GM_LD + kk]);
+                    b[p][t] = *reinterpret_cast<const bf16x8 *>(&Ws[cur][p][(64 * wn + 32 * t + (lane & 31)) * GM_LD + kk]);
                 }
 #pragma unroll
             for (int i = 0; i < 2; i++)
@@ -166,6 +208,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
                 }
         }
+        if (k + 1 < nk) stage(cur ^ 1, (k + 1) * GM_BK);
         __syncthreads();
     }
     // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
