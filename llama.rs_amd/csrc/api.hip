@@ -333,7 +333,13 @@ int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y
     if (w->v.type != T_Q4_K && w->v.type != T_Q6_K)
         return fail(LRS_E_UNSUPPORTED, "the GEMM supports Q4_K and Q6_K weights");
     SETDEV(ctx);
-    LRS_HIP(launch_gemm(w->v, a_dev, y_dev, m, w->v.n_out, precision, ctx->stream));
+    // the activation as bf16 planes (hi, and lo for precision 3) in context scratch
+    const size_t n = (size_t)m * w->v.n_in;
+    void *buf = nullptr;
+    LRS_HIP(scratch(ctx, n * 2 * (precision == 3 ? 2 : 1), &buf));
+    __bf16 *hi = (__bf16 *)buf, *lo = precision == 3 ? hi + n : nullptr;
+    LRS_HIP(launch_split_bf16(a_dev, n, hi, lo, ctx->stream));
+    LRS_HIP(launch_gemm(w->v, hi, lo, y_dev, m, w->v.n_out, precision, ctx->stream));
     return LRS_OK;
 }
 

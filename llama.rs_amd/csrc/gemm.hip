@@ -26,16 +26,18 @@ namespace lrs {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 
 constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 64;
 constexpr int GM_LD = GM_BK + 8;  // padded LDS row (bf16 elements)
 
 struct GemmArgs {
-    const float *a;      // [M][K]
-    float *y;            // [M][ldy]
-    const uint8_t *q;    // weight, tiled layout (tiled.h)
+    const __bf16 *ahi, *alo;  // A [M][K] as bf16 (hi, and lo = bf16(a - hi) for PREC 3)
+    float *y;                 // [M][ldy]
+    const uint8_t *q;         // weight, tiled layout (tiled.h)
     uint32_t M, N, K, units, ldy;
-    uint32_t accum;      // 1: y += A W^T (residual add), 0: y = A W^T
+    uint32_t accum;           // 1: y += A W^T (residual add), 0: y = A W^T
+    uint32_t nm, nn;          // output tiles along M and N
 };
 
 __device__ __forceinline__ uint4 ldq16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -132,22 +134,30 @@ __device__ __forceinline__ void put32(__bf16 *hi, __bf16 *lo, const float (&v)[3
 }
 
 // Software pipeline over K: step k's operands sit in LDS buffer k & 1 while
-// step k+1's activations and raw weight bytes are in flight to registers;
-// the wavefronts issue step k's MFMAs, then convert / dequantize step k+1
-// into the other buffer (VALU work that overlaps the matrix cores), then one
-// barrier.
+// step k+1's activations (already bf16, split once per GEMM input by
+// k_split_bf16) and raw weight bytes are in flight to registers; the
+// wavefronts issue step k's MFMAs, then dequantize step k+1 into the other
+// buffer (VALU work that overlaps the matrix cores), then one barrier.
+//
+// Tile order: workgroup b runs on XCD b % 8 (round-robin dispatch); the
+// tiles are numbered M-block-major and XCD x takes the x-th contiguous run
+// of them, so the workgroups of one XCD share one or two activation blocks,
+// which stay in that XCD's L2.
 template <uint32_t T, int PREC>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
     constexpr int NS = PREC == 3 ? 2 : 1;  // hi (+ lo) planes
     __shared__ __attribute__((aligned(16))) __bf16 As[2][NS][GM_BM * GM_LD];
     __shared__ __attribute__((aligned(16))) __bf16 Ws[2][NS][GM_BN * GM_LD];
+    const uint32_t ntile = g.nm * g.nn, per = (ntile + 7) / 8;
+    const uint32_t t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (t >= ntile) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t m0 = blockIdx.y * GM_BM, n0 = blockIdx.x * GM_BN;
+    const uint32_t m0 = (t / g.nn) * GM_BM, n0 = (t % g.nn) * GM_BN;
     const uint32_t wm = wave >> 1, wn = wave & 1;  // wave's 64 x 64 quarter
     // staging roles: thread t handles row t/2, half t%2 (32 of the 64 K)
     const uint32_t sr = tid >> 1, sh = (tid & 1) * 32;
     const uint32_t am = min(m0 + sr, g.M - 1), wr = min(n0 + sr, g.N - 1);
-    const float *arow = g.a + (size_t)am * g.K + sh;
+    const size_t aoff = (size_t)am * g.K + sh;
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -157,35 +167,28 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    float4 ar[8];
-    WRaw<T> wraw;
-    auto fetch = [&](uint32_t k0) {
-        const float4 *ap = reinterpret_cast<const float4 *>(arow + k0);
-#pragma unroll
-        for (int c = 0; c < 8; c++) ar[c] = ap[c];
-        wload<T>(g, wr, k0 + sh, wraw);
-    };
-    auto stage = [&](int buf, uint32_t k0) {
-        float v[32];
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            v[4 * c] = ar[c].x;
-            v[4 * c + 1] = ar[c].y;
-            v[4 * c + 2] = ar[c].z;
-            v[4 * c + 3] = ar[c].w;
-        }
-        put32<PREC>(&As[buf][0][sr * GM_LD + sh], &As[buf][NS - 1][sr * GM_LD + sh], v);
-        wdeq<T>(wraw, k0 + sh, v);
-        put32<PREC>(&Ws[buf][0][sr * GM_LD + sh], &Ws[buf][NS - 1][sr * GM_LD + sh], v);
-    };
-
-    const uint32_t nk = g.K / GM_BK;
-    fetch(0);
-    stage(0, 0);
-    __syncthreads();
-    for (uint32_t k = 0; k < nk; k++) {
-        const int cur = k & 1;
-        if (k + 1 < nk) fetch((k + 1) * GM_BK);
+    // two register sets: step k + 2 is loaded while step k is multiplied and
+    // step k + 1 dequantized
+    u32x4 a0[NS][4], a1[NS][4];
+    WRaw<T> w0, w1;
+#define LRS_GFETCH(A, W, K0)                                                                  \
+    do {                                                                                      \
+        _Pragma("unroll") for (int p = 0; p < NS; p++) {                                       \
+            const u32x4 *ap = reinterpret_cast<const u32x4 *>((p == 0 ? g.ahi : g.alo) + aoff + (K0)); \
+            _Pragma("unroll") for (int c = 0; c < 4; c++) A[p][c] = ap[c];                    \
+        }                                                                                     \
+        wload<T>(g, wr, (K0) + sh, W);                                                        \
+    } while (0)
+#define LRS_GSTAGE(BUF, A, W, K0)                                                             \
+    do {                                                                                      \
+        _Pragma("unroll") for (int p = 0; p < NS; p++)                                         \
+            _Pragma("unroll") for (int c = 0; c < 4; c++)                                      \
+                *reinterpret_cast<u32x4 *>(&As[BUF][p][sr * GM_LD + sh + 8 * c]) = A[p][c];    \
+        float v_[32];                                                                         \
+        wdeq<T>(W, (K0) + sh, v_);                                                            \
+        put32<PREC>(&Ws[BUF][0][sr * GM_LD + sh], &Ws[BUF][NS - 1][sr * GM_LD + sh], v_);     \
+    } while (0)
+    auto mma = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int ks = 0; ks < GM_BK / 16; ks++) {
             const uint32_t kk = 16 * ks + 8 * (lane >> 5);
@@ -193,9 +196,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
 #pragma unroll
             for (int p = 0; p < NS; p++)
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    a[p][t] = *reinterpret_cast<const bf16x8 *>(&As[cur][p][(64 * wm + 32 * t + (lane & 31)) * GM_LD + kk]);
-                    b[p][t] = *reinterpret_cast<const bf16x8 *>(&Ws[cur][p][(64 * wn + 32 * t + (lane & 31)) * GM_LD + kk]);
+                for (int u = 0; u < 2; u++) {
+                    a[p][u] = *reinterpret_cast<const bf16x8 *>(&As[buf][p][(64 * wm + 32 * u + (lane & 31)) * GM_LD + kk]);
+                    b[p][u] = *reinterpret_cast<const bf16x8 *>(&Ws[buf][p][(64 * wn + 32 * u + (lane & 31)) * GM_LD + kk]);
                 }
 #pragma unroll
             for (int i = 0; i < 2; i++)
@@ -208,9 +211,27 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
                 }
         }
-        if (k + 1 < nk) stage(cur ^ 1, (k + 1) * GM_BK);
+    };
+
+    // nk is even (K % 128 == 0): two steps per trip, no branch in the loop;
+    // the last trip's look-ahead loads repeat the final step (unused)
+    const uint32_t nk = g.K / GM_BK;
+    LRS_GFETCH(a0, w0, 0);
+    LRS_GFETCH(a1, w1, GM_BK);
+    LRS_GSTAGE(0, a0, w0, 0);
+    __syncthreads();
+    for (uint32_t k = 0; k < nk; k += 2) {
+        LRS_GFETCH(a0, w0, min(k + 2, nk - 1) * GM_BK);
+        mma(0);
+        LRS_GSTAGE(1, a1, w1, (k + 1) * GM_BK);
+        __syncthreads();
+        LRS_GFETCH(a1, w1, min(k + 3, nk - 1) * GM_BK);
+        mma(1);
+        LRS_GSTAGE(0, a0, w0, min(k + 2, nk - 1) * GM_BK);
         __syncthreads();
     }
+#undef LRS_GFETCH
+#undef LRS_GSTAGE
     // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
 #pragma unroll
     for (int i = 0; i < 2; i++)
@@ -228,11 +249,42 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
         }
 }
 
-hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint32_t ldy, int prec,
-                       hipStream_t s, bool accum) {
-    if (M == 0 || w.n_in % GM_BK) return hipErrorInvalidValue;
+// a -> bf16 hi (round to nearest even) and, if lo, bf16(a - hi): the
+// activation planes of the GEMM, 4 elements per thread
+__global__ __launch_bounds__(256) void k_split_bf16(const float *__restrict__ a, size_t n4,
+                                                    __bf16 *__restrict__ hi, __bf16 *__restrict__ lo) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4 v = reinterpret_cast<const float4 *>(a)[i];
+    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+    bf16x4 h, l;
+    h[0] = to_bf16(v.x);
+    h[1] = to_bf16(v.y);
+    h[2] = to_bf16(v.z);
+    h[3] = to_bf16(v.w);
+    reinterpret_cast<bf16x4 *>(hi)[i] = h;
+    if (lo) {
+        l[0] = to_bf16(v.x - (float)h[0]);
+        l[1] = to_bf16(v.y - (float)h[1]);
+        l[2] = to_bf16(v.z - (float)h[2]);
+        l[3] = to_bf16(v.w - (float)h[3]);
+        reinterpret_cast<bf16x4 *>(lo)[i] = l;
+    }
+}
+
+hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, hipStream_t s) {
+    if (n % 4) return hipErrorInvalidValue;
+    const size_t n4 = n / 4;
+    hipLaunchKernelGGL(k_split_bf16, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a, n4, hi, lo);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
+                       uint32_t ldy, int prec, hipStream_t s, bool accum) {
+    if (M == 0 || w.n_in % (2 * GM_BK) || (prec == 3 && !alo)) return hipErrorInvalidValue;
     GemmArgs g;
-    g.a = a;
+    g.ahi = ahi;
+    g.alo = alo;
     g.y = y;
     g.q = w.q;
     g.M = M;
@@ -241,12 +293,14 @@ hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint3
     g.units = tunits(w.type, w.n_in);
     g.ldy = ldy;
     g.accum = accum ? 1u : 0u;
-    dim3 grid((w.n_out + GM_BN - 1) / GM_BN, (M + GM_BM - 1) / GM_BM);
+    g.nm = (M + GM_BM - 1) / GM_BM;
+    g.nn = (w.n_out + GM_BN - 1) / GM_BN;
+    const uint32_t grid = 8 * ((g.nm * g.nn + 7) / 8);
     void (*fn)(GemmArgs) = nullptr;
     if (w.type == T_Q4_K) fn = prec == 3 ? k_gemm<T_Q4_K, 3> : k_gemm<T_Q4_K, 1>;
     else if (w.type == T_Q6_K) fn = prec == 3 ? k_gemm<T_Q6_K, 3> : k_gemm<T_Q6_K, 1>;
     else return hipErrorNotSupported;
-    hipLaunchKernelGGL(fn, grid, dim3(256), 0, s, g);
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 

@@ -98,9 +98,12 @@ hipError_t launch_argmax_finish(const unsigned long long *keys, uint32_t n, uint
 // y[c] = W x[c] for cols columns (packs x, then one matvec per column)
 hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
                          hipStream_t s);
-// Y[M][ldy] = A[M][K] W^T on the matrix cores (prec 1: bf16, 3: bf16 hi/lo split)
-hipError_t launch_gemm(WeightView w, const float *a, float *y, uint32_t M, uint32_t ldy, int prec,
-                       hipStream_t s, bool accum = false);
+// Y[M][ldy] = A[M][K] W^T on the matrix cores; A given as bf16 planes
+// (prec 1: hi only; 3: hi + lo, three products) from launch_split_bf16
+hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
+                       uint32_t ldy, int prec, hipStream_t s, bool accum = false);
+// hi = bf16(a), lo = bf16(a - hi) (lo may be null); n a multiple of 4
+hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, hipStream_t s);
 // batched prompt block (prefill.hip)
 hipError_t launch_rmsnorm_rows(const float *X, const float *w, float eps, uint32_t E, uint32_t n,
                                float *Y, hipStream_t s);

@@ -30,6 +30,7 @@
 #include "pack_dev.h"
 #include "quant_dev.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -98,6 +99,7 @@ struct lrs_model {
     // gate / up, token ids
     uint32_t pb_cap = 0;
     float *pX = nullptr, *pXN, *pQt, *pKt, *pVt, *pQ, *pATT, *pG, *pU;
+    __bf16 *pA16 = nullptr;  // bf16 hi / lo planes of the current GEMM input
     uint32_t *ptok;
     _Float16 *kv;                // all layers' caches
     uint32_t *step_host;         // pinned
@@ -819,7 +821,7 @@ static constexpr uint32_t PREFILL_BLOCK = 512;
 // every matmul weight has a GEMM kernel and the attention shape is supported
 static bool prefill_capable(const lrs_model *m) {
     auto ok = [](const lrs_weight *w) {
-        return (w->v.type == T_Q4_K || w->v.type == T_Q6_K) && w->v.n_in % 64 == 0;
+        return (w->v.type == T_Q4_K || w->v.type == T_Q6_K) && w->v.n_in % 128 == 0;
     };
     const lrs_config &c = m->cfg;
     if (m->hybrid) return false;  // the recurrence runs token by token
@@ -847,6 +849,8 @@ static int ensure_prefill(lrs_model *m) {
         (rc = dev_alloc(m, B * qd * 4, (void **)&m->pATT)) ||
         (rc = dev_alloc(m, B * c.n_ff * 4, (void **)&m->pG)) ||
         (rc = dev_alloc(m, B * c.n_ff * 4, (void **)&m->pU)) ||
+        (rc = dev_alloc(m, B * std::max<size_t>(std::max<size_t>(c.n_embd, qd), c.n_ff) * 4,
+                        (void **)&m->pA16)) ||
         (rc = dev_alloc(m, B * 4, (void **)&m->ptok)))
         return rc;
     m->pb_cap = PREFILL_BLOCK;
@@ -861,24 +865,33 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
     hipStream_t s = m->ctx->stream;
     const uint32_t qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim, E = c.n_embd;
     constexpr int P = 3;
+    // GEMM inputs as bf16 hi / lo planes: hi at pA16, lo right after the
+    // rows x cols hi plane
+    __bf16 *const hi = m->pA16;
+    auto lo = [&](uint32_t rows, uint32_t cols) { return hi + (size_t)rows * cols; };
+    auto split = [&](const float *a, size_t n) { return launch_split_bf16(a, n, hi, hi + n, s); };
     LRS_HIP(hipMemcpyAsync(m->ptok, tokens, nb * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     LRS_HIP(launch_dequant_rows(m->embd->v, m->ptok, nb, m->pX, s));
     for (uint32_t l = 0; l < c.n_layer; l++) {
         const DevLayer &L = m->layers[l];
         LRS_HIP(launch_rmsnorm_rows(m->pX, L.attn_norm, c.rms_eps, E, nb, m->pXN, s));
-        LRS_HIP(launch_gemm(L.q->v, m->pXN, m->pQt, nb, qd, P, s));
-        LRS_HIP(launch_gemm(L.k->v, m->pXN, m->pKt, nb, kvd, P, s));
-        LRS_HIP(launch_gemm(L.v->v, m->pXN, m->pVt, nb, kvd, P, s));
+        LRS_HIP(split(m->pXN, (size_t)nb * E));
+        LRS_HIP(launch_gemm(L.q->v, hi, lo(nb, E), m->pQt, nb, qd, P, s));
+        LRS_HIP(launch_gemm(L.k->v, hi, lo(nb, E), m->pKt, nb, kvd, P, s));
+        LRS_HIP(launch_gemm(L.v->v, hi, lo(nb, E), m->pVt, nb, kvd, P, s));
         LRS_HIP(launch_qkv_post(m->pQt, m->pKt, m->pVt, L.bq, L.bk, L.bv, m->freq, m->pQ, L.kc,
                                 L.vc, nb, pos0, qd, kvd, c.head_dim, c.rope_dim, c.ctx, s));
         LRS_HIP(launch_attn_prefill(m->pQ, L.kc, L.vc, m->pATT, nb, pos0, c.n_head, c.n_head_kv,
                                     c.head_dim, c.ctx, s));
-        LRS_HIP(launch_gemm(L.o->v, m->pATT, m->pX, nb, E, P, s, true));
+        LRS_HIP(split(m->pATT, (size_t)nb * qd));
+        LRS_HIP(launch_gemm(L.o->v, hi, lo(nb, qd), m->pX, nb, E, P, s, true));
         LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, m->pXN, s));
-        LRS_HIP(launch_gemm(L.gate->v, m->pXN, m->pG, nb, c.n_ff, P, s));
-        LRS_HIP(launch_gemm(L.up->v, m->pXN, m->pU, nb, c.n_ff, P, s));
+        LRS_HIP(split(m->pXN, (size_t)nb * E));
+        LRS_HIP(launch_gemm(L.gate->v, hi, lo(nb, E), m->pG, nb, c.n_ff, P, s));
+        LRS_HIP(launch_gemm(L.up->v, hi, lo(nb, E), m->pU, nb, c.n_ff, P, s));
         LRS_HIP(launch_swiglu_rows(m->pG, m->pU, (size_t)nb * c.n_ff, s));
-        LRS_HIP(launch_gemm(L.down->v, m->pG, m->pX, nb, E, P, s, true));
+        LRS_HIP(split(m->pG, (size_t)nb * c.n_ff));
+        LRS_HIP(launch_gemm(L.down->v, hi, lo(nb, c.n_ff), m->pX, nb, E, P, s, true));
     }
     return LRS_OK;
 }
