@@ -9,6 +9,10 @@ Workloads:
           at positions 511.., then the cache is rewound and K timed tokens are
           decoded at the same positions 511..511+K-1 (attention length
           512..511+K, the config's 128 tokens after a 512-token prompt).
+  q8      config 1: one Q8_0 4096x4096 matvec (d ~ U[1e-3,1e-2], qs ~ U[-127,127],
+          x ~ N(0,1) f32); a step is one lrs_matvec_dev call (activation pack +
+          matrix-core matvec), rotating over 16 weight copies (285 MB, beyond
+          the 256 MB MALL) so every weight byte comes from HBM.
   layer   config 2: one Qwen2.5-14B-shaped layer matvec set, weights rotated
           over 4 copies so every byte comes from HBM; a step is 7 matvecs.
   hybrid  config 4: 27B-scale hybrid model (64 layers, gated full attention
@@ -309,6 +313,24 @@ def bench_layer(lrs, ctx, steps, warmup):
     return dict(ms=ms, bytes=set_bytes, gbs=set_bytes / (ms * 1e-3) / 1e9)
 
 
+def bench_q8(lrs, ctx, steps, warmup):
+    n = 4096
+    copies = 16
+    ws = [lrs.Weight.generate(ctx, Q8_0, 900 + c, n, n, mode=0, d_lo=1e-3, d_hi=1e-2)
+          for c in range(copies)]
+    xbuf, ybuf = ctx.alloc(4 * n), ctx.alloc(4 * n)
+    xbuf.upload(np.random.default_rng(1234).standard_normal(n).astype(np.float32))
+    for s in range(warmup):
+        ws[s % copies].matvec_dev(xbuf, ybuf)
+    ctx.sync()
+    ctx.timer_start()
+    for s in range(steps):
+        ws[s % copies].matvec_dev(xbuf, ybuf)
+    us = ctx.timer_stop() * 1e3 / steps
+    b = gguf_bytes(Q8_0, n, n) + 4 * n + 4 * n
+    return dict(us=us, bytes=b, gbs=b / us / 1e3)
+
+
 def bench_gemm(lrs, ctx, steps, warmup, m, precision):
     """Config 5: M tokens x 5120 activations against Q4_K gate/up 13824x5120 and
     Q6_K down 5120x13824 (the config-2 FFN), on the matrix cores."""
@@ -338,8 +360,9 @@ def bench_gemm(lrs, ctx, steps, warmup, m, precision):
 
 def run_pmc(lrs, ctx):
     """Kernels for the counter passes: the copy calibration (an F32 tensor's
-    identity dequant: 4 B read + 4 B written per element, grid-stride) and the
-    dominant decode op rotating over 4 layers of the 32B shape."""
+    identity dequant: 4 B read + 4 B written per element, grid-stride), the
+    dominant decode ops rotating over 4 layers of the 32B shape, and the same
+    on a 4-layer block of the config-4 hybrid shape."""
     from llama_rs_amd.model import synthetic_model
 
     n = 128 << 20  # 512 MiB read + 512 MiB written
@@ -355,6 +378,17 @@ def run_pmc(lrs, ctx):
         us, b = m.profile(op, 8 if op != "head" else 2)
         log(f"[pmc] {op}: {us:.2f} us/launch, {b} algorithmic weight bytes")
     m.close()
+    # config 4: the same ops on a 4-layer block of the hybrid shape (3 delta-net
+    # layers + 1 gated attention layer)
+    from llama_rs_amd.model import QWEN35_27B, synthetic_hybrid_model
+
+    hm = synthetic_hybrid_model(ctx, dict(QWEN35_27B, n_layer=4), seed=1, mode=0, d_lo=1e-3,
+                                d_hi=1e-2)
+    hm.decode_batch(np.arange(8, dtype=np.uint32), 0)
+    for op in ("gateup", "down", "dn_proj", "dn_step", "dn_out", "head"):
+        us, b = hm.profile(op, 6 if op != "head" else 2)
+        log(f"[pmc] hybrid {op}: {us:.2f} us/launch, {b} algorithmic bytes")
+    hm.close()
 
 
 def main():
@@ -363,7 +397,7 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "hybrid", "layer", "gemm", "pmc"])
+                    choices=["decode", "hybrid", "q8", "layer", "gemm", "pmc"])
     ap.add_argument("--m", type=int, default=512, help="gemm: prompt tokens (config 5: 128/512/2048)")
     ap.add_argument("--precision", type=int, default=1, choices=[1, 3],
                     help="gemm: 1 = bf16 operands, 3 = bf16 hi/lo split")
@@ -403,6 +437,22 @@ def main():
                "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": peak,
                             "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
                             "traffic": None}}
+        print(json.dumps(out), flush=True)
+        ctx.close()
+        return
+    if a.workload == "q8":
+        r = bench_q8(lrs, ctx, a.steps, a.warmup)
+        out = {"metric": "quant matvec HBM GB/s, single Q8_0 4096x4096 matvec (batch-1)",
+               "value": round(r["gbs"], 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+               "warmup": a.warmup, "ms_per_step": round(r["us"] / 1e3, 6),
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+               "data": "synthetic (seeded Q8_0 blocks, BASELINE distributions; x ~ N(0,1))",
+               "config": {"workload": "config1-q8_0-matvec-4096", "batch": 1,
+                          "copies_rotated": 16, "bytes_per_matvec": r["bytes"],
+                          "us_per_matvec": round(r["us"], 3)},
+               "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1),
+                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}}
         print(json.dumps(out), flush=True)
         ctx.close()
         return

@@ -16,7 +16,7 @@
 //   norm    y_j = o_j / sqrt(mean_j(o^2) + eps) * norm_w[j] * silu(z_j)
 //
 // The rows of a head are independent in the rule, so a head is split over
-// D/32 workgroups of 32 rows (one pack block each): the state streams from
+// D/32 workgroups of 32 rows (one pack block each, on one XCD): the state streams from
 // 4 x more CUs than one workgroup per head would use.  Each workgroup
 // recomputes the head's gates, q and k (a few KB, L2-resident), packs its 32
 // y values without the head's RMS factor and leaves its share of sum(o^2);
@@ -53,7 +53,19 @@ template <int D>
 __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
     constexpr uint32_t R = D / 32;    // workgroups per head (32 rows each)
     constexpr int PPL = D / 32;       // float4 pieces of a row per lane (8 lanes per row)
-    const uint32_t r = blockIdx.x, hh = blockIdx.y, tid = threadIdx.x;
+    // workgroup b runs on XCD b % 8: with v_heads % 8 == 0 the R workgroups of
+    // a head get ids of one residue mod 8, so the head's gate rows are fetched
+    // into one XCD's L2 once instead of once per workgroup
+    uint32_t r, hh;
+    if (a.v_heads % 8 == 0) {
+        const uint32_t x = blockIdx.x & 7, sl = blockIdx.x >> 3;
+        hh = x + 8 * (sl / R);
+        r = sl % R;
+    } else {
+        hh = blockIdx.x / R;
+        r = blockIdx.x % R;
+    }
+    const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63, wave = tid >> 6;
     const uint32_t rho = tid >> 3, lam = tid & 7;  // row of the lane group, lane in the group
     const uint32_t j = 32 * r + rho;
@@ -68,6 +80,33 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
 #pragma unroll
     for (int c = 0; c < PPL; c++) st[c] = srow[8 * c + lam];
 
+    // causal conv + SiLU of q, k (key head kh) and this workgroup's v rows
+    // (dn_conv.comp); the current input goes to ring slot pos % W, written
+    // once per channel: q/k by workgroup 0 of value head kh, v by its owner.
+    // Two channels per thread (2D + 32 <= 512); their loads, like the gate
+    // rows' below, are issued before any of them is used.
+    const uint32_t pos = a.step[1];
+    const uint32_t W = a.d_conv, wslot = pos % W;
+    const bool own_qk = r == 0 && hh < a.k_heads;
+    constexpr int WM = 8;  // d_conv <= 8
+    float xc[2], wt[2][WM], wn[2][WM];
+    uint32_t chs[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const uint32_t c = tid + 256 * u;
+        const uint32_t ch = c < D ? kh * D + c
+                            : c < 2 * D ? KD + kh * D + (c - D)
+                                        : 2 * KD + hh * D + 32 * r + (c - 2 * D);
+        chs[u] = ch;
+        if (c < 2 * D + 32) {
+            xc[u] = a.qkv[ch];
+#pragma unroll
+            for (int t = 0; t < WM; t++) {
+                if ((uint32_t)t < W) wt[u][t] = a.conv_w[(size_t)ch * W + t];
+                if ((uint32_t)t + 1 < W) wn[u][t] = a.win[(size_t)((pos + 1 + t) % W) * CD + ch];
+            }
+        }
+    }
     // gate projections of hn = rmsnorm(x) * attn_norm (dn_gates.comp): every
     // load of a thread's elements is issued before the first product
     {
@@ -105,33 +144,8 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
         }
     }
 
-    // causal conv + SiLU of q, k (key head kh) and this workgroup's v rows
-    // (dn_conv.comp); the current input goes to ring slot pos % W, written
-    // once per channel: q/k by workgroup 0 of value head kh, v by its owner.
-    // Two channels per thread (2D + 32 <= 512), all loads issued first.
-    const uint32_t pos = a.step[1];
-    const uint32_t W = a.d_conv, wslot = pos % W;
-    const bool own_qk = r == 0 && hh < a.k_heads;
+    // conv + SiLU
     {
-        constexpr int WM = 8;  // d_conv <= 8
-        float xc[2], wt[2][WM], wn[2][WM];
-        uint32_t chs[2];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const uint32_t c = tid + 256 * u;
-            const uint32_t ch = c < D ? kh * D + c
-                                : c < 2 * D ? KD + kh * D + (c - D)
-                                            : 2 * KD + hh * D + 32 * r + (c - 2 * D);
-            chs[u] = ch;
-            if (c < 2 * D + 32) {
-                xc[u] = a.qkv[ch];
-#pragma unroll
-                for (int t = 0; t < WM; t++) {
-                    if ((uint32_t)t < W) wt[u][t] = a.conv_w[(size_t)ch * W + t];
-                    if ((uint32_t)t + 1 < W) wn[u][t] = a.win[(size_t)((pos + 1 + t) % W) * CD + ch];
-                }
-            }
-        }
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const uint32_t c = tid + 256 * u;
@@ -240,8 +254,8 @@ hipError_t launch_dn_step(const DnArgs &a, uint32_t d_state, hipStream_t s) {
         a.n_embd % 4 || a.n_embd > 8192)
         return hipErrorInvalidValue;
     switch (d_state) {
-    case 64: hipLaunchKernelGGL(k_dn_step<64>, dim3(2, a.v_heads), dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL(k_dn_step<128>, dim3(4, a.v_heads), dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL(k_dn_step<64>, dim3(2 * a.v_heads), dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL(k_dn_step<128>, dim3(4 * a.v_heads), dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
