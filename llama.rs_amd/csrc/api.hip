@@ -334,12 +334,15 @@ int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y
         return fail(LRS_E_UNSUPPORTED, "the GEMM supports Q4_K and Q6_K weights");
     SETDEV(ctx);
     // the activation as bf16 planes (hi, and lo for precision 3) in context scratch
-    const size_t n = (size_t)m * w->v.n_in;
+    // (and the K-slice partials when the GEMM is split over K)
+    const size_t n = (size_t)m * w->v.n_in, ab = (n * 2 * (precision == 3 ? 2 : 1) + 255) & ~(size_t)255;
+    const size_t wb = gemm_work_bytes(m, w->v.n_out, w->v.n_in);
     void *buf = nullptr;
-    LRS_HIP(scratch(ctx, n * 2 * (precision == 3 ? 2 : 1), &buf));
+    LRS_HIP(scratch(ctx, ab + wb, &buf));
     __bf16 *hi = (__bf16 *)buf, *lo = precision == 3 ? hi + n : nullptr;
     LRS_HIP(launch_split_bf16(a_dev, n, hi, lo, ctx->stream));
-    LRS_HIP(launch_gemm(w->v, hi, lo, y_dev, m, w->v.n_out, precision, ctx->stream));
+    LRS_HIP(launch_gemm(w->v, hi, lo, y_dev, m, w->v.n_out, precision, ctx->stream, false,
+                        wb ? (float *)((char *)buf + ab) : nullptr));
     return LRS_OK;
 }
 

@@ -11,14 +11,14 @@
 //           lo*hi): ~2^-16 relative per product, for prefill whose logits must
 //           match the f32 reference
 //
-// Tiling.  A 256-thread workgroup owns a 128 (tokens) x 128 (weight rows)
-// output tile; each of its 4 wavefronts a 64 x 64 quarter = 2 x 2 MFMA tiles
-// of 32 x 32.  K advances 64 at a time (one Q4_K qs group / a quarter of a
-// Q6_K super-block): every thread stages 32 activations (f32 -> bf16) and
-// dequantizes 32 weights of one row (bit-exact f32 dequant as in dequant.rs,
-// then bf16) into a double-buffered LDS tile, and each wavefront issues 4 K16
-// steps x 4 tiles of MFMA.  LDS rows are padded to 72 bf16 so the 32 lanes
-// that read 32 different rows at one K offset hit distinct banks.
+// Tiling.  A 512-thread workgroup owns a 128 (tokens) x 128 (weight rows)
+// output tile; each of its 8 wavefronts a 64 x 32 part = 2 MFMA tiles of
+// 32 x 32.  K advances 64 at a time: every thread stages 16 activations
+// (bf16, split from f32 once per GEMM input) and dequantizes 16 weights of
+// one row (bit-exact f32 dequant as in dequant.rs, then bf16) into a
+// double-buffered LDS tile, and each wavefront issues 4 K16 steps x 2 tiles
+// of MFMA.  LDS rows are padded to 72 bf16 so the 32 lanes that read 32
+// different rows at one K offset hit distinct banks.
 #include "lrs_internal.h"
 #include "quant_dev.h"
 
@@ -38,45 +38,43 @@ struct GemmArgs {
     uint32_t M, N, K, units, ldy;
     uint32_t accum;           // 1: y += A W^T (residual add), 0: y = A W^T
     uint32_t nm, nn;          // output tiles along M and N
+    uint32_t ks;              // K slices: slice z writes part + z*M*N (then k_reduce_ks)
+    float *part;
 };
 
-__device__ __forceinline__ uint4 ldq16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+__device__ __forceinline__ u32x4 ldq16(const uint8_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
-// Raw GGUF bytes a thread needs for 32 consecutive weights of row n starting
-// at element e (e % 32 == 0): loaded one K-step ahead, dequantized after the
-// current step's matrix-core work has been issued
+// Raw GGUF bytes a thread needs for 16 consecutive weights of row n starting
+// at element e (e % 16 == 0), loaded three K-steps ahead and dequantized
+// after the current step's matrix-core work has been issued
 template <uint32_t T> struct WRaw;
-template <> struct WRaw<T_Q4_K> { uint4 hd, q0, q1; };
-template <> struct WRaw<T_Q6_K> { uint4 l0, l1, h0, h1; uint32_t sc, d; };
+template <> struct WRaw<T_Q4_K> { u32x4 hd, qs; };
+template <> struct WRaw<T_Q6_K> { u32x4 ql, qh; uint32_t sc, d; };
 
 template <uint32_t T>
 __device__ __forceinline__ void wload(const GemmArgs &g, uint32_t n, uint32_t e, WRaw<T> &w) {
     const uint32_t o = e & 255, r = n & 15;  // offset inside the super-block, row in the tile
+    const uint32_t l0 = o & 16;               // first or second 16 of a 32-element run
     const uint8_t *c = g.q + ((size_t)(n >> 4) * g.units + (e >> 8)) * tchunk_bytes(T);
     if constexpr (T == T_Q4_K) {
-        const uint32_t j = o >> 6;  // qs group
-        // qs bytes 32j..32j+31 = pieces (g, r) with g = 2(j&1), 2(j&1)+1 of half j>>1
-        const uint8_t *qp = c + 256 + 1024 * (j >> 1) + 16 * (16 * (2 * (j & 1)) + r);
+        // qs[32j + l0 ..+16), j = o / 64: piece (g, r), g = 2(j&1) + l0/16, of half j>>1
+        const uint32_t j = o >> 6, pg = 2 * (j & 1) + (l0 >> 4);
         w.hd = ldq16(c + 16 * r);
-        w.q0 = ldq16(qp);
-        w.q1 = ldq16(qp + 256);
+        w.qs = ldq16(c + 256 + 1024 * (j >> 1) + 16 * (16 * pg + r));
     } else {  // T_Q6_K
-        const uint32_t h = o >> 7, quarter = (o >> 5) & 3;  // elements 128h + 32 quarter + l
-        // ql[64h + 32(quarter&1) + l] and qh[32h + l]: pieces g = 2h (l < 16), 2h+1 (l >= 16)
-        const uint8_t *ql = c + 256 + 1024 * (quarter & 1) + 16 * (16 * (2 * h) + r);
-        const uint8_t *qh = c + 2304 + 16 * (16 * (2 * h) + r);
-        w.l0 = ldq16(ql);
-        w.l1 = ldq16(ql + 256);
-        w.h0 = ldq16(qh);
-        w.h1 = ldq16(qh + 256);
-        w.sc = *reinterpret_cast<const uint16_t *>(c + 16 * r + 8 * h + 2 * quarter);
+        // elements 128h + 32 quarter + l: ql[64h + 32(quarter&1) + l], qh[32h + l],
+        // pieces g = 2h + l0/16; scale byte 8h + l0/16 + 2 quarter
+        const uint32_t h = o >> 7, quarter = (o >> 5) & 3, pg = 2 * h + (l0 >> 4);
+        w.ql = ldq16(c + 256 + 1024 * (quarter & 1) + 16 * (16 * pg + r));
+        w.qh = ldq16(c + 2304 + 16 * (16 * pg + r));
+        w.sc = c[16 * r + 8 * h + (l0 >> 4) + 2 * quarter];
         w.d = *reinterpret_cast<const uint16_t *>(c + 3328 + 2 * r);
     }
 }
 
-// the 32 weights in f32, exactly as ggml_cpu::dequant (dequant.rs:101-258)
+// the 16 weights in f32, exactly as ggml_cpu::dequant (dequant.rs:101-258)
 template <uint32_t T>
-__device__ __forceinline__ void wdeq(const WRaw<T> &w, uint32_t e, float (&v)[32]) {
+__device__ __forceinline__ void wdeq(const WRaw<T> &w, uint32_t e, float (&v)[16]) {
     const uint32_t o = e & 255;
     if constexpr (T == T_Q4_K) {
         const uint32_t j = o >> 6, hi = (o >> 5) & 1;  // qs group, high nibbles
@@ -89,38 +87,36 @@ __device__ __forceinline__ void wdeq(const WRaw<T> &w, uint32_t e, float (&v)[32
         const uint32_t m = jj < 4 ? (bz & 63) : ((bw >> 4) | ((bz >> 6) << 4));
         const float dv = h2f((uint16_t)(w.hd.x & 0xFFFF)), mv = h2f((uint16_t)(w.hd.x >> 16));
         const float d1 = __fmul_rn(dv, (float)sc), m1 = __fmul_rn(mv, (float)m);
-        const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        const uint32_t qw[4] = {w.qs.x, w.qs.y, w.qs.z, w.qs.w};
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
+        for (int i = 0; i < 16; i++) {
             const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xFF;
             const uint32_t q = hi ? (byte >> 4) : (byte & 15);
             v[i] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
         }
     } else {  // T_Q6_K
         const uint32_t quarter = (o >> 5) & 3;
-        const float dv = h2f((uint16_t)w.d);
-        const float ds0 = __fmul_rn(dv, (float)(int8_t)(w.sc & 0xFF));
-        const float ds1 = __fmul_rn(dv, (float)(int8_t)(w.sc >> 8));
-        const uint32_t lw[8] = {w.l0.x, w.l0.y, w.l0.z, w.l0.w, w.l1.x, w.l1.y, w.l1.z, w.l1.w};
-        const uint32_t hw[8] = {w.h0.x, w.h0.y, w.h0.z, w.h0.w, w.h1.x, w.h1.y, w.h1.z, w.h1.w};
+        const float ds = __fmul_rn(h2f((uint16_t)w.d), (float)(int8_t)(w.sc & 0xFF));
+        const uint32_t lw[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
+        const uint32_t hw[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
+        for (int i = 0; i < 16; i++) {
             const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xFF;
             const uint32_t hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xFF;
             const uint32_t lo = quarter < 2 ? (lb & 15) : (lb >> 4);
             const int q = (int)(lo | (((hb >> (2 * quarter)) & 3) << 4)) - 32;
-            v[i] = __fmul_rn(i < 16 ? ds0 : ds1, (float)q);
+            v[i] = __fmul_rn(ds, (float)q);
         }
     }
 }
 
 __device__ __forceinline__ __bf16 to_bf16(float v) { return (__bf16)v; }
 
-// stores 32 values as bf16 (hi) and, for PREC 3, the bf16 remainders (lo)
+// stores 16 values as bf16 (hi) and, for PREC 3, the bf16 remainders (lo)
 template <int PREC>
-__device__ __forceinline__ void put32(__bf16 *hi, __bf16 *lo, const float (&v)[32]) {
+__device__ __forceinline__ void put16(__bf16 *hi, __bf16 *lo, const float (&v)[16]) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
+    for (int c = 0; c < 2; c++) {
         bf16x8 h, l;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -133,120 +129,145 @@ __device__ __forceinline__ void put32(__bf16 *hi, __bf16 *lo, const float (&v)[3
     }
 }
 
-// Software pipeline over K: step k's operands sit in LDS buffer k & 1 while
-// step k+1's activations (already bf16, split once per GEMM input by
-// k_split_bf16) and raw weight bytes are in flight to registers; the
-// wavefronts issue step k's MFMAs, then dequantize step k+1 into the other
-// buffer (VALU work that overlaps the matrix cores), then one barrier.
+// 512 threads = 8 wavefronts, each a 64 (tokens) x 32 (rows) part of the
+// 128 x 128 tile (2 MFMA tiles of 32 x 32).  Software pipeline over K: step
+// k's operands sit in LDS buffer k & 1; the activations (already bf16, split
+// once per GEMM input by k_split_bf16) and raw weight bytes of steps k+1..k+3
+// are in flight to four rotating register sets; each step the wavefronts
+// load step k+3, issue step k's MFMAs, then dequantize step k+1 into the
+// other buffer (VALU work that overlaps the matrix cores), then one barrier.
+// K-quant rows are whole super-blocks (K % 256 == 0), so the loop runs four
+// steps per trip with no tail.
 //
 // Tile order: workgroup b runs on XCD b % 8 (round-robin dispatch); the
 // tiles are numbered M-block-major and XCD x takes the x-th contiguous run
 // of them, so the workgroups of one XCD share one or two activation blocks,
 // which stay in that XCD's L2.
 template <uint32_t T, int PREC>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs g) {
+__global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     constexpr int NS = PREC == 3 ? 2 : 1;  // hi (+ lo) planes
     __shared__ __attribute__((aligned(16))) __bf16 As[2][NS][GM_BM * GM_LD];
     __shared__ __attribute__((aligned(16))) __bf16 Ws[2][NS][GM_BN * GM_LD];
-    const uint32_t ntile = g.nm * g.nn, per = (ntile + 7) / 8;
-    const uint32_t t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (t >= ntile) return;
+    const uint32_t ntile = g.nm * g.nn * g.ks, per = (ntile + 7) / 8;
+    const uint32_t t0 = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (t0 >= ntile) return;
+    const uint32_t kz = t0 / (g.nm * g.nn), t = t0 % (g.nm * g.nn);  // K slice, output tile
+    const uint32_t kspan = g.K / g.ks;                                 // a multiple of 256
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t m0 = (t / g.nn) * GM_BM, n0 = (t % g.nn) * GM_BN;
-    const uint32_t wm = wave >> 1, wn = wave & 1;  // wave's 64 x 64 quarter
-    // staging roles: thread t handles row t/2, half t%2 (32 of the 64 K)
-    const uint32_t sr = tid >> 1, sh = (tid & 1) * 32;
+    const uint32_t wm = wave >> 2, wn = wave & 3;  // wave's 64 x 32 part
+    // staging roles: thread t handles row t/4, K quarter t%4 (16 of the 64)
+    const uint32_t sr = tid >> 2, sq = (tid & 3) * 16;
     const uint32_t am = min(m0 + sr, g.M - 1), wr = min(n0 + sr, g.N - 1);
-    const size_t aoff = (size_t)am * g.K + sh;
+    const size_t aoff = (size_t)am * g.K + sq + (size_t)kz * kspan;
+    const uint32_t kbase = kz * kspan;  // weight element offset of the slice
 
-    f32x16 acc[2][2];
+    f32x16 acc[2];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
 
-    // two register sets: step k + 2 is loaded while step k is multiplied and
-    // step k + 1 dequantized
-    u32x4 a0[NS][4], a1[NS][4];
-    WRaw<T> w0, w1;
+    u32x4 a0[NS][2], a1[NS][2], a2[NS][2], a3[NS][2];
+    WRaw<T> w0, w1, w2, w3;
 #define LRS_GFETCH(A, W, K0)                                                                  \
     do {                                                                                      \
         _Pragma("unroll") for (int p = 0; p < NS; p++) {                                       \
             const u32x4 *ap = reinterpret_cast<const u32x4 *>((p == 0 ? g.ahi : g.alo) + aoff + (K0)); \
-            _Pragma("unroll") for (int c = 0; c < 4; c++) A[p][c] = ap[c];                    \
+            A[p][0] = ap[0];                                                                  \
+            A[p][1] = ap[1];                                                                  \
         }                                                                                     \
-        wload<T>(g, wr, (K0) + sh, W);                                                        \
+        wload<T>(g, wr, kbase + (K0) + sq, W);                                                \
     } while (0)
 #define LRS_GSTAGE(BUF, A, W, K0)                                                             \
     do {                                                                                      \
-        _Pragma("unroll") for (int p = 0; p < NS; p++)                                         \
-            _Pragma("unroll") for (int c = 0; c < 4; c++)                                      \
-                *reinterpret_cast<u32x4 *>(&As[BUF][p][sr * GM_LD + sh + 8 * c]) = A[p][c];    \
-        float v_[32];                                                                         \
-        wdeq<T>(W, (K0) + sh, v_);                                                            \
-        put32<PREC>(&Ws[BUF][0][sr * GM_LD + sh], &Ws[BUF][NS - 1][sr * GM_LD + sh], v_);     \
+        _Pragma("unroll") for (int p = 0; p < NS; p++) {                                       \
+            *reinterpret_cast<u32x4 *>(&As[BUF][p][sr * GM_LD + sq]) = A[p][0];               \
+            *reinterpret_cast<u32x4 *>(&As[BUF][p][sr * GM_LD + sq + 8]) = A[p][1];           \
+        }                                                                                     \
+        float v_[16];                                                                         \
+        wdeq<T>(W, kbase + (K0) + sq, v_);                                                    \
+        put16<PREC>(&Ws[BUF][0][sr * GM_LD + sq], &Ws[BUF][NS - 1][sr * GM_LD + sq], v_);     \
     } while (0)
     auto mma = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int ks = 0; ks < GM_BK / 16; ks++) {
             const uint32_t kk = 16 * ks + 8 * (lane >> 5);
-            bf16x8 a[NS][2], b[NS][2];
+            bf16x8 a[NS][2], b[NS];
 #pragma unroll
-            for (int p = 0; p < NS; p++)
+            for (int p = 0; p < NS; p++) {
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
+                for (int u = 0; u < 2; u++)
                     a[p][u] = *reinterpret_cast<const bf16x8 *>(&As[buf][p][(64 * wm + 32 * u + (lane & 31)) * GM_LD + kk]);
-                    b[p][u] = *reinterpret_cast<const bf16x8 *>(&Ws[buf][p][(64 * wn + 32 * u + (lane & 31)) * GM_LD + kk]);
-                }
+                b[p] = *reinterpret_cast<const bf16x8 *>(&Ws[buf][p][(32 * wn + (lane & 31)) * GM_LD + kk]);
+            }
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    if constexpr (PREC == 3) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0][j], acc[i][j], 0, 0, 0);
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1][j], acc[i][j], 0, 0, 0);
-                    }
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 2; i++) {
+                if constexpr (PREC == 3) {
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0], acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1], acc[i], 0, 0, 0);
                 }
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0], acc[i], 0, 0, 0);
+            }
         }
     };
 
-    // nk is even (K % 128 == 0): two steps per trip, no branch in the loop;
-    // the last trip's look-ahead loads repeat the final step (unused)
-    const uint32_t nk = g.K / GM_BK;
+    const uint32_t nk = kspan / GM_BK;  // a multiple of 4
+    auto kc = [&](uint32_t k) { return min(k, nk - 1) * GM_BK; };  // look-ahead past the end repeats the last step (unused)
     LRS_GFETCH(a0, w0, 0);
-    LRS_GFETCH(a1, w1, GM_BK);
+    LRS_GFETCH(a1, w1, kc(1));
+    LRS_GFETCH(a2, w2, kc(2));
     LRS_GSTAGE(0, a0, w0, 0);
     __syncthreads();
-    for (uint32_t k = 0; k < nk; k += 2) {
-        LRS_GFETCH(a0, w0, min(k + 2, nk - 1) * GM_BK);
+    for (uint32_t k = 0; k < nk; k += 4) {
+        LRS_GFETCH(a3, w3, kc(k + 3));
         mma(0);
-        LRS_GSTAGE(1, a1, w1, (k + 1) * GM_BK);
+        LRS_GSTAGE(1, a1, w1, kc(k + 1));
         __syncthreads();
-        LRS_GFETCH(a1, w1, min(k + 3, nk - 1) * GM_BK);
+        LRS_GFETCH(a0, w0, kc(k + 4));
         mma(1);
-        LRS_GSTAGE(0, a0, w0, min(k + 2, nk - 1) * GM_BK);
+        LRS_GSTAGE(0, a2, w2, kc(k + 2));
+        __syncthreads();
+        LRS_GFETCH(a1, w1, kc(k + 5));
+        mma(0);
+        LRS_GSTAGE(1, a3, w3, kc(k + 3));
+        __syncthreads();
+        LRS_GFETCH(a2, w2, kc(k + 6));
+        mma(1);
+        LRS_GSTAGE(0, a0, w0, kc(k + 4));
         __syncthreads();
     }
 #undef LRS_GFETCH
 #undef LRS_GSTAGE
     // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
+    const uint32_t n = n0 + 32 * wn + (lane & 31);
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint32_t n = n0 + 64 * wn + 32 * j + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < g.M && n < g.N) {
+        for (int r = 0; r < 16; r++) {
+            const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m < g.M && n < g.N) {
+                if (g.ks > 1) {
+                    g.part[((size_t)kz * g.M + m) * g.N + n] = acc[i][r];
+                } else {
                     float *o = g.y + (size_t)m * g.ldy + n;
-                    *o = g.accum ? *o + acc[i][j][r] : acc[i][j][r];
+                    *o = g.accum ? *o + acc[i][r] : acc[i][r];
                 }
             }
         }
+}
+
+// y[m][n] (+)= sum over the K slices of part[z][m][n], slices in order
+__global__ __launch_bounds__(256) void k_reduce_ks(const float *__restrict__ part, float *__restrict__ y,
+                                                   uint32_t M, uint32_t N, uint32_t ldy, uint32_t ks,
+                                                   uint32_t accum) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)M * N) return;
+    const uint32_t m = (uint32_t)(i / N), n = (uint32_t)(i % N);
+    float v = part[i];
+    for (uint32_t z = 1; z < ks; z++) v += part[(size_t)z * M * N + i];
+    float *o = y + (size_t)m * ldy + n;
+    *o = accum ? *o + v : v;
 }
 
 // a -> bf16 hi (round to nearest even) and, if lo, bf16(a - hi): the
@@ -279,9 +300,37 @@ hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, h
     return hipGetLastError();
 }
 
+// K slices for a GEMM with fewer output tiles than CUs (the long-K o / down
+// projections): the slice count ks divides K into whole super-blocks and
+// minimises the rounds of 256 workgroups (one per CU) each slice-sized unit
+// of work takes, ceil(tiles * ks / 256) / ks, plus a small charge for the
+// reduction pass; ties keep fewer slices
+uint32_t gemm_ksplit(uint32_t M, uint32_t N, uint32_t K) {
+    const uint32_t tiles = ((M + GM_BM - 1) / GM_BM) * ((N + GM_BN - 1) / GM_BN);
+    const uint32_t units = K / 256;
+    uint32_t best = 1;
+    if (tiles >= 256) return 1;  // a full round already; partial traffic would cost more
+    double best_cost = 1.0;
+    for (uint32_t ks = 2; ks <= 8; ks++) {
+        if (units % ks || units / ks < 4) continue;
+        const double cost = (double)((tiles * ks + 255) / 256) / ks + 0.05;
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = ks;
+        }
+    }
+    return best;
+}
+
+// scratch of the K-sliced form (at most 8 * M * N floats)
+size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K) {
+    const uint32_t ks = gemm_ksplit(M, N, K);
+    return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
+}
+
 hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
-                       uint32_t ldy, int prec, hipStream_t s, bool accum) {
-    if (M == 0 || w.n_in % (2 * GM_BK) || (prec == 3 && !alo)) return hipErrorInvalidValue;
+                       uint32_t ldy, int prec, hipStream_t s, bool accum, float *work) {
+    if (M == 0 || w.n_in % (4 * GM_BK) || (prec == 3 && !alo)) return hipErrorInvalidValue;
     GemmArgs g;
     g.ahi = ahi;
     g.alo = alo;
@@ -295,12 +344,19 @@ hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float
     g.accum = accum ? 1u : 0u;
     g.nm = (M + GM_BM - 1) / GM_BM;
     g.nn = (w.n_out + GM_BN - 1) / GM_BN;
-    const uint32_t grid = 8 * ((g.nm * g.nn + 7) / 8);
+    g.ks = work ? gemm_ksplit(M, g.N, g.K) : 1;
+    g.part = work;
+    const uint32_t grid = 8 * ((g.nm * g.nn * g.ks + 7) / 8);
     void (*fn)(GemmArgs) = nullptr;
     if (w.type == T_Q4_K) fn = prec == 3 ? k_gemm<T_Q4_K, 3> : k_gemm<T_Q4_K, 1>;
     else if (w.type == T_Q6_K) fn = prec == 3 ? k_gemm<T_Q6_K, 3> : k_gemm<T_Q6_K, 1>;
     else return hipErrorNotSupported;
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(256), 0, s, g);
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(512), 0, s, g);
+    if (g.ks > 1) {
+        const size_t n = (size_t)M * g.N;
+        hipLaunchKernelGGL(k_reduce_ks, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, work, y,
+                           M, g.N, ldy, g.ks, g.accum);
+    }
     return hipGetLastError();
 }
 

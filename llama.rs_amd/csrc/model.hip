@@ -100,6 +100,7 @@ struct lrs_model {
     uint32_t pb_cap = 0;
     float *pX = nullptr, *pXN, *pQt, *pKt, *pVt, *pQ, *pATT, *pG, *pU;
     __bf16 *pA16 = nullptr;  // bf16 hi / lo planes of the current GEMM input
+    float *pWork = nullptr;  // K-slice partials of the split GEMMs
     uint32_t *ptok;
     _Float16 *kv;                // all layers' caches
     uint32_t *step_host;         // pinned
@@ -851,6 +852,8 @@ static int ensure_prefill(lrs_model *m) {
         (rc = dev_alloc(m, B * c.n_ff * 4, (void **)&m->pU)) ||
         (rc = dev_alloc(m, B * std::max<size_t>(std::max<size_t>(c.n_embd, qd), c.n_ff) * 4,
                         (void **)&m->pA16)) ||
+        // K-sliced o / down GEMMs: at most 8 slices of [rows][n_embd] partials
+        (rc = dev_alloc(m, 8 * B * c.n_embd * 4, (void **)&m->pWork)) ||
         (rc = dev_alloc(m, B * 4, (void **)&m->ptok)))
         return rc;
     m->pb_cap = PREFILL_BLOCK;
@@ -884,14 +887,14 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
         LRS_HIP(launch_attn_prefill(m->pQ, L.kc, L.vc, m->pATT, nb, pos0, c.n_head, c.n_head_kv,
                                     c.head_dim, c.ctx, s));
         LRS_HIP(split(m->pATT, (size_t)nb * qd));
-        LRS_HIP(launch_gemm(L.o->v, hi, lo(nb, qd), m->pX, nb, E, P, s, true));
+        LRS_HIP(launch_gemm(L.o->v, hi, lo(nb, qd), m->pX, nb, E, P, s, true, m->pWork));
         LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, m->pXN, s));
         LRS_HIP(split(m->pXN, (size_t)nb * E));
         LRS_HIP(launch_gemm(L.gate->v, hi, lo(nb, E), m->pG, nb, c.n_ff, P, s));
         LRS_HIP(launch_gemm(L.up->v, hi, lo(nb, E), m->pU, nb, c.n_ff, P, s));
         LRS_HIP(launch_swiglu_rows(m->pG, m->pU, (size_t)nb * c.n_ff, s));
         LRS_HIP(split(m->pG, (size_t)nb * c.n_ff));
-        LRS_HIP(launch_gemm(L.down->v, hi, lo(nb, c.n_ff), m->pX, nb, E, P, s, true));
+        LRS_HIP(launch_gemm(L.down->v, hi, lo(nb, c.n_ff), m->pX, nb, E, P, s, true, m->pWork));
     }
     return LRS_OK;
 }

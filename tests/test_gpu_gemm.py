@@ -34,7 +34,9 @@ def rel_l2(a, b):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q6_K])
-@pytest.mark.parametrize("m,n,k", [(1, 200, 512), (7, 128, 256), (130, 300, 768), (256, 256, 1024)])
+# the last two split K over 2 and 4 workgroups (few output tiles, long K)
+@pytest.mark.parametrize("m,n,k", [(1, 200, 512), (7, 128, 256), (130, 300, 768), (256, 256, 1024),
+                                   (64, 256, 4096), (96, 128, 8192)])
 def test_gemm_matches_oracle(lrs, orc, ctx, t, m, n, k):
     w = orc.gen_weight(t, 31 + m + n, n, k, mode=1)
     deq = orc.dequant(t, w).reshape(n, k)
