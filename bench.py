@@ -11,10 +11,12 @@ Workloads:
           512..511+K, the config's 128 tokens after a 512-token prompt).
   q8      config 1: one Q8_0 4096x4096 matvec (d ~ U[1e-3,1e-2], qs ~ U[-127,127],
           x ~ N(0,1) f32); a step is one lrs_matvec_dev call (activation pack +
-          matrix-core matvec), rotating over 16 weight copies (285 MB, beyond
-          the 256 MB MALL) so every weight byte comes from HBM.
+          matrix-core matvec), 16 of them over 16 weight copies (285 MB, beyond
+          the 256 MB MALL, so every weight byte comes from HBM) captured into
+          one HIP graph and replayed.
   layer   config 2: one Qwen2.5-14B-shaped layer matvec set, weights rotated
-          over 4 copies so every byte comes from HBM; a step is 7 matvecs.
+          over 4 copies so every byte comes from HBM; a step is 7 matvecs
+          (one captured HIP graph per copy).
   hybrid  config 4: 27B-scale hybrid model (64 layers, gated full attention
           every 4th: 24 q / 4 kv x 256; 48 gated delta-net layers of 16 heads
           x 128x128 f32 state), random-init Q4_K_M; the 512-token prompt is
@@ -299,36 +301,46 @@ def bench_layer(lrs, ctx, steps, warmup):
     xbuf, ybuf = ctx.alloc(4 * 13824), ctx.alloc(4 * 13824)
     xbuf.upload(np.random.default_rng(7).standard_normal(13824).astype(np.float32))
 
-    def step(s):
-        for w in mats[s % copies]:
-            w.matvec_dev(xbuf, ybuf)
-
+    # one graph per copy: the 7 matvecs of the set (pack + matrix-core matvec each)
+    mats[0][-1].matvec_dev(xbuf, ybuf)  # sizes the context scratch outside the capture
+    ctx.sync()
+    graphs = [ctx.capture(lambda c=c: [w.matvec_dev(xbuf, ybuf) for w in mats[c]])
+              for c in range(copies)]
     for s in range(warmup):
-        step(s)
+        graphs[s % copies].launch()
     ctx.sync()
     ctx.timer_start()
     for s in range(steps):
-        step(s)
+        graphs[s % copies].launch()
     ms = ctx.timer_stop() / steps
+    for g in graphs:
+        g.close()
     return dict(ms=ms, bytes=set_bytes, gbs=set_bytes / (ms * 1e-3) / 1e9)
 
 
 def bench_q8(lrs, ctx, steps, warmup):
+    """16 matvecs (one per weight copy) captured into one HIP graph; a step
+    is one matvec, the graph replayed ceil(steps / 16) times."""
     n = 4096
     copies = 16
     ws = [lrs.Weight.generate(ctx, Q8_0, 900 + c, n, n, mode=0, d_lo=1e-3, d_hi=1e-2)
           for c in range(copies)]
     xbuf, ybuf = ctx.alloc(4 * n), ctx.alloc(4 * n)
     xbuf.upload(np.random.default_rng(1234).standard_normal(n).astype(np.float32))
-    for s in range(warmup):
-        ws[s % copies].matvec_dev(xbuf, ybuf)
+    ws[0].matvec_dev(xbuf, ybuf)  # sizes the context scratch outside the capture
+    ctx.sync()
+    g = ctx.capture(lambda: [w.matvec_dev(xbuf, ybuf) for w in ws])
+    reps = max(1, (steps + copies - 1) // copies)
+    for _ in range(max(1, warmup // copies)):
+        g.launch()
     ctx.sync()
     ctx.timer_start()
-    for s in range(steps):
-        ws[s % copies].matvec_dev(xbuf, ybuf)
-    us = ctx.timer_stop() * 1e3 / steps
+    for _ in range(reps):
+        g.launch()
+    us = ctx.timer_stop() * 1e3 / (reps * copies)
+    g.close()
     b = gguf_bytes(Q8_0, n, n) + 4 * n + 4 * n
-    return dict(us=us, bytes=b, gbs=b / us / 1e3)
+    return dict(us=us, bytes=b, gbs=b / us / 1e3, matvecs=reps * copies)
 
 
 def bench_gemm(lrs, ctx, steps, warmup, m, precision):

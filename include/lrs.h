@@ -137,6 +137,20 @@ int lrs_dev_alloc(lrs_ctx *ctx, size_t bytes, void **dptr);
 int lrs_dev_free(lrs_ctx *ctx, void *dptr);
 int lrs_copy_h2d(lrs_ctx *ctx, void *dst_dev, const void *src, size_t bytes);
 int lrs_copy_d2h(lrs_ctx *ctx, void *dst, const void *src_dev, size_t bytes);
+/* Graph capture of the asynchronous entry points (lrs_matvec_dev,
+ * lrs_gemm_dev, copies): between lrs_capture_begin and lrs_capture_end the
+ * calls on the context stream are recorded into a HIP graph instead of run;
+ * lrs_graph_launch replays it on the context stream (async).  The
+ * resolve-once pattern of the reference's recorded command buffers
+ * (resident_forward.rs build_plan, :3678-3762) for kernel-level callers.
+ * Blocking calls, and a first call whose context scratch must grow, fail
+ * inside a capture: make one uncaptured call of the same shape first. */
+typedef struct lrs_graph lrs_graph;
+int lrs_capture_begin(lrs_ctx *ctx);
+int lrs_capture_end(lrs_ctx *ctx, lrs_graph **out);
+int lrs_graph_launch(lrs_graph *g);
+void lrs_graph_destroy(lrs_graph *g);
+
 /* HIP events on the context stream: start, then stop returns elapsed ms. */
 int lrs_timer_start(lrs_ctx *ctx);
 int lrs_timer_stop(lrs_ctx *ctx, float *ms);

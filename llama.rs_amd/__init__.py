@@ -69,6 +69,10 @@ def _load() -> C.CDLL:
         "lrs_copy_h2d": (i32, [vp, vp, vp, sz]),
         "lrs_copy_d2h": (i32, [vp, vp, vp, sz]),
         "lrs_matvec_set_geom": (i32, [i32, i32, i32]),
+        "lrs_capture_begin": (i32, [vp]),
+        "lrs_capture_end": (i32, [vp, pvp]),
+        "lrs_graph_launch": (i32, [vp]),
+        "lrs_graph_destroy": (None, [vp]),
         "lrs_timer_start": (i32, [vp]),
         "lrs_timer_stop": (i32, [vp, C.POINTER(C.c_float)]),
     }
@@ -93,6 +97,28 @@ def _ptr(a: np.ndarray) -> int:
 
 def row_bytes(t: int, n_in: int) -> int:
     return n_in // BLOCK[t] * TYPE_SIZE[t]
+
+
+class Graph:
+    """A captured sequence of device work (lrs_capture_end); launch() replays
+    it on the context stream."""
+
+    def __init__(self, ctx, h):
+        self.ctx, self.h = ctx, h
+
+    def launch(self) -> None:
+        check(lib.lrs_graph_launch(self.h))
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib.lrs_graph_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Context:
@@ -121,6 +147,20 @@ class Context:
 
     def timer_start(self) -> None:
         check(lib.lrs_timer_start(self.h))
+
+    def capture(self, fn) -> "Graph":
+        """Records the device work fn() enqueues on this context's stream
+        (asynchronous *_dev calls only) into a replayable HIP graph."""
+        check(lib.lrs_capture_begin(self.h))
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            rc = lib.lrs_capture_end(self.h, C.byref(g))
+        check(rc)
+        graph = Graph(self, g)
+        self._models.add(graph)
+        return graph
 
     def timer_stop(self) -> float:
         ms = C.c_float()

@@ -74,6 +74,11 @@ static hipError_t scratch(lrs_ctx *ctx, size_t bytes, void **p) {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     lrs_ctx_scratch &s = g_scratch[ctx];
     if (s.n < bytes) {
+        // growing frees the old buffer after a stream sync, which a stream
+        // being captured into a graph cannot do
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return hipErrorStreamCaptureUnsupported;
         if (s.p) {
             hipError_t e = hipStreamSynchronize(ctx->stream);
             if (e != hipSuccess) return e;
@@ -382,6 +387,51 @@ int lrs_copy_d2h(lrs_ctx *ctx, void *dst, const void *src_dev, size_t bytes) {
     LRS_HIP(hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
     LRS_HIP(hipStreamSynchronize(ctx->stream));
     return LRS_OK;
+}
+
+// ---- graph capture of the asynchronous (*_dev) entry points ----
+struct lrs_graph {
+    lrs_ctx *ctx;
+    hipGraphExec_t exec;
+};
+
+int lrs_capture_begin(lrs_ctx *ctx) {
+    if (!ctx) return fail(LRS_E_ARG, "null ctx");
+    SETDEV(ctx);
+    LRS_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return LRS_OK;
+}
+
+int lrs_capture_end(lrs_ctx *ctx, lrs_graph **out) {
+    if (!ctx || !out) return fail(LRS_E_ARG, "null argument");
+    SETDEV(ctx);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return hip_fail(e, "hipStreamEndCapture (a call inside the capture failed or synchronised?)");
+    }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *out = new lrs_graph{ctx, x};
+    return LRS_OK;
+}
+
+int lrs_graph_launch(lrs_graph *g) {
+    if (!g) return fail(LRS_E_ARG, "null graph");
+    SETDEV(g->ctx);
+    LRS_HIP(hipGraphLaunch(g->exec, g->ctx->stream));
+    return LRS_OK;
+}
+
+void lrs_graph_destroy(lrs_graph *g) {
+    if (!g) return;
+    (void)hipSetDevice(g->ctx->device);
+    (void)hipStreamSynchronize(g->ctx->stream);
+    (void)hipGraphExecDestroy(g->exec);
+    delete g;
 }
 
 int lrs_timer_start(lrs_ctx *ctx) {

@@ -267,3 +267,37 @@ def test_matvec_baseline_config_shapes(lrs, orc, ctx, name, t, n_in, n_out):
     got = W.matvec(x)
     ref = orc.matvec(t, host, n_in, n_out, x, threads=THREADS)
     assert rel_l2(got, ref) < MATVEC_TOL, rel_l2(got, ref)
+
+
+def test_captured_graph_replays_match_eager(lrs, orc, ctx):
+    """lrs_capture_begin/end + lrs_graph_launch: two matvecs and a GEMM recorded
+    once, replayed three times with eager work and synchronisations between
+    the replays; every replay equals the eager result bit for bit."""
+    n_in, n_out, m = 1024, 512, 64
+    wa = lrs.Weight.upload(ctx, 12, orc.gen_weight(12, 71, n_out, n_in, mode=1), n_in, n_out)
+    wb = lrs.Weight.upload(ctx, 14, orc.gen_weight(14, 72, n_out, n_in, mode=1), n_in, n_out)
+    rng = np.random.default_rng(3)
+    x = ctx.alloc(4 * n_in * m)
+    x.upload(rng.standard_normal(n_in * m).astype(np.float32))
+    ya, yb, yg = ctx.alloc(4 * n_out), ctx.alloc(4 * n_out), ctx.alloc(4 * n_out * m)
+
+    def work():
+        wa.matvec_dev(x, ya)
+        wb.matvec_dev(x, yb)
+        wa.gemm_dev(x, yg, m, precision=3)
+
+    work()  # eager (also sizes the context scratch outside the capture)
+    ctx.sync()
+    want = [b.download(np.float32, k) for b, k in ((ya, n_out), (yb, n_out), (yg, n_out * m))]
+    g = ctx.capture(work)
+    for rep in range(3):
+        for b in (ya, yb, yg):
+            b.upload(np.full(b.nbytes // 4, np.nan, np.float32))
+        g.launch()
+        ctx.sync()
+        got = [b.download(np.float32, k) for b, k in ((ya, n_out), (yb, n_out), (yg, n_out * m))]
+        for a, b in zip(got, want):
+            assert np.array_equal(a, b), rep
+        wb.matvec_dev(x, ya)  # eager work between the replays
+        ctx.sync()
+    g.close()
