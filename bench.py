@@ -94,7 +94,7 @@ def read_traffic(op):
     """HBM bytes per launch of `op` from the committed rocprofv3 counter
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
     calibration), or None when no summary covers it."""
-    path = os.path.join(REPO, "profiles", "pmc_decode_32b_q4km.md")
+    path = os.path.join(REPO, "profiles", "pmc_decode_q4km.md")
     try:
         txt = open(path).read()
     except OSError:
@@ -513,7 +513,8 @@ def main():
                           "effective_gbs": round(eff_gbs, 1)},
                "roofline": {"bound": "hbm", "achieved": round(d["gbs"], 1),
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
+                            "traffic": read_traffic("hybrid_" + dom),
                             "kernel": OP_NAMES[dom], "op": dom, "kernel_us": round(d["us"], 3),
                             "bytes_per_launch": d["bytes"]},
                "cpu_baseline": cpu}
