@@ -341,7 +341,7 @@ int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y
     // the activation as bf16 planes (hi, and lo for precision 3) in context scratch
     // (and the K-slice partials when the GEMM is split over K)
     const size_t n = (size_t)m * w->v.n_in, ab = (n * 2 * (precision == 3 ? 2 : 1) + 255) & ~(size_t)255;
-    const size_t wb = gemm_work_bytes(m, w->v.n_out, w->v.n_in);
+    const size_t wb = gemm_work_bytes(m, w->v.n_out, w->v.n_in, precision);
     void *buf = nullptr;
     LRS_HIP(scratch(ctx, ab + wb, &buf));
     __bf16 *hi = (__bf16 *)buf, *lo = precision == 3 ? hi + n : nullptr;

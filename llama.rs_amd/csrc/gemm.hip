@@ -28,7 +28,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 
-constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 64;
+constexpr int GM_BN = 128, GM_BK = 64;
 constexpr int GM_LD = GM_BK + 8;  // padded LDS row (bf16 elements)
 
 struct GemmArgs {
@@ -143,10 +143,12 @@ __device__ __forceinline__ void put16(__bf16 *hi, __bf16 *lo, const float (&v)[1
 // tiles are numbered M-block-major and XCD x takes the x-th contiguous run
 // of them, so the workgroups of one XCD share one or two activation blocks,
 // which stay in that XCD's L2.
-template <uint32_t T, int PREC>
+template <uint32_t T, int PREC, int BM>
 __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     constexpr int NS = PREC == 3 ? 2 : 1;  // hi (+ lo) planes
-    __shared__ __attribute__((aligned(16))) __bf16 As[2][NS][GM_BM * GM_LD];
+    constexpr int MT = BM / 64;            // 32-row MFMA tiles per wavefront
+    constexpr int AR = BM / 128;           // activation rows staged per thread
+    __shared__ __attribute__((aligned(16))) __bf16 As[2][NS][BM * GM_LD];
     __shared__ __attribute__((aligned(16))) __bf16 Ws[2][NS][GM_BN * GM_LD];
     const uint32_t ntile = g.nm * g.nn * g.ks, per = (ntile + 7) / 8;
     const uint32_t t0 = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
@@ -154,37 +156,42 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     const uint32_t kz = t0 / (g.nm * g.nn), t = t0 % (g.nm * g.nn);  // K slice, output tile
     const uint32_t kspan = g.K / g.ks;                                 // a multiple of 256
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t m0 = (t / g.nn) * GM_BM, n0 = (t % g.nn) * GM_BN;
-    const uint32_t wm = wave >> 2, wn = wave & 3;  // wave's 64 x 32 part
+    const uint32_t m0 = (t / g.nn) * BM, n0 = (t % g.nn) * GM_BN;
+    const uint32_t wm = wave >> 2, wn = wave & 3;  // wave's BM/2 x 32 part
     // staging roles: thread t handles row t/4, K quarter t%4 (16 of the 64)
     const uint32_t sr = tid >> 2, sq = (tid & 3) * 16;
-    const uint32_t am = min(m0 + sr, g.M - 1), wr = min(n0 + sr, g.N - 1);
-    const size_t aoff = (size_t)am * g.K + sq + (size_t)kz * kspan;
+    const uint32_t wr = min(n0 + sr, g.N - 1);
+    size_t aoff[AR];  // activation rows sr, sr + 128, ...
+#pragma unroll
+    for (int j = 0; j < AR; j++)
+        aoff[j] = (size_t)min(m0 + sr + 128 * j, g.M - 1) * g.K + sq + (size_t)kz * kspan;
     const uint32_t kbase = kz * kspan;  // weight element offset of the slice
 
-    f32x16 acc[2];
+    f32x16 acc[MT];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
 
-    u32x4 a0[NS][2], a1[NS][2], a2[NS][2], a3[NS][2];
+    u32x4 a0[NS][AR][2], a1[NS][AR][2], a2[NS][AR][2], a3[NS][AR][2];
     WRaw<T> w0, w1, w2, w3;
 #define LRS_GFETCH(A, W, K0)                                                                  \
     do {                                                                                      \
-        _Pragma("unroll") for (int p = 0; p < NS; p++) {                                       \
-            const u32x4 *ap = reinterpret_cast<const u32x4 *>((p == 0 ? g.ahi : g.alo) + aoff + (K0)); \
-            A[p][0] = ap[0];                                                                  \
-            A[p][1] = ap[1];                                                                  \
-        }                                                                                     \
+        _Pragma("unroll") for (int p = 0; p < NS; p++)                                         \
+            _Pragma("unroll") for (int j = 0; j < AR; j++) {                                   \
+                const u32x4 *ap = reinterpret_cast<const u32x4 *>((p == 0 ? g.ahi : g.alo) + aoff[j] + (K0)); \
+                A[p][j][0] = ap[0];                                                           \
+                A[p][j][1] = ap[1];                                                           \
+            }                                                                                 \
         wload<T>(g, wr, kbase + (K0) + sq, W);                                                \
     } while (0)
 #define LRS_GSTAGE(BUF, A, W, K0)                                                             \
     do {                                                                                      \
-        _Pragma("unroll") for (int p = 0; p < NS; p++) {                                       \
-            *reinterpret_cast<u32x4 *>(&As[BUF][p][sr * GM_LD + sq]) = A[p][0];               \
-            *reinterpret_cast<u32x4 *>(&As[BUF][p][sr * GM_LD + sq + 8]) = A[p][1];           \
-        }                                                                                     \
+        _Pragma("unroll") for (int p = 0; p < NS; p++)                                         \
+            _Pragma("unroll") for (int j = 0; j < AR; j++) {                                   \
+                *reinterpret_cast<u32x4 *>(&As[BUF][p][(sr + 128 * j) * GM_LD + sq]) = A[p][j][0];     \
+                *reinterpret_cast<u32x4 *>(&As[BUF][p][(sr + 128 * j) * GM_LD + sq + 8]) = A[p][j][1]; \
+            }                                                                                 \
         float v_[16];                                                                         \
         wdeq<T>(W, kbase + (K0) + sq, v_);                                                    \
         put16<PREC>(&Ws[BUF][0][sr * GM_LD + sq], &Ws[BUF][NS - 1][sr * GM_LD + sq], v_);     \
@@ -193,16 +200,16 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
 #pragma unroll
         for (int ks = 0; ks < GM_BK / 16; ks++) {
             const uint32_t kk = 16 * ks + 8 * (lane >> 5);
-            bf16x8 a[NS][2], b[NS];
+            bf16x8 a[NS][MT], b[NS];
 #pragma unroll
             for (int p = 0; p < NS; p++) {
 #pragma unroll
-                for (int u = 0; u < 2; u++)
-                    a[p][u] = *reinterpret_cast<const bf16x8 *>(&As[buf][p][(64 * wm + 32 * u + (lane & 31)) * GM_LD + kk]);
+                for (int u = 0; u < MT; u++)
+                    a[p][u] = *reinterpret_cast<const bf16x8 *>(&As[buf][p][((BM / 2) * wm + 32 * u + (lane & 31)) * GM_LD + kk]);
                 b[p] = *reinterpret_cast<const bf16x8 *>(&Ws[buf][p][(32 * wn + (lane & 31)) * GM_LD + kk]);
             }
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
+            for (int i = 0; i < MT; i++) {
                 if constexpr (PREC == 3) {
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0], acc[i], 0, 0, 0);
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1], acc[i], 0, 0, 0);
@@ -242,10 +249,10 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
     const uint32_t n = n0 + 32 * wn + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const uint32_t m = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const uint32_t m = m0 + (BM / 2) * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m < g.M && n < g.N) {
                 if (g.ks > 1) {
                     g.part[((size_t)kz * g.M + m) * g.N + n] = acc[i][r];
@@ -305,8 +312,12 @@ hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, h
 // minimises the rounds of 256 workgroups (one per CU) each slice-sized unit
 // of work takes, ceil(tiles * ks / 256) / ks, plus a small charge for the
 // reduction pass; ties keep fewer slices
-uint32_t gemm_ksplit(uint32_t M, uint32_t N, uint32_t K) {
-    const uint32_t tiles = ((M + GM_BM - 1) / GM_BM) * ((N + GM_BN - 1) / GM_BN);
+// token tile: 256 for bf16 operands at M >= 512 (twice the MFMA work per
+// dequantized weight: the dequant, not the matrix cores, bounds the 128-row
+// tile), else 128; the hi/lo form keeps 128 (its LDS would not fit)
+static uint32_t gemm_bm(uint32_t M, int prec) { return prec == 1 && M >= 512 ? 256u : 128u; }
+
+static uint32_t ksplit_for(uint32_t tiles, uint32_t K) {
     const uint32_t units = K / 256;
     uint32_t best = 1;
     if (tiles >= 256) return 1;  // a full round already; partial traffic would cost more
@@ -322,15 +333,21 @@ uint32_t gemm_ksplit(uint32_t M, uint32_t N, uint32_t K) {
     return best;
 }
 
+uint32_t gemm_ksplit(uint32_t M, uint32_t N, uint32_t K, int prec) {
+    const uint32_t bm = gemm_bm(M, prec);
+    return ksplit_for(((M + bm - 1) / bm) * ((N + GM_BN - 1) / GM_BN), K);
+}
+
 // scratch of the K-sliced form (at most 8 * M * N floats)
-size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K) {
-    const uint32_t ks = gemm_ksplit(M, N, K);
+size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K, int prec) {
+    const uint32_t ks = gemm_ksplit(M, N, K, prec);
     return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
 }
 
 hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
                        uint32_t ldy, int prec, hipStream_t s, bool accum, float *work) {
     if (M == 0 || w.n_in % (4 * GM_BK) || (prec == 3 && !alo)) return hipErrorInvalidValue;
+    const uint32_t bm = gemm_bm(M, prec);
     GemmArgs g;
     g.ahi = ahi;
     g.alo = alo;
@@ -342,15 +359,18 @@ hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float
     g.units = tunits(w.type, w.n_in);
     g.ldy = ldy;
     g.accum = accum ? 1u : 0u;
-    g.nm = (M + GM_BM - 1) / GM_BM;
+    g.nm = (M + bm - 1) / bm;
     g.nn = (w.n_out + GM_BN - 1) / GM_BN;
-    g.ks = work ? gemm_ksplit(M, g.N, g.K) : 1;
+    g.ks = work ? ksplit_for(g.nm * g.nn, g.K) : 1;
     g.part = work;
     const uint32_t grid = 8 * ((g.nm * g.nn * g.ks + 7) / 8);
     void (*fn)(GemmArgs) = nullptr;
-    if (w.type == T_Q4_K) fn = prec == 3 ? k_gemm<T_Q4_K, 3> : k_gemm<T_Q4_K, 1>;
-    else if (w.type == T_Q6_K) fn = prec == 3 ? k_gemm<T_Q6_K, 3> : k_gemm<T_Q6_K, 1>;
-    else return hipErrorNotSupported;
+    if (w.type == T_Q4_K)
+        fn = prec == 3 ? k_gemm<T_Q4_K, 3, 128> : bm == 256 ? k_gemm<T_Q4_K, 1, 256> : k_gemm<T_Q4_K, 1, 128>;
+    else if (w.type == T_Q6_K)
+        fn = prec == 3 ? k_gemm<T_Q6_K, 3, 128> : bm == 256 ? k_gemm<T_Q6_K, 1, 256> : k_gemm<T_Q6_K, 1, 128>;
+    else
+        return hipErrorNotSupported;
     hipLaunchKernelGGL(fn, dim3(grid), dim3(512), 0, s, g);
     if (g.ks > 1) {
         const size_t n = (size_t)M * g.N;

@@ -100,11 +100,11 @@ hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, 
                          hipStream_t s);
 // Y[M][ldy] = A[M][K] W^T on the matrix cores; A given as bf16 planes
 // (prec 1: hi only; 3: hi + lo, three products) from launch_split_bf16
-// work: gemm_work_bytes(M, N, K) of scratch for the K-sliced form (null: one slice)
+// work: gemm_work_bytes(M, N, K, prec) of scratch for the K-sliced form (null: one slice)
 hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
                        uint32_t ldy, int prec, hipStream_t s, bool accum = false,
                        float *work = nullptr);
-size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K);
+size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K, int prec);
 // hi = bf16(a), lo = bf16(a - hi) (lo may be null); n a multiple of 4
 hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, hipStream_t s);
 // batched prompt block (prefill.hip)

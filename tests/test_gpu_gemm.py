@@ -34,9 +34,11 @@ def rel_l2(a, b):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q6_K])
-# the last two split K over 2 and 4 workgroups (few output tiles, long K)
+# (64, 256, 4096) and (96, 128, 8192) split K over workgroups (few output
+# tiles, long K); m >= 512 uses the 256-token tile at precision 1
 @pytest.mark.parametrize("m,n,k", [(1, 200, 512), (7, 128, 256), (130, 300, 768), (256, 256, 1024),
-                                   (64, 256, 4096), (96, 128, 8192)])
+                                   (64, 256, 4096), (96, 128, 8192), (512, 256, 1024),
+                                   (600, 200, 512)])
 def test_gemm_matches_oracle(lrs, orc, ctx, t, m, n, k):
     w = orc.gen_weight(t, 31 + m + n, n, k, mode=1)
     deq = orc.dequant(t, w).reshape(n, k)
