@@ -278,6 +278,33 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
 /* GGUF bytes of every weight matrix one decoded token streams. */
 size_t lrs_model_bytes_per_token(const lrs_model *m);
 
+/* ------------------------------------------------------------------------ */
+/* GGUF files: gguf::GgufFile (crates/gguf/src/file.rs, parse.rs)            */
+/* ------------------------------------------------------------------------ */
+/* Maps and parses a GGUF v3 file: metadata, tensor infos, data section at
+ * general.alignment (default 32) (GgufFile::parse, parse.rs:64-126). */
+typedef struct lrs_gguf lrs_gguf;
+int lrs_gguf_open(const char *path, lrs_gguf **out);
+void lrs_gguf_close(lrs_gguf *g);
+uint32_t lrs_gguf_version(const lrs_gguf *g);
+uint64_t lrs_gguf_n_tensors(const lrs_gguf *g);
+/* typed metadata reads (MetadataValue::as_u32 / as_f32, types.rs) */
+int lrs_gguf_get_u32(const lrs_gguf *g, const char *key, uint32_t *v);
+int lrs_gguf_get_f32(const lrs_gguf *g, const char *key, float *v);
+int lrs_gguf_get_str(const lrs_gguf *g, const char *key, const char **s);
+int lrs_gguf_array_len(const lrs_gguf *g, const char *key, uint64_t *n);
+/* GgufFile::tensor_data (file.rs:47-75): type, dims (up to 4; dims[0] is
+ * the row length), and the bytes inside the mapping, bounds-checked */
+int lrs_gguf_tensor(const lrs_gguf *g, const char *name, uint32_t *ggml_type, uint64_t *dims,
+                    uint32_t *n_dims, const void **data, size_t *len);
+/* LlamaConfig::from_gguf (config.rs:81-187) + GpuRawWeights::from_gguf /
+ * GpuAuxWeights::from_gguf (gpu.rs:128-600) + ResidentForward::new: uploads
+ * every weight of the file and builds the dense (llama / qwen2) or hybrid
+ * (qwen35: *.ssm.conv_kernel present) model, which owns those weights.
+ * ctx_len 0 keeps the file's context_length.  The file may be closed
+ * afterwards. */
+int lrs_model_load_gguf(lrs_ctx *ctx, const lrs_gguf *g, uint32_t ctx_len, lrs_model **out);
+
 #ifdef __cplusplus
 }
 #endif

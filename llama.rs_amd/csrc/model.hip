@@ -119,7 +119,15 @@ struct lrs_model {
           *dn_part = nullptr;
     void *rec = nullptr;
     size_t rec_bytes = 0;
+    // weights the model owns (built by lrs_model_load_gguf), freed with it
+    std::vector<lrs_weight *> owned;
 };
+
+// hands the loader's uploaded weights to the model
+void lrs_model_adopt_weights(lrs_model *m, std::vector<lrs_weight *> &ws) {
+    m->owned.insert(m->owned.end(), ws.begin(), ws.end());
+    ws.clear();
+}
 
 namespace {
 
@@ -793,6 +801,7 @@ void lrs_model_destroy(lrs_model *m) {
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->step_host) (void)hipHostFree(m->step_host);
     if (m->logits_host) (void)hipHostFree(m->logits_host);
+    for (lrs_weight *w : m->owned) lrs_weight_free(w);
     delete m;
 }
 

@@ -173,3 +173,30 @@ def gpu_hybrid_model(lrs, ctx, cfg, w):
     ot, oa = w["output"]
     out = lrs.Weight.upload(ctx, ot, oa, cfg["n_embd"], cfg["vocab"])
     return HybridForward(ctx, cfg, layers, emb, w["output_norm"][1], out)
+
+
+def write_model_gguf(path, cfg, w):
+    """Writes a host model (dense or hybrid weight dict) as a GGUF file with
+    the tensor names and metadata the loader reads (gpu.rs, config.rs)."""
+    from llama_rs_amd.gguf import GGUF_NAMES, model_kv, vector_dims, write_gguf
+
+    hybrid = "full_attn_interval" in cfg
+    tensors = []
+    for key, (t, arr) in w.items():
+        if key.startswith("blk."):
+            _, l, name = key.split(".", 2)
+            gname = f"blk.{l}.{GGUF_NAMES[name]}"
+        else:
+            gname = key + ".weight"
+            name = key
+        if t == F32:
+            dims = vector_dims(cfg, name, arr.size)
+        else:
+            if key.startswith("blk."):
+                sh = hybrid_shapes(cfg, int(l)) if hybrid else shapes(cfg)
+                n_in, n_out = sh[name]
+            else:
+                n_in, n_out = cfg["n_embd"], cfg["vocab"]
+            dims = [n_in, n_out]
+        tensors.append((gname, t, dims, np.ascontiguousarray(arr).tobytes()))
+    write_gguf(path, model_kv(cfg, "qwen35" if hybrid else "qwen2"), tensors)
