@@ -330,3 +330,285 @@ hipError_t launch_qk_prep(const float *qg, const float *kb, const float *vb, con
 }
 
 }  // namespace lrs
+
+// ---------------------------------------------------------------------------
+// Batched prompt blocks of the hybrid model: nb tokens at positions pos0..,
+// the same formulas as the decode kernels above, with the projections done
+// by the matrix-core GEMMs (plano_delta with n_tok > 1,
+// resident_forward.rs:2252-2470: dn_gates / dn_conv / dn_l2_qk / delta_net /
+// dn_norm take the token dimension).
+// ---------------------------------------------------------------------------
+namespace lrs {
+
+// gates per (token, value head) from the normalised rows hn (dn_gates.comp):
+// gb[t][h] = {e^g, beta}, g = a_h * softplus(alpha_h . hn + dt_h)
+__global__ __launch_bounds__(256) void k_dn_gates_rows(const float *__restrict__ hn,
+                                                       const float *__restrict__ alpha,
+                                                       const float *__restrict__ beta,
+                                                       const float *__restrict__ a,
+                                                       const float *__restrict__ dt,
+                                                       float2 *__restrict__ gb, uint32_t n_embd,
+                                                       uint32_t v_heads) {
+    __shared__ float red[2][4];
+    const uint32_t hh = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *x = hn + (size_t)t * n_embd;
+    const float *al = alpha + (size_t)hh * n_embd, *be = beta + (size_t)hh * n_embd;
+    float pa = 0.f, pb = 0.f;
+    for (uint32_t i = 4 * tid; i < n_embd; i += 1024) {
+        const float4 xv = *reinterpret_cast<const float4 *>(x + i);
+        const float4 av = *reinterpret_cast<const float4 *>(al + i);
+        const float4 bv = *reinterpret_cast<const float4 *>(be + i);
+        pa += (av.x * xv.x + av.y * xv.y) + (av.z * xv.z + av.w * xv.w);
+        pb += (bv.x * xv.x + bv.y * xv.y) + (bv.z * xv.z + bv.w * xv.w);
+    }
+    pa = wave_sum(pa);
+    pb = wave_sum(pb);
+    if (lane == 0) {
+        red[0][wave] = pa;
+        red[1][wave] = pb;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float sa = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        const float sb = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+        const float zz = sa + dt[hh];
+        const float sp = zz > 20.0f ? zz : log1pf(expf(zz));
+        gb[(size_t)t * v_heads + hh] = make_float2(expf(a[hh] * sp), 1.0f / (1.0f + expf(-sb)));
+    }
+}
+
+// causal conv + SiLU over the block, one thread per channel (dn_conv.comp):
+// the window of the W-1 inputs before the block comes from the position ring,
+// the block's inputs are written back to it at their positions
+__global__ __launch_bounds__(256) void k_dn_conv_rows(const float *__restrict__ cin,
+                                                      const float *__restrict__ conv_w,
+                                                      float *__restrict__ win, float *__restrict__ cout,
+                                                      uint32_t cd, uint32_t W, uint32_t nb, uint32_t pos0) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cd) return;
+    constexpr int WM = 8;
+    float w[WM], h[WM];  // taps; h[t] = input at position p - (W-1) + t for the current token p
+#pragma unroll
+    for (int t = 0; t < WM; t++) {
+        w[t] = (uint32_t)t < W ? conv_w[(size_t)c * W + t] : 0.f;
+        h[t] = (uint32_t)t + 1 < W ? win[(size_t)((pos0 + 1 + t) % W) * cd + c] : 0.f;
+    }
+    for (uint32_t i = 0; i < nb; i++) {
+        const float x = cin[(size_t)i * cd + c];
+        float acc = 0.f;
+#pragma unroll
+        for (int t = 0; t < WM; t++)
+            if ((uint32_t)t + 1 < W) acc += h[t] * w[t];
+        float wl = w[0];
+#pragma unroll
+        for (int t = 1; t < WM; t++)
+            if ((uint32_t)t == W - 1) wl = w[t];
+        acc += x * wl;
+        cout[(size_t)i * cd + c] = acc / (1.0f + expf(-acc));
+        // slide: the oldest input leaves, x enters as the newest
+#pragma unroll
+        for (int t = 0; t + 1 < WM; t++)
+            if ((uint32_t)t + 2 < W) h[t] = h[t + 1];
+#pragma unroll
+        for (int t = 0; t < WM; t++)
+            if ((uint32_t)t + 2 == W) h[t] = x;
+    }
+    for (uint32_t i = nb > W ? nb - W : 0; i < nb; i++)
+        win[(size_t)((pos0 + i) % W) * cd + c] = cin[(size_t)i * cd + c];
+}
+
+// L2 norm of each q / k head of each token in place (dn_l2_qk.comp)
+__global__ __launch_bounds__(128) void k_dn_l2_rows(float *__restrict__ co, uint32_t cd,
+                                                    uint32_t d, float eps) {
+    __shared__ float red[2];
+    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    float *x = co + (size_t)t * cd + (size_t)h * d;
+    float ss = 0.f;
+    for (uint32_t i = tid; i < d; i += blockDim.x) ss += x[i] * x[i];
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = blockDim.x > 64 ? red[0] + red[1] : red[0];
+    const float s = 1.0f / sqrtf(tot + eps);
+    for (uint32_t i = tid; i < d; i += blockDim.x) x[i] *= s;
+}
+
+// the delta rule over the block: the state of 32 rows of a head stays in
+// registers across the nb tokens (delta_net.comp's n_tok loop); o[t][h*D + j]
+template <int D>
+__global__ __launch_bounds__(256) void k_dn_block(const float *__restrict__ co, const float2 *__restrict__ gb,
+                                                  float *__restrict__ state, float *__restrict__ o,
+                                                  uint32_t k_heads, uint32_t v_heads, uint32_t nb) {
+    constexpr uint32_t R = D / 32;
+    constexpr int PPL = D / 32;
+    const uint32_t r = blockIdx.x % R, hh = blockIdx.x / R, tid = threadIdx.x;
+    const uint32_t rho = tid >> 3, lam = tid & 7, j = 32 * r + rho;
+    const uint32_t kh = hh % k_heads, KD = k_heads * D, CD = 2 * KD + v_heads * D;
+    const float qscale = 1.0f / sqrtf((float)D);
+    float4 st[PPL];
+    float4 *srow = reinterpret_cast<float4 *>(state + ((size_t)hh * D + j) * D);
+#pragma unroll
+    for (int c = 0; c < PPL; c++) st[c] = srow[8 * c + lam];
+    for (uint32_t t = 0; t < nb; t++) {
+        const float *row = co + (size_t)t * CD;
+        const float4 *q4 = reinterpret_cast<const float4 *>(row + (size_t)kh * D);
+        const float4 *k4 = reinterpret_cast<const float4 *>(row + KD + (size_t)kh * D);
+        float4 kr[PPL], qr[PPL];
+#pragma unroll
+        for (int c = 0; c < PPL; c++) {
+            kr[c] = k4[8 * c + lam];
+            qr[c] = q4[8 * c + lam];
+        }
+        const float vj = row[2 * KD + (size_t)hh * D + j];
+        const float2 g = gb[(size_t)t * v_heads + hh];
+        float pred = 0.f;
+#pragma unroll
+        for (int c = 0; c < PPL; c++) {
+            st[c].x *= g.x;
+            st[c].y *= g.x;
+            st[c].z *= g.x;
+            st[c].w *= g.x;
+            pred += (st[c].x * kr[c].x + st[c].y * kr[c].y) + (st[c].z * kr[c].z + st[c].w * kr[c].w);
+        }
+        pred = sum8(pred);
+        const float delta = (vj - pred) * g.y;
+        float ov = 0.f;
+#pragma unroll
+        for (int c = 0; c < PPL; c++) {
+            st[c].x = fmaf(delta, kr[c].x, st[c].x);
+            st[c].y = fmaf(delta, kr[c].y, st[c].y);
+            st[c].z = fmaf(delta, kr[c].z, st[c].z);
+            st[c].w = fmaf(delta, kr[c].w, st[c].w);
+            ov += (st[c].x * qr[c].x + st[c].y * qr[c].y) + (st[c].z * qr[c].z + st[c].w * qr[c].w);
+        }
+        ov = sum8(ov);
+        if (lam == 0) o[(size_t)t * v_heads * D + (size_t)hh * D + j] = ov * qscale;
+    }
+#pragma unroll
+    for (int c = 0; c < PPL; c++) srow[8 * c + lam] = st[c];
+}
+
+// gated RMSNorm per (token, head): y = o / sqrt(mean(o^2) + eps) * w * silu(z)
+// (dn_norm.comp mode 1)
+__global__ __launch_bounds__(128) void k_dn_gnorm_rows(const float *__restrict__ o, const float *__restrict__ z,
+                                                       const float *__restrict__ nw, float *__restrict__ y,
+                                                       uint32_t vd, uint32_t d, float eps) {
+    __shared__ float red[2];
+    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const size_t base = (size_t)t * vd + (size_t)h * d;
+    float ss = 0.f;
+    for (uint32_t i = tid; i < d; i += blockDim.x) ss += o[base + i] * o[base + i];
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = blockDim.x > 64 ? red[0] + red[1] : red[0];
+    const float s = 1.0f / sqrtf(tot / (float)d + eps);
+    for (uint32_t i = tid; i < d; i += blockDim.x) {
+        const float zz = z[base + i];
+        y[base + i] = (o[base + i] * s) * (nw[i] * (zz / (1.0f + expf(-zz))));
+    }
+}
+
+// gated attention of a block: QK-norm + RoPE per (token, head) at position
+// pos0 + t; q to q[t][h*HD], k / v into the cache
+template <int HD>
+__global__ __launch_bounds__(HD) void k_qk_prep_rows(const float *__restrict__ qg, const float *__restrict__ kb,
+                                                     const float *__restrict__ vb,
+                                                     const float *__restrict__ q_norm,
+                                                     const float *__restrict__ k_norm,
+                                                     const float *__restrict__ freq, float *__restrict__ q,
+                                                     _Float16 *__restrict__ kc, _Float16 *__restrict__ vc,
+                                                     uint32_t n_head, uint32_t n_kv, uint32_t ctx,
+                                                     uint32_t rope_dim, float eps, uint32_t pos0) {
+    __shared__ float red[HD / 64];
+    const uint32_t h = blockIdx.x, t = blockIdx.y, d = threadIdx.x, lane = d & 63, wave = d >> 6;
+    const bool isq = h < n_head;
+    const uint32_t kh = h - n_head;
+    const float x = isq ? qg[((size_t)t * n_head + h) * 2 * HD + d] : kb[((size_t)t * n_kv + kh) * HD + d];
+    const float ss = wave_sum(x * x);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < HD / 64; w++) tot += red[w];
+    const float s = 1.0f / sqrtf(tot / (float)HD + eps);
+    float y = (x * s) * (isq ? q_norm[d] : k_norm[d]);
+    const uint32_t pos = pos0 + t;
+    const float yo = __shfl_xor(y, 1, 64);
+    if (d < rope_dim) {
+        const float th = (float)pos * freq[d >> 1];
+        float sn, cs;
+        sincosf(th, &sn, &cs);
+        y = (d & 1) ? yo * sn + y * cs : y * cs - yo * sn;
+    }
+    if (isq) {
+        q[((size_t)t * n_head + h) * HD + d] = y;
+    } else {
+        const size_t o = ((size_t)kh * ctx + pos) * HD + d;
+        kc[o] = (_Float16)y;
+        vc[o] = (_Float16)vb[((size_t)t * n_kv + kh) * HD + d];
+    }
+}
+
+// att *= sigmoid(gate), gate = second half of each head's Q rows (gate_quant.comp)
+__global__ __launch_bounds__(256) void k_gate_rows(float *__restrict__ att, const float *__restrict__ qg,
+                                                   uint32_t qd, uint32_t hd, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const size_t t = i / qd;
+    const uint32_t e = (uint32_t)(i % qd), h = e / hd, dd = e % hd;
+    const float g = qg[t * 2 * qd + (size_t)h * 2 * hd + hd + dd];
+    att[i] = att[i] * (1.0f / (1.0f + expf(-g)));
+}
+
+hipError_t launch_dn_prefill(const DnBlockArgs &a, hipStream_t s) {
+    const uint32_t D = a.d_state, KD = a.k_heads * D, VD = a.v_heads * D, CD = 2 * KD + VD;
+    if (a.n_embd % 4 || a.d_conv == 0 || a.d_conv > 8 || (D != 64 && D != 128)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_dn_gates_rows, dim3(a.v_heads, a.nb), dim3(256), 0, s, a.hn, a.alpha, a.beta,
+                       a.a, a.dt, a.gb, a.n_embd, a.v_heads);
+    hipLaunchKernelGGL(k_dn_conv_rows, dim3((CD + 255) / 256), dim3(256), 0, s, a.cin, a.conv_w, a.win,
+                       a.cout, CD, a.d_conv, a.nb, a.pos0);
+    hipLaunchKernelGGL(k_dn_l2_rows, dim3(2 * a.k_heads, a.nb), dim3(128), 0, s, a.cout, CD, D, a.eps);
+    if (D == 128)
+        hipLaunchKernelGGL(k_dn_block<128>, dim3(4 * a.v_heads), dim3(256), 0, s, a.cout, a.gb, a.state,
+                           a.o, a.k_heads, a.v_heads, a.nb);
+    else
+        hipLaunchKernelGGL(k_dn_block<64>, dim3(2 * a.v_heads), dim3(256), 0, s, a.cout, a.gb, a.state,
+                           a.o, a.k_heads, a.v_heads, a.nb);
+    hipLaunchKernelGGL(k_dn_gnorm_rows, dim3(a.v_heads, a.nb), dim3(128), 0, s, a.o, a.z, a.norm_w,
+                       a.y, VD, D, a.eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_prep_rows(const float *qg, const float *kb, const float *vb, const float *q_norm,
+                               const float *k_norm, const float *freq, float *q, _Float16 *kc,
+                               _Float16 *vc, uint32_t nb, uint32_t pos0, uint32_t n_head,
+                               uint32_t n_kv, uint32_t head_dim, uint32_t ctx, uint32_t rope_dim,
+                               float eps, hipStream_t s) {
+    const dim3 g(n_head + n_kv, nb);
+    switch (head_dim) {
+    case 64:
+        hipLaunchKernelGGL(k_qk_prep_rows<64>, g, dim3(64), 0, s, qg, kb, vb, q_norm, k_norm, freq, q, kc,
+                           vc, n_head, n_kv, ctx, rope_dim, eps, pos0);
+        break;
+    case 128:
+        hipLaunchKernelGGL(k_qk_prep_rows<128>, g, dim3(128), 0, s, qg, kb, vb, q_norm, k_norm, freq, q,
+                           kc, vc, n_head, n_kv, ctx, rope_dim, eps, pos0);
+        break;
+    case 256:
+        hipLaunchKernelGGL(k_qk_prep_rows<256>, g, dim3(256), 0, s, qg, kb, vb, q_norm, k_norm, freq, q,
+                           kc, vc, n_head, n_kv, ctx, rope_dim, eps, pos0);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_rows(float *att, const float *qg, uint32_t nb, uint32_t qd, uint32_t hd,
+                            hipStream_t s) {
+    const size_t n = (size_t)nb * qd;
+    hipLaunchKernelGGL(k_gate_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, att, qg, qd, hd, n);
+    return hipGetLastError();
+}
+
+}  // namespace lrs

@@ -138,6 +138,28 @@ struct DnArgs {
     float eps;
 };
 hipError_t launch_dn_step(const DnArgs &a, uint32_t d_state, hipStream_t s);
+// delta-net layer of a prompt block of nb tokens at pos0 (after the qkv / z GEMMs)
+struct DnBlockArgs {
+    const float *hn;            // [nb][n_embd] rmsnorm(x) * attn_norm (gate projections)
+    const float *alpha, *beta, *a, *dt, *conv_w, *norm_w;
+    const float *cin;           // [nb][conv_dim] conv input (qkv GEMM output)
+    const float *z;             // [nb][v_heads * D] output gate (GEMM output)
+    float *win, *state;         // the layer's position ring and states
+    float *cout;                // [nb][conv_dim] conv + SiLU, q / k L2-normalised
+    float2 *gb;                 // [nb][v_heads] {e^g, beta}
+    float *o;                   // [nb][v_heads * D] rule output
+    float *y;                   // [nb][v_heads * D] gated norm (ssm_out GEMM input)
+    uint32_t n_embd, k_heads, v_heads, d_state, d_conv, nb, pos0;
+    float eps;
+};
+hipError_t launch_dn_prefill(const DnBlockArgs &a, hipStream_t s);
+hipError_t launch_qk_prep_rows(const float *qg, const float *kb, const float *vb, const float *q_norm,
+                               const float *k_norm, const float *freq, float *q, _Float16 *kc,
+                               _Float16 *vc, uint32_t nb, uint32_t pos0, uint32_t n_head,
+                               uint32_t n_kv, uint32_t head_dim, uint32_t ctx, uint32_t rope_dim,
+                               float eps, hipStream_t s);
+hipError_t launch_gate_rows(float *att, const float *qg, uint32_t nb, uint32_t qd, uint32_t hd,
+                            hipStream_t s);
 hipError_t launch_qk_prep(const float *qg, const float *kb, const float *vb, const float *q_norm,
                           const float *k_norm, const float *freq, const uint32_t *step, float *q,
                           _Float16 *kc, _Float16 *vc, uint32_t n_head, uint32_t n_kv,

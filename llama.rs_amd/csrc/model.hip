@@ -100,6 +100,11 @@ struct lrs_model {
     uint32_t pb_cap = 0;
     float *pX = nullptr, *pXN, *pQt, *pKt, *pVt, *pQ, *pATT, *pG, *pU;
     __bf16 *pA16 = nullptr;  // bf16 hi / lo planes of the current GEMM input
+    // hybrid blocks: Q + gate rows, conv in / out, output gate, rule output,
+    // gated norm, per-(token, head) gates
+    float *pQG = nullptr, *pCI = nullptr, *pCO = nullptr, *pZ = nullptr, *pO = nullptr,
+          *pY = nullptr;
+    float2 *pGB = nullptr;
     float *pWork = nullptr;  // K-slice partials of the split GEMMs
     uint32_t *ptok;
     _Float16 *kv;                // all layers' caches
@@ -834,13 +839,15 @@ static bool prefill_capable(const lrs_model *m) {
         return (w->v.type == T_Q4_K || w->v.type == T_Q6_K) && w->v.n_in % 128 == 0;
     };
     const lrs_config &c = m->cfg;
-    if (m->hybrid) return false;  // the recurrence runs token by token
-    if ((c.head_dim != 64 && c.head_dim != 128) || c.n_head / c.n_head_kv > 8 || c.n_embd % 4)
+    if ((c.head_dim != 64 && c.head_dim != 128 && (c.head_dim != 256 || !m->hybrid)) ||
+        c.n_head / c.n_head_kv > 8 || c.n_embd % 4)
         return false;
-    for (const DevLayer &L : m->layers)
-        if (!ok(L.q) || !ok(L.k) || !ok(L.v) || !ok(L.o) || !ok(L.gate) || !ok(L.up) ||
-            !ok(L.down))
+    for (const DevLayer &L : m->layers) {
+        if (!ok(L.gate) || !ok(L.up) || !ok(L.down)) return false;
+        if (L.dn ? (!ok(L.ssm_qkv) || !ok(L.ssm_gate) || !ok(L.ssm_out))
+                 : (!ok(L.q) || !ok(L.k) || !ok(L.v) || !ok(L.o)))
             return false;
+    }
     return true;
 }
 
@@ -859,12 +866,27 @@ static int ensure_prefill(lrs_model *m) {
         (rc = dev_alloc(m, B * qd * 4, (void **)&m->pATT)) ||
         (rc = dev_alloc(m, B * c.n_ff * 4, (void **)&m->pG)) ||
         (rc = dev_alloc(m, B * c.n_ff * 4, (void **)&m->pU)) ||
-        (rc = dev_alloc(m, B * std::max<size_t>(std::max<size_t>(c.n_embd, qd), c.n_ff) * 4,
+        (rc = dev_alloc(m, B * std::max<size_t>(std::max<size_t>(c.n_embd, qd),
+                                                std::max<size_t>(c.n_ff, (size_t)m->hc.dn_v_heads *
+                                                                             m->hc.dn_state)) * 4,
                         (void **)&m->pA16)) ||
         // K-sliced o / down GEMMs: at most 8 slices of [rows][n_embd] partials
         (rc = dev_alloc(m, 8 * B * c.n_embd * 4, (void **)&m->pWork)) ||
         (rc = dev_alloc(m, B * 4, (void **)&m->ptok)))
         return rc;
+    if (m->hybrid) {
+        const lrs_hybrid_config &hc = m->hc;
+        const size_t VD = (size_t)hc.dn_v_heads * hc.dn_state,
+                     CD = 2 * (size_t)hc.dn_k_heads * hc.dn_state + VD;
+        if ((rc = dev_alloc(m, B * 2 * qd * 4, (void **)&m->pQG)) ||
+            (rc = dev_alloc(m, B * CD * 4, (void **)&m->pCI)) ||
+            (rc = dev_alloc(m, B * CD * 4, (void **)&m->pCO)) ||
+            (rc = dev_alloc(m, B * VD * 4, (void **)&m->pZ)) ||
+            (rc = dev_alloc(m, B * VD * 4, (void **)&m->pO)) ||
+            (rc = dev_alloc(m, B * VD * 4, (void **)&m->pY)) ||
+            (rc = dev_alloc(m, B * hc.dn_v_heads * sizeof(float2), (void **)&m->pGB)))
+            return rc;
+    }
     m->pb_cap = PREFILL_BLOCK;
     return LRS_OK;
 }
@@ -888,6 +910,65 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
         const DevLayer &L = m->layers[l];
         LRS_HIP(launch_rmsnorm_rows(m->pX, L.attn_norm, c.rms_eps, E, nb, m->pXN, s));
         LRS_HIP(split(m->pXN, (size_t)nb * E));
+        if (m->hybrid) {
+            if (L.dn) {
+                // gated delta net over the block (plano_delta with n_tok = nb)
+                const lrs_hybrid_config &hc = m->hc;
+                const uint32_t VD = hc.dn_v_heads * hc.dn_state;
+                const uint32_t CD = 2 * hc.dn_k_heads * hc.dn_state + VD;
+                LRS_HIP(launch_gemm(L.ssm_qkv->v, hi, lo(nb, E), m->pCI, nb, CD, P, s));
+                LRS_HIP(launch_gemm(L.ssm_gate->v, hi, lo(nb, E), m->pZ, nb, VD, P, s));
+                DnBlockArgs da = {};
+                da.hn = m->pXN;
+                da.alpha = L.alpha;
+                da.beta = L.beta;
+                da.a = L.ssm_a;
+                da.dt = L.ssm_dt;
+                da.conv_w = L.conv;
+                da.norm_w = L.ssm_norm;
+                da.cin = m->pCI;
+                da.z = m->pZ;
+                da.win = L.win;
+                da.state = L.state;
+                da.cout = m->pCO;
+                da.gb = m->pGB;
+                da.o = m->pO;
+                da.y = m->pY;
+                da.n_embd = E;
+                da.k_heads = hc.dn_k_heads;
+                da.v_heads = hc.dn_v_heads;
+                da.d_state = hc.dn_state;
+                da.d_conv = hc.dn_conv;
+                da.nb = nb;
+                da.pos0 = pos0;
+                da.eps = c.rms_eps;
+                LRS_HIP(launch_dn_prefill(da, s));
+                LRS_HIP(split(m->pY, (size_t)nb * VD));
+                LRS_HIP(launch_gemm(L.ssm_out->v, hi, lo(nb, VD), m->pX, nb, E, P, s, true, m->pWork));
+            } else {
+                // gated attention: Q (+ gate), k, v; QK-norm + RoPE; causal
+                // attention over the cache; sigmoid gate; o
+                LRS_HIP(launch_gemm(L.q->v, hi, lo(nb, E), m->pQG, nb, 2 * qd, P, s));
+                LRS_HIP(launch_gemm(L.k->v, hi, lo(nb, E), m->pKt, nb, kvd, P, s));
+                LRS_HIP(launch_gemm(L.v->v, hi, lo(nb, E), m->pVt, nb, kvd, P, s));
+                LRS_HIP(launch_qk_prep_rows(m->pQG, m->pKt, m->pVt, L.q_norm, L.k_norm, m->freq, m->pQ,
+                                            L.kc, L.vc, nb, pos0, c.n_head, c.n_head_kv, c.head_dim,
+                                            c.ctx, c.rope_dim, c.rms_eps, s));
+                LRS_HIP(launch_attn_prefill(m->pQ, L.kc, L.vc, m->pATT, nb, pos0, c.n_head, c.n_head_kv,
+                                            c.head_dim, c.ctx, s));
+                LRS_HIP(launch_gate_rows(m->pATT, m->pQG, nb, qd, c.head_dim, s));
+                LRS_HIP(split(m->pATT, (size_t)nb * qd));
+                LRS_HIP(launch_gemm(L.o->v, hi, lo(nb, qd), m->pX, nb, E, P, s, true, m->pWork));
+            }
+            LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, m->pXN, s));
+            LRS_HIP(split(m->pXN, (size_t)nb * E));
+            LRS_HIP(launch_gemm(L.gate->v, hi, lo(nb, E), m->pG, nb, c.n_ff, P, s));
+            LRS_HIP(launch_gemm(L.up->v, hi, lo(nb, E), m->pU, nb, c.n_ff, P, s));
+            LRS_HIP(launch_swiglu_rows(m->pG, m->pU, (size_t)nb * c.n_ff, s));
+            LRS_HIP(split(m->pG, (size_t)nb * c.n_ff));
+            LRS_HIP(launch_gemm(L.down->v, hi, lo(nb, c.n_ff), m->pX, nb, E, P, s, true, m->pWork));
+            continue;
+        }
         LRS_HIP(launch_gemm(L.q->v, hi, lo(nb, E), m->pQt, nb, qd, P, s));
         LRS_HIP(launch_gemm(L.k->v, hi, lo(nb, E), m->pKt, nb, kvd, P, s));
         LRS_HIP(launch_gemm(L.v->v, hi, lo(nb, E), m->pVt, nb, kvd, P, s));

@@ -59,10 +59,14 @@ def test_hybrid_decode_and_greedy_match_oracle(lrs, orc, ctx, name, cfg, mix):
 
 
 def test_hybrid_batch_reset_and_position_rule(lrs, orc, ctx):
+    """decode_batch runs the prompt block through the GEMMs, the block
+    delta-net kernels and the batched gated attention; the token loop and the
+    block agree with the oracle and with each other (argmax), and the state
+    the block leaves (recurrent states, conv ring, KV) carries the decode on."""
     cfg = modelgen.HY_TINY
     w = modelgen.hybrid_host_model(orc, cfg, seed=22)
     gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
-    assert gm.batch_size() == 1
+    assert gm.batch_size() == 512
     toks = [3, 1, 4, 1, 5, 9, 2, 6]
     for p, t in enumerate(toks):
         last = gm.decode(t, p)
@@ -71,15 +75,34 @@ def test_hybrid_batch_reset_and_position_rule(lrs, orc, ctx):
         gm.decode(toks[0], 3)
     gm.reset()
     b = gm.decode_batch(toks, 0)
-    assert np.array_equal(b, last)  # same launches, same state after reset
-    o = orc.HybridModel(cfg, w, kv_f16=True, threads=8).forward(toks)
-    assert rel_l2(b, o) < LOGIT_TOL
+    om = orc.HybridModel(cfg, w, kv_f16=True, threads=8)
+    o = om.forward(toks)
+    assert rel_l2(b, o) < LOGIT_TOL and rel_l2(last, o) < LOGIT_TOL
+    assert int(np.argmax(b)) == int(np.argmax(last)) == int(np.argmax(o))
     assert len(gm) == len(toks)
-    # decode_batch continues the sequence
+    # decode_batch / decode continue the sequence from the block's state
     nxt = gm.decode_batch([7, 8], len(toks))
-    o2 = orc.HybridModel(cfg, w, kv_f16=True, threads=8)
-    o2.forward(toks)
-    assert rel_l2(nxt, o2.forward([7, 8])) < LOGIT_TOL
+    assert rel_l2(nxt, om.forward([7, 8])) < LOGIT_TOL
+    for p, t in enumerate([11, 12, 13], start=len(toks) + 2):
+        assert rel_l2(gm.decode(t, p), om.forward([t])) < LOGIT_TOL
+
+
+@pytest.mark.parametrize("name,cfg", [("hy-tiny", modelgen.HY_TINY), ("hy-mid", modelgen.HY_MID)])
+def test_hybrid_prompt_block_matches_oracle(lrs, orc, ctx, name, cfg):
+    """A 40-token prompt in one block (ring wrap, state carried across
+    tokens inside the block kernel), then decode steps."""
+    cfg = dict(cfg, ctx=64)
+    w = modelgen.hybrid_host_model(orc, cfg, seed=25)
+    gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
+    om = orc.HybridModel(cfg, w, kv_f16=True, threads=8)
+    prompt = np.random.default_rng(9).integers(0, cfg["vocab"], 40).tolist()
+    g = gm.decode_batch(prompt, 0)
+    o = om.forward(prompt)
+    assert rel_l2(g, o) < LOGIT_TOL, rel_l2(g, o)
+    for p, t in enumerate([1, 2, 3, 4], start=40):
+        g, o = gm.decode(t, p), om.forward([t])
+        assert rel_l2(g, o) < LOGIT_TOL, (p, rel_l2(g, o))
+        assert int(np.argmax(g)) == int(np.argmax(o))
 
 
 def test_hybrid_rejects_bad_shapes(lrs, orc, ctx):
