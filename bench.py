@@ -24,6 +24,12 @@ Workloads:
           greedy tokens are timed at positions 511..  (warmup runs on a separate
           pass: the recurrent state cannot be rewound, so the model is reset
           and the prompt replayed before the timed tokens).
+  prefill config 5 through the full model: a prompt of M tokens (--m: 128 /
+          512 / 2048) consumed by the 32B-shaped model of config 3 in blocks of
+          512 tokens (bf16 hi/lo matrix-core GEMMs for every projection,
+          batched norm / RoPE / causal attention); a step is one whole prompt.
+          Reports prompt tok/s and the algorithmic matmul TFLOP/s (2 x M x
+          weight elements; the hi/lo split issues three bf16 products each).
   pmc     profiling helper for the rocprofv3 counter passes: a plain copy
           kernel of known size (calibration) and the dominant decode kernel
           on a 4-layer model of the 32B shape.
@@ -372,6 +378,38 @@ def bench_gemm(lrs, ctx, steps, warmup, m, precision):
     return dict(per=per, us=tot_us, tflops=tot_flop / tot_us / 1e6, flop=tot_flop)
 
 
+def bench_prefill(lrs, ctx, steps, warmup, m_tok):
+    """Config 5 through the full 32B-shaped model: one step = an m_tok-token
+    prompt at positions 0.. (decode_batch: logits of the last token)."""
+    from llama_rs_amd.model import synthetic_model
+
+    cfg = cfg32()
+    if not 1 <= m_tok < cfg["ctx"]:
+        raise SystemExit(f"--m must be within 1..{cfg['ctx'] - 1}")
+    m = synthetic_model(ctx, cfg, seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
+    rng = np.random.default_rng(4321)
+    prompt = rng.integers(0, cfg["vocab"], m_tok).astype(np.uint32)
+    for _ in range(max(1, warmup)):
+        m.decode_batch(prompt, 0)  # the first call allocates the prompt-block buffers
+    ctx.sync()
+    ctx.timer_start()
+    w0 = time.perf_counter()
+    for _ in range(steps):
+        m.decode_batch(prompt, 0)
+    ctx.sync()
+    wall = time.perf_counter() - w0
+    ev_ms = ctx.timer_stop()
+    E, F, qd = cfg["n_embd"], cfg["n_ff"], cfg["n_head"] * cfg["head_dim"]
+    kvd = cfg["n_head_kv"] * cfg["head_dim"]
+    per_tok = 2.0 * cfg["n_layer"] * (E * qd + 2 * E * kvd + qd * E + 3 * E * F)
+    s_step = wall / steps
+    log(f"[bench] prompt {m_tok} tokens: {s_step * 1e3:.1f} ms per prompt (events "
+        f"{ev_ms / steps:.1f} ms) -> {m_tok / s_step:.0f} tok/s, batch_size {m.batch_size()}")
+    m.close()
+    return dict(s=s_step, tok_s=m_tok / s_step, flop=per_tok * m_tok,
+                tflops=per_tok * m_tok / s_step / 1e12)
+
+
 def run_pmc(lrs, ctx):
     """Kernels for the counter passes: the copy calibration (an F32 tensor's
     identity dequant: 4 B read + 4 B written per element, grid-stride), the
@@ -411,8 +449,9 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "hybrid", "q8", "layer", "gemm", "pmc"])
-    ap.add_argument("--m", type=int, default=512, help="gemm: prompt tokens (config 5: 128/512/2048)")
+                    choices=["decode", "hybrid", "q8", "layer", "gemm", "prefill", "pmc"])
+    ap.add_argument("--m", type=int, default=512,
+                    help="gemm / prefill: prompt tokens (config 5: 128/512/2048)")
     ap.add_argument("--precision", type=int, default=1, choices=[1, 3],
                     help="gemm: 1 = bf16 operands, 3 = bf16 hi/lo split")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
@@ -451,6 +490,24 @@ def main():
                "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": peak,
                             "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
                             "traffic": None}}
+        print(json.dumps(out), flush=True)
+        ctx.close()
+        return
+    if a.workload == "prefill":
+        r = bench_prefill(lrs, ctx, a.steps, a.warmup, a.m)
+        peak = 2500.0  # MI355X dense bf16 MFMA
+        out = {"metric": "prefill tok/s through the 32B-shaped Q4_K_M model (config 5)",
+               "value": round(r["tok_s"], 1), "unit": "tok/s", "n_gpus": 1,
+               "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(r["s"] * 1e3, 3),
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+               "dtype": "bf16x3",
+               "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU; "
+                       "prompt ids uniform random, seed 4321)",
+               "config": {"workload": "config5-prefill-32b-model", "m": a.m,
+                          "block": 512, "matmul_flop_per_prompt": r["flop"]},
+               "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": peak,
+                            "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
+                            "traffic": None, "mfma_work_per_flop": 3}}
         print(json.dumps(out), flush=True)
         ctx.close()
         return

@@ -227,7 +227,9 @@ typedef struct {
 /* Builds a hybrid model: the same decode / decode_batch / greedy / reset
  * entry points apply.  Its recurrent state cannot be rewound: every decode
  * must continue at the current length (pos == lrs_model_len) and
- * lrs_reset clears the states and conv windows; batch_size() is 1. */
+ * lrs_reset clears the states and conv windows.  batch_size() is 512 when
+ * every matmul weight is Q4_K or Q6_K (prompt blocks: GEMM projections and
+ * block delta-net kernels), else 1. */
 int lrs_hybrid_create(lrs_ctx *ctx, const lrs_hybrid_config *cfg, const lrs_hybrid_layer *layers,
                       const lrs_weight *token_embd, const float *output_norm,
                       const lrs_weight *output, lrs_model **out);

@@ -247,10 +247,12 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     pack_half(o, (h * HD + d) >> 5, out);
 }
 
-// split count: about one workgroup per CU (256 = splits x KV heads)
+// split count: about one workgroup per CU (256 = splits x KV heads), at
+// most 32 (measured on the decode benches: 32 splits beat 64 for 4 KV heads
+// x 256 dims, and 16 / 32 tie for 8 x 128; 8 and 64 are slower)
 uint32_t attn_splits(uint32_t n_kv) {
     const uint32_t S = 256 / n_kv;
-    return S < 1 ? 1 : S > 64 ? 64 : S;
+    return S < 1 ? 1 : S > 32 ? 32 : S;
 }
 
 using AttnFn = void (*)(AttnArgs);

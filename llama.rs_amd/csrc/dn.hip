@@ -377,44 +377,31 @@ __global__ __launch_bounds__(256) void k_dn_gates_rows(const float *__restrict__
     }
 }
 
-// causal conv + SiLU over the block, one thread per channel (dn_conv.comp):
-// the window of the W-1 inputs before the block comes from the position ring,
-// the block's inputs are written back to it at their positions
+// causal conv + SiLU over the block (dn_conv.comp): thread (channel c, row t)
+// sums tap j times the input at position pos0 + t - (W-1) + j; inputs before
+// the block come from the position ring (position P in slot P % W)
 __global__ __launch_bounds__(256) void k_dn_conv_rows(const float *__restrict__ cin,
                                                       const float *__restrict__ conv_w,
-                                                      float *__restrict__ win, float *__restrict__ cout,
-                                                      uint32_t cd, uint32_t W, uint32_t nb, uint32_t pos0) {
-    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+                                                      const float *__restrict__ win, float *__restrict__ cout,
+                                                      uint32_t cd, uint32_t W, uint32_t pos0) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
     if (c >= cd) return;
-    constexpr int WM = 8;
-    float w[WM], h[WM];  // taps; h[t] = input at position p - (W-1) + t for the current token p
-#pragma unroll
-    for (int t = 0; t < WM; t++) {
-        w[t] = (uint32_t)t < W ? conv_w[(size_t)c * W + t] : 0.f;
-        h[t] = (uint32_t)t + 1 < W ? win[(size_t)((pos0 + 1 + t) % W) * cd + c] : 0.f;
+    float acc = 0.f;
+    for (uint32_t j = 0; j < W; j++) {
+        const int i = (int)t - (int)(W - 1) + (int)j;  // block row of the input (< 0: before the block)
+        const float x = i >= 0 ? cin[(size_t)i * cd + c] : win[(size_t)((pos0 + W + i) % W) * cd + c];
+        acc += x * conv_w[(size_t)c * W + j];
     }
-    for (uint32_t i = 0; i < nb; i++) {
-        const float x = cin[(size_t)i * cd + c];
-        float acc = 0.f;
-#pragma unroll
-        for (int t = 0; t < WM; t++)
-            if ((uint32_t)t + 1 < W) acc += h[t] * w[t];
-        float wl = w[0];
-#pragma unroll
-        for (int t = 1; t < WM; t++)
-            if ((uint32_t)t == W - 1) wl = w[t];
-        acc += x * wl;
-        cout[(size_t)i * cd + c] = acc / (1.0f + expf(-acc));
-        // slide: the oldest input leaves, x enters as the newest
-#pragma unroll
-        for (int t = 0; t + 1 < WM; t++)
-            if ((uint32_t)t + 2 < W) h[t] = h[t + 1];
-#pragma unroll
-        for (int t = 0; t < WM; t++)
-            if ((uint32_t)t + 2 == W) h[t] = x;
-    }
-    for (uint32_t i = nb > W ? nb - W : 0; i < nb; i++)
-        win[(size_t)((pos0 + i) % W) * cd + c] = cin[(size_t)i * cd + c];
+    cout[(size_t)t * cd + c] = acc / (1.0f + expf(-acc));
+}
+
+// the block's last min(W, nb) inputs go to the ring at their positions (after
+// k_dn_conv_rows has read the ring)
+__global__ __launch_bounds__(256) void k_dn_ring_rows(const float *__restrict__ cin, float *__restrict__ win,
+                                                      uint32_t cd, uint32_t W, uint32_t nb, uint32_t pos0) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x, i = nb - 1 - blockIdx.y;
+    if (c >= cd) return;
+    win[(size_t)((pos0 + i) % W) * cd + c] = cin[(size_t)i * cd + c];
 }
 
 // L2 norm of each q / k head of each token in place (dn_l2_qk.comp)
@@ -434,55 +421,104 @@ __global__ __launch_bounds__(128) void k_dn_l2_rows(float *__restrict__ co, uint
 }
 
 // the delta rule over the block: the state of 32 rows of a head stays in
-// registers across the nb tokens (delta_net.comp's n_tok loop); o[t][h*D + j]
+// registers across the nb tokens (delta_net.comp's n_tok loop).  The tokens'
+// q and k rows, this workgroup's 32 v values and the gates go through LDS in
+// chunks of DNB_T tokens; the next chunk's loads are in flight while the
+// current chunk is processed.  o[t][h*D + j]
+constexpr uint32_t DNB_T = 16;
 template <int D>
 __global__ __launch_bounds__(256) void k_dn_block(const float *__restrict__ co, const float2 *__restrict__ gb,
                                                   float *__restrict__ state, float *__restrict__ o,
                                                   uint32_t k_heads, uint32_t v_heads, uint32_t nb) {
     constexpr uint32_t R = D / 32;
     constexpr int PPL = D / 32;
+    constexpr uint32_t NP = D / 2 + 9;                  // float4 pieces per token: q, k, 32 v, gates
+    constexpr uint32_t TF = 4 * NP;                     // floats per token in LDS
+    constexpr uint32_t PPT = (DNB_T * NP + 255) / 256;  // pieces per thread per chunk
+    __shared__ __attribute__((aligned(16))) float buf[2][DNB_T * TF];
     const uint32_t r = blockIdx.x % R, hh = blockIdx.x / R, tid = threadIdx.x;
     const uint32_t rho = tid >> 3, lam = tid & 7, j = 32 * r + rho;
     const uint32_t kh = hh % k_heads, KD = k_heads * D, CD = 2 * KD + v_heads * D;
     const float qscale = 1.0f / sqrtf((float)D);
+    float4 pre[PPT];
+    auto fetch = [&](uint32_t c0) {
+#pragma unroll
+        for (uint32_t p = 0; p < PPT; p++) {
+            const uint32_t i = tid + 256 * p, t = i / NP, w = i % NP;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < DNB_T * NP && c0 + t < nb) {
+                const float *row = co + (size_t)(c0 + t) * CD;
+                if (w < D / 4)
+                    v = reinterpret_cast<const float4 *>(row + (size_t)kh * D)[w];
+                else if (w < D / 2)
+                    v = reinterpret_cast<const float4 *>(row + KD + (size_t)kh * D)[w - D / 4];
+                else if (w < D / 2 + 8)
+                    v = reinterpret_cast<const float4 *>(row + 2 * KD + (size_t)hh * D + 32 * r)[w - D / 2];
+                else {
+                    const float2 g = gb[(size_t)(c0 + t) * v_heads + hh];
+                    v = make_float4(g.x, g.y, 0.f, 0.f);
+                }
+            }
+            pre[p] = v;
+        }
+    };
+    auto stash = [&](float *b) {
+#pragma unroll
+        for (uint32_t p = 0; p < PPT; p++) {
+            const uint32_t i = tid + 256 * p;
+            if (i < DNB_T * NP) reinterpret_cast<float4 *>(b)[i] = pre[p];
+        }
+    };
     float4 st[PPL];
     float4 *srow = reinterpret_cast<float4 *>(state + ((size_t)hh * D + j) * D);
 #pragma unroll
     for (int c = 0; c < PPL; c++) st[c] = srow[8 * c + lam];
-    for (uint32_t t = 0; t < nb; t++) {
-        const float *row = co + (size_t)t * CD;
-        const float4 *q4 = reinterpret_cast<const float4 *>(row + (size_t)kh * D);
-        const float4 *k4 = reinterpret_cast<const float4 *>(row + KD + (size_t)kh * D);
-        float4 kr[PPL], qr[PPL];
+    fetch(0);
+    stash(buf[0]);
+    __syncthreads();
+    uint32_t cur = 0;
+    for (uint32_t c0 = 0; c0 < nb; c0 += DNB_T) {
+        const bool more = c0 + DNB_T < nb;
+        if (more) fetch(c0 + DNB_T);
+        const uint32_t nt = min(DNB_T, nb - c0);
+        for (uint32_t tt = 0; tt < nt; tt++) {
+            const float *tk = buf[cur] + tt * TF;
+            const float4 *q4 = reinterpret_cast<const float4 *>(tk);
+            const float4 *k4 = reinterpret_cast<const float4 *>(tk + D);
+            float4 kr[PPL], qr[PPL];
 #pragma unroll
-        for (int c = 0; c < PPL; c++) {
-            kr[c] = k4[8 * c + lam];
-            qr[c] = q4[8 * c + lam];
-        }
-        const float vj = row[2 * KD + (size_t)hh * D + j];
-        const float2 g = gb[(size_t)t * v_heads + hh];
-        float pred = 0.f;
+            for (int c = 0; c < PPL; c++) {
+                kr[c] = k4[8 * c + lam];
+                qr[c] = q4[8 * c + lam];
+            }
+            const float vj = tk[2 * D + rho];
+            const float2 g = make_float2(tk[2 * D + 32], tk[2 * D + 33]);
+            float pred = 0.f;
 #pragma unroll
-        for (int c = 0; c < PPL; c++) {
-            st[c].x *= g.x;
-            st[c].y *= g.x;
-            st[c].z *= g.x;
-            st[c].w *= g.x;
-            pred += (st[c].x * kr[c].x + st[c].y * kr[c].y) + (st[c].z * kr[c].z + st[c].w * kr[c].w);
-        }
-        pred = sum8(pred);
-        const float delta = (vj - pred) * g.y;
-        float ov = 0.f;
+            for (int c = 0; c < PPL; c++) {
+                st[c].x *= g.x;
+                st[c].y *= g.x;
+                st[c].z *= g.x;
+                st[c].w *= g.x;
+                pred += (st[c].x * kr[c].x + st[c].y * kr[c].y) + (st[c].z * kr[c].z + st[c].w * kr[c].w);
+            }
+            pred = sum8(pred);
+            const float delta = (vj - pred) * g.y;
+            float ov = 0.f;
 #pragma unroll
-        for (int c = 0; c < PPL; c++) {
-            st[c].x = fmaf(delta, kr[c].x, st[c].x);
-            st[c].y = fmaf(delta, kr[c].y, st[c].y);
-            st[c].z = fmaf(delta, kr[c].z, st[c].z);
-            st[c].w = fmaf(delta, kr[c].w, st[c].w);
-            ov += (st[c].x * qr[c].x + st[c].y * qr[c].y) + (st[c].z * qr[c].z + st[c].w * qr[c].w);
+            for (int c = 0; c < PPL; c++) {
+                st[c].x = fmaf(delta, kr[c].x, st[c].x);
+                st[c].y = fmaf(delta, kr[c].y, st[c].y);
+                st[c].z = fmaf(delta, kr[c].z, st[c].z);
+                st[c].w = fmaf(delta, kr[c].w, st[c].w);
+                ov += (st[c].x * qr[c].x + st[c].y * qr[c].y) + (st[c].z * qr[c].z + st[c].w * qr[c].w);
+            }
+            ov = sum8(ov);
+            if (lam == 0) o[(size_t)(c0 + tt) * v_heads * D + (size_t)hh * D + j] = ov * qscale;
         }
-        ov = sum8(ov);
-        if (lam == 0) o[(size_t)t * v_heads * D + (size_t)hh * D + j] = ov * qscale;
+        if (more) stash(buf[cur ^ 1]);
+        __syncthreads();
+        cur ^= 1;
     }
 #pragma unroll
     for (int c = 0; c < PPL; c++) srow[8 * c + lam] = st[c];
@@ -563,11 +599,14 @@ __global__ __launch_bounds__(256) void k_gate_rows(float *__restrict__ att, cons
 
 hipError_t launch_dn_prefill(const DnBlockArgs &a, hipStream_t s) {
     const uint32_t D = a.d_state, KD = a.k_heads * D, VD = a.v_heads * D, CD = 2 * KD + VD;
-    if (a.n_embd % 4 || a.d_conv == 0 || a.d_conv > 8 || (D != 64 && D != 128)) return hipErrorInvalidValue;
+    if (a.nb == 0 || a.n_embd % 4 || a.d_conv == 0 || a.d_conv > 8 || (D != 64 && D != 128))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_dn_gates_rows, dim3(a.v_heads, a.nb), dim3(256), 0, s, a.hn, a.alpha, a.beta,
                        a.a, a.dt, a.gb, a.n_embd, a.v_heads);
-    hipLaunchKernelGGL(k_dn_conv_rows, dim3((CD + 255) / 256), dim3(256), 0, s, a.cin, a.conv_w, a.win,
-                       a.cout, CD, a.d_conv, a.nb, a.pos0);
+    hipLaunchKernelGGL(k_dn_conv_rows, dim3((CD + 255) / 256, a.nb), dim3(256), 0, s, a.cin, a.conv_w,
+                       a.win, a.cout, CD, a.d_conv, a.pos0);
+    hipLaunchKernelGGL(k_dn_ring_rows, dim3((CD + 255) / 256, min(a.d_conv, a.nb)), dim3(256), 0, s, a.cin,
+                       a.win, CD, a.d_conv, a.nb, a.pos0);
     hipLaunchKernelGGL(k_dn_l2_rows, dim3(2 * a.k_heads, a.nb), dim3(128), 0, s, a.cout, CD, D, a.eps);
     if (D == 128)
         hipLaunchKernelGGL(k_dn_block<128>, dim3(4 * a.v_heads), dim3(256), 0, s, a.cout, a.gb, a.state,
