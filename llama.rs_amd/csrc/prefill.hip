@@ -175,6 +175,207 @@ __global__ __launch_bounds__(256) void k_attn_prefill(AttnPre a) {
     }
 }
 
+// The same attention on the matrix cores (head_dim 64 / 128).  Workgroup
+// (32-token query block, KV head), one wavefront per query head of the GQA
+// group.  Per chunk of 32 cache positions each wavefront forms the transposed
+// score tile S^T = K Q^T (32 positions x 32 queries) with
+// v_mfma_f32_32x32x16_f16: K is the f16 cache (exact), Q is split into f16
+// hi + lo after scaling each query by a power of two (2^-e >= 1 / max |q|),
+// so the products carry 22 bits of q.  In that layout a lane owns one query
+// and 16 of the chunk's positions, so the online softmax (running max m,
+// sum l) needs one cross-lane step per reduction.  The probabilities, split
+// into f16 hi + lo, are the B operand of O^T += V^T P^T straight from the
+// score registers: the K index of that product is the position order in
+// which the score layout holds them (4 positions of the lane's half, then the
+// 4 positions 8 further), and V^T is read from LDS in the same order.
+// K is staged with global_load_lds into an XOR-swizzled row layout
+// (conflict-free 16-byte reads), V through registers into a transposed,
+// padded layout; both are double-buffered with the next chunk's loads in
+// flight during the current chunk's matrix work.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int HD, int REP>
+__global__ __launch_bounds__(64 * REP) void k_attn_pf_mma(AttnPre a) {
+    constexpr int NT = 64 * REP;
+    constexpr int KS = HD / 16;           // K-steps of S^T (16 dims each)
+    constexpr int OT = HD / 32;           // O^T tiles of 32 dims
+    constexpr int NPR = HD / 8;           // 16-byte pieces per K / V row
+    constexpr int NPC = 32 * NPR;         // pieces per chunk
+    constexpr int VLD = 36;               // V^T row (f16): 72 B, conflict-free 8-byte reads
+    constexpr int NVP = (NPC + NT - 1) / NT;
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][32 * HD];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[2][HD * VLD];
+    const uint32_t qb = blockIdx.x, kh = blockIdx.y;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hf = lane >> 5;
+    const uint32_t h = kh * REP + wave;
+    const uint32_t q0 = qb * 32, qi = q0 + (lane & 31);
+    const uint32_t qr = qi < a.n ? qi : a.n - 1;  // lanes past the block compute a copy, store nothing
+    const uint32_t qpos = a.pos0 + qr;
+    const uint32_t kend = a.pos0 + min(q0 + 32, a.n);  // positions 0..kend-1 are attended
+    const uint32_t nch = (kend + 31) / 32;
+    const _Float16 *kb = a.kc + (size_t)kh * a.ctx * HD;
+    const _Float16 *vb = a.vc + (size_t)kh * a.ctx * HD;
+
+    // K chunk c -> Ks[buf]: LDS slot s (16 B) holds row s / NPR, piece
+    // (s % NPR) ^ (row % NPR); wavefront instruction i fills slots 64i..64i+63
+    auto stage_k = [&](uint32_t c, uint32_t buf) {
+        for (uint32_t i = wave; i < NPC / 64; i += REP) {
+            const uint32_t sl = 64 * i + lane, row = sl / NPR, pc = (sl % NPR) ^ (row % NPR);
+            const uint32_t kp = min(32 * c + row, kend - 1);  // past the end: any finite row (masked)
+            __builtin_amdgcn_global_load_lds(kb + (size_t)kp * HD + 8 * pc,
+                                             (lds_void_t *)(Ks[buf] + 64 * 8 * i), 16, 0, 0);
+        }
+    };
+    // V chunk c: piece p = (row p % 32, dims 8 (p / 32)..) through registers
+    uint4 vr[NVP];
+    auto load_v = [&](uint32_t c) {
+#pragma unroll
+        for (int j = 0; j < NVP; j++) {
+            const uint32_t p = tid + NT * j;
+            if (p < (uint32_t)NPC) {
+                const uint32_t row = p % 32, kp = min(32 * c + row, kend - 1);
+                vr[j] = *reinterpret_cast<const uint4 *>(vb + (size_t)kp * HD + 8 * (p / 32));
+            }
+        }
+    };
+    auto store_v = [&](uint32_t buf) {
+#pragma unroll
+        for (int j = 0; j < NVP; j++) {
+            const uint32_t p = tid + NT * j;
+            if (p < (uint32_t)NPC) {
+                const uint32_t row = p % 32, d0 = 8 * (p / 32);
+                const _Float16 *hv = reinterpret_cast<const _Float16 *>(&vr[j]);
+#pragma unroll
+                for (int e = 0; e < 8; e++) Vt[buf][(d0 + e) * VLD + row] = hv[e];
+            }
+        }
+    };
+
+    // this lane's query: dims 16 k + 8 hf .. + 7 of every K-step, scaled by
+    // 2^-e (e from the head's max |q|, both halves), split into f16 hi + lo
+    f16x8_t qh[KS], ql[KS];
+    float qsc;
+    {
+        const float *qp = a.q + ((size_t)qr * a.n_head + h) * HD + 8 * hf;
+        float qv[KS][8];
+        float qm = 0.f;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(qp + 16 * k);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qp + 16 * k + 4);
+            qv[k][0] = x0.x; qv[k][1] = x0.y; qv[k][2] = x0.z; qv[k][3] = x0.w;
+            qv[k][4] = x1.x; qv[k][5] = x1.y; qv[k][6] = x1.z; qv[k][7] = x1.w;
+#pragma unroll
+            for (int e = 0; e < 8; e++) qm = fmaxf(qm, fabsf(qv[k][e]));
+        }
+        qm = fmaxf(qm, __shfl_xor(qm, 32, 64));
+        int ex;
+        frexpf(qm, &ex);
+        ex = ex < -60 ? -60 : ex;
+        qsc = ldexpf(1.0f, ex) * a.scale;
+#pragma unroll
+        for (int k = 0; k < KS; k++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float x = ldexpf(qv[k][e], -ex);
+                const _Float16 xh = (_Float16)x;
+                qh[k][e] = xh;
+                ql[k][e] = (_Float16)(x - (float)xh);
+            }
+    }
+
+    f32x16_t o[OT];
+#pragma unroll
+    for (int t = 0; t < OT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[t][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    stage_k(0, 0);
+    load_v(0);
+    store_v(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (uint32_t c = 0; c < nch; c++) {
+        const uint32_t cur = c & 1;
+        const bool more = c + 1 < nch;
+        if (more) {
+            stage_k(c + 1, cur ^ 1);
+            load_v(c + 1);
+        }
+        // S^T = K Q^T: lane (query l%32) gets positions 8(r/4) + 4 hf + r%4
+        f32x16_t sc;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sc[r] = 0.f;
+        const uint32_t krow = lane & 31;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const uint32_t sl = krow * NPR + ((2 * k + hf) ^ (krow % NPR));
+            const f16x8_t kf = *reinterpret_cast<const f16x8_t *>(Ks[cur] + 8 * sl);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[k], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[k], sc, 0, 0, 0);
+        }
+        // online softmax of this query over the chunk (causal mask)
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t kp = 32 * c + 8 * (r >> 2) + 4 * hf + (r & 3);
+            sc[r] = kp <= qpos ? sc[r] * qsc : -INFINITY;
+            cmax = fmaxf(cmax, sc[r]);
+        }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        const float mn = fmaxf(m, cmax);  // finite: position 0 is in the first chunk
+        const float alpha = expf(m - mn);
+        float ps = 0.f;
+        f16x8_t ph[2], pl[2];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float p = expf(sc[r] - mn);
+            ps += p;
+            const _Float16 x = (_Float16)p;
+            ph[r >> 3][r & 7] = x;
+            pl[r >> 3][r & 7] = (_Float16)(p - (float)x);
+        }
+        ps += __shfl_xor(ps, 32, 64);
+        l = l * alpha + ps;
+        m = mn;
+        // O^T (dims x queries) = alpha O^T + V^T P^T; K slot j of step s is
+        // position 16 s + 4 hf + j (j < 4) or 16 s + 8 + 4 hf + j - 4
+#pragma unroll
+        for (int t = 0; t < OT; t++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[t][r] *= alpha;
+            const _Float16 *vrow = Vt[cur] + (32 * t + (lane & 31)) * VLD + 4 * hf;
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const f16x4_t v0 = *reinterpret_cast<const f16x4_t *>(vrow + 16 * st);
+                const f16x4_t v1 = *reinterpret_cast<const f16x4_t *>(vrow + 16 * st + 8);
+                const f16x8_t va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pl[st], o[t], 0, 0, 0);
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph[st], o[t], 0, 0, 0);
+            }
+        }
+        if (more) store_v(cur ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+    // out[token][head][dim]: lane holds dims 32 t + 8 (r/4) + 4 hf + r%4
+    if (qi < a.n) {
+        const float inv = 1.0f / l;
+        float *op = a.out + ((size_t)qi * a.n_head + h) * HD;
+#pragma unroll
+        for (int t = 0; t < OT; t++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<float4 *>(op + 32 * t + 8 * g + 4 * hf) =
+                    make_float4(o[t][4 * g] * inv, o[t][4 * g + 1] * inv, o[t][4 * g + 2] * inv,
+                                o[t][4 * g + 3] * inv);
+    }
+}
+
 // G = silu(G) * U elementwise (ops.rs:978-988)
 __global__ void k_swiglu_rows(float *__restrict__ G, const float *__restrict__ U, size_t n) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
@@ -206,8 +407,21 @@ hipError_t launch_qkv_post(const float *qt, const float *kt, const float *vt, co
 hipError_t launch_attn_prefill(const float *q, const _Float16 *kc, const _Float16 *vc, float *out,
                                uint32_t n, uint32_t pos0, uint32_t n_head, uint32_t n_kv,
                                uint32_t hd, uint32_t ctx, hipStream_t s) {
-    if (n_head / n_kv > 8) return hipErrorInvalidValue;
+    if (n == 0 || n_kv == 0 || n_head % n_kv || n_head / n_kv > 8) return hipErrorInvalidValue;
     AttnPre a = {q, kc, vc, out, n, pos0, n_head, n_kv, ctx, 1.0f / sqrtf((float)hd)};
+    if (hd == 64 || hd == 128) {
+        const dim3 g((n + 31) / 32, n_kv);
+        void (*fn)(AttnPre) = nullptr;
+#define LRS_PF_REP(R)                                                                 \
+    case R: fn = hd == 64 ? k_attn_pf_mma<64, R> : k_attn_pf_mma<128, R>; break;
+        switch (n_head / n_kv) {
+            LRS_PF_REP(1) LRS_PF_REP(2) LRS_PF_REP(3) LRS_PF_REP(4)
+            LRS_PF_REP(5) LRS_PF_REP(6) LRS_PF_REP(7) LRS_PF_REP(8)
+        }
+#undef LRS_PF_REP
+        hipLaunchKernelGGL(fn, g, dim3(64 * (n_head / n_kv)), 0, s, a);
+        return hipGetLastError();
+    }
     dim3 grid(n, n_kv);
     switch (hd) {
     case 64: hipLaunchKernelGGL(k_attn_prefill<64>, grid, dim3(256), 0, s, a); break;
