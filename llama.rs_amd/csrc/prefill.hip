@@ -86,10 +86,8 @@ __global__ void k_qkv_post(QkvPost a) {
     }
 }
 
-// Causal GQA attention of token b (position pos0 + b) over cache positions
-// 0..pos0+b, online softmax over chunks of 64 positions staged in LDS (K
-// transposed so that lane = position reads conflict-free).  One workgroup per
-// (token, KV head); wavefront w handles query heads w, w+4, ... of the group.
+// Causal GQA attention of the block: token b (position pos0 + b) attends to
+// cache positions 0..pos0+b (attention.rs:76-166 per token).
 struct AttnPre {
     const float *q;                 // [n][n_head * hd]
     const _Float16 *kc, *vc;        // [n_kv][ctx][hd]
@@ -98,86 +96,11 @@ struct AttnPre {
     float scale;
 };
 
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_prefill(AttnPre a) {
-    constexpr int CH = 64;
-    constexpr int DPL = HD / 64;  // dims per lane in the V sum
-    __shared__ float kt[HD][CH + 1];
-    __shared__ _Float16 vs[CH][HD];
-    __shared__ float qs[8][HD];
-    __shared__ float ps[4][CH];
-    const uint32_t b = blockIdx.x, kh = blockIdx.y;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t rep = a.n_head / a.n_kv, h0 = kh * rep;
-    const uint32_t L = a.pos0 + b + 1;
-    const size_t qrow = (size_t)b * a.n_head * HD;
-    for (uint32_t i = tid; i < rep * HD; i += 256) qs[i / HD][i % HD] = a.q[qrow + (size_t)h0 * HD + i];
-
-    float m[2], l[2], acc[2][DPL];
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-        m[s] = -INFINITY;
-        l[s] = 0.f;
-#pragma unroll
-        for (int k = 0; k < DPL; k++) acc[s][k] = 0.f;
-    }
-    const _Float16 *kbase = a.kc + (size_t)kh * a.ctx * HD;
-    const _Float16 *vbase = a.vc + (size_t)kh * a.ctx * HD;
-    for (uint32_t c0 = 0; c0 < L; c0 += CH) {
-        const uint32_t nc = min((uint32_t)CH, L - c0);
-        __syncthreads();  // the previous chunk is consumed (and q is staged)
-        for (uint32_t i = tid; i < CH * HD; i += 256) {
-            const uint32_t j = i / HD, d = i % HD;
-            const bool ok = j < nc;
-            kt[d][j] = ok ? (float)kbase[(size_t)(c0 + j) * HD + d] : 0.f;
-            vs[j][d] = ok ? vbase[(size_t)(c0 + j) * HD + d] : (_Float16)0.f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const uint32_t r = wave + 4 * s;
-            if (r >= rep) continue;
-            // score of position c0 + lane
-            float sc = 0.f;
-#pragma unroll 8
-            for (int d = 0; d < HD; d++) sc = fmaf(qs[r][d], kt[d][lane], sc);
-            sc = lane < nc ? sc * a.scale : -INFINITY;
-            float mc = sc;
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o, 64));
-            const float mn = fmaxf(m[s], mc);
-            const float alpha = expf(m[s] - mn);  // m = -inf at the first chunk: 0
-            const float p = lane < nc ? expf(sc - mn) : 0.f;
-            float ls = p;
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) ls += __shfl_xor(ls, o, 64);
-            l[s] = l[s] * alpha + ls;
-            m[s] = mn;
-            ps[wave][lane] = p;
-            // V sum: lane owns dims DPL*lane .. DPL*lane + DPL - 1 (wave-local
-            // LDS row: written and read by this wavefront only)
-#pragma unroll
-            for (int k = 0; k < DPL; k++) acc[s][k] *= alpha;
-            for (uint32_t j = 0; j < nc; j++) {
-                const float pj = ps[wave][j];
-#pragma unroll
-                for (int k = 0; k < DPL; k++) acc[s][k] = fmaf(pj, (float)vs[j][DPL * lane + k], acc[s][k]);
-            }
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-        const uint32_t r = wave + 4 * s;
-        if (r >= rep) continue;
-#pragma unroll
-        for (int k = 0; k < DPL; k++)
-            a.out[qrow + (size_t)(h0 + r) * HD + DPL * lane + k] = acc[s][k] / l[s];
-    }
-}
-
-// The same attention on the matrix cores (head_dim 64 / 128).  Workgroup
-// (32-token query block, KV head), one wavefront per query head of the GQA
-// group.  Per chunk of 32 cache positions each wavefront forms the transposed
+// On the matrix cores: workgroup (32-token query block,
+// KV head, group of NW query heads of the GQA group), one wavefront per query
+// head: NW = the whole group for head_dim <= 128; at head_dim 256 at most 4
+// wavefronts (the query and output registers of a wavefront exceed half the
+// register file, so one wavefront per SIMD).  Per chunk of 32 cache positions each wavefront forms the transposed
 // score tile S^T = K Q^T (32 positions x 32 queries) with
 // v_mfma_f32_32x32x16_f16: K is the f16 cache (exact), Q is split into f16
 // hi + lo after scaling each query by a power of two (2^-e >= 1 / max |q|),
@@ -189,28 +112,34 @@ __global__ __launch_bounds__(256) void k_attn_prefill(AttnPre a) {
 // which the score layout holds them (4 positions of the lane's half, then the
 // 4 positions 8 further), and V^T is read from LDS in the same order.
 // K is staged with global_load_lds into an XOR-swizzled row layout
-// (conflict-free 16-byte reads), V through registers into a transposed,
-// padded layout; both are double-buffered with the next chunk's loads in
-// flight during the current chunk's matrix work.
+// (conflict-free 16-byte reads), V into a transposed, padded layout: through
+// registers, or at head_dim 256 (no registers to spare) through a row-major
+// LDS copy transposed after each chunk.  The next chunk's loads are in flight
+// during the current chunk's matrix work.
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int HD, int REP>
-__global__ __launch_bounds__(64 * REP) void k_attn_pf_mma(AttnPre a) {
-    constexpr int NT = 64 * REP;
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_pf_mma(AttnPre a) {
+    constexpr int NT = 64 * NW;
     constexpr int KS = HD / 16;           // K-steps of S^T (16 dims each)
     constexpr int OT = HD / 32;           // O^T tiles of 32 dims
     constexpr int NPR = HD / 8;           // 16-byte pieces per K / V row
     constexpr int NPC = 32 * NPR;         // pieces per chunk
     constexpr int VLD = 36;               // V^T row (f16): 72 B, conflict-free 8-byte reads
     constexpr int NVP = (NPC + NT - 1) / NT;
+    constexpr bool VLDS = HD > 128;       // V staged through LDS instead of registers
     __shared__ __attribute__((aligned(16))) _Float16 Ks[2][32 * HD];
     __shared__ __attribute__((aligned(16))) _Float16 Vt[2][HD * VLD];
-    const uint32_t qb = blockIdx.x, kh = blockIdx.y;
+    __shared__ __attribute__((aligned(16))) _Float16 Vraw[VLDS ? 32 * HD : 8];
+    const uint32_t rep = a.n_head / a.n_kv, ng = (rep + NW - 1) / NW;
+    const uint32_t qb = blockIdx.x, kh = blockIdx.y / ng;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hf = lane >> 5;
-    const uint32_t h = kh * REP + wave;
+    const uint32_t hl = (blockIdx.y % ng) * NW + wave;  // query head within the group
+    const bool hact = hl < rep;                         // an idle wavefront stages and stores nothing
+    const uint32_t h = kh * rep + (hact ? hl : rep - 1);
     const uint32_t q0 = qb * 32, qi = q0 + (lane & 31);
     const uint32_t qr = qi < a.n ? qi : a.n - 1;  // lanes past the block compute a copy, store nothing
     const uint32_t qpos = a.pos0 + qr;
@@ -222,18 +151,36 @@ __global__ __launch_bounds__(64 * REP) void k_attn_pf_mma(AttnPre a) {
     // K chunk c -> Ks[buf]: LDS slot s (16 B) holds row s / NPR, piece
     // (s % NPR) ^ (row % NPR); wavefront instruction i fills slots 64i..64i+63
     auto stage_k = [&](uint32_t c, uint32_t buf) {
-        for (uint32_t i = wave; i < NPC / 64; i += REP) {
+        for (uint32_t i = wave; i < NPC / 64; i += NW) {
             const uint32_t sl = 64 * i + lane, row = sl / NPR, pc = (sl % NPR) ^ (row % NPR);
             const uint32_t kp = min(32 * c + row, kend - 1);  // past the end: any finite row (masked)
             __builtin_amdgcn_global_load_lds(kb + (size_t)kp * HD + 8 * pc,
                                              (lds_void_t *)(Ks[buf] + 64 * 8 * i), 16, 0, 0);
         }
     };
-    // V chunk c: piece p = (row p % 32, dims 8 (p / 32)..) through registers
-    uint4 vr[NVP];
+    // V chunk c: piece p = (row p % 32, dims 8 (p / 32)..), through registers
+    // (load_v, store_v) or, at head_dim 256, global_load_lds into Vraw slot p
+    // and an LDS transpose (vraw_to_vt)
+    uint4 vr[VLDS ? 1 : NVP];
+    auto stage_vraw = [&](uint32_t c) {
+        for (uint32_t i = wave; i < NPC / 64; i += NW) {
+            const uint32_t p = 64 * i + lane, row = p % 32, kp = min(32 * c + row, kend - 1);
+            __builtin_amdgcn_global_load_lds(vb + (size_t)kp * HD + 8 * (p / 32),
+                                             (lds_void_t *)(Vraw + 64 * 8 * i), 16, 0, 0);
+        }
+    };
+    auto vraw_to_vt = [&](uint32_t buf) {
+        for (uint32_t p = tid; p < (uint32_t)NPC; p += NT) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(Vraw + 8 * p);
+            const _Float16 *hv = reinterpret_cast<const _Float16 *>(&v);
+            const uint32_t row = p % 32, d0 = 8 * (p / 32);
+#pragma unroll
+            for (int e = 0; e < 8; e++) Vt[buf][(d0 + e) * VLD + row] = hv[e];
+        }
+    };
     auto load_v = [&](uint32_t c) {
 #pragma unroll
-        for (int j = 0; j < NVP; j++) {
+        for (int j = 0; j < (VLDS ? 1 : NVP); j++) {
             const uint32_t p = tid + NT * j;
             if (p < (uint32_t)NPC) {
                 const uint32_t row = p % 32, kp = min(32 * c + row, kend - 1);
@@ -243,7 +190,7 @@ __global__ __launch_bounds__(64 * REP) void k_attn_pf_mma(AttnPre a) {
     };
     auto store_v = [&](uint32_t buf) {
 #pragma unroll
-        for (int j = 0; j < NVP; j++) {
+        for (int j = 0; j < (VLDS ? 1 : NVP); j++) {
             const uint32_t p = tid + NT * j;
             if (p < (uint32_t)NPC) {
                 const uint32_t row = p % 32, d0 = 8 * (p / 32);
@@ -295,8 +242,15 @@ __global__ __launch_bounds__(64 * REP) void k_attn_pf_mma(AttnPre a) {
     float m = -INFINITY, l = 0.f;
 
     stage_k(0, 0);
-    load_v(0);
-    store_v(0);
+    if constexpr (VLDS) {
+        stage_vraw(0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        vraw_to_vt(0);
+    } else {
+        load_v(0);
+        store_v(0);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (uint32_t c = 0; c < nch; c++) {
@@ -304,7 +258,10 @@ __global__ __launch_bounds__(64 * REP) void k_attn_pf_mma(AttnPre a) {
         const bool more = c + 1 < nch;
         if (more) {
             stage_k(c + 1, cur ^ 1);
-            load_v(c + 1);
+            if constexpr (VLDS)
+                stage_vraw(c + 1);
+            else
+                load_v(c + 1);
         }
         // S^T = K Q^T: lane (query l%32) gets positions 8(r/4) + 4 hf + r%4
         f32x16_t sc;
@@ -358,12 +315,20 @@ __global__ __launch_bounds__(64 * REP) void k_attn_pf_mma(AttnPre a) {
                 o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, ph[st], o[t], 0, 0, 0);
             }
         }
-        if (more) store_v(cur ^ 1);
+        if constexpr (!VLDS) {
+            if (more) store_v(cur ^ 1);
+        }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        if constexpr (VLDS) {
+            if (more) {
+                vraw_to_vt(cur ^ 1);
+                __syncthreads();
+            }
+        }
     }
     // out[token][head][dim]: lane holds dims 32 t + 8 (r/4) + 4 hf + r%4
-    if (qi < a.n) {
+    if (qi < a.n && hact) {
         const float inv = 1.0f / l;
         float *op = a.out + ((size_t)qi * a.n_head + h) * HD;
 #pragma unroll
@@ -409,26 +374,32 @@ hipError_t launch_attn_prefill(const float *q, const _Float16 *kc, const _Float1
                                uint32_t hd, uint32_t ctx, hipStream_t s) {
     if (n == 0 || n_kv == 0 || n_head % n_kv || n_head / n_kv > 8) return hipErrorInvalidValue;
     AttnPre a = {q, kc, vc, out, n, pos0, n_head, n_kv, ctx, 1.0f / sqrtf((float)hd)};
+    const uint32_t rep = n_head / n_kv;
+    // wavefronts per workgroup: the whole group, or at head_dim 256 an even
+    // share of it in groups of at most 4
+    const uint32_t nw = hd == 256 ? (rep + (rep + 3) / 4 - 1) / ((rep + 3) / 4) : rep;
+    void (*fn)(AttnPre) = nullptr;
+#define LRS_PF_NW(W)                                                                     \
+    case W:                                                                              \
+        fn = hd == 64 ? k_attn_pf_mma<64, W> : hd == 128 ? k_attn_pf_mma<128, W> : nullptr; \
+        break;
     if (hd == 64 || hd == 128) {
-        const dim3 g((n + 31) / 32, n_kv);
-        void (*fn)(AttnPre) = nullptr;
-#define LRS_PF_REP(R)                                                                 \
-    case R: fn = hd == 64 ? k_attn_pf_mma<64, R> : k_attn_pf_mma<128, R>; break;
-        switch (n_head / n_kv) {
-            LRS_PF_REP(1) LRS_PF_REP(2) LRS_PF_REP(3) LRS_PF_REP(4)
-            LRS_PF_REP(5) LRS_PF_REP(6) LRS_PF_REP(7) LRS_PF_REP(8)
+        switch (nw) {
+            LRS_PF_NW(1) LRS_PF_NW(2) LRS_PF_NW(3) LRS_PF_NW(4)
+            LRS_PF_NW(5) LRS_PF_NW(6) LRS_PF_NW(7) LRS_PF_NW(8)
         }
-#undef LRS_PF_REP
-        hipLaunchKernelGGL(fn, g, dim3(64 * (n_head / n_kv)), 0, s, a);
-        return hipGetLastError();
+    } else if (hd == 256) {
+        switch (nw) {
+        case 1: fn = k_attn_pf_mma<256, 1>; break;
+        case 2: fn = k_attn_pf_mma<256, 2>; break;
+        case 3: fn = k_attn_pf_mma<256, 3>; break;
+        case 4: fn = k_attn_pf_mma<256, 4>; break;
+        }
     }
-    dim3 grid(n, n_kv);
-    switch (hd) {
-    case 64: hipLaunchKernelGGL(k_attn_prefill<64>, grid, dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL(k_attn_prefill<128>, grid, dim3(256), 0, s, a); break;
-    case 256: hipLaunchKernelGGL(k_attn_prefill<256>, grid, dim3(256), 0, s, a); break;
-    default: return hipErrorInvalidValue;
-    }
+#undef LRS_PF_NW
+    if (!fn) return hipErrorInvalidValue;
+    const uint32_t ng = (rep + nw - 1) / nw;
+    hipLaunchKernelGGL(fn, dim3((n + 31) / 32, n_kv * ng), dim3(64 * nw), 0, s, a);
     return hipGetLastError();
 }
 
