@@ -72,10 +72,17 @@ __device__ __forceinline__ void wload(const GemmArgs &g, uint32_t n, uint32_t e,
     }
 }
 
-// the 16 weights in f32, exactly as ggml_cpu::dequant (dequant.rs:101-258)
+// the 16 weights in f32, exactly as ggml_cpu::dequant (dequant.rs:101-258):
+// wprep decodes the run's scale (and min), wdeq4 the weights 4c..4c+3, so the
+// dequant can be spread between the matrix-core ops of a pipeline step
+struct DeqPrep {
+    float a, b;    // Q4_K: d * sc, dmin * m; Q6_K: d * scale
+    uint32_t sel;  // Q4_K: high nibbles; Q6_K: quarter of the half
+};
 template <uint32_t T>
-__device__ __forceinline__ void wdeq(const WRaw<T> &w, uint32_t e, float (&v)[16]) {
+__device__ __forceinline__ DeqPrep wprep(const WRaw<T> &w, uint32_t e) {
     const uint32_t o = e & 255;
+    DeqPrep p;
     if constexpr (T == T_Q4_K) {
         const uint32_t j = o >> 6, hi = (o >> 5) & 1;  // qs group, high nibbles
         // get_scale_min_k4 (dequant.rs:101-110): scale bytes 0-3, 4-7, 8-11 are
@@ -86,26 +93,35 @@ __device__ __forceinline__ void wdeq(const WRaw<T> &w, uint32_t e, float (&v)[16
         const uint32_t sc = jj < 4 ? (by & 63) : ((bw & 0xF) | ((by >> 6) << 4));
         const uint32_t m = jj < 4 ? (bz & 63) : ((bw >> 4) | ((bz >> 6) << 4));
         const float dv = h2f((uint16_t)(w.hd.x & 0xFFFF)), mv = h2f((uint16_t)(w.hd.x >> 16));
-        const float d1 = __fmul_rn(dv, (float)sc), m1 = __fmul_rn(mv, (float)m);
-        const uint32_t qw[4] = {w.qs.x, w.qs.y, w.qs.z, w.qs.w};
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t byte = (qw[i >> 2] >> (8 * (i & 3))) & 0xFF;
-            const uint32_t q = hi ? (byte >> 4) : (byte & 15);
-            v[i] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
-        }
+        p.a = __fmul_rn(dv, (float)sc);
+        p.b = __fmul_rn(mv, (float)m);
+        p.sel = hi;
     } else {  // T_Q6_K
-        const uint32_t quarter = (o >> 5) & 3;
-        const float ds = __fmul_rn(h2f((uint16_t)w.d), (float)(int8_t)(w.sc & 0xFF));
-        const uint32_t lw[4] = {w.ql.x, w.ql.y, w.ql.z, w.ql.w};
-        const uint32_t hw[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+        p.a = __fmul_rn(h2f((uint16_t)w.d), (float)(int8_t)(w.sc & 0xFF));
+        p.b = 0.f;
+        p.sel = (o >> 5) & 3;
+    }
+    return p;
+}
+template <uint32_t T>
+__device__ __forceinline__ void wdeq4(const WRaw<T> &w, const DeqPrep &p, int c, float (&v)[16]) {
+    if constexpr (T == T_Q4_K) {
+        const uint32_t qw = c == 0 ? w.qs.x : c == 1 ? w.qs.y : c == 2 ? w.qs.z : w.qs.w;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t lb = (lw[i >> 2] >> (8 * (i & 3))) & 0xFF;
-            const uint32_t hb = (hw[i >> 2] >> (8 * (i & 3))) & 0xFF;
-            const uint32_t lo = quarter < 2 ? (lb & 15) : (lb >> 4);
-            const int q = (int)(lo | (((hb >> (2 * quarter)) & 3) << 4)) - 32;
-            v[i] = __fmul_rn(ds, (float)q);
+        for (int i = 0; i < 4; i++) {
+            const uint32_t byte = (qw >> (8 * i)) & 0xFF;
+            const uint32_t q = p.sel ? (byte >> 4) : (byte & 15);
+            v[4 * c + i] = __fsub_rn(__fmul_rn(p.a, (float)q), p.b);
+        }
+    } else {  // T_Q6_K: q = (ql nibble | qh 2 bits << 4) - 32
+        const uint32_t lw = c == 0 ? w.ql.x : c == 1 ? w.ql.y : c == 2 ? w.ql.z : w.ql.w;
+        const uint32_t hw = c == 0 ? w.qh.x : c == 1 ? w.qh.y : c == 2 ? w.qh.z : w.qh.w;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lb = (lw >> (8 * i)) & 0xFF, hb = (hw >> (8 * i)) & 0xFF;
+            const uint32_t lo = p.sel < 2 ? (lb & 15) : (lb >> 4);
+            const int q = (int)(lo | (((hb >> (2 * p.sel)) & 3) << 4)) - 32;
+            v[4 * c + i] = __fmul_rn(p.a, (float)q);
         }
     }
 }
@@ -193,31 +209,60 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
                 *reinterpret_cast<u32x4 *>(&As[BUF][p][(sr + 128 * j) * GM_LD + sq + 8]) = A[p][j][1]; \
             }                                                                                 \
         float v_[16];                                                                         \
-        wdeq<T>(W, kbase + (K0) + sq, v_);                                                    \
+        const DeqPrep dp_ = wprep<T>(W, kbase + (K0) + sq);                                   \
+        _Pragma("unroll") for (int c = 0; c < 4; c++) wdeq4<T>(W, dp_, c, v_);                \
         put16<PREC>(&Ws[BUF][0][sr * GM_LD + sq], &Ws[BUF][NS - 1][sr * GM_LD + sq], v_);     \
     } while (0)
-    auto mma = [&](int buf) __attribute__((always_inline)) {
+    // operand fragments of sub-step ks (K16) from LDS buffer buf
+    auto frag = [&](int buf, int ks, bf16x8 (&a)[NS][MT], bf16x8 (&b)[NS]) __attribute__((always_inline)) {
+        const uint32_t kk = 16 * ks + 8 * (lane >> 5);
 #pragma unroll
-        for (int ks = 0; ks < GM_BK / 16; ks++) {
-            const uint32_t kk = 16 * ks + 8 * (lane >> 5);
-            bf16x8 a[NS][MT], b[NS];
+        for (int p = 0; p < NS; p++) {
 #pragma unroll
-            for (int p = 0; p < NS; p++) {
-#pragma unroll
-                for (int u = 0; u < MT; u++)
-                    a[p][u] = *reinterpret_cast<const bf16x8 *>(&As[buf][p][((BM / 2) * wm + 32 * u + (lane & 31)) * GM_LD + kk]);
-                b[p] = *reinterpret_cast<const bf16x8 *>(&Ws[buf][p][(32 * wn + (lane & 31)) * GM_LD + kk]);
-            }
-#pragma unroll
-            for (int i = 0; i < MT; i++) {
-                if constexpr (PREC == 3) {
-                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0], acc[i], 0, 0, 0);
-                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1], acc[i], 0, 0, 0);
-                }
-                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0], acc[i], 0, 0, 0);
-            }
+            for (int u = 0; u < MT; u++)
+                a[p][u] = *reinterpret_cast<const bf16x8 *>(&As[buf][p][((BM / 2) * wm + 32 * u + (lane & 31)) * GM_LD + kk]);
+            b[p] = *reinterpret_cast<const bf16x8 *>(&Ws[buf][p][(32 * wn + (lane & 31)) * GM_LD + kk]);
         }
     };
+    auto mfma = [&](const bf16x8 (&a)[NS][MT], const bf16x8 (&b)[NS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            if constexpr (PREC == 3) {
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0], acc[i], 0, 0, 0);
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1], acc[i], 0, 0, 0);
+            }
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0], acc[i], 0, 0, 0);
+        }
+    };
+    // one pipeline step: step k's four K16 sub-steps from buffer buf (the
+    // fragments of sub-step ks+1 read while sub-step ks's matrix-core ops
+    // run), step k+1's activations copied into the other buffer first and
+    // its weights dequantized a quarter after each sub-step, so the VALU
+    // work overlaps the matrix cores
+#define LRS_GSTEP(BUF, A, W, K0)                                                              \
+    do {                                                                                      \
+        _Pragma("unroll") for (int p = 0; p < NS; p++)                                         \
+            _Pragma("unroll") for (int j = 0; j < AR; j++) {                                   \
+                *reinterpret_cast<u32x4 *>(&As[1 - (BUF)][p][(sr + 128 * j) * GM_LD + sq]) = A[p][j][0];     \
+                *reinterpret_cast<u32x4 *>(&As[1 - (BUF)][p][(sr + 128 * j) * GM_LD + sq + 8]) = A[p][j][1]; \
+            }                                                                                 \
+        const DeqPrep dp_ = wprep<T>(W, kbase + (K0) + sq);                                   \
+        float v_[16];                                                                         \
+        bf16x8 fa0[NS][MT], fb0[NS], fa1[NS][MT], fb1[NS];                                    \
+        frag(BUF, 0, fa0, fb0);                                                               \
+        frag(BUF, 1, fa1, fb1);                                                               \
+        mfma(fa0, fb0);                                                                       \
+        wdeq4<T>(W, dp_, 0, v_);                                                              \
+        frag(BUF, 2, fa0, fb0);                                                               \
+        mfma(fa1, fb1);                                                                       \
+        wdeq4<T>(W, dp_, 1, v_);                                                              \
+        frag(BUF, 3, fa1, fb1);                                                               \
+        mfma(fa0, fb0);                                                                       \
+        wdeq4<T>(W, dp_, 2, v_);                                                              \
+        mfma(fa1, fb1);                                                                       \
+        wdeq4<T>(W, dp_, 3, v_);                                                              \
+        put16<PREC>(&Ws[1 - (BUF)][0][sr * GM_LD + sq], &Ws[1 - (BUF)][NS - 1][sr * GM_LD + sq], v_); \
+    } while (0)
 
     const uint32_t nk = kspan / GM_BK;  // a multiple of 4
     auto kc = [&](uint32_t k) { return min(k, nk - 1) * GM_BK; };  // look-ahead past the end repeats the last step (unused)
@@ -228,24 +273,21 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     __syncthreads();
     for (uint32_t k = 0; k < nk; k += 4) {
         LRS_GFETCH(a3, w3, kc(k + 3));
-        mma(0);
-        LRS_GSTAGE(1, a1, w1, kc(k + 1));
+        LRS_GSTEP(0, a1, w1, kc(k + 1));
         __syncthreads();
         LRS_GFETCH(a0, w0, kc(k + 4));
-        mma(1);
-        LRS_GSTAGE(0, a2, w2, kc(k + 2));
+        LRS_GSTEP(1, a2, w2, kc(k + 2));
         __syncthreads();
         LRS_GFETCH(a1, w1, kc(k + 5));
-        mma(0);
-        LRS_GSTAGE(1, a3, w3, kc(k + 3));
+        LRS_GSTEP(0, a3, w3, kc(k + 3));
         __syncthreads();
         LRS_GFETCH(a2, w2, kc(k + 6));
-        mma(1);
-        LRS_GSTAGE(0, a0, w0, kc(k + 4));
+        LRS_GSTEP(1, a0, w0, kc(k + 4));
         __syncthreads();
     }
 #undef LRS_GFETCH
 #undef LRS_GSTAGE
+#undef LRS_GSTEP
     // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
     const uint32_t n = n0 + 32 * wn + (lane & 31);
 #pragma unroll
