@@ -162,7 +162,11 @@ __device__ __forceinline__ void put16(__bf16 *hi, __bf16 *lo, const float (&v)[1
 template <uint32_t T, int PREC, int BM>
 __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     constexpr int NS = PREC == 3 ? 2 : 1;  // hi (+ lo) planes
-    constexpr int MT = BM / 64;            // 32-row MFMA tiles per wavefront
+    // wavefront grid: WM x WN = 8 wavefronts, each (BM / WM) x (128 / WN) of
+    // the tile in MT x NT MFMA tiles of 32 x 32 (the 256-token tile uses 4 x 2
+    // wavefronts of 64 x 64: fewer LDS operand reads per matrix-core op)
+    constexpr int WM = BM == 256 ? 4 : 2, WN = 8 / WM;
+    constexpr int MT = BM / WM / 32, NT = GM_BN / WN / 32;
     constexpr int AR = BM / 128;           // activation rows staged per thread
     __shared__ __attribute__((aligned(16))) __bf16 As[2][NS][BM * GM_LD];
     __shared__ __attribute__((aligned(16))) __bf16 Ws[2][NS][GM_BN * GM_LD];
@@ -173,7 +177,7 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     const uint32_t kspan = g.K / g.ks;                                 // a multiple of 256
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t m0 = (t / g.nn) * BM, n0 = (t % g.nn) * GM_BN;
-    const uint32_t wm = wave >> 2, wn = wave & 3;  // wave's BM/2 x 32 part
+    const uint32_t wm = wave / WN, wn = wave % WN;
     // staging roles: thread t handles row t/4, K quarter t%4 (16 of the 64)
     const uint32_t sr = tid >> 2, sq = (tid & 3) * 16;
     const uint32_t wr = min(n0 + sr, g.N - 1);
@@ -183,11 +187,13 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
         aoff[j] = (size_t)min(m0 + sr + 128 * j, g.M - 1) * g.K + sq + (size_t)kz * kspan;
     const uint32_t kbase = kz * kspan;  // weight element offset of the slice
 
-    f32x16 acc[MT];
+    f32x16 acc[MT][NT];
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) acc[i][r] = 0.f;
+        for (int jn = 0; jn < NT; jn++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][jn][r] = 0.f;
 
     u32x4 a0[NS][AR][2], a1[NS][AR][2], a2[NS][AR][2], a3[NS][AR][2];
     WRaw<T> w0, w1, w2, w3;
@@ -214,25 +220,29 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
         put16<PREC>(&Ws[BUF][0][sr * GM_LD + sq], &Ws[BUF][NS - 1][sr * GM_LD + sq], v_);     \
     } while (0)
     // operand fragments of sub-step ks (K16) from LDS buffer buf
-    auto frag = [&](int buf, int ks, bf16x8 (&a)[NS][MT], bf16x8 (&b)[NS]) __attribute__((always_inline)) {
+    auto frag = [&](int buf, int ks, bf16x8 (&a)[NS][MT], bf16x8 (&b)[NS][NT]) __attribute__((always_inline)) {
         const uint32_t kk = 16 * ks + 8 * (lane >> 5);
 #pragma unroll
         for (int p = 0; p < NS; p++) {
 #pragma unroll
             for (int u = 0; u < MT; u++)
-                a[p][u] = *reinterpret_cast<const bf16x8 *>(&As[buf][p][((BM / 2) * wm + 32 * u + (lane & 31)) * GM_LD + kk]);
-            b[p] = *reinterpret_cast<const bf16x8 *>(&Ws[buf][p][(32 * wn + (lane & 31)) * GM_LD + kk]);
+                a[p][u] = *reinterpret_cast<const bf16x8 *>(&As[buf][p][((BM / WM) * wm + 32 * u + (lane & 31)) * GM_LD + kk]);
+#pragma unroll
+            for (int u = 0; u < NT; u++)
+                b[p][u] = *reinterpret_cast<const bf16x8 *>(&Ws[buf][p][((GM_BN / WN) * wn + 32 * u + (lane & 31)) * GM_LD + kk]);
         }
     };
-    auto mfma = [&](const bf16x8 (&a)[NS][MT], const bf16x8 (&b)[NS]) __attribute__((always_inline)) {
+    auto mfma = [&](const bf16x8 (&a)[NS][MT], const bf16x8 (&b)[NS][NT]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < MT; i++) {
-            if constexpr (PREC == 3) {
-                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0], acc[i], 0, 0, 0);
-                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1], acc[i], 0, 0, 0);
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+            for (int jn = 0; jn < NT; jn++) {
+                if constexpr (PREC == 3) {
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][i], b[0][jn], acc[i][jn], 0, 0, 0);
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[1][jn], acc[i][jn], 0, 0, 0);
+                }
+                acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0][jn], acc[i][jn], 0, 0, 0);
             }
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0][i], b[0], acc[i], 0, 0, 0);
-        }
     };
     // one pipeline step: step k's four K16 sub-steps from buffer buf (the
     // fragments of sub-step ks+1 read while sub-step ks's matrix-core ops
@@ -248,7 +258,7 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
             }                                                                                 \
         const DeqPrep dp_ = wprep<T>(W, kbase + (K0) + sq);                                   \
         float v_[16];                                                                         \
-        bf16x8 fa0[NS][MT], fb0[NS], fa1[NS][MT], fb1[NS];                                    \
+        bf16x8 fa0[NS][MT], fb0[NS][NT], fa1[NS][MT], fb1[NS][NT];                            \
         frag(BUF, 0, fa0, fb0);                                                               \
         frag(BUF, 1, fa1, fb1);                                                               \
         mfma(fa0, fb0);                                                                       \
@@ -289,21 +299,24 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
 #undef LRS_GSTAGE
 #undef LRS_GSTEP
     // D layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column l%32
-    const uint32_t n = n0 + 32 * wn + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < MT; i++)
+    for (int jn = 0; jn < NT; jn++) {
+        const uint32_t n = n0 + (GM_BN / WN) * wn + 32 * jn + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const uint32_t m = m0 + (BM / 2) * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (m < g.M && n < g.N) {
-                if (g.ks > 1) {
-                    g.part[((size_t)kz * g.M + m) * g.N + n] = acc[i][r];
-                } else {
-                    float *o = g.y + (size_t)m * g.ldy + n;
-                    *o = g.accum ? *o + acc[i][r] : acc[i][r];
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t m = m0 + (BM / WM) * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < g.M && n < g.N) {
+                    if (g.ks > 1) {
+                        g.part[((size_t)kz * g.M + m) * g.N + n] = acc[i][jn][r];
+                    } else {
+                        float *o = g.y + (size_t)m * g.ldy + n;
+                        *o = g.accum ? *o + acc[i][jn][r] : acc[i][jn][r];
+                    }
                 }
             }
-        }
+    }
 }
 
 // y[m][n] (+)= sum over the K slices of part[z][m][n], slices in order
