@@ -52,7 +52,12 @@ __device__ __forceinline__ float hf16(uint32_t h) {
     __builtin_memcpy(&v, &b, 2);
     return (float)v;
 }
-__device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+// weight bytes are read once per token: non-temporal loads
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
 __device__ __forceinline__ v4i asv(uint4 u) {
     v4i r = {(int)u.x, (int)u.y, (int)u.z, (int)u.w};
     return r;
