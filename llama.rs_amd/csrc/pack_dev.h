@@ -6,17 +6,31 @@
 
 namespace lrs {
 
+// DPP lane exchange within a row of 16 lanes
+template <int CTRL>
+__device__ __forceinline__ float pk_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
 // Packs one 32-element block held one element per lane by the 32 lanes of a
 // half wavefront (lane i of the half = element i).  Writes the 3 digit bytes
-// of the element and, from lane 0 of the half, the block's meta.
+// of the element and, from lane 0 of the half, the block's meta.  The max and
+// the 16-element sums reduce over rows of 16 lanes with DPP (quad_perm
+// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then one exchange
+// between the two rows of the half.
 __device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p) {
     const uint32_t i = threadIdx.x & 31;
     float amax = fabsf(v);
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    amax = fmaxf(amax, pk_dpp<0xB1>(amax));
+    amax = fmaxf(amax, pk_dpp<0x4E>(amax));
+    amax = fmaxf(amax, pk_dpp<0x141>(amax));
+    amax = fmaxf(amax, pk_dpp<0x140>(amax));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     float r16 = v;  // sum of this lane's 16-element run
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) r16 += __shfl_xor(r16, o, 64);
+    r16 += pk_dpp<0xB1>(r16);
+    r16 += pk_dpp<0x4E>(r16);
+    r16 += pk_dpp<0x141>(r16);
+    r16 += pk_dpp<0x140>(r16);
     const float other = __shfl_xor(r16, 16, 64);
     int e;
     frexpf(amax, &e);
