@@ -55,6 +55,13 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
 }
+// max over each row of 16 lanes, in every lane of the row
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    return fmaxf(v, dpp_f<0x140>(v));
+}
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
     v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
@@ -227,13 +234,13 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     // wave 0: M = max over the splits (splits <= 64), weights, denominator
     if (wave == 0) {
         const float ms = lane < splits ? pl[lane * ST + HD] : -INFINITY;
-        float M = ms;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        float M = row_max(ms);  // rows of 16 by DPP, then across the rows
+        M = fmaxf(M, __shfl_xor(M, 16, 64));
+        M = fmaxf(M, __shfl_xor(M, 32, 64));
         const float w = ms == -INFINITY ? 0.f : expf(ms - M);  // empty splits weigh 0
-        float den = lane < splits ? w * pl[lane * ST + HD + 1] : 0.f;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
+        float den = group_sum<16>(lane < splits ? w * pl[lane * ST + HD + 1] : 0.f);
+        den += __shfl_xor(den, 16, 64);
+        den += __shfl_xor(den, 32, 64);
         if (lane < splits) wsh[lane] = w;
         if (lane == 0) red[0] = den;
     }

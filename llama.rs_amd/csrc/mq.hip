@@ -364,6 +364,10 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
             const float4 v = *reinterpret_cast<const float4 *>(a.xres + i);
             ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
         }
+        // the wavefront's sum now, while the weight and pack loads are in
+        // flight, not in the epilogue
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -409,8 +413,6 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         v[t] += __shfl_xor(v[t], 32, 64);
     }
     // red layout: [W][TPW][16] partials, then [W] sums of squares
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     if (lane < 16) {
 #pragma unroll
         for (int t = 0; t < TPW; t++) red[(wave * TPW + t) * 16 + lane] = v[t];
