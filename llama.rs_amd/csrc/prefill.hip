@@ -1,11 +1,12 @@
 // prefill.hip — the per-token ops of a batched prompt block (n tokens at
 // positions pos0 .. pos0+n-1) around the matrix-core GEMMs of gemm.hip:
 // RMSNorm per row, bias + RoPE + f16 KV append after the q/k/v GEMMs,
-// causal GQA attention over the cache, SwiGLU.  Same formulas and operation
-// order as the decode kernels (Model::forward, crates/llama-model/src/
-// model.rs:99-266; ops.rs:56-66, 952-988; attention.rs:76-166), which is what
-// the reference's prefill_residente (gpu.rs:673-697) drives in blocks of
-// batch_size() tokens.
+// causal GQA attention over the cache, SwiGLU.  The formulas of the decode
+// kernels (Model::forward, crates/llama-model/src/model.rs:99-266; ops.rs:
+// 56-66, 952-988; attention.rs:76-166), which is what the reference's
+// prefill_residente (gpu.rs:673-697) drives in blocks of batch_size() tokens;
+// the attention runs on the matrix cores (f16 hi/lo operands, f32
+// accumulation), so its summation order differs from the per-token kernel.
 #include "lrs_internal.h"
 
 namespace lrs {
