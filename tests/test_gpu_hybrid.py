@@ -87,10 +87,13 @@ def test_hybrid_batch_reset_and_position_rule(lrs, orc, ctx):
         assert rel_l2(gm.decode(t, p), om.forward([t])) < LOGIT_TOL
 
 
-@pytest.mark.parametrize("name,cfg", [("hy-tiny", modelgen.HY_TINY), ("hy-mid", modelgen.HY_MID)])
+@pytest.mark.parametrize("name,cfg", [("hy-tiny", modelgen.HY_TINY), ("hy-mid", modelgen.HY_MID),
+                                      ("hy-gqa5-256", dict(modelgen.HY_MID, n_head=5))])
 def test_hybrid_prompt_block_matches_oracle(lrs, orc, ctx, name, cfg):
     """A 40-token prompt in one block (ring wrap, state carried across
-    tokens inside the block kernel), then decode steps."""
+    tokens inside the block kernel), then decode steps.  5 query heads per KV
+    head at head_dim 256 splits the group over two workgroups of 3 wavefronts
+    in the prompt attention, one of them idle."""
     cfg = dict(cfg, ctx=64)
     w = modelgen.hybrid_host_model(orc, cfg, seed=25)
     gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
