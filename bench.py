@@ -335,20 +335,29 @@ def bench_q8(lrs, ctx, steps, warmup):
           for c in range(copies)]
     xbuf, ybuf = ctx.alloc(4 * n), ctx.alloc(4 * n)
     xbuf.upload(np.random.default_rng(1234).standard_normal(n).astype(np.float32))
-    ws[0].matvec_dev(xbuf, ybuf)  # sizes the context scratch outside the capture
-    ctx.sync()
-    g = ctx.capture(lambda: [w.matvec_dev(xbuf, ybuf) for w in ws])
     reps = max(1, (steps + copies - 1) // copies)
-    for _ in range(max(1, warmup // copies)):
-        g.launch()
-    ctx.sync()
-    ctx.timer_start()
-    for _ in range(reps):
-        g.launch()
-    us = ctx.timer_stop() * 1e3 / (reps * copies)
-    g.close()
+
+    def timed(mv):
+        mv(ws[0])  # sizes the context scratch outside the capture
+        ctx.sync()
+        g = ctx.capture(lambda: [mv(w) for w in ws])
+        for _ in range(max(1, warmup // copies)):
+            g.launch()
+        ctx.sync()
+        ctx.timer_start()
+        for _ in range(reps):
+            g.launch()
+        t = ctx.timer_stop() * 1e3 / (reps * copies)
+        g.close()
+        return t
+
+    us = timed(lambda w: w.matvec_dev(xbuf, ybuf))
+    # second labelled row: the int8-activation path of the reference's CPU
+    # forward for Q8_0 weights (x rounded to Q8_0, then the same matvec)
+    us_actq = timed(lambda w: w.matvec_actq_dev(xbuf, ybuf))
+    log(f"[bench] q8_0 matvec {us:.2f} us; int8-activation (actq) variant {us_actq:.2f} us")
     b = gguf_bytes(Q8_0, n, n) + 4 * n + 4 * n
-    return dict(us=us, bytes=b, gbs=b / us / 1e3, matvecs=reps * copies)
+    return dict(us=us, us_actq=us_actq, bytes=b, gbs=b / us / 1e3, matvecs=reps * copies)
 
 
 def bench_gemm(lrs, ctx, steps, warmup, m, precision):
@@ -520,7 +529,8 @@ def main():
                "data": "synthetic (seeded Q8_0 blocks, BASELINE distributions; x ~ N(0,1))",
                "config": {"workload": "config1-q8_0-matvec-4096", "batch": 1,
                           "copies_rotated": 16, "bytes_per_matvec": r["bytes"],
-                          "us_per_matvec": round(r["us"], 3)},
+                          "us_per_matvec": round(r["us"], 3),
+                          "us_per_matvec_int8_activation": round(r["us_actq"], 3)},
                "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1),
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}}

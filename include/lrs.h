@@ -114,6 +114,23 @@ int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y,
 int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
                    uint32_t cols);
 
+/* The int8-activation path the reference's CPU Model::forward takes for Q8_0
+ * weights (crates/llama-model/src/ops.rs), on device buffers, enqueued on
+ * the context stream (async).
+ * lrs_quantize_q8_0_dev: x [n] f32 -> n/32 GGUF Q8_0 blocks (34 bytes each,
+ * f16 d then 32 int8) at q8_dev, bit-exact with quantize_q8_0 (ops.rs:343-368,
+ * round half away from zero: half_even = 0) or quantize_q8_0_avx2
+ * (ops.rs:284-340, round half to even: half_even = 1); n a multiple of 32.
+ * lrs_matvec_q8_0_actq_dev: y = W x for `cols` columns with each column
+ * rounded as above first, matmul_q8_0_actq (ops.rs:728-886) with the block
+ * dot of q8_0_q8_0_dot_scalar (ops.rs:704-724): exact int32 block sums
+ * times dw * dx, summed in f32 (order differs: within 1e-4 relative L2).
+ * Q8_0 weights only (LRS_E_UNSUPPORTED otherwise). */
+int lrs_quantize_q8_0_dev(lrs_ctx *ctx, const float *x_dev, uint32_t n, int half_even,
+                          uint8_t *q8_dev);
+int lrs_matvec_q8_0_actq_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev,
+                             float *y_dev, uint32_t cols, int half_even);
+
 /* Batched prefill GEMM on the matrix cores: y [m * n_out] = a [m * n_in] W^T,
  * device f32 buffers, enqueued on the context stream (async).  Replaces the
  * prefill matmul matmul::dispatch_mul_mm_q4k / shaders/mul_mm.comp

@@ -64,6 +64,8 @@ def _load() -> C.CDLL:
         "lrs_matvec_f32": (i32, [vp, vp, vp, vp, u32]),
         "lrs_matvec_dev": (i32, [vp, vp, vp, vp, u32]),
         "lrs_gemm_dev": (i32, [vp, vp, vp, vp, u32, i32]),
+        "lrs_quantize_q8_0_dev": (i32, [vp, vp, u32, i32, vp]),
+        "lrs_matvec_q8_0_actq_dev": (i32, [vp, vp, vp, vp, u32, i32]),
         "lrs_dev_alloc": (i32, [vp, sz, pvp]),
         "lrs_dev_free": (i32, [vp, vp]),
         "lrs_copy_h2d": (i32, [vp, vp, vp, sz]),
@@ -266,6 +268,29 @@ class Weight:
     def matvec_dev(self, x: DeviceBuffer, y: DeviceBuffer, cols: int = 1) -> None:
         check(lib.lrs_matvec_dev(self.ctx.h, self.h, x.ptr, y.ptr, cols))
 
+    def matvec_actq_dev(self, x: DeviceBuffer, y: DeviceBuffer, cols: int = 1,
+                        half_even: bool = True) -> None:
+        """matmul_q8_0_actq (ops.rs:728-886): x rounded to Q8_0 first (async)."""
+        check(lib.lrs_matvec_q8_0_actq_dev(self.ctx.h, self.h, x.ptr, y.ptr, cols,
+                                           int(half_even)))
+
+    def matvec_actq(self, x: np.ndarray, half_even: bool = True) -> np.ndarray:
+        """Host wrapper of matvec_actq_dev: x [cols, n_in] -> [cols, n_out]."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        cols = x.size // self.n_in
+        if cols * self.n_in != x.size:
+            raise ModelError(-1, f"x has {x.size} elements, not a multiple of n_in={self.n_in}")
+        xb, yb = self.ctx.alloc(x.nbytes), self.ctx.alloc(4 * cols * self.n_out)
+        try:
+            xb.upload(x)
+            self.matvec_actq_dev(xb, yb, cols, half_even)
+            self.ctx.sync()
+            y = yb.download(np.float32, cols * self.n_out)
+        finally:
+            xb.free()
+            yb.free()
+        return y.reshape(cols, self.n_out) if x.ndim == 2 else y
+
     def gemm_dev(self, a: DeviceBuffer, y: DeviceBuffer, m: int, precision: int = 1) -> None:
         """Y[m][n_out] = A[m][n_in] W^T on the matrix cores (async, device buffers)."""
         check(lib.lrs_gemm_dev(self.ctx.h, self.h, a.ptr, y.ptr, m, precision))
@@ -306,6 +331,24 @@ def dequant_to_f32(ctx: Context, t: int, data) -> np.ndarray:
     out = np.empty(max(n, 1), np.float32)
     check(lib.lrs_dequant_f32(ctx.h, t, _ptr(a), a.nbytes, _ptr(out)))
     return out[:n]
+
+
+def quantize_q8_0(ctx: Context, x: np.ndarray, half_even: bool = True) -> np.ndarray:
+    """quantize_q8_0 / quantize_q8_0_avx2 (ops.rs:284-368) on the GPU: GGUF
+    Q8_0 bytes of x, bit-exact; half_even selects the AVX2 path's rounding."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    if x.size == 0 or x.size % 32:
+        raise ModelError(-1, "n must be a positive multiple of 32")
+    nb = x.size // 32 * 34
+    xb, qb = ctx.alloc(x.nbytes), ctx.alloc(nb)
+    try:
+        xb.upload(x)
+        check(lib.lrs_quantize_q8_0_dev(ctx.h, xb.ptr, x.size, int(half_even), qb.ptr))
+        ctx.sync()
+        return qb.download(np.uint8, nb)
+    finally:
+        xb.free()
+        qb.free()
 
 
 class GpuMatmul:

@@ -309,6 +309,29 @@ int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float 
     return LRS_OK;
 }
 
+int lrs_quantize_q8_0_dev(lrs_ctx *ctx, const float *x_dev, uint32_t n, int half_even,
+                          uint8_t *q8_dev) {
+    if (!ctx || !x_dev || !q8_dev) return fail(LRS_E_ARG, "null argument");
+    if (n == 0 || n % 32) return fail(LRS_E_ARG, "n must be a positive multiple of 32");
+    SETDEV(ctx);
+    LRS_HIP(launch_q8act(x_dev, n, n / 32, half_even ? 1 : 0, q8_dev, XPack{nullptr, nullptr},
+                         ctx->stream));
+    return LRS_OK;
+}
+
+int lrs_matvec_q8_0_actq_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev,
+                             float *y_dev, uint32_t cols, int half_even) {
+    if (!ctx || !w || !x_dev || !y_dev) return fail(LRS_E_ARG, "null argument");
+    if (cols == 0) return fail(LRS_E_ARG, "cols must be >= 1");
+    if (w->v.type != T_Q8_0)
+        return fail(LRS_E_UNSUPPORTED, "the int8-activation matvec takes Q8_0 weights");
+    SETDEV(ctx);
+    void *pack = nullptr;
+    LRS_HIP(scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack));
+    LRS_HIP(launch_matvec_actq(w->v, x_dev, y_dev, cols, pack, half_even ? 1 : 0, ctx->stream));
+    return LRS_OK;
+}
+
 int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y, uint32_t cols) {
     if (!ctx || !w || !x || !y) return fail(LRS_E_ARG, "null argument");
     int rc = matvec_check(w, cols);

@@ -98,6 +98,13 @@ hipError_t launch_argmax_finish(const unsigned long long *keys, uint32_t n, uint
 // y[c] = W x[c] for cols columns (packs x, then one matvec per column)
 hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
                          hipStream_t s);
+// Q8_0 activation quantization (reference CPU forward): GGUF Q8_0 bytes to
+// q8 (n / 32 blocks) and / or the matvec pack p (nxb blocks) when non-null
+hipError_t launch_q8act(const float *x, uint32_t n, uint32_t nxb, int half_even, uint8_t *q8,
+                        XPack p, hipStream_t s);
+// launch_matvec with each column rounded to Q8_0 first (Q8_0 weights only)
+hipError_t launch_matvec_actq(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
+                              int half_even, hipStream_t s);
 // Y[M][ldy] = A[M][K] W^T on the matrix cores; A given as bf16 planes
 // (prec 1: hi only; 3: hi + lo, three products) from launch_split_bf16
 // work: gemm_work_bytes(M, N, K, prec) of scratch for the K-sliced form (null: one slice)

@@ -93,6 +93,65 @@ hipError_t launch_xpack(const float *x, const float *nw, uint32_t n, uint32_t nx
     return hipGetLastError();
 }
 
+// Q8_0 activation quantization of the reference's CPU forward for Q8_0
+// weights: quantize_q8_0 (ops.rs:343-368, round half away from zero) and
+// quantize_q8_0_avx2 (ops.rs:284-340, round half to even; its saturating
+// packs clamp like the scalar clamp).  Per 32 elements d = max|x| / 127,
+// q = round(x * (1 / d)) clamped to [-128, 127], d kept as f16; the quotients
+// use the f32 d, and both divisions are IEEE (correctly rounded).  One lane
+// per element, a half wavefront per block (max by DPP within rows of 16,
+// then one exchange).  Writes the GGUF Q8_0 bytes (q8, n / 32 blocks) and/or
+// the pack the matvec reads: digits (0, 0, q) and scale f16(d) widened, so
+// the matrix-core dot of a Q8_0 weight block is the exact i32 sum(qw * qx)
+// times dw * dx (the sums of the pack are unused for Q8_0 weights).
+__global__ __launch_bounds__(256) void k_q8act(const float *__restrict__ x, uint32_t n,
+                                               uint32_t nxb, int half_even, uint8_t *q8,
+                                               XPack p) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= 32 * nxb) return;  // whole half-waves leave together
+    const uint32_t b = e >> 5, i = e & 31;
+    const float v = e < n ? x[e] : 0.f;
+    float amax = fabsf(v);
+    amax = fmaxf(amax, pk_dpp<0xB1>(amax));
+    amax = fmaxf(amax, pk_dpp<0x4E>(amax));
+    amax = fmaxf(amax, pk_dpp<0x141>(amax));
+    amax = fmaxf(amax, pk_dpp<0x140>(amax));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    const float d = amax > 0.f ? amax / 127.0f : 0.f;
+    const float di = d > 0.f ? 1.0f / d : 0.f;
+    const float t = v * di;
+    float r = half_even ? __builtin_rintf(t) : roundf(t);
+    r = fminf(fmaxf(r, -128.f), 127.f);
+    const int8_t q = (int8_t)(int)r;
+    const _Float16 dh = (_Float16)d;
+    if (q8 && e < n) {
+        uint8_t *o = q8 + 34 * (size_t)b;
+        o[2 + i] = (uint8_t)q;
+        if (i == 0) {
+            uint16_t hb;
+            __builtin_memcpy(&hb, &dh, 2);
+            o[0] = (uint8_t)(hb & 0xFF);
+            o[1] = (uint8_t)(hb >> 8);
+        }
+    }
+    if (p.dig) {
+        int8_t *dg = p.dig + (size_t)b * 96 + i;
+        dg[0] = 0;
+        dg[32] = 0;
+        dg[64] = q;
+        if (i == 0)
+            *reinterpret_cast<float4 *>(p.meta + 4 * (size_t)b) = make_float4((float)dh, 0.f, 0.f, 0.f);
+    }
+}
+
+hipError_t launch_q8act(const float *x, uint32_t n, uint32_t nxb, int half_even, uint8_t *q8,
+                        XPack p, hipStream_t s) {
+    const uint32_t threads = 32 * nxb;
+    hipLaunchKernelGGL(k_q8act, dim3((threads + 255) / 256), dim3(256), 0, s, x, n, nxb,
+                       half_even, q8, p);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // per-type unit registers and loads (tiled layout, tiled.h)
 // ---------------------------------------------------------------------------
@@ -661,6 +720,30 @@ MqGeom store_geom(uint32_t t, uint32_t n_in, uint32_t n_out) {
     if (tiles >= 1024) return {1, 2, 2, 2};
     if (tiles >= 256) return {1, 2, 4, 2};
     return {1, 1, 4, 2};
+}
+
+// matmul_q8_0_actq (ops.rs:728-886): each column's activation rounded to
+// Q8_0 (k_q8act), then the matrix-core matvec over that pack
+hipError_t launch_matvec_actq(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
+                              int half_even, hipStream_t s) {
+    if (w.type != T_Q8_0) return hipErrorInvalidValue;
+    const uint32_t nxb = pack_blocks(w.type, w.n_in);
+    const XPack xp = xpack_at(pack, nxb);
+    for (uint32_t c = 0; c < cols; c++) {
+        hipError_t e = launch_q8act(x + (size_t)c * w.n_in, w.n_in, nxb, half_even, nullptr, xp, s);
+        if (e != hipSuccess) return e;
+        MqArgs a = {};
+        a.n_seg = 1;
+        a.seg[0].w = w.q;
+        a.seg[0].rows = w.n_out;
+        a.seg[0].out = y + (size_t)c * w.n_out;
+        a.n_in = w.n_in;
+        a.nxb = nxb;
+        a.xin = xp;
+        e = launch_mq(a, w.type, w.type, store_geom(w.type, w.n_in, w.n_out), MQ_STORE, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, void *pack,

@@ -53,6 +53,11 @@ def lib() -> C.CDLL:
         L.lrso_matvec.restype = C.c_int
         L.lrso_matvec.argtypes = [C.c_uint32, u8p, C.c_size_t, C.c_uint32, C.c_uint32,
                                   f32p, f32p, C.c_uint32, C.c_int]
+        L.lrso_quantize_q8_0.restype = C.c_int
+        L.lrso_quantize_q8_0.argtypes = [f32p, C.c_uint32, C.c_int, u8p]
+        L.lrso_matvec_q8_0_actq.restype = C.c_int
+        L.lrso_matvec_q8_0_actq.argtypes = [u8p, C.c_size_t, C.c_uint32, C.c_uint32, f32p,
+                                            C.c_int, f32p]
         L.lrso_hash.restype = C.c_uint64
         L.lrso_hash.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32]
         L.lrso_gen_blocks.restype = C.c_int
@@ -153,6 +158,27 @@ def matvec(t: int, w, n_in: int, n_out: int, x: np.ndarray, threads: int = 1) ->
     if rc != 0:
         raise ValueError(f"matvec error {rc}")
     return y.reshape(cols, n_out) if x.ndim == 2 else y
+
+
+def quantize_q8_0(x: np.ndarray, half_even: bool = True) -> np.ndarray:
+    """GGUF Q8_0 bytes of x (ops.rs:284-368; half_even: the AVX2 rounding)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.zeros(x.size // 32 * 34, dtype=np.uint8)
+    if lib().lrso_quantize_q8_0(_f32(x), x.size, int(half_even), _u8(out)) != 0:
+        raise ValueError("n must be a multiple of 32")
+    return out
+
+
+def matvec_q8_0_actq(w, n_in: int, n_out: int, x: np.ndarray,
+                     half_even: bool = True) -> np.ndarray:
+    """matmul_q8_0_actq of one column (ops.rs:704-724, 728-886)."""
+    a = _as_u8(w)
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    y = np.zeros(n_out, dtype=np.float32)
+    if lib().lrso_matvec_q8_0_actq(_u8(a), len(a), n_in, n_out, _f32(x), int(half_even),
+                                   _f32(y)) != 0:
+        raise ValueError("bad Q8_0 actq shape")
+    return y
 
 
 def gen_blocks(t: int, seed: int, n_blocks: int, block0: int = 0, mode: int = 0,

@@ -312,6 +312,71 @@ int lrso_matvec(uint32_t type, const uint8_t *w, size_t w_len, uint32_t n_in,
 }
 
 /* ------------------------------------------------------------------------- */
+/* int8-activation path of Model::forward for Q8_0 weights                   */
+/* ------------------------------------------------------------------------- */
+/* quantize_q8_0 (ops.rs:343-368: scalar, f32::round = half away from zero)
+ * and quantize_q8_0_avx2 (ops.rs:284-340: cvtps2dq under the default MXCSR =
+ * half to even; the saturating packs clamp like the scalar clamp): per 32
+ * elements d = max|x| / 127, q = round(x * (1 / d)) in [-128, 127], d stored
+ * as f16 (the quotients use the f32 d, not its f16 rounding).  out: n / 32
+ * GGUF Q8_0 blocks of 34 bytes. */
+int lrso_quantize_q8_0(const float *x, uint32_t n, int half_even, uint8_t *out) {
+    if (n % 32) return -1;
+    for (uint32_t b = 0; b < n / 32; b++) {
+        const float *blk = x + 32 * (size_t)b;
+        float m = 0.0f; /* fold(0.0, f32::max) over |x| */
+        for (int i = 0; i < 32; i++) {
+            const float a = fabsf(blk[i]);
+            m = a > m ? a : m;
+        }
+        const float d = m > 0.0f ? m / 127.0f : 0.0f;
+        const float di = d > 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t h = lrso_f32_to_f16(d);
+        uint8_t *o = out + 34 * (size_t)b;
+        o[0] = (uint8_t)(h & 0xFF);
+        o[1] = (uint8_t)(h >> 8);
+        for (int i = 0; i < 32; i++) {
+            const float t = blk[i] * di;
+            float r = half_even ? nearbyintf(t) : roundf(t);
+            if (r < -128.0f) r = -128.0f;
+            if (r > 127.0f) r = 127.0f;
+            o[2 + i] = (uint8_t)(int8_t)(int)r;
+        }
+    }
+    return 0;
+}
+
+/* matmul_q8_0_actq (ops.rs:728-886) for one column with the scalar block dot
+ * q8_0_q8_0_dot_scalar (ops.rs:704-724): acc += dw * dx * (float)sum(qw * qx)
+ * block by block from 0.0; x is quantized first (quantize_q8_0_split,
+ * ops.rs:371-384). */
+int lrso_matvec_q8_0_actq(const uint8_t *w, size_t w_len, uint32_t n_in, uint32_t n_out,
+                          const float *x, int half_even, float *y) {
+    if (n_in % 32) return -1;
+    const uint32_t nb = n_in / 32;
+    if (w_len != (size_t)nb * 34 * n_out) return -1;
+    uint8_t *xq = (uint8_t *)malloc((size_t)nb * 34 + 1);
+    if (!xq) return -3;
+    lrso_quantize_q8_0(x, n_in, half_even, xq);
+    for (uint32_t r = 0; r < n_out; r++) {
+        const uint8_t *wr = w + (size_t)r * nb * 34;
+        float acc = 0.0f;
+        for (uint32_t b = 0; b < nb; b++) {
+            const uint8_t *bw = wr + 34 * (size_t)b, *bx = xq + 34 * (size_t)b;
+            const float dw = lrso_f16_to_f32((uint16_t)(bw[0] | (bw[1] << 8)));
+            const float dx = lrso_f16_to_f32((uint16_t)(bx[0] | (bx[1] << 8)));
+            int32_t dot = 0;
+            for (int i = 0; i < 32; i++) dot += (int32_t)(int8_t)bw[2 + i] * (int32_t)(int8_t)bx[2 + i];
+            const float s = dw * dx;
+            acc = acc + s * (float)dot;
+        }
+        y[r] = acc;
+    }
+    free(xq);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
 /* synthetic blocks                                                          */
 /* ------------------------------------------------------------------------- */
 static uint64_t mix64(uint64_t z) {

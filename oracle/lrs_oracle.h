@@ -69,6 +69,12 @@ int64_t lrso_dequant(uint32_t type, const uint8_t *bytes, size_t len, float *out
 int lrso_matvec(uint32_t type, const uint8_t *w, size_t w_len, uint32_t n_in,
                 uint32_t n_out, const float *x, float *y, uint32_t cols,
                 int n_threads);
+/* Q8_0 activation quantization (ops.rs:284-368; half_even: the AVX2 path,
+ * else the scalar path) into n/32 GGUF Q8_0 blocks, and the int8-activation
+ * Q8_0 matvec of one column (ops.rs:704-724, 728-886). */
+int lrso_quantize_q8_0(const float *x, uint32_t n, int half_even, uint8_t *out);
+int lrso_matvec_q8_0_actq(const uint8_t *w, size_t w_len, uint32_t n_in, uint32_t n_out,
+                          const float *x, int half_even, float *y);
 
 /* ---- deterministic synthetic blocks (counter-based, identical on GPU) ---- */
 uint64_t lrso_hash(uint64_t seed, uint64_t block, uint32_t j);

@@ -301,3 +301,64 @@ def test_captured_graph_replays_match_eager(lrs, orc, ctx):
         wb.matvec_dev(x, ya)  # eager work between the replays
         ctx.sync()
     g.close()
+
+
+# --------------------------------------------------------------------------
+# int8-activation Q8_0 path (ops.rs:284-385, 704-724, 728-886)
+# --------------------------------------------------------------------------
+def q8_inputs(seed):
+    """normal data, blocks with exact ties (max 127 * 2^s), a zero block, an
+    f16-underflowing block and a large block"""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(32 * 512).astype(np.float32)
+    for b in range(0, 64):
+        s = int(rng.integers(-30, 20))
+        k = rng.integers(-127, 128, size=32) + np.where(rng.random(32) < 0.5, 0.5, 0.0)
+        k = np.clip(k, -127, 127)
+        k[0] = 127
+        x[32 * b:32 * b + 32] = (k * 2.0 ** s).astype(np.float32)
+    x[32 * 64:32 * 65] = 0.0
+    x[32 * 65:32 * 66] *= np.float32(2.0 ** -45)
+    x[32 * 66:32 * 67] *= np.float32(1e30)
+    return x
+
+
+@pytest.mark.parametrize("half_even", [True, False])
+def test_q8_quantize_bit_exact(lrs, orc, ctx, half_even):
+    x = q8_inputs(3)
+    got = lrs.quantize_q8_0(ctx, x, half_even)
+    ref = orc.quantize_q8_0(x, half_even)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("n_in,n_out", [(32, 2), (1056, 37), (4096, 4096), (13824, 64)])
+@pytest.mark.parametrize("half_even", [True, False])
+def test_q8_actq_matvec_matches_oracle(lrs, orc, ctx, n_in, n_out, half_even):
+    w = orc.gen_weight(Q8_0, 21, n_out, n_in)
+    x = orc.gen_normal(22, n_in) * np.float32(3.0)
+    got = lrs.Weight.upload(ctx, Q8_0, w, n_in, n_out).matvec_actq(x, half_even)
+    ref = orc.matvec_q8_0_actq(w, n_in, n_out, x, half_even)
+    assert rel_l2(got, ref) < MATVEC_TOL
+
+
+def test_q8_actq_reference_fixture_exact(lrs, ctx):
+    """ops.rs:1212-1245 fixture: y = [20 f16(32/127), 8 f16(32/127)] exactly."""
+    w = np.array(f16b(1.0) + [1, 2] + [0] * 30 + f16b(2.0) + [1] + [0] * 31, np.uint8)
+    x = np.arange(1, 33, dtype=np.float32)
+    y = lrs.Weight.upload(ctx, Q8_0, w, 32, 2).matvec_actq(x)
+    assert y.tolist() == [5.0390625, 2.015625]
+
+
+def test_q8_actq_columns_and_errors(lrs, orc, ctx):
+    n_in, n_out = 512, 16
+    w = orc.gen_weight(Q8_0, 23, n_out, n_in)
+    W = lrs.Weight.upload(ctx, Q8_0, w, n_in, n_out)
+    xs = np.stack([orc.gen_normal(30 + c, n_in) for c in range(3)])
+    yb = W.matvec_actq(xs)
+    for c in range(3):
+        assert np.array_equal(yb[c], W.matvec_actq(xs[c]))
+    w4 = orc.gen_weight(Q4_K, 24, n_out, n_in)
+    with pytest.raises(lrs.ModelError):
+        lrs.Weight.upload(ctx, Q4_K, w4, n_in, n_out).matvec_actq(xs[0])
+    with pytest.raises(lrs.ModelError):
+        lrs.quantize_q8_0(ctx, np.ones(33, np.float32))

@@ -375,3 +375,80 @@ def test_forward_context_overflow_and_bad_token(orc):
         m.forward([4, 5])  # 3 + 2 > ctx: attention.rs:36-40
     with pytest.raises(ValueError):
         m.forward([cfg["vocab"]])
+
+
+# --------------------------------------------------------------------------
+# int8-activation Q8_0 path (ops.rs:284-385, 704-724, 728-886)
+# --------------------------------------------------------------------------
+def _q8_block(d_bits, qs):
+    return np.array([d_bits & 0xFF, d_bits >> 8] + [q & 0xFF for q in qs], np.uint8)
+
+
+def test_q8_quantize_ties_follow_each_rounding(orc):
+    """max|x| = 127 makes d = 1 and 1/d = 1 exactly, so q = round(x): the
+    AVX2 path (cvtps2dq) rounds ties to even, the scalar path away from 0."""
+    x = np.zeros(32, np.float32)
+    x[:10] = [127, 2.5, -2.5, 3.5, 0.5, -0.5, 1.5, -1.5, -127, 126.5]
+    even = orc.quantize_q8_0(x, half_even=True)
+    away = orc.quantize_q8_0(x, half_even=False)
+    assert np.array_equal(even, _q8_block(0x3C00, [127, 2, -2, 4, 0, 0, 2, -2, -127, 126] + [0] * 22))
+    assert np.array_equal(away, _q8_block(0x3C00, [127, 3, -3, 4, 1, -1, 2, -2, -127, 127] + [0] * 22))
+
+
+def test_q8_quantize_power_of_two_scales(orc):
+    """max|x| = 127 * 2^s gives d = 2^s exactly, so q = round(x / 2^s) and
+    d's f16 bits are fixed; integers and integer + 1/2 over many scales."""
+    rng = np.random.default_rng(5)
+    for s in (-20, -7, 0, 3, 9):
+        k = rng.integers(-127, 128, size=32).astype(np.float64)
+        k[0] = 127
+        k[1:8] += 0.5 * np.sign(rng.standard_normal(7))
+        k = np.clip(k, -127, 127)
+        x = (k * 2.0 ** s).astype(np.float32)
+        for he in (True, False):
+            got = orc.quantize_q8_0(x, half_even=he)
+            q = np.rint(k) if he else np.sign(k) * np.floor(np.abs(k) + 0.5)
+            dbits = int(np.array([2.0 ** s], np.float16).view(np.uint16)[0])
+            assert np.array_equal(got, _q8_block(dbits, q.astype(int).tolist())), (s, he)
+
+
+def test_q8_quantize_zero_and_underflowing_scale(orc):
+    x = np.zeros(64, np.float32)
+    # second block: d = 2^-40 underflows f16 (stored as 0) while q uses the f32 d
+    x[32:] = (np.arange(32) - 16).astype(np.float32) * np.float32(2.0 ** -40)
+    x[32] = np.float32(127 * 2.0 ** -40)
+    got = orc.quantize_q8_0(x)
+    assert np.array_equal(got[:34], np.zeros(34, np.uint8))
+    qs = [127] + list(range(-15, 16))
+    assert np.array_equal(got[34:], _q8_block(0, qs))
+
+
+def test_q8_actq_reference_fixture_closed_form(orc):
+    """The fixture of ops.rs:1212-1245 (rows d=1 q=[1,2,0..], d=2 q=[1,0..];
+    x = 1..32).  d = 32/127, q1 = round(1/d) = 4, q2 = 8, f16(d) =
+    0.251953125, so y = [20 * f16(d), 2 * 4 * f16(d)] exactly; the
+    reference's own bar is 1 % of the f32 result [5, 2]."""
+    w = np.concatenate([_q8_block(0x3C00, [1, 2] + [0] * 30), _q8_block(0x4000, [1] + [0] * 31)])
+    x = np.arange(1, 33, dtype=np.float32)
+    for he in (True, False):
+        y = orc.matvec_q8_0_actq(w, 32, 2, x, half_even=he)
+        assert y.tolist() == [5.0390625, 2.015625]
+        assert abs(y[0] - 5.0) / 5.0 < 0.01 and abs(y[1] - 2.0) / 2.0 < 0.01
+
+
+def test_q8_actq_matches_integer_brute_force(orc):
+    """Block sums recomputed in exact integer arithmetic from the quantized
+    bytes (float64 scaling): catches index / sign / scale slips in the dot."""
+    n_in, n_out = 256, 9
+    w = orc.gen_weight(Q8_0, 11, n_out, n_in)
+    x = orc.gen_normal(12, n_in)
+    xq = orc.quantize_q8_0(x).reshape(-1, 34)
+    wq = w.reshape(n_out, -1, 34)
+    f16 = lambda b: b[..., :2].copy().view(np.float16)[..., 0].astype(np.float64)
+    dots = (wq[..., 2:].view(np.int8).astype(np.int64) * xq[None, :, 2:].view(np.int8)).sum(-1)
+    ref = (f16(wq) * f16(xq)[None, :] * dots).sum(-1)
+    y = orc.matvec_q8_0_actq(w, n_in, n_out, x)
+    assert np.allclose(y, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+    # and it stays within the activation rounding of the f32 path
+    y32 = orc.matvec(Q8_0, w, n_in, n_out, x)
+    assert np.linalg.norm(y - y32) / np.linalg.norm(y32) < 2e-2
