@@ -299,6 +299,25 @@ def cpu_baseline_decode(threads):
                       f"+ 8x the head slice = {s_tok:.2f} s"}
 
 
+class GraphOrDirect:
+    """The launches of fn captured into one HIP graph, or (LRS_GRAPH=0, for
+    kernel-tracing tools) issued directly on the context stream each time."""
+
+    def __init__(self, ctx, fn):
+        self.fn = fn
+        self.g = None if os.environ.get("LRS_GRAPH") == "0" else ctx.capture(fn)
+
+    def launch(self):
+        if self.g is None:
+            self.fn()
+        else:
+            self.g.launch()
+
+    def close(self):
+        if self.g is not None:
+            self.g.close()
+
+
 def bench_layer(lrs, ctx, steps, warmup):
     cfg2 = [(Q4_K, 5120, 5120), (Q4_K, 5120, 1024), (Q6_K, 5120, 1024), (Q4_K, 5120, 5120),
             (Q4_K, 5120, 13824), (Q4_K, 5120, 13824), (Q6_K, 13824, 5120)]
@@ -312,7 +331,7 @@ def bench_layer(lrs, ctx, steps, warmup):
     # one graph per copy: the 7 matvecs of the set (pack + matrix-core matvec each)
     mats[0][-1].matvec_dev(xbuf, ybuf)  # sizes the context scratch outside the capture
     ctx.sync()
-    graphs = [ctx.capture(lambda c=c: [w.matvec_dev(xbuf, ybuf) for w in mats[c]])
+    graphs = [GraphOrDirect(ctx, lambda c=c: [w.matvec_dev(xbuf, ybuf) for w in mats[c]])
               for c in range(copies)]
     for s in range(warmup):
         graphs[s % copies].launch()
@@ -340,7 +359,7 @@ def bench_q8(lrs, ctx, steps, warmup):
     def timed(mv):
         mv(ws[0])  # sizes the context scratch outside the capture
         ctx.sync()
-        g = ctx.capture(lambda: [mv(w) for w in ws])
+        g = GraphOrDirect(ctx, lambda: [mv(w) for w in ws])
         for _ in range(max(1, warmup // copies)):
             g.launch()
         ctx.sync()
