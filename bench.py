@@ -262,6 +262,38 @@ def cpu_baseline_hybrid(threads):
                       f"= {s_tok:.2f} s"}
 
 
+def cpu_baseline_q8(threads):
+    """Config 1 on the host: the oracle's dequant + sequential f32 dot
+    (weights.rs:95-124 + ops.rs:78-101, rows in chunks of 32 over `threads`)
+    on the 4096x4096 Q8_0 matvec, and, as a second labelled row, the
+    int8-activation path Model::forward takes for Q8_0 weights
+    (matmul_q8_0_actq, ops.rs:704-724, 728-886; one thread, scalar)."""
+    import oracle
+
+    n = 4096
+    w = oracle.gen_weight(Q8_0, 900, n, n)
+    x = oracle.gen_normal(1, n)
+    b = gguf_bytes(Q8_0, n, n) + 8 * n
+
+    def rate(fn, secs):
+        fn()
+        k, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < secs:
+            fn()
+            k += 1
+        return k, (time.perf_counter() - t0) / k
+
+    k1, t1 = rate(lambda: oracle.matvec(Q8_0, w, n, n, x, threads=threads), 4.0)
+    k2, t2 = rate(lambda: oracle.matvec_q8_0_actq(w, n, n, x), 4.0)
+    return {"value": round(b / t1 / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle dequant + f32 dot, {k1} matvecs of Q8_0 4096x4096 "
+                      f"({t1 * 1e3:.2f} ms each, {threads} threads); second row: the "
+                      f"int8-activation matmul_q8_0_actq restatement, {k2} matvecs "
+                      f"({t2 * 1e3:.2f} ms each, 1 thread)",
+            "int8_activation": {"value": round(b / t2 / 1e9, 2), "unit": "GB/s", "cores": 1,
+                                "kind": "port"}}
+
+
 def cpu_baseline_decode(threads):
     """The oracle (C restatement of Model::forward: per-row dequant + sequential
     f32 dot, rows in chunks of 32 over `threads`) on a bounded sample of the
@@ -553,8 +585,10 @@ def main():
                "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1),
                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}}
-        print(json.dumps(out), flush=True)
         ctx.close()
+        if not a.no_cpu:
+            out["cpu_baseline"] = cpu_baseline_q8(threads)
+        print(json.dumps(out), flush=True)
         return
     if a.workload == "layer":
         r = bench_layer(lrs, ctx, a.steps, a.warmup)
