@@ -3,7 +3,7 @@
  *
  * This is the drop-in boundary: a thin Rust `extern "C"` crate implements the
  * reference's `llama_model::GpuMatmul` and `llama_model::GpuResidentDecode`
- * traits on top of these calls.  All arguments are plain
+ * traits on top of these calls, one trait method per call.  All arguments are plain
  * pointers and sizes; no HIP or torch type crosses the boundary.
  *
  * Conventions (mirroring the reference's error and ownership rules):
