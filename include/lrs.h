@@ -161,7 +161,12 @@ int lrs_copy_d2h(lrs_ctx *ctx, void *dst, const void *src_dev, size_t bytes);
  * resolve-once pattern of the reference's recorded command buffers
  * (resident_forward.rs build_plan, :3678-3762) for kernel-level callers.
  * Blocking calls, and a first call whose context scratch must grow, fail
- * inside a capture: make one uncaptured call of the same shape first. */
+ * inside a capture: make one uncaptured call of the same shape first.
+ * A graph records the address of the context's scratch buffer, so while any
+ * graph of the context is alive a call that would grow the scratch fails with
+ * LRS_E_ARG and leaves the buffer in place (make the largest call before
+ * capturing, or destroy the graphs first).  Graphs must be destroyed before
+ * their context. */
 typedef struct lrs_graph lrs_graph;
 int lrs_capture_begin(lrs_ctx *ctx);
 int lrs_capture_end(lrs_ctx *ctx, lrs_graph **out);
@@ -201,7 +206,9 @@ typedef struct {
  * any dequantizable type (the row of each token is dequantized on the GPU,
  * TokenEmbd::linha gpu.rs:297-304); matvec weights Q8_0/Q4_K/Q5_K/Q6_K.
  * With the environment variable LRS_GRAPH=0 no graph is captured and every
- * token issues the same kernel launches directly (for tracing tools). */
+ * token issues the same kernel launches directly; the same holds when
+ * ROCPROF_KERNEL_TRACE or ROCPROF_COUNTER_COLLECTION is set (rocprofv3 sets
+ * them for the program it traces). */
 int lrs_model_create(lrs_ctx *ctx, const lrs_config *cfg, const lrs_layer_weights *layers,
                      const lrs_weight *token_embd, const float *output_norm,
                      const lrs_weight *output, lrs_model **out);

@@ -61,7 +61,10 @@ static int alloc_weight(lrs_ctx *ctx, uint32_t t, uint32_t n_in, uint32_t n_out,
 
 using namespace lrs;
 
-// per-context device scratch for the blocking host-buffer entry points
+// per-context device scratch of the entry points that need a staging buffer
+// (input pack, host-buffer staging, GEMM operand planes).  Graphs captured on
+// the context record its address, so while any of them is alive the buffer
+// must not move: growth is refused instead (lrs_ctx::live_graphs).
 struct lrs_ctx_scratch {
     void *p = nullptr;
     size_t n = 0;
@@ -70,29 +73,34 @@ static std::mutex g_scratch_mu;
 static std::unordered_map<lrs_ctx *, lrs_ctx_scratch> g_scratch;
 
 namespace lrs {
-static hipError_t scratch(lrs_ctx *ctx, size_t bytes, void **p) {
+static int ctx_scratch(lrs_ctx *ctx, size_t bytes, void **p) {
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     lrs_ctx_scratch &s = g_scratch[ctx];
     if (s.n < bytes) {
+        if (ctx->live_graphs > 0)
+            return fail(LRS_E_ARG, "context scratch must grow to " + std::to_string(bytes) +
+                                       " bytes but " + std::to_string(ctx->live_graphs) +
+                                       " captured graph(s) still use it: destroy them first, or "
+                                       "make the largest call before capturing");
         // growing frees the old buffer after a stream sync, which a stream
         // being captured into a graph cannot do
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return hipErrorStreamCaptureUnsupported;
+            return hip_fail(hipErrorStreamCaptureUnsupported, "context scratch growth inside a capture");
         if (s.p) {
             hipError_t e = hipStreamSynchronize(ctx->stream);
-            if (e != hipSuccess) return e;
+            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize(scratch)");
             (void)hipFree(s.p);
             s.p = nullptr;
             s.n = 0;
         }
         size_t n = bytes < (1u << 20) ? (1u << 20) : bytes;
         hipError_t e = hipMalloc(&s.p, n);
-        if (e != hipSuccess) return e;
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch)");
         s.n = n;
     }
     *p = s.p;
-    return hipSuccess;
+    return LRS_OK;
 }
 }  // namespace lrs
 
@@ -304,7 +312,7 @@ int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float 
     if (rc) return rc;
     SETDEV(ctx);
     void *pack = nullptr;
-    LRS_HIP(scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack));
+    if (int rc_ = ctx_scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack)) return rc_;
     LRS_HIP(launch_matvec(w->v, x_dev, y_dev, cols, pack, ctx->stream));
     return LRS_OK;
 }
@@ -327,7 +335,7 @@ int lrs_matvec_q8_0_actq_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_d
         return fail(LRS_E_UNSUPPORTED, "the int8-activation matvec takes Q8_0 weights");
     SETDEV(ctx);
     void *pack = nullptr;
-    LRS_HIP(scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack));
+    if (int rc_ = ctx_scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack)) return rc_;
     LRS_HIP(launch_matvec_actq(w->v, x_dev, y_dev, cols, pack, half_even ? 1 : 0, ctx->stream));
     return LRS_OK;
 }
@@ -342,7 +350,7 @@ int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y, 
     const size_t pb = xpack_bytes(pack_blocks(w->v.type, w->v.n_in));
     auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
     void *buf = nullptr;
-    LRS_HIP(scratch(ctx, up(xb) + up(yb) + pb, &buf));
+    if (int rc_ = ctx_scratch(ctx, up(xb) + up(yb) + pb, &buf)) return rc_;
     float *xd = (float *)buf;
     float *yd = (float *)((char *)buf + up(xb));
     void *pack = (char *)buf + up(xb) + up(yb);
@@ -366,7 +374,7 @@ int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y
     const size_t n = (size_t)m * w->v.n_in, ab = (n * 2 * (precision == 3 ? 2 : 1) + 255) & ~(size_t)255;
     const size_t wb = gemm_work_bytes(m, w->v.n_out, w->v.n_in, precision);
     void *buf = nullptr;
-    LRS_HIP(scratch(ctx, ab + wb, &buf));
+    if (int rc_ = ctx_scratch(ctx, ab + wb, &buf)) return rc_;
     __bf16 *hi = (__bf16 *)buf, *lo = precision == 3 ? hi + n : nullptr;
     LRS_HIP(launch_split_bf16(a_dev, n, hi, lo, ctx->stream));
     LRS_HIP(launch_gemm(w->v, hi, lo, y_dev, m, w->v.n_out, precision, ctx->stream, false,
@@ -438,6 +446,10 @@ int lrs_capture_end(lrs_ctx *ctx, lrs_graph **out) {
     e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        ctx->live_graphs++;
+    }
     *out = new lrs_graph{ctx, x};
     return LRS_OK;
 }
@@ -454,6 +466,10 @@ void lrs_graph_destroy(lrs_graph *g) {
     (void)hipSetDevice(g->ctx->device);
     (void)hipStreamSynchronize(g->ctx->stream);
     (void)hipGraphExecDestroy(g->exec);
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        g->ctx->live_graphs--;
+    }
     delete g;
 }
 

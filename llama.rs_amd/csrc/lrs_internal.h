@@ -179,6 +179,7 @@ struct lrs_ctx {
     int device;
     hipStream_t stream;
     hipEvent_t ev0, ev1;
+    int live_graphs = 0;  // lrs_graph objects captured on this context and not destroyed
 };
 
 struct lrs_weight {

@@ -35,6 +35,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <strings.h>
 #include <vector>
 
 namespace lrs {
@@ -110,6 +111,7 @@ struct lrs_model {
     _Float16 *kv;                // all layers' caches
     uint32_t *step_host;         // pinned
     float *logits_host;          // pinned
+    uint32_t *gen_host;          // pinned [gen_cap]: generated tokens on their way out
     hipGraphExec_t g_logits = nullptr, g_greedy = nullptr;
     uint32_t len = 0;
     size_t gguf_bytes_per_token = 0;
@@ -511,6 +513,22 @@ hipError_t run_forward(lrs_model *m, bool greedy) {
 
 size_t wbytes(const lrs_weight *w) { return lrs_weight_gguf_bytes(w); }
 
+// Whether the per-token forward is captured into HIP graphs.  LRS_GRAPH=0
+// issues the same launches directly on the stream instead.  So does a
+// process running under rocprofv3 kernel tracing or counter collection (it
+// exports ROCPROF_KERNEL_TRACE / ROCPROF_COUNTER_COLLECTION to the program):
+// a traced run of back-to-back graph launches ended in a host SIGSEGV inside
+// the profiler's own code, so traced runs replay the launches directly.
+bool env_on(const char *name) {
+    const char *v = getenv(name);
+    return v && v[0] && strcmp(v, "0") != 0 && strcasecmp(v, "false") != 0;
+}
+bool use_graphs() {
+    const char *ge = getenv("LRS_GRAPH");
+    if (ge && ge[0] == '0') return false;
+    return !env_on("ROCPROF_KERNEL_TRACE") && !env_on("ROCPROF_COUNTER_COLLECTION");
+}
+
 // allocations shared by the dense and hybrid models, then the graph capture;
 // pack_a_elems: elements of the o-projection's input pack beyond n_head*head_dim
 int finish_model(lrs_model *m, const float *output_norm, const std::vector<float> &fr,
@@ -551,15 +569,12 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
     if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=
+            hipSuccess ||
+        hipHostMalloc((void **)&m->gen_host, m->gen_cap * sizeof(uint32_t), hipHostMallocDefault) !=
             hipSuccess)
         return fail(LRS_E_OOM, "pinned host buffers");
-    // LRS_GRAPH=0 replays the same launches directly on the stream instead
-    // (for tools that cannot trace kernels inside graph launches)
-    const char *ge = getenv("LRS_GRAPH");
-    const bool graphs = !(ge && ge[0] == '0');
-    if (graphs &&
-        ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy))))
-        return rc;
+    if (!use_graphs()) return LRS_OK;
+    if ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy))) return rc;
     return LRS_OK;
 }
 
@@ -808,6 +823,7 @@ void lrs_model_destroy(lrs_model *m) {
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->step_host) (void)hipHostFree(m->step_host);
     if (m->logits_host) (void)hipHostFree(m->logits_host);
+    if (m->gen_host) (void)hipHostFree(m->gen_host);
     for (lrs_weight *w : m->owned) lrs_weight_free(w);
     delete m;
 }
@@ -1146,8 +1162,10 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
     m->step_host[2] = 0;
     LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     for (uint32_t i = 0; i < n_gen; i++) LRS_HIP(run_forward(m, true));
-    LRS_HIP(hipMemcpyAsync(out_tokens, m->gen, n_gen * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    // through the pinned buffer: the caller's memory is pageable
+    LRS_HIP(hipMemcpyAsync(m->gen_host, m->gen, n_gen * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
     LRS_HIP(hipStreamSynchronize(s));
+    memcpy(out_tokens, m->gen_host, n_gen * sizeof(uint32_t));
     m->len = pos0 + n_prompt + n_gen - 1;
     return LRS_OK;
 }

@@ -303,6 +303,43 @@ def test_captured_graph_replays_match_eager(lrs, orc, ctx):
     g.close()
 
 
+def test_scratch_growth_refused_while_a_graph_lives(lrs, orc):
+    """A graph records the context scratch address: a call that would grow
+    the scratch while the graph is alive fails (LRS_E_ARG) and leaves the
+    buffer in place, so the graph still replays correctly; once the graph is
+    destroyed the same call succeeds."""
+    c = lrs.Context()
+    try:
+        n_in, n_out = 1024, 256
+        w = lrs.Weight.upload(c, Q4_K, orc.gen_weight(Q4_K, 81, n_out, n_in, mode=1), n_in, n_out)
+        x = c.alloc(4 * n_in)
+        x.upload(orc.gen_normal(82, n_in))
+        y = c.alloc(4 * n_out)
+        w.matvec_dev(x, y)  # sizes the scratch (1 MiB minimum) outside the capture
+        c.sync()
+        want = y.download(np.float32, n_out)
+        g = c.capture(lambda: w.matvec_dev(x, y))
+        # a GEMM whose bf16 operand planes need more than the current scratch
+        m = 1024
+        big = lrs.Weight.upload(c, Q4_K, orc.gen_weight(Q4_K, 83, 256, 4096, mode=1), 4096, 256)
+        a = c.alloc(4 * m * 4096)
+        yg = c.alloc(4 * m * 256)
+        with pytest.raises(lrs.ModelError) as e:
+            big.gemm_dev(a, yg, m, precision=3)
+        assert e.value.code == -1 and "graph" in str(e.value)
+        y.upload(np.full(n_out, np.nan, np.float32))
+        g.launch()
+        c.sync()
+        assert np.array_equal(y.download(np.float32, n_out), want)
+        g.close()
+        a.upload(np.zeros(m * 4096, np.float32))
+        big.gemm_dev(a, yg, m, precision=3)  # grows now
+        c.sync()
+        assert not np.any(yg.download(np.float32, m * 256))
+    finally:
+        c.close()
+
+
 # --------------------------------------------------------------------------
 # int8-activation Q8_0 path (ops.rs:284-385, 704-724, 728-886)
 # --------------------------------------------------------------------------
