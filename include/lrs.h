@@ -268,6 +268,17 @@ int lrs_decode_batch(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t 
                      float *logits);
 /* GpuResidentDecode::batch_size (tokens per decode_batch block). */
 uint32_t lrs_batch_size(const lrs_model *m);
+/* Numerics of Q8_0 weights in a dense model.  Off (the default): every
+ * weight, Q8_0 included, multiplies the f32 activation (kept to 22 bits per
+ * 32-element block), i.e. dequant + f32 matmul, within 1e-3 of that forward.
+ * On: a Q8_0 weight multiplies its input rounded like the reference CPU
+ * forward does (RawTensor::matmul_into, crates/llama-model/src/weights.rs:
+ * 109-124: quantize_q8_0_split with the AVX2 quantizer, ops.rs:284-340, then
+ * exact int8 block dots, matmul_q8_0_actq ops.rs:728-886).  That rounding is
+ * discontinuous: logits follow the reference to ~1e-7 until an activation
+ * lands on the other side of a rounding boundary because of f32 summation
+ * order, after which they can differ by ~1e-2.  Re-captures the token graphs. */
+int lrs_model_set_q8_rounding(lrs_model *m, int on);
 /* GpuResidentDecode::reset: cache length back to 0. */
 void lrs_reset(lrs_model *m);
 /* Current cache length (ResidentState::len). */

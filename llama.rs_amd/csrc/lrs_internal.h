@@ -102,6 +102,9 @@ hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, 
 // q8 (n / 32 blocks) and / or the matvec pack p (nxb blocks) when non-null
 hipError_t launch_q8act(const float *x, uint32_t n, uint32_t nxb, int half_even, uint8_t *q8,
                         XPack p, hipStream_t s);
+// Q8_0-rounded pack (p.q8 set) of rmsnorm(x) * w, n a multiple of 256
+hipError_t launch_q8norm(const float *x, const float *w, uint32_t n, float eps, XPack p,
+                         hipStream_t s);
 // launch_matvec with each column rounded to Q8_0 first (Q8_0 weights only)
 hipError_t launch_matvec_actq(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
                               int half_even, hipStream_t s);

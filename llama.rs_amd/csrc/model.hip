@@ -75,6 +75,9 @@ struct DevLayer {
     float *alpha = nullptr, *beta = nullptr, *ssm_a = nullptr, *ssm_dt = nullptr;
     float *conv = nullptr, *ssm_norm = nullptr;
     float *win = nullptr, *state = nullptr;  // conv input ring [d_conv][conv_dim], S [v][D][D]
+    // dense model, Q8_0 weights: which matmul inputs take the reference
+    // forward's Q8_0 rounding (weights.rs:113-117) instead of the 22-bit pack
+    bool qkv_q8 = false, o_q8 = false, ffn_q8 = false, down_q8 = false;
 };
 
 struct lrs_model {
@@ -89,6 +92,10 @@ struct lrs_model {
     // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
     // SwiGLU output
     XPack pk_n, pk_f, pk_a, pk_s;
+    // Q8_0-rounded pack of an RMSNorm'd input (q/k/v, gate/up or head input)
+    // of Q8_0 weights
+    XPack pk_q8 = {};
+    bool head_q8 = false;
     uint32_t *step, *gen;  // step = {token, pos, n_generated}
     uint32_t gen_cap;
     // greedy: per-workgroup argmax keys of the head (ops.rs:1035-1045: the
@@ -230,6 +237,13 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
     sv.kind = 2;
     sv.bias = L.bv;
     sv.kv = L.vc;
+    if (L.qkv_q8) {
+        // Q8_0 segments read rmsnorm(x) * attn_norm rounded to Q8_0 (the norm
+        // is inside the pack: no RMS factor on their results)
+        hipError_t e = launch_q8norm(m->x, L.attn_norm, c.n_embd, c.rms_eps, m->pk_q8,
+                                     m->ctx->stream);
+        if (e != hipSuccess) return e;
+    }
     const lrs_weight *ws[3] = {L.q, L.k, L.v};
     const MqSeg segs[3] = {sq, sk, sv};
     const uint32_t tq = L.q->v.type, tv = L.v->v.type;
@@ -256,6 +270,9 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
         }
         a.n_seg0 = a.n_seg;
         a.nxb = pack_blocks(t, c.n_embd);
+        const bool q8 = L.qkv_q8 && t == T_Q8_0;
+        a.xin = q8 ? m->pk_q8 : m->pk_n;
+        a.xres = q8 ? nullptr : m->x;
         hipError_t e = launch_mq(a, t, t, G_QKV, MQ_QKV, m->ctx->stream);
         if (e != hipSuccess) return e;
     }
@@ -268,7 +285,9 @@ hipError_t op_attn(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
     const float *gate = m->hybrid ? m->qg + c.head_dim : nullptr;
-    return launch_attention(m->qbuf, L.kc, L.vc, m->pa, m->pk_a, m->step, c.n_head, c.n_head_kv,
+    XPack out = m->pk_a;
+    out.q8 = L.o_q8;
+    return launch_attention(m->qbuf, L.kc, L.vc, m->pa, out, m->step, c.n_head, c.n_head_kv,
                             c.head_dim, c.ctx, m->a_splits, m->ctx->stream, gate,
                             2 * c.head_dim);
 }
@@ -415,7 +434,15 @@ hipError_t op_gateup(lrs_model *m, uint32_t l) {
     a.xin = m->pk_f;
     a.xres = m->x;
     a.eps = c.rms_eps;
+    if (L.ffn_q8) {
+        hipError_t e = launch_q8norm(m->x, L.ffn_norm, c.n_embd, c.rms_eps, m->pk_q8,
+                                     m->ctx->stream);
+        if (e != hipSuccess) return e;
+        a.xin = m->pk_q8;
+        a.xres = nullptr;
+    }
     a.xout = m->pk_s;
+    a.xout.q8 = L.down_q8;
     return launch_mq(a, L.gate->v.type, L.gate->v.type, gateup_geom(c.n_ff), MQ_SWIGLU,
                      m->ctx->stream);
 }
@@ -450,6 +477,13 @@ hipError_t op_head(lrs_model *m, bool greedy) {
     a.xin = m->pk_n;
     a.xres = m->x;
     a.eps = c.rms_eps;
+    if (m->head_q8) {
+        hipError_t e = launch_q8norm(m->x, m->output_norm, c.n_embd, c.rms_eps, m->pk_q8,
+                                     m->ctx->stream);
+        if (e != hipSuccess) return e;
+        a.xin = m->pk_q8;
+        a.xres = nullptr;
+    }
     if (greedy) a.amax = m->amax;
     uint32_t wgs = 0, kpw = 0;
     hipError_t e = launch_mq(a, m->output->v.type, m->output->v.type, G_HEAD, MQ_STORE,
@@ -513,6 +547,20 @@ hipError_t run_forward(lrs_model *m, bool greedy) {
 
 size_t wbytes(const lrs_weight *w) { return lrs_weight_gguf_bytes(w); }
 
+// RawTensor::matmul_into (weights.rs:109-124): with the reference rounding on,
+// a Q8_0 weight multiplies its input rounded to Q8_0 (quantize_q8_0_split);
+// otherwise, and for every other type, the f32 input (the 22-bit pack)
+void set_q8_flags(lrs_model *m, bool on) {
+    for (DevLayer &D : m->layers) {
+        if (D.dn || !D.q) continue;  // dense layers only
+        D.qkv_q8 = on && (D.q->v.type == T_Q8_0 || D.k->v.type == T_Q8_0 || D.v->v.type == T_Q8_0);
+        D.o_q8 = on && D.o->v.type == T_Q8_0;
+        D.ffn_q8 = on && D.gate->v.type == T_Q8_0;
+        D.down_q8 = on && D.down->v.type == T_Q8_0;
+    }
+    m->head_q8 = on && !m->hybrid && m->output->v.type == T_Q8_0;
+}
+
 // Whether the per-token forward is captured into HIP graphs.  LRS_GRAPH=0
 // issues the same launches directly on the stream instead.  So does a
 // process running under rocprofv3 kernel tracing or counter collection (it
@@ -527,6 +575,17 @@ bool use_graphs() {
     const char *ge = getenv("LRS_GRAPH");
     if (ge && ge[0] == '0') return false;
     return !env_on("ROCPROF_KERNEL_TRACE") && !env_on("ROCPROF_COUNTER_COLLECTION");
+}
+
+// (re)captures the per-token graphs unless graphs are off
+int capture_graphs(lrs_model *m) {
+    if (m->g_logits) (void)hipGraphExecDestroy(m->g_logits);
+    if (m->g_greedy) (void)hipGraphExecDestroy(m->g_greedy);
+    m->g_logits = m->g_greedy = nullptr;
+    if (!use_graphs()) return LRS_OK;
+    int rc;
+    if ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy))) return rc;
+    return LRS_OK;
 }
 
 // allocations shared by the dense and hybrid models, then the graph capture;
@@ -564,6 +623,9 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         m->pk_a = xpack_at(p, nq);
         if ((rc = dev_alloc(m, xpack_bytes(nf), &p))) return rc;
         m->pk_s = xpack_at(p, nf);
+        if ((rc = dev_alloc(m, xpack_bytes(ne), &p))) return rc;
+        m->pk_q8 = xpack_at(p, ne);
+        m->pk_q8.q8 = 1;
     }
     if (hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess) return fail(LRS_E_HIP, "memset");
     if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
@@ -573,9 +635,7 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         hipHostMalloc((void **)&m->gen_host, m->gen_cap * sizeof(uint32_t), hipHostMallocDefault) !=
             hipSuccess)
         return fail(LRS_E_OOM, "pinned host buffers");
-    if (!use_graphs()) return LRS_OK;
-    if ((rc = capture(m, false, &m->g_logits)) || (rc = capture(m, true, &m->g_greedy))) return rc;
-    return LRS_OK;
+    return capture_graphs(m);
 }
 
 }  // namespace
@@ -1116,6 +1176,15 @@ void lrs_reset(lrs_model *m) {
 }
 
 uint32_t lrs_model_len(const lrs_model *m) { return m ? m->len : 0; }
+
+int lrs_model_set_q8_rounding(lrs_model *m, int on) {
+    if (!m) return fail(LRS_E_ARG, "null model");
+    if (m->hybrid) return fail(LRS_E_UNSUPPORTED, "the Q8_0 input rounding applies to dense models");
+    LRS_HIP(hipSetDevice(m->ctx->device));
+    LRS_HIP(hipStreamSynchronize(m->ctx->stream));
+    set_q8_flags(m, on != 0);
+    return capture_graphs(m);
+}
 
 int lrs_decode_greedy(lrs_model *m, uint32_t token, uint32_t pos, uint32_t *next) {
     if (!m || !next) return fail(LRS_E_ARG, "null argument");

@@ -93,6 +93,38 @@ hipError_t launch_xpack(const float *x, const float *nw, uint32_t n, uint32_t nx
     return hipGetLastError();
 }
 
+// rmsnorm_and_scale (ops.rs:56-66) of x, then the Q8_0 rounding of the
+// result (p.q8 set): the input of a Q8_0 weight after an RMSNorm in
+// Model::forward (weights.rs:113-117, quantize_q8_0_split).  Every workgroup
+// reduces the sum of squares of the whole vector itself (n is a few thousand
+// elements), then packs its 256 elements; n is a multiple of 256.
+__global__ __launch_bounds__(256) void k_q8norm(const float *__restrict__ x,
+                                                const float *__restrict__ w, uint32_t n,
+                                                float eps, XPack p) {
+    __shared__ float part[4];
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) {
+        const float v = x[i];
+        ss += v * v;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+    const uint32_t e = blockIdx.x * 256 + threadIdx.x;
+    const float v = (x[e] * scale) * w[e];
+    pack_half(v, e >> 5, p);
+}
+
+hipError_t launch_q8norm(const float *x, const float *w, uint32_t n, float eps, XPack p,
+                         hipStream_t s) {
+    if (n % 256 || !p.q8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_q8norm, dim3(n / 256), dim3(256), 0, s, x, w, n, eps, p);
+    return hipGetLastError();
+}
+
 // Q8_0 activation quantization of the reference's CPU forward for Q8_0
 // weights: quantize_q8_0 (ops.rs:343-368, round half away from zero) and
 // quantize_q8_0_avx2 (ops.rs:284-340, round half to even; its saturating

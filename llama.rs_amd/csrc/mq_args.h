@@ -13,9 +13,14 @@ namespace lrs {
 // elements ride along for the K-quant min / Q6_K offset terms.
 //   dig  [nxb][3][32] int8: digit d of element i at 96 b + 32 d + i
 //   meta [nxb] float4 {scale, sum of the 32 elements, sum of 0..15, sum of 16..31}
+// With q8 set the pack instead holds the reference forward's Q8_0 rounding of
+// the block (quantize_q8_0_avx2, ops.rs:284-340): digits (0, 0, q) with
+// q = round-half-even(x / d) in [-128, 127], d = max |x| / 127, and meta.x =
+// f16(d) widened (the sums are unused: only Q8_0 weights read such a pack).
 struct XPack {
     int8_t *dig;
     float *meta;
+    uint32_t q8;
 };
 
 // bytes of a pack of nxb blocks (digits, then meta, both 16-aligned)
@@ -24,6 +29,7 @@ inline XPack xpack_at(void *base, uint32_t nxb) {
     XPack p;
     p.dig = reinterpret_cast<int8_t *>(base);
     p.meta = reinterpret_cast<float *>(reinterpret_cast<char *>(base) + (size_t)nxb * 96);
+    p.q8 = 0;
     return p;
 }
 

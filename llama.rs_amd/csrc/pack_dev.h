@@ -26,6 +26,21 @@ __device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p) {
     amax = fmaxf(amax, pk_dpp<0x141>(amax));
     amax = fmaxf(amax, pk_dpp<0x140>(amax));
     amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    if (p.q8) {
+        // Model::forward's input of a Q8_0 weight (weights.rs:113-117):
+        // quantize_q8_0_avx2 (ops.rs:284-340), IEEE divisions, half to even
+        const float d = amax > 0.f ? amax / 127.0f : 0.f;
+        const float di = d > 0.f ? 1.0f / d : 0.f;
+        const float r = fminf(fmaxf(__builtin_rintf(v * di), -128.f), 127.f);
+        int8_t *dg = p.dig + (size_t)blk * 96 + i;
+        dg[0] = 0;
+        dg[32] = 0;
+        dg[64] = (int8_t)(int)r;
+        if (i == 0)
+            *reinterpret_cast<float4 *>(p.meta + 4 * (size_t)blk) =
+                make_float4((float)(_Float16)d, 0.f, 0.f, 0.f);
+        return;
+    }
     float r16 = v;  // sum of this lane's 16-element run
     r16 += pk_dpp<0xB1>(r16);
     r16 += pk_dpp<0x4E>(r16);

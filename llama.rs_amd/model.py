@@ -69,6 +69,7 @@ def _bind():
         "lrs_model_profile": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.POINTER(C.c_float),
                                         C.POINTER(C.c_size_t)]),
         "lrs_model_bytes_per_token": (C.c_size_t, [vp]),
+        "lrs_model_set_q8_rounding": (C.c_int, [vp, C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -138,6 +139,11 @@ class ResidentForward:
 
     def __len__(self) -> int:
         return int(lib.lrs_model_len(self.h))
+
+    def set_q8_rounding(self, on: bool) -> None:
+        """Q8_0 weights multiply their input rounded to Q8_0 like the reference
+        CPU forward (weights.rs:109-124), instead of the f32 activation."""
+        check(lib.lrs_model_set_q8_rounding(self.h, int(bool(on))))
 
     # --- device-side greedy ------------------------------------------------
     def decode_greedy(self, token: int, pos: int) -> int:

@@ -82,6 +82,7 @@ def lib() -> C.CDLL:
         L.lrso_model_forward.argtypes = [C.c_void_p, u32p, C.c_uint32, f32p]
         L.lrso_model_forward_partial.restype = C.c_int
         L.lrso_model_forward_partial.argtypes = [C.c_void_p, u32p, C.c_uint32, C.c_uint32]
+        L.lrso_model_set_q8_actq.argtypes = [C.c_void_p, C.c_int]
         L.lrso_model_len.restype = C.c_uint32
         L.lrso_model_len.argtypes = [C.c_void_p]
         L.lrso_model_reset.argtypes = [C.c_void_p]
@@ -317,7 +318,8 @@ class Model:
     ``weights`` maps names to ``(type, np.ndarray[uint8 or float32])``; the
     arrays must outlive the model (they are borrowed)."""
 
-    def __init__(self, cfg: dict, weights: dict, kv_f16: bool = True, threads: int = 1):
+    def __init__(self, cfg: dict, weights: dict, kv_f16: bool = True, threads: int = 1,
+                 q8_actq: bool = True):
         self.cfg = cfg
         self._keep = weights
         c = _Cfg(cfg["n_layer"], cfg["n_embd"], cfg["n_head"], cfg["n_head_kv"],
@@ -337,6 +339,9 @@ class Model:
         if not h:
             raise ValueError("oracle model: bad shapes")
         self._h = h
+        # Q8_0 weights: the reference forward's int8-activation path
+        # (weights.rs:113-117), or dequant + f32 matmul when False
+        lib().lrso_model_set_q8_actq(h, int(q8_actq))
 
     def forward(self, tokens) -> np.ndarray:
         toks = np.ascontiguousarray(tokens, dtype=np.uint32)

@@ -280,12 +280,38 @@ typedef struct {
     const float *x; float *y; uint32_t cols;
 } mv_ctx;
 
+/* Each output is the sequential left fold of ops.rs:89-91.  Columns are taken
+ * eight at a time with eight independent accumulators over an interleaved
+ * copy of x (xt[i][c]): every accumulator still adds its products in index
+ * order, so the results are bit-identical to one column at a time, with
+ * eight times the instruction-level parallelism for batched prompts. */
+typedef struct {
+    uint32_t type; const uint8_t *w; size_t row_bytes; uint32_t n_in, n_out;
+    const float *x; float *y; uint32_t cols;
+    const float *xt;  /* [cols/8][n_in][8] */
+} mv_ctx8;
+
 static void mv_rows(void *p, uint32_t r0, uint32_t r1) {
-    mv_ctx *c = (mv_ctx *)p;
+    mv_ctx8 *c = (mv_ctx8 *)p;
     float *row = (float *)malloc(sizeof(float) * c->n_in);
+    const uint32_t full = c->xt ? c->cols / 8 * 8 : 0;
     for (uint32_t j = r0; j < r1; j++) {
         lrso_dequant(c->type, c->w + (size_t)j * c->row_bytes, c->row_bytes, row);
-        for (uint32_t t = 0; t < c->cols; t++) {
+        for (uint32_t t0 = 0; t0 < full; t0 += 8) {
+            const float *xg = c->xt + (size_t)t0 * c->n_in;
+            float acc[8];
+            for (int k = 0; k < 8; k++) acc[k] = -0.0f;
+            for (uint32_t i = 0; i < c->n_in; i++) {
+                const float wi = row[i];
+                const float *xi = xg + 8 * (size_t)i;
+                for (int k = 0; k < 8; k++) {
+                    const float p2 = wi * xi[k];
+                    acc[k] = acc[k] + p2;
+                }
+            }
+            for (int k = 0; k < 8; k++) c->y[(size_t)(t0 + k) * c->n_out + j] = acc[k];
+        }
+        for (uint32_t t = full; t < c->cols; t++) {
             const float *xr = c->x + (size_t)t * c->n_in;
             float acc = -0.0f; /* f32 Iterator::sum starts from -0.0 */
             for (uint32_t i = 0; i < c->n_in; i++) {
@@ -306,8 +332,21 @@ int lrso_matvec(uint32_t type, const uint8_t *w, size_t w_len, uint32_t n_in,
     if (n_in % (uint32_t)bs != 0) return -1;
     size_t row_bytes = (size_t)(n_in / (uint32_t)bs) * (size_t)ts;
     if (w_len != row_bytes * n_out) return -1;
-    mv_ctx c = {type, w, row_bytes, n_in, n_out, x, y, cols};
+    float *xt = NULL;
+    if (cols >= 8) {
+        const uint32_t groups = cols / 8;
+        xt = (float *)malloc(sizeof(float) * (size_t)groups * 8 * n_in);
+        if (!xt) return -3;
+        for (uint32_t g = 0; g < groups; g++)
+            for (uint32_t k = 0; k < 8; k++) {
+                const float *xr = x + (size_t)(8 * g + k) * n_in;
+                float *dst = xt + (size_t)g * 8 * n_in + k;
+                for (uint32_t i = 0; i < n_in; i++) dst[8 * (size_t)i] = xr[i];
+            }
+    }
+    mv_ctx8 c = {type, w, row_bytes, n_in, n_out, x, y, cols, xt};
     par_rows(mv_rows, &c, n_out, n_threads);
+    free(xt);
     return 0;
 }
 
@@ -350,19 +389,17 @@ int lrso_quantize_q8_0(const float *x, uint32_t n, int half_even, uint8_t *out) 
  * q8_0_q8_0_dot_scalar (ops.rs:704-724): acc += dw * dx * (float)sum(qw * qx)
  * block by block from 0.0; x is quantized first (quantize_q8_0_split,
  * ops.rs:371-384). */
-int lrso_matvec_q8_0_actq(const uint8_t *w, size_t w_len, uint32_t n_in, uint32_t n_out,
-                          const float *x, int half_even, float *y) {
-    if (n_in % 32) return -1;
-    const uint32_t nb = n_in / 32;
-    if (w_len != (size_t)nb * 34 * n_out) return -1;
-    uint8_t *xq = (uint8_t *)malloc((size_t)nb * 34 + 1);
-    if (!xq) return -3;
-    lrso_quantize_q8_0(x, n_in, half_even, xq);
-    for (uint32_t r = 0; r < n_out; r++) {
-        const uint8_t *wr = w + (size_t)r * nb * 34;
+typedef struct {
+    const uint8_t *w, *xq; uint32_t nb; float *y;
+} actq_ctx;
+
+static void actq_rows(void *p, uint32_t r0, uint32_t r1) {
+    const actq_ctx *c = (const actq_ctx *)p;
+    for (uint32_t r = r0; r < r1; r++) {
+        const uint8_t *wr = c->w + (size_t)r * c->nb * 34;
         float acc = 0.0f;
-        for (uint32_t b = 0; b < nb; b++) {
-            const uint8_t *bw = wr + 34 * (size_t)b, *bx = xq + 34 * (size_t)b;
+        for (uint32_t b = 0; b < c->nb; b++) {
+            const uint8_t *bw = wr + 34 * (size_t)b, *bx = c->xq + 34 * (size_t)b;
             const float dw = lrso_f16_to_f32((uint16_t)(bw[0] | (bw[1] << 8)));
             const float dx = lrso_f16_to_f32((uint16_t)(bx[0] | (bx[1] << 8)));
             int32_t dot = 0;
@@ -370,10 +407,27 @@ int lrso_matvec_q8_0_actq(const uint8_t *w, size_t w_len, uint32_t n_in, uint32_
             const float s = dw * dx;
             acc = acc + s * (float)dot;
         }
-        y[r] = acc;
+        c->y[r] = acc;
     }
+}
+
+int lrso_matvec_q8_0_actq_mt(const uint8_t *w, size_t w_len, uint32_t n_in, uint32_t n_out,
+                             const float *x, int half_even, float *y, int n_threads) {
+    if (n_in % 32) return -1;
+    const uint32_t nb = n_in / 32;
+    if (w_len != (size_t)nb * 34 * n_out) return -1;
+    uint8_t *xq = (uint8_t *)malloc((size_t)nb * 34 + 1);
+    if (!xq) return -3;
+    lrso_quantize_q8_0(x, n_in, half_even, xq);
+    actq_ctx c = {w, xq, nb, y};
+    par_rows(actq_rows, &c, n_out, n_threads);
     free(xq);
     return 0;
+}
+
+int lrso_matvec_q8_0_actq(const uint8_t *w, size_t w_len, uint32_t n_in, uint32_t n_out,
+                          const float *x, int half_even, float *y) {
+    return lrso_matvec_q8_0_actq_mt(w, w_len, n_in, n_out, x, half_even, y, 1);
 }
 
 /* ------------------------------------------------------------------------- */
@@ -593,6 +647,7 @@ struct lrso_model {
     float *kc, *vc;     /* [n_layer][ctx][kv_dim] */
     uint32_t len;
     int kv_f16, n_threads;
+    int q8_actq; /* Q8_0 weights through quantize_q8_0_split + matmul_q8_0_actq */
 };
 
 static int tensor_ok(const lrso_tensor *t, uint32_t n_in, uint32_t n_out) {
@@ -636,8 +691,11 @@ lrso_model *lrso_model_create(const lrso_config *cfg, const lrso_tensor *token_e
     m->vc = (float *)calloc(cap, sizeof(float));
     m->kv_f16 = kv_f16;
     m->n_threads = n_threads;
+    m->q8_actq = 1;
     return m;
 }
+
+void lrso_model_set_q8_actq(lrso_model *m, int on) { m->q8_actq = on; }
 
 static float *tensor_f32(const lrso_tensor *t, uint32_t n) {
     float *o = (float *)malloc(sizeof(float) * n);
@@ -645,8 +703,20 @@ static float *tensor_f32(const lrso_tensor *t, uint32_t n) {
     return o;
 }
 
+/* RawTensor::matmul_into (weights.rs:109-124): a Q8_0 weight whose n_in is a
+ * multiple of 32 takes the int8-activation path, each token's activation
+ * rounded by quantize_q8_0_split (ops.rs:371-384; on x86 with AVX2, the
+ * half-to-even quantize_q8_0_avx2, ops.rs:284-340 and :347-352) and
+ * multiplied by matmul_q8_0_actq (ops.rs:728-886); every other weight is
+ * dequantized to f32 and multiplied by ops::matmul (ops.rs:78-101). */
 static void mm(lrso_model *m, const lrso_tensor *t, const float *x, uint32_t n_in,
                uint32_t n_out, uint32_t n_tok, float *y) {
+    if (m->q8_actq && t->type == LRSO_Q8_0 && n_in % 32 == 0) {
+        for (uint32_t k = 0; k < n_tok; k++)
+            lrso_matvec_q8_0_actq_mt(t->bytes, t->len, n_in, n_out, x + (size_t)k * n_in, 1,
+                                     y + (size_t)k * n_out, m->n_threads);
+        return;
+    }
     lrso_matvec(t->type, t->bytes, t->len, n_in, n_out, x, y, n_tok, m->n_threads);
 }
 

@@ -75,6 +75,9 @@ int lrso_matvec(uint32_t type, const uint8_t *w, size_t w_len, uint32_t n_in,
 int lrso_quantize_q8_0(const float *x, uint32_t n, int half_even, uint8_t *out);
 int lrso_matvec_q8_0_actq(const uint8_t *w, size_t w_len, uint32_t n_in, uint32_t n_out,
                           const float *x, int half_even, float *y);
+/* the same over n_threads threads (rows in chunks of 32) */
+int lrso_matvec_q8_0_actq_mt(const uint8_t *w, size_t w_len, uint32_t n_in, uint32_t n_out,
+                             const float *x, int half_even, float *y, int n_threads);
 
 /* ---- deterministic synthetic blocks (counter-based, identical on GPU) ---- */
 uint64_t lrso_hash(uint64_t seed, uint64_t block, uint32_t j);
@@ -145,6 +148,9 @@ int lrso_model_forward(lrso_model *m, const uint32_t *tokens, uint32_t n_tok,
  * to time a bounded sample of a large model for the CPU baseline. */
 int lrso_model_forward_partial(lrso_model *m, const uint32_t *tokens, uint32_t n_tok,
                                uint32_t n_layers_run);
+/* on (the default): Q8_0 weights take the reference forward's int8-activation
+ * path (weights.rs:113-117); off: dequant + f32 matmul like the K-quants */
+void lrso_model_set_q8_actq(lrso_model *m, int on);
 uint32_t lrso_model_len(const lrso_model *m);
 void lrso_model_reset(lrso_model *m);
 void lrso_model_destroy(lrso_model *m);

@@ -84,6 +84,48 @@ def test_q6_k_all_zero_ql_qh(orc):  # dequant.rs:410-464
                 assert out[base + l + off] == (-32.0 if l < 16 else 0.0)
 
 
+def test_q6_k_one_hot_quant_bits(orc):
+    """Every single set bit of ql (128 bytes) and qh (64 bytes) with d = 1 and
+    all scales 1: exactly one element moves from -32 to 2^k - 32.  Positions
+    from the GGUF Q6_K layout: per 128-element half n, ql[64n + j] low nibble
+    is quant bits 0-3 of element 128n + j and its high nibble of element
+    128n + j + 64; qh[32n + l] bit pair p is quant bits 4-5 of element
+    128n + l + 32p."""
+    base = [0] * 128 + [0] * 64 + [1] * 16 + f16b(1.0)
+    for byte in range(192):
+        for bit in range(8):
+            blk = list(base)
+            blk[byte] = 1 << bit
+            out = orc.dequant(Q6_K, bytes(blk))
+            if byte < 128:
+                n, j = byte // 64, byte % 64
+                elem = 128 * n + j + (64 if bit >= 4 else 0)
+                k = bit % 4
+            else:
+                n, l = (byte - 128) // 32, (byte - 128) % 32
+                elem = 128 * n + l + 32 * (bit // 2)
+                k = 4 + bit % 2
+            exp = np.full(256, -32.0, np.float32)
+            exp[elem] = float((1 << k) - 32)
+            assert np.array_equal(out, exp), (byte, bit)
+
+
+def test_q6_k_one_hot_scale_slots(orc):
+    """One nonzero int8 scale s (slot i) with d = 1 and all quants 0: exactly
+    the 16 elements of that slot read -32 * s; slot 8n + 2p + m covers
+    elements 128n + 32p + 16m .. +15."""
+    for slot in range(16):
+        for s in (1, -1, 127, -128):
+            sc = [0] * 16
+            sc[slot] = s & 0xFF
+            out = orc.dequant(Q6_K, bytes([0] * 192 + sc + f16b(1.0)))
+            n, r = slot // 8, slot % 8
+            e0 = 128 * n + 32 * (r // 2) + 16 * (r % 2)
+            exp = np.zeros(256, np.float32)
+            exp[e0:e0 + 16] = -32.0 * s
+            assert np.array_equal(out, exp), (slot, s)
+
+
 @pytest.mark.parametrize("t,bad", [(Q8_0, 33), (Q4_0, 17), (Q4_K, 143), (Q5_K, 175),
                                    (Q6_K, 209)])
 def test_bad_size_is_an_error(orc, t, bad):  # dequant.rs BadSize arms
