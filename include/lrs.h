@@ -114,6 +114,19 @@ int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y,
 int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
                    uint32_t cols);
 
+/* lrs_matvec_dev that allocates nothing: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The input pack
+ * lives in a static device array of the library (160 KiB, one copy per GPU,
+ * held until the process ends) instead of the context scratch, so n_in is
+ * limited to LRS_NOALLOC_MAX_N_IN (LRS_E_ARG beyond).  Every call on one GPU
+ * shares that array: calls on the same stream are ordered, calls that
+ * overlap on one GPU (other streams or contexts) race.  Async on the context
+ * stream; results equal lrs_matvec_dev's. */
+#define LRS_NOALLOC_MAX_N_IN 46592u
+int lrs_matvec_dev_noalloc(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
+                           uint32_t cols);
+
 /* The int8-activation path the reference's CPU Model::forward takes for Q8_0
  * weights (crates/llama-model/src/ops.rs), on device buffers, enqueued on
  * the context stream (async).

@@ -31,6 +31,10 @@ TYPE_NAME = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q
              Q6_K: "Q6_K"}
 
 
+# largest n_in of lrs_matvec_dev_noalloc (LRS_NOALLOC_MAX_N_IN)
+NOALLOC_MAX_N_IN = 46592
+
+
 class ModelError(RuntimeError):
     """Mirror of llama_model::ModelError::Gpu(String)."""
 
@@ -63,6 +67,7 @@ def _load() -> C.CDLL:
         "lrs_weight_dequant_dev": (i32, [vp, vp, vp]),
         "lrs_matvec_f32": (i32, [vp, vp, vp, vp, u32]),
         "lrs_matvec_dev": (i32, [vp, vp, vp, vp, u32]),
+        "lrs_matvec_dev_noalloc": (i32, [vp, vp, vp, vp, u32]),
         "lrs_gemm_dev": (i32, [vp, vp, vp, vp, u32, i32]),
         "lrs_quantize_q8_0_dev": (i32, [vp, vp, u32, i32, vp]),
         "lrs_matvec_q8_0_actq_dev": (i32, [vp, vp, vp, vp, u32, i32]),
@@ -267,6 +272,11 @@ class Weight:
 
     def matvec_dev(self, x: DeviceBuffer, y: DeviceBuffer, cols: int = 1) -> None:
         check(lib.lrs_matvec_dev(self.ctx.h, self.h, x.ptr, y.ptr, cols))
+
+    def matvec_dev_noalloc(self, x: DeviceBuffer, y: DeviceBuffer, cols: int = 1) -> None:
+        """matvec_dev with the input pack in the library's static device array
+        (no allocation; n_in <= NOALLOC_MAX_N_IN)."""
+        check(lib.lrs_matvec_dev_noalloc(self.ctx.h, self.h, x.ptr, y.ptr, cols))
 
     def matvec_actq_dev(self, x: DeviceBuffer, y: DeviceBuffer, cols: int = 1,
                         half_even: bool = True) -> None:

@@ -104,6 +104,40 @@ static int ctx_scratch(lrs_ctx *ctx, size_t bytes, void **p) {
 }
 }  // namespace lrs
 
+// ---- input pack of lrs_matvec_dev_noalloc ---------------------------------
+// A static device array instead of the context scratch: the pack of one
+// column of an input of up to LRS_NOALLOC_MAX_N_IN elements (3.5 bytes per
+// element, fully rewritten by every call, so nothing has to start at zero).
+// Each GPU holds its own copy until the process ends.  In host code `scratch`
+// only names the symbol: the device address of each GPU's copy comes from
+// hipGetSymbolAddress, resolved once per device by lrs_ctx_create.
+static constexpr size_t NOALLOC_PACK_BYTES = 160 * 1024;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_PACK_BYTES];
+static constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_noalloc_mu;
+static void *g_noalloc_ptr[NOALLOC_MAX_DEVICES];
+
+namespace lrs {
+// with `device` current: the device address of this GPU's `scratch`
+static int noalloc_init(int device) {
+    if (device >= NOALLOC_MAX_DEVICES)
+        return fail(LRS_E_UNSUPPORTED, "device index " + std::to_string(device) + " above " +
+                                           std::to_string(NOALLOC_MAX_DEVICES - 1));
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (g_noalloc_ptr[device]) return LRS_OK;
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(LRS_E_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_noalloc_ptr[device] = p;
+    return LRS_OK;
+}
+static void *noalloc_ptr(int device) {
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    return device >= 0 && device < NOALLOC_MAX_DEVICES ? g_noalloc_ptr[device] : nullptr;
+}
+}  // namespace lrs
+
 #define SETDEV(ctx) LRS_HIP(hipSetDevice((ctx)->device))
 
 extern "C" {
@@ -135,6 +169,7 @@ int lrs_ctx_create(int device, lrs_ctx **out) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(LRS_E_UNSUPPORTED, std::string("liblrs is built for gfx950, device is ") +
                                            prop.gcnArchName);
+    if (int rc = noalloc_init(device)) return rc;
     lrs_ctx *c = new lrs_ctx();
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -313,6 +348,23 @@ int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float 
     SETDEV(ctx);
     void *pack = nullptr;
     if (int rc_ = ctx_scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack)) return rc_;
+    LRS_HIP(launch_matvec(w->v, x_dev, y_dev, cols, pack, ctx->stream));
+    return LRS_OK;
+}
+
+int lrs_matvec_dev_noalloc(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
+                           uint32_t cols) {
+    if (!ctx || !w || !x_dev || !y_dev) return fail(LRS_E_ARG, "null argument");
+    int rc = matvec_check(w, cols);
+    if (rc) return rc;
+    const size_t need = xpack_bytes(pack_blocks(w->v.type, w->v.n_in));
+    if (w->v.n_in > LRS_NOALLOC_MAX_N_IN || need > NOALLOC_PACK_BYTES)
+        return fail(LRS_E_ARG, "n_in=" + std::to_string(w->v.n_in) +
+                                   " is above the no-allocation matvec's maximum of " +
+                                   std::to_string(LRS_NOALLOC_MAX_N_IN));
+    void *pack = noalloc_ptr(ctx->device);
+    if (!pack) return fail(LRS_E_HIP, "static pack of this device not resolved");
+    SETDEV(ctx);
     LRS_HIP(launch_matvec(w->v, x_dev, y_dev, cols, pack, ctx->stream));
     return LRS_OK;
 }
