@@ -63,6 +63,7 @@ OP_NAMES = {"qkv": "fused RMSNorm + q/k/v matvec + bias + RoPE + f16 KV append",
             "o": "attn_output matvec + residual add",
             "gateup": "fused RMSNorm + ffn_gate/ffn_up Q4_K matvec + SwiGLU",
             "down": "ffn_down Q6_K matvec + residual add",
+            "ffn": "the layer's FFN as the token plan runs it (gate/up + down, split on two streams)",
             "head": "final RMSNorm + output head Q6_K matvec"}
 PROMPT = 512
 
@@ -88,7 +89,7 @@ def op_profile(m, n_layer):
     """Average duration of every fused op (HIP events on the model's stream;
     per-layer ops rotate over all layers so weights stream from HBM)."""
     ops = {}
-    for op in ("qkv", "attn", "o", "gateup", "down", "head"):
+    for op in ("qkv", "attn", "o", "gateup", "down", "ffn", "head"):
         iters = 2 * n_layer if op != "head" else 8
         us, b = m.profile(op, iters)
         mult = n_layer if op != "head" else 1
@@ -486,9 +487,9 @@ def run_pmc(lrs, ctx):
     log(f"[pmc] copy calibration: {3} launches of {4 * n} B read + {4 * n} B written")
     m = synthetic_model(ctx, cfg32(4), seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
     m.decode_batch(np.arange(8, dtype=np.uint32), 0)
-    for op in ("gateup", "down", "head"):
+    for op in ("qkv", "attn", "o", "gateup", "down", "head"):
         us, b = m.profile(op, 8 if op != "head" else 2)
-        log(f"[pmc] {op}: {us:.2f} us/launch, {b} algorithmic weight bytes")
+        log(f"[pmc] {op}: {us:.2f} us/launch, {b} algorithmic bytes")
     m.close()
     # config 4: the same ops on a 4-layer block of the hybrid shape (3 delta-net
     # layers + 1 gated attention layer)

@@ -464,6 +464,12 @@ hipError_t op_down(lrs_model *m, uint32_t l) {
                      m->ctx->stream);
 }
 
+// the FFN of layer l: gate/up + SwiGLU, then down + residual
+hipError_t op_ffn(lrs_model *m, uint32_t l) {
+    hipError_t e = op_gateup(m, l);
+    return e != hipSuccess ? e : op_down(m, l);
+}
+
 // logits = W_out (rmsnorm(x) * output_norm); greedy: each wavefront of
 // outputs also leaves the argmax key of its rows, reduced by op_argmax
 hipError_t op_head(lrs_model *m, bool greedy) {
@@ -512,9 +518,7 @@ hipError_t enqueue_forward(lrs_model *m, bool greedy) {
         } else if ((e = op_qkv(m, l)) != hipSuccess || (e = op_attn(m, l)) != hipSuccess) {
             return e;
         }
-        if ((e = op_o(m, l)) != hipSuccess || (e = op_gateup(m, l)) != hipSuccess ||
-            (e = op_down(m, l)) != hipSuccess)
-            return e;
+        if ((e = op_o(m, l)) != hipSuccess || (e = op_ffn(m, l)) != hipSuccess) return e;
     }
     if ((e = op_head(m, greedy)) != hipSuccess) return e;
     if (greedy && (e = op_argmax(m)) != hipSuccess) return e;
@@ -628,6 +632,7 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         m->pk_q8.q8 = 1;
     }
     if (hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess) return fail(LRS_E_HIP, "memset");
+    }
     if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=
@@ -1242,7 +1247,7 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
 int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, size_t *bytes) {
     if (!m || !avg_us || iters == 0) return fail(LRS_E_ARG, "null argument");
     const lrs_config &c = m->cfg;
-    if (op > LRS_OP_QK_PREP) return fail(LRS_E_ARG, "unknown op");
+    if (op > LRS_OP_FFN) return fail(LRS_E_ARG, "unknown op");
     const bool dn_op = op == LRS_OP_DN_PROJ || op == LRS_OP_DN_STEP || op == LRS_OP_DN_OUT;
     const bool attn_op = op == LRS_OP_QKV || op == LRS_OP_ATTN || op == LRS_OP_O ||
                          op == LRS_OP_QK_PREP;
@@ -1289,6 +1294,7 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
         case LRS_OP_O: b = wbytes(D.o) + qd4 + 2 * E4; break;
         case LRS_OP_GATEUP: b = wbytes(D.gate) + wbytes(D.up) + 2 * E4 + (size_t)c.n_ff * 4; break;
         case LRS_OP_DOWN: b = wbytes(D.down) + (size_t)c.n_ff * 4 + 2 * E4; break;
+        case LRS_OP_FFN: b = wbytes(D.gate) + wbytes(D.up) + wbytes(D.down) + 3 * E4; break;
         }
     } else {
         b = wbytes(m->output) + 2 * E4 + (size_t)c.vocab * 4;
@@ -1306,6 +1312,7 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
         case LRS_OP_O: case LRS_OP_DN_OUT: return op_o(m, l);
         case LRS_OP_GATEUP: return op_gateup(m, l);
         case LRS_OP_DOWN: return op_down(m, l);
+        case LRS_OP_FFN: return op_ffn(m, l);
         case LRS_OP_QK_PREP: return op_qk_prep(m, l);
         case LRS_OP_DN_PROJ: return op_dn_proj(m, l);
         case LRS_OP_DN_STEP: return op_dn_step(m, l);

@@ -482,18 +482,40 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
     for (int t = 0; t < TPW; t++) acc[t] = accm[t] = 0.f;
 
-    for (uint32_t u0 = u_lo; u0 < u_hi; u0 += P) {
+    // steady state: every unit's successor P units ahead is in range, so the
+    // loads are unconditional and each register set is refilled in place
+    // right after its unit is consumed (P units stay in flight; a
+    // conditional refill would make the compiler copy the sets at the loop
+    // back-edge and wait for every load there)
+    uint32_t u0 = u_lo;
+    for (; u0 + 2 * P <= u_hi; u0 += P) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
-            const uint32_t u = u0 + i;
-            if (u >= u_hi) break;
-            udot<T, TPW>(wr[i], u, lds, lp, al, lane, acc, accm);
-            if (u + P < u_hi) {
+            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc, accm);
 #pragma unroll
-                for (int t = 0; t < TPW; t++) wload<T>(wr[i][t], wt[t] + (size_t)(u + P) * tchunk_bytes(T), lane);
+            for (int t = 0; t < TPW; t++)
+                wload<T>(wr[i][t], wt[t] + (size_t)(u0 + P + i) * tchunk_bytes(T), lane);
+            // keep the refill here: the scheduler would otherwise sink every
+            // refill to the end of the loop body and drain the queue first
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // tail: fewer than 2P units left, the last refills
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        if (u0 + i < u_hi) {
+            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc, accm);
+            if (u0 + P + i < u_hi) {
+#pragma unroll
+                for (int t = 0; t < TPW; t++)
+                    wload<T>(wr[i][t], wt[t] + (size_t)(u0 + P + i) * tchunk_bytes(T), lane);
             }
         }
     }
+    u0 += P;
+#pragma unroll
+    for (int i = 0; i < P; i++)
+        if (u0 + i < u_hi) udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc, accm);
 
     // row sums: lanes n, n+16, n+32, n+48 hold sub-block classes of row n
     float v[TPW];
@@ -590,8 +612,13 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     }
 }
 
+// two workgroups of up to 8 wavefronts per CU (at most 128 VGPRs), else one
+template <int W>
+constexpr int mq_waves_per_eu() { return W <= 8 ? (2 * W + 3) / 4 : (W + 3) / 4; }
+
 template <uint32_t T0, uint32_t T1, int TPW, int TG, int KS, int P, int EPI>
-__global__ __launch_bounds__(64 * TG * KS) void k_mq(MqArgs a) {
+__global__ __launch_bounds__(64 * TG * KS)
+__attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq(MqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float red[TG * KS * TPW * 16 + TG * KS];
     uint32_t si = 0;
@@ -622,6 +649,7 @@ static MqFn pick(const MqGeom &g) {
     LRS_MQ_CASE(1, 2, 6, 2)
     LRS_MQ_CASE(1, 2, 6, 1)
     LRS_MQ_CASE(1, 2, 8, 1)
+    LRS_MQ_CASE(1, 2, 8, 2)
     // Q8_0 units are 64 elements: deeper prefetch over more K-slices
     if constexpr (T0 == T_Q8_0 && T1 == T_Q8_0 && EPI == MQ_STORE) {
         LRS_MQ_CASE(1, 1, 8, 6)
