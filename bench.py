@@ -486,7 +486,8 @@ def run_pmc(lrs, ctx):
     ctx.sync()
     log(f"[pmc] copy calibration: {3} launches of {4 * n} B read + {4 * n} B written")
     m = synthetic_model(ctx, cfg32(4), seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
-    m.decode_batch(np.arange(8, dtype=np.uint32), 0)
+    # a 512-token cache, so attention reads the decode-time length
+    m.decode_batch(np.arange(PROMPT, dtype=np.uint32) % cfg32(4)["vocab"], 0)
     for op in ("qkv", "attn", "o", "gateup", "down", "head"):
         us, b = m.profile(op, 8 if op != "head" else 2)
         log(f"[pmc] {op}: {us:.2f} us/launch, {b} algorithmic bytes")

@@ -152,7 +152,7 @@ int lrs_matvec_q8_0_actq_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_d
  * accumulation.  precision 1: each operand rounded to bf16 once;
  * precision 3: each split into bf16 hi + lo and three products summed
  * (~2^-16 relative, for prefill that must match the f32 forward).
- * Weights: Q4_K, Q6_K; n_in a multiple of 64. */
+ * Weights: Q4_K, Q5_K, Q6_K, Q8_0; n_in a multiple of 256. */
 int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y_dev, uint32_t m,
                  int precision);
 
@@ -265,7 +265,7 @@ typedef struct {
  * entry points apply.  Its recurrent state cannot be rewound: every decode
  * must continue at the current length (pos == lrs_model_len) and
  * lrs_reset clears the states and conv windows.  batch_size() is 512 when
- * every matmul weight is Q4_K or Q6_K (prompt blocks: GEMM projections and
+ * every matmul weight is Q4_K, Q5_K, Q6_K or Q8_0 (prompt blocks: GEMM projections and
  * block delta-net kernels), else 1. */
 int lrs_hybrid_create(lrs_ctx *ctx, const lrs_hybrid_config *cfg, const lrs_hybrid_layer *layers,
                       const lrs_weight *token_embd, const float *output_norm,

@@ -418,8 +418,10 @@ int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y
     if (!ctx || !w || !a_dev || !y_dev) return fail(LRS_E_ARG, "null argument");
     if (m == 0) return fail(LRS_E_ARG, "m must be >= 1");
     if (precision != 1 && precision != 3) return fail(LRS_E_ARG, "precision must be 1 or 3");
-    if (w->v.type != T_Q4_K && w->v.type != T_Q6_K)
-        return fail(LRS_E_UNSUPPORTED, "the GEMM supports Q4_K and Q6_K weights");
+    if (w->v.type != T_Q4_K && w->v.type != T_Q5_K && w->v.type != T_Q6_K && w->v.type != T_Q8_0)
+        return fail(LRS_E_UNSUPPORTED, "the GEMM supports Q4_K, Q5_K, Q6_K and Q8_0 weights");
+    if (w->v.n_in % 256)
+        return fail(LRS_E_ARG, "the GEMM needs n_in to be a multiple of 256");
     SETDEV(ctx);
     // the activation as bf16 planes (hi, and lo for precision 3) in context scratch
     // (and the K-slice partials when the GEMM is split over K)

@@ -1,7 +1,7 @@
 // gemm.hip — dequantize x GEMM for batched prefill on the gfx950 matrix cores.
 //
 // Y[m][n] = sum_k A[m][k] * W[n][k]: A = M tokens x K activations (f32 in
-// HBM), W = a resident N x K GGUF weight (Q4_K or Q6_K).  Replaces the
+// HBM), W = a resident N x K GGUF weight (Q4_K, Q5_K, Q6_K or Q8_0).  Replaces the
 // reference's prefill GEMM (shaders/mul_mm.comp, dispatched by
 // matmul::dispatch_mul_mm_q4k, crates/llama-vulkan/src/matmul.rs:433-465),
 // which quantizes A to int8; here both operands go to the MFMA units as bf16
@@ -50,13 +50,28 @@ __device__ __forceinline__ u32x4 ldq16(const uint8_t *p) { return *reinterpret_c
 template <uint32_t T> struct WRaw;
 template <> struct WRaw<T_Q4_K> { u32x4 hd, qs; };
 template <> struct WRaw<T_Q6_K> { u32x4 ql, qh; uint32_t sc, d; };
+template <> struct WRaw<T_Q5_K> { u32x4 hd, qh, qs; };
+template <> struct WRaw<T_Q8_0> { u32x4 qs; uint32_t d; };
 
 template <uint32_t T>
 __device__ __forceinline__ void wload(const GemmArgs &g, uint32_t n, uint32_t e, WRaw<T> &w) {
     const uint32_t o = e & 255, r = n & 15;  // offset inside the super-block, row in the tile
     const uint32_t l0 = o & 16;               // first or second 16 of a 32-element run
-    const uint8_t *c = g.q + ((size_t)(n >> 4) * g.units + (e >> 8)) * tchunk_bytes(T);
-    if constexpr (T == T_Q4_K) {
+    const uint8_t *c = g.q + ((size_t)(n >> 4) * g.units + e / tunit_elems(T)) * tchunk_bytes(T);
+    if constexpr (T == T_Q8_0) {
+        // 64-element units of two blocks: piece g = 2 block + 16-byte half,
+        // then the 16 rows' f16 d of both blocks (tiled.h)
+        const uint32_t o6 = e & 63, b = o6 >> 5, pg = 2 * b + ((o6 >> 4) & 1);
+        w.qs = ldq16(c + 16 * (16 * pg + r));
+        w.d = *reinterpret_cast<const uint16_t *>(c + 1024 + 4 * r + 2 * b);
+    } else if constexpr (T == T_Q5_K) {
+        // as Q4_K with qs after the qh halves; qh[l0 .. l0 + 16) of row r is
+        // half l0 / 16 of the row's qh (dequant.rs:157-203)
+        const uint32_t j = o >> 6, pg = 2 * (j & 1) + (l0 >> 4);
+        w.hd = ldq16(c + 16 * r);
+        w.qh = ldq16(c + 256 + 16 * (16 * (l0 >> 4) + r));
+        w.qs = ldq16(c + 768 + 1024 * (j >> 1) + 16 * (16 * pg + r));
+    } else if constexpr (T == T_Q4_K) {
         // qs[32j + l0 ..+16), j = o / 64: piece (g, r), g = 2(j&1) + l0/16, of half j>>1
         const uint32_t j = o >> 6, pg = 2 * (j & 1) + (l0 >> 4);
         w.hd = ldq16(c + 16 * r);
@@ -76,14 +91,20 @@ __device__ __forceinline__ void wload(const GemmArgs &g, uint32_t n, uint32_t e,
 // wprep decodes the run's scale (and min), wdeq4 the weights 4c..4c+3, so the
 // dequant can be spread between the matrix-core ops of a pipeline step
 struct DeqPrep {
-    float a, b;    // Q4_K: d * sc, dmin * m; Q6_K: d * scale
-    uint32_t sel;  // Q4_K: high nibbles; Q6_K: quarter of the half
+    float a, b;    // Q4_K / Q5_K: d * sc, dmin * m; Q6_K: d * scale; Q8_0: d
+    uint32_t sel;  // Q4_K / Q5_K: high nibbles; Q6_K: quarter of the half
+    uint32_t sub;  // Q5_K: sub-block (its bit of qh)
 };
 template <uint32_t T>
 __device__ __forceinline__ DeqPrep wprep(const WRaw<T> &w, uint32_t e) {
     const uint32_t o = e & 255;
     DeqPrep p;
-    if constexpr (T == T_Q4_K) {
+    p.sub = 0;
+    if constexpr (T == T_Q8_0) {
+        p.a = h2f((uint16_t)w.d);
+        p.b = 0.f;
+        p.sel = 0;
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         const uint32_t j = o >> 6, hi = (o >> 5) & 1;  // qs group, high nibbles
         // get_scale_min_k4 (dequant.rs:101-110): scale bytes 0-3, 4-7, 8-11 are
         // header words y, z, w; sub-block jj reads byte jj & 3 of each
@@ -96,6 +117,7 @@ __device__ __forceinline__ DeqPrep wprep(const WRaw<T> &w, uint32_t e) {
         p.a = __fmul_rn(dv, (float)sc);
         p.b = __fmul_rn(mv, (float)m);
         p.sel = hi;
+        p.sub = jj;
     } else {  // T_Q6_K
         p.a = __fmul_rn(h2f((uint16_t)w.d), (float)(int8_t)(w.sc & 0xFF));
         p.b = 0.f;
@@ -105,12 +127,21 @@ __device__ __forceinline__ DeqPrep wprep(const WRaw<T> &w, uint32_t e) {
 }
 template <uint32_t T>
 __device__ __forceinline__ void wdeq4(const WRaw<T> &w, const DeqPrep &p, int c, float (&v)[16]) {
-    if constexpr (T == T_Q4_K) {
+    if constexpr (T == T_Q8_0) {
+        // dequant.rs:58-76: q * d
         const uint32_t qw = c == 0 ? w.qs.x : c == 1 ? w.qs.y : c == 2 ? w.qs.z : w.qs.w;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            v[4 * c + i] = __fmul_rn((float)(int8_t)((qw >> (8 * i)) & 0xFF), p.a);
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        const uint32_t qw = c == 0 ? w.qs.x : c == 1 ? w.qs.y : c == 2 ? w.qs.z : w.qs.w;
+        uint32_t hw = 0;
+        if constexpr (T == T_Q5_K) hw = c == 0 ? w.qh.x : c == 1 ? w.qh.y : c == 2 ? w.qh.z : w.qh.w;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t byte = (qw >> (8 * i)) & 0xFF;
-            const uint32_t q = p.sel ? (byte >> 4) : (byte & 15);
+            uint32_t q = p.sel ? (byte >> 4) : (byte & 15);
+            if constexpr (T == T_Q5_K) q += ((hw >> (8 * i + p.sub)) & 1) << 4;
             v[4 * c + i] = __fsub_rn(__fmul_rn(p.a, (float)q), p.b);
         }
     } else {  // T_Q6_K: q = (ql nibble | qh 2 bits << 4) - 32
@@ -420,12 +451,15 @@ hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float
     g.part = work;
     const uint32_t grid = 8 * ((g.nm * g.nn * g.ks + 7) / 8);
     void (*fn)(GemmArgs) = nullptr;
-    if (w.type == T_Q4_K)
-        fn = prec == 3 ? k_gemm<T_Q4_K, 3, 128> : bm == 256 ? k_gemm<T_Q4_K, 1, 256> : k_gemm<T_Q4_K, 1, 128>;
-    else if (w.type == T_Q6_K)
-        fn = prec == 3 ? k_gemm<T_Q6_K, 3, 128> : bm == 256 ? k_gemm<T_Q6_K, 1, 256> : k_gemm<T_Q6_K, 1, 128>;
-    else
-        return hipErrorNotSupported;
+#define LRS_GEMM_PICK(TT) prec == 3 ? k_gemm<TT, 3, 128> : bm == 256 ? k_gemm<TT, 1, 256> : k_gemm<TT, 1, 128>
+    switch (w.type) {
+    case T_Q4_K: fn = LRS_GEMM_PICK(T_Q4_K); break;
+    case T_Q5_K: fn = LRS_GEMM_PICK(T_Q5_K); break;
+    case T_Q6_K: fn = LRS_GEMM_PICK(T_Q6_K); break;
+    case T_Q8_0: fn = LRS_GEMM_PICK(T_Q8_0); break;
+    default: return hipErrorNotSupported;
+    }
+#undef LRS_GEMM_PICK
     hipLaunchKernelGGL(fn, dim3(grid), dim3(512), 0, s, g);
     if (g.ks > 1) {
         const size_t n = (size_t)M * g.N;

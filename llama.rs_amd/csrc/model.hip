@@ -632,7 +632,6 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         m->pk_q8.q8 = 1;
     }
     if (hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess) return fail(LRS_E_HIP, "memset");
-    }
     if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=
@@ -918,8 +917,15 @@ static constexpr uint32_t PREFILL_BLOCK = 512;
 
 // every matmul weight has a GEMM kernel and the attention shape is supported
 static bool prefill_capable(const lrs_model *m) {
-    auto ok = [](const lrs_weight *w) {
-        return (w->v.type == T_Q4_K || w->v.type == T_Q6_K) && w->v.n_in % 128 == 0;
+    // with the reference's Q8_0 input rounding on, Q8_0 weights stay on the
+    // token path (the GEMM multiplies the f32 activations)
+    const bool q8_ok = std::none_of(m->layers.begin(), m->layers.end(), [](const DevLayer &L) {
+        return L.qkv_q8 || L.o_q8 || L.ffn_q8 || L.down_q8;
+    });
+    auto ok = [q8_ok](const lrs_weight *w) {
+        const uint32_t t = w->v.type;
+        return (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || (t == T_Q8_0 && q8_ok)) &&
+               w->v.n_in % 256 == 0;
     };
     const lrs_config &c = m->cfg;
     if ((c.head_dim != 64 && c.head_dim != 128 && (c.head_dim != 256 || !m->hybrid)) ||

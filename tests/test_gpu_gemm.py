@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
-Q4_K, Q6_K = 12, 14
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 
 
 @pytest.fixture(scope="module")
@@ -33,7 +33,7 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a - b) / np.linalg.norm(b))
 
 
-@pytest.mark.parametrize("t", [Q4_K, Q6_K])
+@pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
 # (64, 256, 4096) and (96, 128, 8192) split K over workgroups (few output
 # tiles, long K); m >= 512 uses the 256-token tile at precision 1
 @pytest.mark.parametrize("m,n,k", [(1, 200, 512), (7, 128, 256), (130, 300, 768), (256, 256, 1024),
@@ -66,7 +66,8 @@ def test_gemm_row_of_one_hot_activations_is_a_weight_column(lrs, orc, ctx):
 
 
 def test_gemm_rejects_bad_arguments(lrs, orc, ctx):
-    w = lrs.Weight.upload(ctx, 8, orc.gen_weight(8, 1, 4, 64), 64, 4)  # Q8_0
+    # n_in must be a multiple of 256 (one K-step of the tile), for Q8_0 too
+    w = lrs.Weight.upload(ctx, Q8_0, orc.gen_weight(Q8_0, 1, 4, 64), 64, 4)
     with pytest.raises(lrs.ModelError):
         w.gemm(np.zeros((2, 64), np.float32))
     w4 = lrs.Weight.upload(ctx, Q4_K, orc.gen_weight(Q4_K, 1, 4, 256), 256, 4)

@@ -158,21 +158,26 @@ def test_decode_batch_matches_token_loop_and_reset_is_deterministic(lrs, orc, ct
 # logits track the oracle to ~1e-5 and a 1e-3 miss would be a real defect.
 PREFILL_CASES = [
     # crosses the 512-token block boundary
-    ("tiny-q4km-600", dict(modelgen.TINY, ctx=640), 600, 21),
-    ("gqa5-q4km-150", modelgen.GQA5, 150, 21),
-    ("gqa5-q4km-40", modelgen.GQA5, 40, 23),
+    ("tiny-q4km-600", dict(modelgen.TINY, ctx=640), None, 600, 21),
+    ("gqa5-q4km-150", modelgen.GQA5, None, 150, 21),
+    ("gqa5-q4km-40", modelgen.GQA5, None, 40, 23),
+    # every GEMM weight type: Q5_K, Q8_0, and Q8_0 beside K-quants
+    ("gqa5-q5km-150", modelgen.GQA5, modelgen.Q5_K_M, 150, 21),
+    ("gqa5-q8_0-150", modelgen.GQA5, modelgen.ALL_Q8_0, 150, 21),
+    ("tiny-mixed-q8_0-600", dict(modelgen.TINY, ctx=640), MIXED_Q8_0, 600, 22),
 ]
 
 
-@pytest.mark.parametrize("name,cfg,n,seed", PREFILL_CASES, ids=[c[0] for c in PREFILL_CASES])
-def test_batched_prompt_matches_oracle(lrs, orc, ctx, name, cfg, n, seed):
+@pytest.mark.parametrize("name,cfg,mix,n,seed", PREFILL_CASES,
+                         ids=[c[0] for c in PREFILL_CASES])
+def test_batched_prompt_matches_oracle(lrs, orc, ctx, name, cfg, mix, n, seed):
     """The batched prompt (GEMM + batched RMSNorm / RoPE / causal attention)
     against Model::forward over the same prompt, then decode steps that read
     the cache it wrote, then 32 greedy steps after a batched prompt."""
-    w = modelgen.host_model(orc, cfg, seed=seed, mode=0, d_lo=1e-3, d_hi=1e-2)
+    w = modelgen.host_model(orc, cfg, seed=seed, mix=mix, mode=0, d_lo=1e-3, d_hi=1e-2)
     gm = modelgen.gpu_model(lrs, ctx, cfg, w)
     assert gm.batch_size() == 512
-    om = orc.Model(cfg, w, kv_f16=True, threads=8)
+    om = orc.Model(cfg, w, kv_f16=True, threads=8, q8_actq=False)
     prompt = np.random.default_rng(9).integers(0, cfg["vocab"], n).tolist()
     g = gm.decode_batch(prompt, 0)
     o = om.forward(prompt)
@@ -189,14 +194,14 @@ def test_batched_prompt_matches_oracle(lrs, orc, ctx, name, cfg, n, seed):
     k = n // 3
     gm.decode_batch(prompt[:k], 0)
     g2 = gm.decode_batch(prompt[k:], k)
-    om2 = orc.Model(cfg, w, kv_f16=True, threads=8)
+    om2 = orc.Model(cfg, w, kv_f16=True, threads=8, q8_actq=False)
     o2 = om2.forward(prompt)
     assert rel_l2(g2, o2) < LOGIT_TOL
     assert int(np.argmax(g2)) == int(np.argmax(o2))
     # greedy generation after a batched prompt
     gm.reset()
     short = prompt[:20]
-    om3 = orc.Model(cfg, w, kv_f16=True, threads=8)
+    om3 = orc.Model(cfg, w, kv_f16=True, threads=8, q8_actq=False)
     assert gm.generate_greedy(short, 32).tolist() == modelgen.oracle_greedy(om3, short, 32)
 
 
@@ -226,15 +231,22 @@ def test_prefill_in_blocks_matches_token_by_token(lrs, orc, ctx):
 
 
 def test_token_path_models_report_batch_size_one(lrs, orc, ctx):
+    """With the Q8_0 input rounding on, Q8_0 weights need their int8 products:
+    the model reports batch_size() 1 and decode_batch runs the token loop
+    (bit-identical to it); switched off, the GEMM path comes back."""
     cfg = modelgen.TINY
     w = modelgen.host_model(orc, cfg, seed=15, mix=modelgen.ALL_Q8_0)
     gm = modelgen.gpu_model(lrs, ctx, cfg, w)
+    assert gm.batch_size() == 512
+    gm.set_q8_rounding(True)
     assert gm.batch_size() == 1
     toks = [1, 2, 3, 4]
     for p, t in enumerate(toks):
         last = gm.decode(t, p)
     gm.reset()
     assert np.array_equal(gm.decode_batch(toks, 0), last)
+    gm.set_q8_rounding(False)
+    assert gm.batch_size() == 512
 
 
 def test_errors(lrs, orc, ctx):
