@@ -63,7 +63,7 @@ OP_NAMES = {"qkv": "fused RMSNorm + q/k/v matvec + bias + RoPE + f16 KV append",
             "o": "attn_output matvec + residual add",
             "gateup": "fused RMSNorm + ffn_gate/ffn_up Q4_K matvec + SwiGLU",
             "down": "ffn_down Q6_K matvec + residual add",
-            "ffn": "the layer's FFN as the token plan runs it (gate/up + down, split on two streams)",
+            "ffn": "the layer's FFN as the token plan runs it (gate/up + SwiGLU launch, then down + residual)",
             "head": "final RMSNorm + output head Q6_K matvec"}
 PROMPT = 512
 
