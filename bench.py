@@ -14,9 +14,11 @@ Workloads:
           matrix-core matvec), 16 of them over 16 weight copies (285 MB, beyond
           the 256 MB MALL, so every weight byte comes from HBM) captured into
           one HIP graph and replayed.
-  layer   config 2: one Qwen2.5-14B-shaped layer matvec set, weights rotated
-          over 4 copies so every byte comes from HBM; a step is 7 matvecs
-          (one captured HIP graph per copy).
+  layer   config 2: one Qwen2.5-14B-shaped layer matvec set through the token
+          plan's fused launches (q/k/v in one launch, o, gate/up + SwiGLU,
+          down) of a 4-layer model of that shape, rotating over the layers so
+          every byte comes from HBM; also, labelled, the same 7 matvecs as
+          separate lrs_matvec_dev calls (one captured HIP graph per copy).
   hybrid  config 4: 27B-scale hybrid model (64 layers, gated full attention
           every 4th: 24 q / 4 kv x 256; 48 gated delta-net layers of 16 heads
           x 128x128 f32 state), random-init Q4_K_M; the 512-token prompt goes
@@ -36,7 +38,10 @@ Workloads:
 
 One JSON line (driver contract) with a roofline object for the dominant
 kernel, measured with HIP events on the model's stream, and the CPU oracle
-timed on a bounded sample of the same workload.
+(its -O3 -march=native timing build, compiled on the host that runs it)
+timed on a bounded sample of the same workload.  The default decode line
+also carries labelled lines for configs 1, 2, 4 and 5 under "configs"
+(--no-sub skips them).
 """
 from __future__ import annotations
 
@@ -110,7 +115,7 @@ def read_traffic(op):
     return int(mt.group(1)) if mt else None
 
 
-def bench_decode(lrs, ctx, steps, warmup):
+def bench_decode(lrs, ctx, steps, warmup, prefill_ms=()):
     from llama_rs_amd.model import synthetic_model
 
     cfg = cfg32()
@@ -158,10 +163,12 @@ def bench_decode(lrs, ctx, steps, warmup):
     for k, v in ops.items():
         log(f"[bench]   {k:7s} {v['us']:8.2f} us/launch {v['gbs']:7.0f} GB/s  "
             f"{v['per_token_us'] / 1e3:.3f} ms/token")
+    # config 5 through the same model: whole prompts of each length
+    prefill = {m_tok: time_prompts(m, ctx, cfg, m_tok, 2, 1) for m_tok in prefill_ms}
     m.close()
     return dict(cfg=cfg, ms_tok=ms_tok, ev_ms_tok=ev_ms / steps, tok_bytes=tok_bytes,
                 prefill_tok_s=(PROMPT - 1) / prefill_s,
-                kv_bytes=kv_bytes, w_bytes=m.bytes_per_token, ops=ops)
+                kv_bytes=kv_bytes, w_bytes=m.bytes_per_token, ops=ops, prefill=prefill)
 
 
 HY_OPS = ("dn_proj", "dn_step", "dn_out", "qkv", "qk_prep", "attn", "o", "gateup", "down",
@@ -226,15 +233,105 @@ def bench_hybrid(lrs, ctx, steps, warmup):
                 rec_bytes=rec_bytes, w_bytes=m.bytes_per_token, ops=ops, prefill_s=prefill_s)
 
 
+_TIMING = {}
+
+
+def cpu_oracle():
+    """The oracle module switched to its -O3 -march=native timing build,
+    compiled once per process on this host (the parity build stays as it is
+    on disk)."""
+    import tempfile
+
+    import oracle
+
+    if "path" not in _TIMING:
+        _TIMING["path"] = oracle.use_timing_build(tempfile.mkdtemp(prefix="lrs_oracle_"))
+    return oracle
+
+
+def host_info(threads):
+    """nproc, the threads this process may run on, the CPU model and the NUMA
+    layout of the host that times the CPU baseline."""
+    info = {"nproc": os.cpu_count(), "threads_used": threads,
+            "build": "gcc -O3 -march=native (the oracle sources, built on this host)"}
+    try:
+        info["affinity_cpus"] = len(os.sched_getaffinity(0))
+    except OSError:
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            info["cpu_model"] = next((ln.split(":", 1)[1].strip() for ln in f
+                                      if ln.startswith("model name")), None)
+    except OSError:
+        info["cpu_model"] = None
+    nodes, base = {}, "/sys/devices/system/node"
+    try:
+        for d in sorted(os.listdir(base)):
+            if d.startswith("node") and d[4:].isdigit():
+                with open(os.path.join(base, d, "cpulist")) as f:
+                    nodes[d] = f.read().strip()
+    except OSError:
+        pass
+    info["numa_nodes"] = nodes
+    return info
+
+
+def timed_rate(fn, secs):
+    """(calls, seconds per call) of fn over about `secs` seconds, after one
+    untimed call."""
+    fn()
+    k, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < secs:
+        fn()
+        k += 1
+    return k, (time.perf_counter() - t0) / k
+
+
+def cpu_baseline_layer(threads):
+    """Config 2 on the host: the oracle's 7 matvecs of the 14B layer set
+    (dequant + sequential f32 dot per row, rows in chunks of 32 over
+    `threads`), each weight its own seeded matrix."""
+    oracle = cpu_oracle()
+    ws = [(t, oracle.gen_weight(t, 100 + i, n_out, n_in), n_in, n_out)
+          for i, (t, n_in, n_out) in enumerate(CFG14_SET)]
+    xs = {n: oracle.gen_normal(7, n) for n in (5120, 13824)}
+    b = sum(gguf_bytes(t, n_in, n_out) + 4 * (n_in + n_out) for t, n_in, n_out in CFG14_SET)
+    k, t = timed_rate(lambda: [oracle.matvec(tt, w, n_in, n_out, xs[n_in], threads=threads)
+                               for tt, w, n_in, n_out in ws], 6.0)
+    return {"value": round(b / t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle dequant + f32 dot over the 7 matvecs of the set, {k} sets "
+                      f"({t * 1e3:.1f} ms each, {threads} threads)",
+            "host": host_info(threads)}
+
+
+def cpu_baseline_gemm(threads, m):
+    """Config 5 on the host: the oracle's batched matvec (8 columns per pass,
+    dequant + sequential f32 dot) for m tokens over 1/64 of the rows of each
+    FFN weight, scaled to the whole set."""
+    oracle = cpu_oracle()
+    shapes = [(Q4_K, 5120, 13824), (Q4_K, 5120, 13824), (Q6_K, 13824, 5120)]
+    part = [(t, oracle.gen_weight(t, 500 + i, n_out // 64, n_in), n_in, n_out // 64)
+            for i, (t, n_in, n_out) in enumerate(shapes)]
+    xs = {n: oracle.gen_normal(5, m * n).reshape(m, n) for n in (5120, 13824)}
+    k, t = timed_rate(lambda: [oracle.matvec(tt, w, n_in, n_out, xs[n_in], threads=threads)
+                               for tt, w, n_in, n_out in part], 6.0)
+    flop = sum(2.0 * m * n_in * n_out for _, n_in, n_out in shapes)
+    return {"value": round(flop / (64 * t) / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle batched matvec, {m} columns over 1/64 of the rows of gate/up/down, "
+                      f"{k} passes ({t * 1e3:.1f} ms each, {threads} threads); whole set = 64x",
+            "host": host_info(threads)}
+
+
 def cpu_baseline_hybrid(threads):
     """The oracle's hybrid forward on a bounded sample of config 4: one block of
     4 layers of the full shape (3 delta-net + 1 gated attention) timed over
     repeated tokens, plus 1/16 of the Q6_K output head's rows; scaled to one
     token = 16 blocks + the whole head."""
     import modelgen
-    import oracle
     from llama_rs_amd.model import QWEN35_27B
 
+    oracle = cpu_oracle()
     lc = dict(QWEN35_27B, n_layer=4, vocab=256, ctx=1024)
     w = modelgen.hybrid_host_model(oracle, lc, seed=3, mode=0, d_lo=1e-3, d_hi=1e-2)
     om = oracle.HybridModel(lc, w, kv_f16=True, threads=threads)
@@ -260,7 +357,7 @@ def cpu_baseline_hybrid(threads):
                       f"(3 delta-net + 1 gated attention) of the config-4 shape "
                       f"({t_block * 1e3:.1f} ms each) + {nh} matvecs over 1/16 of the Q6_K "
                       f"output head; per token = 16 blocks + 16x the head slice "
-                      f"= {s_tok:.2f} s"}
+                      f"= {s_tok:.2f} s", "host": host_info(threads)}
 
 
 def cpu_baseline_q8(threads):
@@ -269,30 +366,23 @@ def cpu_baseline_q8(threads):
     on the 4096x4096 Q8_0 matvec, and, as a second labelled row, the
     int8-activation path Model::forward takes for Q8_0 weights
     (matmul_q8_0_actq, ops.rs:704-724, 728-886; one thread, scalar)."""
-    import oracle
-
+    oracle = cpu_oracle()
     n = 4096
     w = oracle.gen_weight(Q8_0, 900, n, n)
     x = oracle.gen_normal(1, n)
     b = gguf_bytes(Q8_0, n, n) + 8 * n
-
-    def rate(fn, secs):
-        fn()
-        k, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < secs:
-            fn()
-            k += 1
-        return k, (time.perf_counter() - t0) / k
-
-    k1, t1 = rate(lambda: oracle.matvec(Q8_0, w, n, n, x, threads=threads), 4.0)
-    k2, t2 = rate(lambda: oracle.matvec_q8_0_actq(w, n, n, x), 4.0)
+    k1, t1 = timed_rate(lambda: oracle.matvec(Q8_0, w, n, n, x, threads=threads), 4.0)
+    k2, t2 = timed_rate(lambda: oracle.matvec_q8_0_actq(w, n, n, x), 4.0)
     return {"value": round(b / t1 / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"oracle dequant + f32 dot, {k1} matvecs of Q8_0 4096x4096 "
                       f"({t1 * 1e3:.2f} ms each, {threads} threads); second row: the "
                       f"int8-activation matmul_q8_0_actq restatement, {k2} matvecs "
-                      f"({t2 * 1e3:.2f} ms each, 1 thread)",
+                      f"({t2 * 1e3:.2f} ms each)",
             "int8_activation": {"value": round(b / t2 / 1e9, 2), "unit": "GB/s", "cores": 1,
-                                "kind": "port"}}
+                                "kind": "port",
+                                "note": "scalar single-thread restatement, not the reference's "
+                                        "rayon + AVX2 8-row kernels (ops.rs:766-880)"},
+            "host": host_info(threads)}
 
 
 def cpu_baseline_decode(threads):
@@ -302,8 +392,8 @@ def cpu_baseline_decode(threads):
     repeated tokens, plus 1/8 of the Q6_K output head's rows; scaled to one
     token = 64 layers + the whole head."""
     import modelgen
-    import oracle
 
+    oracle = cpu_oracle()
     lc = cfg32(1)
     lc.update(vocab=256, ctx=1024)
     w = modelgen.host_model(oracle, lc, seed=3, mode=0, d_lo=1e-3, d_hi=1e-2)
@@ -329,7 +419,7 @@ def cpu_baseline_decode(threads):
             "sample": f"oracle Model::forward restatement: {n} single-token passes through one "
                       f"32B-shape Q4_K_M layer ({t_layer * 1e3:.1f} ms each, positions 1..{n}) "
                       f"+ {nh} matvecs over 1/8 of the Q6_K output head; per token = 64 layers "
-                      f"+ 8x the head slice = {s_tok:.2f} s"}
+                      f"+ 8x the head slice = {s_tok:.2f} s", "host": host_info(threads)}
 
 
 class GraphOrDirect:
@@ -351,17 +441,36 @@ class GraphOrDirect:
             self.g.close()
 
 
+CFG14 = dict(n_layer=4, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_ff=13824,
+             vocab=256, rope_dim=128, ctx=1024, rms_eps=1e-6, freq_base=1e6)
+CFG14_SET = [(Q4_K, 5120, 5120), (Q4_K, 5120, 1024), (Q6_K, 5120, 1024), (Q4_K, 5120, 5120),
+             (Q4_K, 5120, 13824), (Q4_K, 5120, 13824), (Q6_K, 13824, 5120)]
+
+
 def bench_layer(lrs, ctx, steps, warmup):
-    cfg2 = [(Q4_K, 5120, 5120), (Q4_K, 5120, 1024), (Q6_K, 5120, 1024), (Q4_K, 5120, 5120),
-            (Q4_K, 5120, 13824), (Q4_K, 5120, 13824), (Q6_K, 13824, 5120)]
-    copies = 4  # 4 x 174.4 MB of distinct weights per rotation (> the 256 MB MALL)
+    """Config 2 through the token plan's fused launches: a 4-layer model of the
+    14B shape (4 x 174 MB of weights, beyond the 256 MB MALL); a step is one
+    layer's q/k/v, o, gate/up and down launches (lrs_model_profile
+    LRS_OP_MATVECS, rotating over the layers).  Also timed, as a labelled
+    second figure: the 7 matvecs as separate lrs_matvec_dev calls."""
+    from llama_rs_amd.model import synthetic_model
+
+    cfg = CFG14
+    m = synthetic_model(ctx, cfg, seed=2, mode=0, d_lo=1e-3, d_hi=1e-2)
+    m.decode_batch(np.arange(8, dtype=np.uint32), 0)  # a valid cache position
+    nl = cfg["n_layer"]
+    m.profile("matvecs", max(nl, warmup))
+    us, b = m.profile("matvecs", max(steps, nl))
+    op_us = {op: m.profile(op, 4 * nl)[0] for op in ("qkv", "o", "gateup", "down")}
+    m.close()
+    log(f"[bench] 14B layer matvec set through the fused launches: {us:.2f} us "
+        f"({b / us / 1e3:.0f} GB/s); " + ", ".join(f"{k} {v:.2f}" for k, v in op_us.items()))
+
+    copies = 4
     mats = [[lrs.Weight.generate(ctx, t, 100 * c + i, n_in, n_out)
-             for i, (t, n_in, n_out) in enumerate(cfg2)] for c in range(copies)]
-    set_bytes = sum(gguf_bytes(t, n_in, n_out) + 4 * (n_in + n_out) for t, n_in, n_out in cfg2)
+             for i, (t, n_in, n_out) in enumerate(CFG14_SET)] for c in range(copies)]
     xbuf, ybuf = ctx.alloc(4 * 13824), ctx.alloc(4 * 13824)
     xbuf.upload(np.random.default_rng(7).standard_normal(13824).astype(np.float32))
-
-    # one graph per copy: the 7 matvecs of the set (pack + matrix-core matvec each)
     mats[0][-1].matvec_dev(xbuf, ybuf)  # sizes the context scratch outside the capture
     ctx.sync()
     graphs = [GraphOrDirect(ctx, lambda c=c: [w.matvec_dev(xbuf, ybuf) for w in mats[c]])
@@ -372,10 +481,14 @@ def bench_layer(lrs, ctx, steps, warmup):
     ctx.timer_start()
     for s in range(steps):
         graphs[s % copies].launch()
-    ms = ctx.timer_stop() / steps
+    us_sep = ctx.timer_stop() * 1e3 / steps
     for g in graphs:
         g.close()
-    return dict(ms=ms, bytes=set_bytes, gbs=set_bytes / (ms * 1e-3) / 1e9)
+    for ws in mats:
+        for w in ws:
+            w.free()
+    log(f"[bench] the same set as 7 separate matvecs: {us_sep:.2f} us")
+    return dict(us=us, bytes=b, gbs=b / us / 1e3, op_us=op_us, us_separate=us_sep, layers=nl)
 
 
 def bench_q8(lrs, ctx, steps, warmup):
@@ -439,15 +552,11 @@ def bench_gemm(lrs, ctx, steps, warmup, m, precision):
     return dict(per=per, us=tot_us, tflops=tot_flop / tot_us / 1e6, flop=tot_flop)
 
 
-def bench_prefill(lrs, ctx, steps, warmup, m_tok):
+def time_prompts(m, ctx, cfg, m_tok, steps, warmup):
     """Config 5 through the full 32B-shaped model: one step = an m_tok-token
     prompt at positions 0.. (decode_batch: logits of the last token)."""
-    from llama_rs_amd.model import synthetic_model
-
-    cfg = cfg32()
     if not 1 <= m_tok < cfg["ctx"]:
         raise SystemExit(f"--m must be within 1..{cfg['ctx'] - 1}")
-    m = synthetic_model(ctx, cfg, seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
     rng = np.random.default_rng(4321)
     prompt = rng.integers(0, cfg["vocab"], m_tok).astype(np.uint32)
     for _ in range(max(1, warmup)):
@@ -466,17 +575,29 @@ def bench_prefill(lrs, ctx, steps, warmup, m_tok):
     s_step = wall / steps
     log(f"[bench] prompt {m_tok} tokens: {s_step * 1e3:.1f} ms per prompt (events "
         f"{ev_ms / steps:.1f} ms) -> {m_tok / s_step:.0f} tok/s, batch_size {m.batch_size()}")
-    m.close()
-    return dict(s=s_step, tok_s=m_tok / s_step, flop=per_tok * m_tok,
+    return dict(s=s_step, tok_s=m_tok / s_step, flop=per_tok * m_tok, steps=steps,
                 tflops=per_tok * m_tok / s_step / 1e12)
+
+
+def bench_prefill(lrs, ctx, steps, warmup, m_tok):
+    from llama_rs_amd.model import synthetic_model
+
+    cfg = cfg32()
+    m = synthetic_model(ctx, cfg, seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
+    r = time_prompts(m, ctx, cfg, m_tok, steps, warmup)
+    m.close()
+    return r
 
 
 def run_pmc(lrs, ctx):
     """Kernels for the counter passes: the copy calibration (an F32 tensor's
-    identity dequant: 4 B read + 4 B written per element, grid-stride), the
-    dominant decode ops rotating over 4 layers of the 32B shape, and the same
-    on a 4-layer block of the config-4 hybrid shape."""
-    from llama_rs_amd.model import synthetic_model
+    identity dequant: 4 B read + 4 B written per element, grid-stride), then
+    phases separated by a marker launch (the same identity dequant on 4096
+    elements): the decode ops rotating over 4 layers of the 32B shape; the
+    same on a 4-layer block of the config-4 hybrid shape; the config-1 Q8_0
+    matvec; the config-2 layer ops on 4 layers of the 14B shape; the config-5
+    GEMMs at m = 512."""
+    from llama_rs_amd.model import QWEN35_27B, synthetic_hybrid_model, synthetic_model
 
     n = 128 << 20  # 512 MiB read + 512 MiB written
     src = lrs.Weight.upload(ctx, F32, np.zeros(n, np.float32), n, 1)
@@ -485,6 +606,14 @@ def run_pmc(lrs, ctx):
         src.dequant_dev(dst)
     ctx.sync()
     log(f"[pmc] copy calibration: {3} launches of {4 * n} B read + {4 * n} B written")
+    msrc = lrs.Weight.upload(ctx, F32, np.zeros(4096, np.float32), 4096, 1)
+
+    def marker(name):
+        msrc.dequant_dev(dst)
+        ctx.sync()
+        log(f"[pmc] phase {name}")
+
+    marker("dense32")
     m = synthetic_model(ctx, cfg32(4), seed=1, mode=0, d_lo=1e-3, d_hi=1e-2)
     # a 512-token cache, so attention reads the decode-time length
     m.decode_batch(np.arange(PROMPT, dtype=np.uint32) % cfg32(4)["vocab"], 0)
@@ -492,10 +621,9 @@ def run_pmc(lrs, ctx):
         us, b = m.profile(op, 8 if op != "head" else 2)
         log(f"[pmc] {op}: {us:.2f} us/launch, {b} algorithmic bytes")
     m.close()
+    marker("hybrid27")
     # config 4: the same ops on a 4-layer block of the hybrid shape (3 delta-net
     # layers + 1 gated attention layer)
-    from llama_rs_amd.model import QWEN35_27B, synthetic_hybrid_model
-
     hm = synthetic_hybrid_model(ctx, dict(QWEN35_27B, n_layer=4), seed=1, mode=0, d_lo=1e-3,
                                 d_hi=1e-2)
     hm.decode_batch(np.arange(8, dtype=np.uint32), 0)
@@ -503,6 +631,195 @@ def run_pmc(lrs, ctx):
         us, b = hm.profile(op, 6 if op != "head" else 2)
         log(f"[pmc] hybrid {op}: {us:.2f} us/launch, {b} algorithmic bytes")
     hm.close()
+    marker("q8")
+    # config 1: the Q8_0 4096x4096 matvec (activation pack + matvec), 4 copies
+    ws = [lrs.Weight.generate(ctx, Q8_0, 900 + c, 4096, 4096, mode=0, d_lo=1e-3, d_hi=1e-2)
+          for c in range(4)]
+    xb, yb = ctx.alloc(4 * 4096), ctx.alloc(4 * 4096)
+    xb.upload(np.random.default_rng(1234).standard_normal(4096).astype(np.float32))
+    for i in range(8):
+        ws[i % 4].matvec_dev(xb, yb)
+    ctx.sync()
+    log(f"[pmc] q8 matvec: {gguf_bytes(Q8_0, 4096, 4096) + 8 * 4096} algorithmic bytes")
+    for w in ws:
+        w.free()
+    marker("layer14")
+    lm = synthetic_model(ctx, CFG14, seed=2, mode=0, d_lo=1e-3, d_hi=1e-2)
+    lm.decode_batch(np.arange(8, dtype=np.uint32), 0)
+    for op in ("qkv", "o", "gateup", "down"):
+        us, b = lm.profile(op, 8)
+        log(f"[pmc] l14 {op}: {us:.2f} us/launch, {b} algorithmic bytes")
+    lm.close()
+    marker("gemm")
+    # config 5: the FFN GEMMs at m = 512 (bf16 operands)
+    mm = 512
+    gw = [lrs.Weight.generate(ctx, t, 500 + i, n_in, n_out)
+          for i, (t, n_in, n_out) in enumerate([(Q4_K, 5120, 13824), (Q6_K, 13824, 5120)])]
+    ab, yb2 = ctx.alloc(4 * mm * 13824), ctx.alloc(4 * mm * 13824)
+    ab.upload(np.random.default_rng(5).standard_normal(mm * 13824).astype(np.float32))
+    for w in gw:
+        for _ in range(2):
+            w.gemm_dev(ab, yb2, mm, 1)
+    ctx.sync()
+    log("[pmc] gemm: Q4_K 13824x5120 and Q6_K 5120x13824 at m = 512, 2 launches each")
+    marker("end")
+
+
+DTYPE = "f32 in/out; activations as 22-bit block fixed point (3 int8 digits) on int8 MFMA"
+
+
+def common(a, value, unit, ms, higher=True):
+    return {"value": value, "unit": unit, "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+            "ms_per_step": ms, "higher_is_better": higher, "scaling": "weak",
+            "vs_baseline": None}
+
+
+def line_decode(lrs, ctx, a, threads, prefill_ms=()):
+    r = bench_decode(lrs, ctx, a.steps, a.warmup, prefill_ms)
+    ops = r["ops"]
+    dom = max(ops, key=lambda k: ops[k]["per_token_us"])
+    d = ops[dom]
+    cpu = None if a.no_cpu else cpu_baseline_decode(threads)
+    eff_gbs = r["tok_bytes"] / (r["ms_tok"] * 1e-3) / 1e9
+    cfg = r["cfg"]
+    out = {"metric": METRIC, **common(a, round(1e3 / r["ms_tok"], 2), "tok/s", round(r["ms_tok"], 4)),
+           "dtype": DTYPE,
+           "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU, BASELINE "
+                   "distributions; prompt token ids uniform random, seed 1234)",
+           "config": {"workload": "config3-qwen2.5-32b-shape-q4_k_m-greedy-decode",
+                      "prompt": PROMPT, "decode_tokens": a.steps, "n_layer": cfg["n_layer"],
+                      "n_embd": cfg["n_embd"], "n_head": cfg["n_head"],
+                      "n_head_kv": cfg["n_head_kv"], "n_ff": cfg["n_ff"], "vocab": cfg["vocab"],
+                      "kv": "f16", "ctx": cfg["ctx"],
+                      "weights": "q,k,o,gate,up,token_embd Q4_K; v,down,output Q6_K",
+                      "bytes_per_token": int(r["tok_bytes"]),
+                      "token_roofline_frac": round(eff_gbs / HBM_PEAK_GBS, 4),
+                      "effective_gbs": round(eff_gbs, 1),
+                      "prompt_tok_s": round(r["prefill_tok_s"], 1),
+                      "op_us": {k: round(v["us"], 2) for k, v in ops.items()}},
+           "roofline": {"bound": "hbm", "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
+                        "traffic": read_traffic(dom), "kernel": OP_NAMES[dom], "op": dom,
+                        "kernel_us": round(d["us"], 3), "bytes_per_launch": d["bytes"]},
+           "cpu_baseline": cpu}
+    return out, r
+
+
+def line_hybrid(lrs, ctx, a, threads):
+    r = bench_hybrid(lrs, ctx, a.steps, a.warmup)
+    ops = r["ops"]
+    dom = max(ops, key=lambda k: ops[k]["per_token_us"])
+    d = ops[dom]
+    cpu = None if a.no_cpu else cpu_baseline_hybrid(threads)
+    cfg = r["cfg"]
+    eff_gbs = r["tok_bytes"] / (r["ms_tok"] * 1e-3) / 1e9
+    return {"metric": "batch-1 decode tok/s, hybrid attention + gated delta-net 27B-scale "
+                      "Q4_K_M (config 4)",
+            **common(a, round(1e3 / r["ms_tok"], 2), "tok/s", round(r["ms_tok"], 4)),
+            "dtype": DTYPE,
+            "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU, "
+                    "BASELINE distributions; f32 delta-net vectors seeded; prompt ids "
+                    "uniform random, seed 1234)",
+            "config": {"workload": "config4-hybrid-27b-scale-q4_k_m-greedy-decode",
+                       "prompt": PROMPT, "decode_tokens": a.steps,
+                       **{k: cfg[k] for k in ("n_layer", "n_embd", "n_head", "n_head_kv",
+                                              "head_dim", "n_ff", "vocab",
+                                              "full_attn_interval", "dn_k_heads",
+                                              "dn_v_heads", "dn_state", "dn_conv",
+                                              "rope_dim")},
+                       "weights": "q,k,o,gate,up,ssm_qkv,ssm_gate,ssm_out,token_embd Q4_K; "
+                                  "v,down,output Q6_K; alpha/beta/conv/norms f32",
+                       "bytes_per_token": int(r["tok_bytes"]),
+                       "token_roofline_frac": round(eff_gbs / HBM_PEAK_GBS, 4),
+                       "effective_gbs": round(eff_gbs, 1),
+                       "prompt_tok_s": round((PROMPT - 1) / r["prefill_s"], 1),
+                       "op_us": {k: round(v["us"], 2) for k, v in ops.items()}},
+            "roofline": {"bound": "hbm", "achieved": round(d["gbs"], 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": read_traffic("hybrid_" + dom),
+                         "kernel": OP_NAMES[dom], "op": dom, "kernel_us": round(d["us"], 3),
+                         "bytes_per_launch": d["bytes"]},
+            "cpu_baseline": cpu}
+
+
+def line_q8(lrs, ctx, a, threads):
+    r = bench_q8(lrs, ctx, a.steps, a.warmup)
+    return {"metric": "quant matvec HBM GB/s, single Q8_0 4096x4096 matvec (batch-1)",
+            **common(a, round(r["gbs"], 2), "GB/s", round(r["us"] / 1e3, 6)),
+            "dtype": DTYPE,
+            "data": "synthetic (seeded Q8_0 blocks, BASELINE distributions; x ~ N(0,1))",
+            "config": {"workload": "config1-q8_0-matvec-4096", "batch": 1,
+                       "copies_rotated": 16, "bytes_per_matvec": r["bytes"],
+                       "us_per_matvec": round(r["us"], 3),
+                       "us_per_matvec_int8_activation": round(r["us_actq"], 3)},
+            "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": read_traffic("q8_matvec"),
+                         "kernel": "lrs_matvec_dev: activation pack + Q8_0 matrix-core matvec",
+                         "op": "q8_matvec", "kernel_us": round(r["us"], 3),
+                         "bytes_per_launch": r["bytes"]},
+            "cpu_baseline": None if a.no_cpu else cpu_baseline_q8(threads)}
+
+
+def line_layer(lrs, ctx, a, threads):
+    r = bench_layer(lrs, ctx, a.steps, a.warmup)
+    tr = [read_traffic("l14_" + op) for op in ("qkv", "o", "gateup", "down")]
+    return {"metric": "quant matvec HBM GB/s, Qwen2.5-14B layer matvec set (batch-1 decode)",
+            **common(a, round(r["gbs"], 2), "GB/s", round(r["us"] / 1e3, 5)),
+            "dtype": DTYPE,
+            "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU, BASELINE "
+                    "distributions)",
+            "config": {"workload": "config2-qwen2.5-14b-layer-matvec-set", "batch": 1,
+                       "layers_rotated": r["layers"], "bytes_per_set": r["bytes"],
+                       "us_per_set": round(r["us"], 3),
+                       "op_us": {k: round(v, 2) for k, v in r["op_us"].items()},
+                       "us_per_set_as_7_separate_matvecs": round(r["us_separate"], 3)},
+            "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": sum(tr) if all(t is not None for t in tr) else None,
+                         "kernel": "the layer's matvec launches of the token plan: q/k/v (one "
+                                   "launch), o, gate/up + SwiGLU, down",
+                         "op": "matvecs", "kernel_us": round(r["us"], 3),
+                         "bytes_per_launch": r["bytes"]},
+            "cpu_baseline": None if a.no_cpu else cpu_baseline_layer(threads)}
+
+
+def line_gemm(lrs, ctx, a, threads, m, precision):
+    r = bench_gemm(lrs, ctx, a.steps, a.warmup, m, precision)
+    for k, v in r["per"].items():
+        log(f"[bench]   {k:9s} {v['us']:9.1f} us {v['tflops']:8.1f} TFLOP/s")
+    peak = 2500.0  # MI355X dense bf16 MFMA
+    return {"metric": "prefill dequant-GEMM TFLOP/s (config 5 FFN set, MFMA)",
+            **common(a, round(r["tflops"], 2), "TFLOP/s", round(r["us"] / 1e3, 5)),
+            "dtype": "bf16 operands, f32 accumulate" if precision == 1 else
+                     "bf16 hi/lo split operands (3 products), f32 accumulate",
+            "data": "synthetic (seeded GGUF blocks, x ~ N(0,1))",
+            "config": {"workload": "config5-prefill-gemm-ffn", "m": m,
+                       "weights": "gate/up Q4_K 13824x5120, down Q6_K 5120x13824",
+                       "flop_per_step": r["flop"],
+                       "op_us": {k: round(v["us"], 2) for k, v in r["per"].items()}},
+            "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": peak,
+                         "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
+                         "traffic": read_traffic("gemm_set") if (m, precision) == (512, 1)
+                         else None},
+            "cpu_baseline": None if a.no_cpu else cpu_baseline_gemm(threads, m)}
+
+
+def prefill_line(a, m_tok, r):
+    peak = 2500.0  # MI355X dense bf16 MFMA
+    return {"metric": "prefill tok/s through the 32B-shaped Q4_K_M model (config 5)",
+            **common(a, round(r["tok_s"], 1), "tok/s", round(r["s"] * 1e3, 3)),
+            "dtype": "bf16 hi/lo split operands (3 products), f32 accumulate",
+            "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU; "
+                    "prompt ids uniform random, seed 4321)",
+            "config": {"workload": "config5-prefill-32b-model", "m": m_tok,
+                       "block": 512, "matmul_flop_per_prompt": r["flop"]},
+            "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": peak,
+                         "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
+                         "traffic": None, "mfma_work_per_flop": 3}}
 
 
 def main():
@@ -516,7 +833,9 @@ def main():
                     help="gemm / prefill: prompt tokens (config 5: 128/512/2048)")
     ap.add_argument("--precision", type=int, default=1, choices=[1, 3],
                     help="gemm: 1 = bf16 operands, 3 = bf16 hi/lo split")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-sub", action="store_true",
+                    help="decode: skip the labelled lines of configs 1, 2, 4 and 5")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {a.gpus}): the decode path keeps the "
@@ -530,162 +849,39 @@ def main():
     lrs = load_product()
     ctx = lrs.Context()
     log(f"[bench] workload={a.workload} steps={a.steps} warmup={a.warmup}")
+    threads = min(16, os.cpu_count() or 1)
     if a.workload == "pmc":
         run_pmc(lrs, ctx)
-        ctx.close()
-        return
-    threads = min(16, os.cpu_count() or 1)
-    if a.workload == "gemm":
-        r = bench_gemm(lrs, ctx, a.steps, a.warmup, a.m, a.precision)
-        for k, v in r["per"].items():
-            log(f"[bench]   {k:9s} {v['us']:9.1f} us {v['tflops']:8.1f} TFLOP/s")
-        peak = 2500.0  # MI355X dense bf16 MFMA
-        out = {"metric": "prefill dequant-GEMM TFLOP/s (config 5 FFN set, MFMA)",
-               "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1,
-               "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(r["us"] / 1e3, 5),
-               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-               "dtype": "bf16" if a.precision == 1 else "bf16x3",
-               "data": "synthetic (seeded GGUF blocks, x ~ N(0,1))",
-               "config": {"workload": "config5-prefill-gemm-ffn", "m": a.m,
-                          "weights": "gate/up Q4_K 13824x5120, down Q6_K 5120x13824",
-                          "flop_per_step": r["flop"]},
-               "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": peak,
-                            "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
-                            "traffic": None}}
-        print(json.dumps(out), flush=True)
-        ctx.close()
-        return
-    if a.workload == "prefill":
+    elif a.workload == "gemm":
+        print(json.dumps(line_gemm(lrs, ctx, a, threads, a.m, a.precision)), flush=True)
+    elif a.workload == "prefill":
         r = bench_prefill(lrs, ctx, a.steps, a.warmup, a.m)
-        peak = 2500.0  # MI355X dense bf16 MFMA
-        out = {"metric": "prefill tok/s through the 32B-shaped Q4_K_M model (config 5)",
-               "value": round(r["tok_s"], 1), "unit": "tok/s", "n_gpus": 1,
-               "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(r["s"] * 1e3, 3),
-               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-               "dtype": "bf16x3",
-               "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU; "
-                       "prompt ids uniform random, seed 4321)",
-               "config": {"workload": "config5-prefill-32b-model", "m": a.m,
-                          "block": 512, "matmul_flop_per_prompt": r["flop"]},
-               "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 1), "peak": peak,
-                            "unit": "TFLOP/s", "frac": round(r["tflops"] / peak, 4),
-                            "traffic": None, "mfma_work_per_flop": 3}}
+        print(json.dumps(prefill_line(a, a.m, r)), flush=True)
+    elif a.workload == "q8":
+        print(json.dumps(line_q8(lrs, ctx, a, threads)), flush=True)
+    elif a.workload == "layer":
+        print(json.dumps(line_layer(lrs, ctx, a, threads)), flush=True)
+    elif a.workload == "hybrid":
+        print(json.dumps(line_hybrid(lrs, ctx, a, threads)), flush=True)
+    else:
+        sub = not a.no_sub
+        out, r = line_decode(lrs, ctx, a, threads, prefill_ms=(128, 512, 2048) if sub else ())
+        if sub:
+            # the other BASELINE configs, each with its own roofline and CPU baseline
+            sa = argparse.Namespace(**vars(a))
+            sa.steps, sa.warmup = min(a.steps, 64), min(a.warmup, 8)
+            out["configs"] = {
+                "config1": line_q8(lrs, ctx, sa, threads),
+                "config2": line_layer(lrs, ctx, sa, threads),
+                "config4": line_hybrid(lrs, ctx, a, threads),
+                "config5_gemm": line_gemm(lrs, ctx, argparse.Namespace(**dict(
+                    vars(a), steps=10, warmup=2)), threads, 512, 1),
+                "config5_prefill": {str(m): prefill_line(argparse.Namespace(**dict(
+                    vars(a), steps=p["steps"], warmup=1)), m, p)
+                    for m, p in r["prefill"].items()},
+            }
         print(json.dumps(out), flush=True)
-        ctx.close()
-        return
-    if a.workload == "q8":
-        r = bench_q8(lrs, ctx, a.steps, a.warmup)
-        out = {"metric": "quant matvec HBM GB/s, single Q8_0 4096x4096 matvec (batch-1)",
-               "value": round(r["gbs"], 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
-               "warmup": a.warmup, "ms_per_step": round(r["us"] / 1e3, 6),
-               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-               "data": "synthetic (seeded Q8_0 blocks, BASELINE distributions; x ~ N(0,1))",
-               "config": {"workload": "config1-q8_0-matvec-4096", "batch": 1,
-                          "copies_rotated": 16, "bytes_per_matvec": r["bytes"],
-                          "us_per_matvec": round(r["us"], 3),
-                          "us_per_matvec_int8_activation": round(r["us_actq"], 3)},
-               "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1),
-                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "traffic": None}}
-        ctx.close()
-        if not a.no_cpu:
-            out["cpu_baseline"] = cpu_baseline_q8(threads)
-        print(json.dumps(out), flush=True)
-        return
-    if a.workload == "layer":
-        r = bench_layer(lrs, ctx, a.steps, a.warmup)
-        out = {"metric": "quant matvec HBM GB/s, Qwen2.5-14B layer matvec set (batch-1 decode)",
-               "value": round(r["gbs"], 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
-               "warmup": a.warmup, "ms_per_step": round(r["ms"], 5), "higher_is_better": True,
-               "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-               "data": "synthetic (seeded GGUF blocks, BASELINE distributions)",
-               "config": {"workload": "config2-qwen2.5-14b-layer-matvec-set", "batch": 1,
-                          "copies_rotated": 4}}
-        print(json.dumps(out), flush=True)
-        ctx.close()
-        return
-
-    if a.workload == "hybrid":
-        r = bench_hybrid(lrs, ctx, a.steps, a.warmup)
-        ops = r["ops"]
-        dom = max(ops, key=lambda k: ops[k]["per_token_us"])
-        d = ops[dom]
-        ctx.close()
-        cpu = None if a.no_cpu else cpu_baseline_hybrid(threads)
-        cfg = r["cfg"]
-        eff_gbs = r["tok_bytes"] / (r["ms_tok"] * 1e-3) / 1e9
-        out = {"metric": "batch-1 decode tok/s, hybrid attention + gated delta-net 27B-scale "
-                         "Q4_K_M (config 4)",
-               "value": round(1e3 / r["ms_tok"], 2), "unit": "tok/s", "n_gpus": 1,
-               "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(r["ms_tok"], 4),
-               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-               "dtype": "f32",
-               "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU, "
-                       "BASELINE distributions; f32 delta-net vectors seeded; prompt ids "
-                       "uniform random, seed 1234)",
-               "config": {"workload": "config4-hybrid-27b-scale-q4_k_m-greedy-decode",
-                          "prompt": PROMPT, "decode_tokens": a.steps,
-                          **{k: cfg[k] for k in ("n_layer", "n_embd", "n_head", "n_head_kv",
-                                                 "head_dim", "n_ff", "vocab",
-                                                 "full_attn_interval", "dn_k_heads",
-                                                 "dn_v_heads", "dn_state", "dn_conv",
-                                                 "rope_dim")},
-                          "weights": "q,k,o,gate,up,ssm_qkv,ssm_gate,ssm_out,token_embd Q4_K; "
-                                     "v,down,output Q6_K; alpha/beta/conv/norms f32",
-                          "bytes_per_token": int(r["tok_bytes"]),
-                          "token_roofline_frac": round(eff_gbs / HBM_PEAK_GBS, 4),
-                          "effective_gbs": round(eff_gbs, 1),
-                          "prompt_tok_s": round((PROMPT - 1) / r["prefill_s"], 1)},
-               "roofline": {"bound": "hbm", "achieved": round(d["gbs"], 1),
-                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
-                            "traffic": read_traffic("hybrid_" + dom),
-                            "kernel": OP_NAMES[dom], "op": dom, "kernel_us": round(d["us"], 3),
-                            "bytes_per_launch": d["bytes"]},
-               "cpu_baseline": cpu}
-        print(json.dumps(out), flush=True)
-        return
-
-    r = bench_decode(lrs, ctx, a.steps, a.warmup)
-    ops = r["ops"]
-    dom = max(ops, key=lambda k: ops[k]["per_token_us"])
-    d = ops[dom]
     ctx.close()
-    cpu = None if a.no_cpu else cpu_baseline_decode(threads)
-    tok_s = 1e3 / r["ms_tok"]
-    eff_gbs = r["tok_bytes"] / (r["ms_tok"] * 1e-3) / 1e9
-    cfg = r["cfg"]
-    out = {
-        "metric": METRIC,
-        "value": round(tok_s, 2),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
-        "ms_per_step": round(r["ms_tok"], 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (random-init Q4_K_M GGUF blocks generated on the GPU, BASELINE "
-                "distributions; prompt token ids uniform random, seed 1234)",
-        "config": {"workload": "config3-qwen2.5-32b-shape-q4_k_m-greedy-decode",
-                   "prompt": PROMPT, "decode_tokens": a.steps, "n_layer": cfg["n_layer"],
-                   "n_embd": cfg["n_embd"], "n_head": cfg["n_head"],
-                   "n_head_kv": cfg["n_head_kv"], "n_ff": cfg["n_ff"], "vocab": cfg["vocab"],
-                   "kv": "f16", "ctx": cfg["ctx"],
-                   "weights": "q,k,o,gate,up,token_embd Q4_K; v,down,output Q6_K",
-                   "bytes_per_token": int(r["tok_bytes"]),
-                   "token_roofline_frac": round(eff_gbs / HBM_PEAK_GBS, 4),
-                   "effective_gbs": round(eff_gbs, 1),
-                   "prompt_tok_s": round(r["prefill_tok_s"], 1)},
-        "roofline": {"bound": "hbm", "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(dom), "kernel": OP_NAMES[dom], "op": dom,
-                     "kernel_us": round(d["us"], 3), "bytes_per_launch": d["bytes"]},
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

@@ -326,6 +326,10 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
 #define LRS_OP_QK_PREP 9u
 /* the whole FFN of a layer: gate/up + SwiGLU, then down + residual */
 #define LRS_OP_FFN 10u
+/* dense models: every matvec of a layer as the token plan launches them
+ * (q/k/v, o, gate/up, down with their fused norms and epilogues), without
+ * the attention between q/k/v and o */
+#define LRS_OP_MATVECS 11u
 int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, size_t *bytes);
 /* GGUF bytes of every weight matrix one decoded token streams. */
 size_t lrs_model_bytes_per_token(const lrs_model *m);

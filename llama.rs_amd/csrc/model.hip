@@ -1253,7 +1253,8 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
 int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, size_t *bytes) {
     if (!m || !avg_us || iters == 0) return fail(LRS_E_ARG, "null argument");
     const lrs_config &c = m->cfg;
-    if (op > LRS_OP_FFN) return fail(LRS_E_ARG, "unknown op");
+    if (op > LRS_OP_MATVECS) return fail(LRS_E_ARG, "unknown op");
+    if (op == LRS_OP_MATVECS && m->hybrid) return fail(LRS_E_ARG, "op needs a dense model");
     const bool dn_op = op == LRS_OP_DN_PROJ || op == LRS_OP_DN_STEP || op == LRS_OP_DN_OUT;
     const bool attn_op = op == LRS_OP_QKV || op == LRS_OP_ATTN || op == LRS_OP_O ||
                          op == LRS_OP_QK_PREP;
@@ -1301,6 +1302,13 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
         case LRS_OP_GATEUP: b = wbytes(D.gate) + wbytes(D.up) + 2 * E4 + (size_t)c.n_ff * 4; break;
         case LRS_OP_DOWN: b = wbytes(D.down) + (size_t)c.n_ff * 4 + 2 * E4; break;
         case LRS_OP_FFN: b = wbytes(D.gate) + wbytes(D.up) + wbytes(D.down) + 3 * E4; break;
+        case LRS_OP_MATVECS:
+            // q/k/v (norm input + residual for the RMS sum, q out, K/V rows
+            // appended), o (input, residual read + written), the FFN
+            b = wbytes(D.q) + wbytes(D.k) + wbytes(D.v) + 2 * E4 + qd4 + (size_t)kvd * 2 * 2 +
+                (D.bq ? qd4 + (size_t)kvd * 8 : 0) + wbytes(D.o) + qd4 + 2 * E4 + wbytes(D.gate) +
+                wbytes(D.up) + wbytes(D.down) + 3 * E4;
+            break;
         }
     } else {
         b = wbytes(m->output) + 2 * E4 + (size_t)c.vocab * 4;
@@ -1319,6 +1327,11 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
         case LRS_OP_GATEUP: return op_gateup(m, l);
         case LRS_OP_DOWN: return op_down(m, l);
         case LRS_OP_FFN: return op_ffn(m, l);
+        case LRS_OP_MATVECS: {
+            hipError_t e;
+            if ((e = op_qkv(m, l)) != hipSuccess || (e = op_o(m, l)) != hipSuccess) return e;
+            return op_ffn(m, l);
+        }
         case LRS_OP_QK_PREP: return op_qk_prep(m, l);
         case LRS_OP_DN_PROJ: return op_dn_proj(m, l);
         case LRS_OP_DN_STEP: return op_dn_step(m, l);

@@ -159,7 +159,8 @@ class ResidentForward:
         return out
 
     OPS = {"qkv": 0, "attn": 1, "o": 2, "gateup": 3, "down": 4, "head": 5,
-           "dn_proj": 6, "dn_step": 7, "dn_out": 8, "qk_prep": 9, "ffn": 10}
+           "dn_proj": 6, "dn_step": 7, "dn_out": 8, "qk_prep": 9, "ffn": 10,
+           "matvecs": 11}
 
     def profile(self, op: str, iters: int):
         """(mean us per launch, bytes per launch) of one fused op, outside the graph."""

@@ -32,6 +32,18 @@ def build(force: bool = False) -> str:
     return LIB_PATH
 
 
+def use_timing_build(out_dir: str) -> str:
+    """Compile the same sources with ``-O3 -march=native`` (floating-point
+    contraction allowed) into ``out_dir`` on the host that runs it, and make
+    every later call of this module use that library.  It is the CPU
+    baseline's timing build; the parity tests use the exact build above."""
+    global LIB_PATH, _lib
+    path = os.path.join(out_dir, "liblrs_oracle_timing.so")
+    subprocess.run(["make", "-s", "-C", HERE, "timing", f"TIMING_OUT={path}"], check=True)
+    LIB_PATH, _lib = path, None
+    return path
+
+
 _lib = None
 
 
