@@ -10,8 +10,8 @@ Workloads:
           decoded at the same positions 511..511+K-1 (attention length
           512..511+K, the config's 128 tokens after a 512-token prompt).
   q8      config 1: one Q8_0 4096x4096 matvec (d ~ U[1e-3,1e-2], qs ~ U[-127,127],
-          x ~ N(0,1) f32); a step is one lrs_matvec_dev call (activation pack +
-          matrix-core matvec), 16 of them over 16 weight copies (285 MB, beyond
+          x ~ N(0,1) f32); a step is one lrs_matvec_dev call (one launch: each
+          workgroup packs x, then the matrix-core matvec), 16 of them over 16 weight copies (285 MB, beyond
           the 256 MB MALL, so every weight byte comes from HBM) captured into
           one HIP graph and replayed.
   layer   config 2: one Qwen2.5-14B-shaped layer matvec set through the token
@@ -757,7 +757,8 @@ def line_q8(lrs, ctx, a, threads):
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                          "traffic": read_traffic("q8_matvec"),
-                         "kernel": "lrs_matvec_dev: activation pack + Q8_0 matrix-core matvec",
+                         "kernel": "lrs_matvec_dev: Q8_0 matrix-core matvec, each workgroup "
+                                   "packing the f32 input itself (one launch)",
                          "op": "q8_matvec", "kernel_us": round(r["us"], 3),
                          "bytes_per_launch": r["bytes"]},
             "cpu_baseline": None if a.no_cpu else cpu_baseline_q8(threads)}

@@ -107,10 +107,17 @@ int lrs_weight_dequant_dev(lrs_ctx *ctx, const lrs_weight *w, float *out_dev);
  * to every resident type, and matmul::dispatch_{q8_0,q4_k,q5_k,q6_k}_matvec
  * (crates/llama-vulkan/src/matmul.rs:36-430).  The activation keeps 22
  * significant bits per 32-element block (three exact int8 digits on the
- * matrix cores; the reference rounds it to 8 bits).  Blocking. */
+ * matrix cores; the reference rounds it to 8 bits).  Up to 8 columns (Q8_0)
+ * or 4 (K-quants) share each weight load, as the reference's COLS
+ * specialisation (shaders/q5_k_matvec.comp:43-47, q8_0_matvec.comp:8-10)
+ * does; each column's result is bit-identical to a one-column call.
+ * Blocking. */
 int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y,
                    uint32_t cols);
-/* Same on device buffers, enqueued on the context stream (async). */
+/* Same on device buffers, enqueued on the context stream (async).  Q8_0
+ * weights, several columns and inputs of up to 4096 elements are packed by
+ * the matvec launch itself (no scratch); wider single K-quant columns take a
+ * pack launch into the context scratch first. */
 int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float *y_dev,
                    uint32_t cols);
 

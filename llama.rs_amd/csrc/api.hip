@@ -346,8 +346,10 @@ int lrs_matvec_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev, float 
     int rc = matvec_check(w, cols);
     if (rc) return rc;
     SETDEV(ctx);
-    void *pack = nullptr;
-    if (int rc_ = ctx_scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack)) return rc_;
+    void *pack = nullptr;  // only the staged form needs one
+    if (!matvec_packs_in_kernel(w->v, cols))
+        if (int rc_ = ctx_scratch(ctx, xpack_bytes(pack_blocks(w->v.type, w->v.n_in)), &pack))
+            return rc_;
     LRS_HIP(launch_matvec(w->v, x_dev, y_dev, cols, pack, ctx->stream));
     return LRS_OK;
 }
@@ -365,7 +367,7 @@ int lrs_matvec_dev_noalloc(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev
     void *pack = noalloc_ptr(ctx->device);
     if (!pack) return fail(LRS_E_HIP, "static pack of this device not resolved");
     SETDEV(ctx);
-    LRS_HIP(launch_matvec(w->v, x_dev, y_dev, cols, pack, ctx->stream));
+    LRS_HIP(launch_matvec_staged(w->v, x_dev, y_dev, cols, pack, ctx->stream));
     return LRS_OK;
 }
 
@@ -399,13 +401,14 @@ int lrs_matvec_f32(lrs_ctx *ctx, const lrs_weight *w, const float *x, float *y, 
     SETDEV(ctx);
     const size_t xb = (size_t)cols * w->v.n_in * sizeof(float);
     const size_t yb = (size_t)cols * w->v.n_out * sizeof(float);
-    const size_t pb = xpack_bytes(pack_blocks(w->v.type, w->v.n_in));
+    const size_t pb =
+        matvec_packs_in_kernel(w->v, cols) ? 0 : xpack_bytes(pack_blocks(w->v.type, w->v.n_in));
     auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
     void *buf = nullptr;
     if (int rc_ = ctx_scratch(ctx, up(xb) + up(yb) + pb, &buf)) return rc_;
     float *xd = (float *)buf;
     float *yd = (float *)((char *)buf + up(xb));
-    void *pack = (char *)buf + up(xb) + up(yb);
+    void *pack = pb ? (char *)buf + up(xb) + up(yb) : nullptr;
     LRS_HIP(hipMemcpyAsync(xd, x, xb, hipMemcpyHostToDevice, ctx->stream));
     LRS_HIP(launch_matvec(w->v, xd, yd, cols, pack, ctx->stream));
     LRS_HIP(hipMemcpyAsync(y, yd, yb, hipMemcpyDeviceToHost, ctx->stream));

@@ -95,9 +95,17 @@ inline uint32_t pack_blocks(uint32_t t, uint32_t n_in) {
 // reduces argmax keys (amax_key) into step {token, pos, n} and out[n]
 hipError_t launch_argmax_finish(const unsigned long long *keys, uint32_t n, uint32_t *step,
                                 uint32_t *out, uint32_t out_cap, hipStream_t s);
-// y[c] = W x[c] for cols columns (packs x, then one matvec per column)
+// y[c] = W x[c] for cols columns: when matvec_packs_in_kernel, up to 8
+// columns per launch share each weight load and every workgroup packs its
+// input columns itself (`pack` unused, may be null); otherwise the staged
+// form below with `pack` (xpack_bytes of the weight)
 hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
                          hipStream_t s);
+bool matvec_packs_in_kernel(WeightView w, uint32_t cols);
+// the staged form: each column packed into `pack` by its own launch, then one
+// matvec launch per column over that pack (same results)
+hipError_t launch_matvec_staged(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
+                                hipStream_t s);
 // Q8_0 activation quantization (reference CPU forward): GGUF Q8_0 bytes to
 // q8 (n / 32 blocks) and / or the matvec pack p (nxb blocks) when non-null
 hipError_t launch_q8act(const float *x, uint32_t n, uint32_t nxb, int half_even, uint8_t *q8,

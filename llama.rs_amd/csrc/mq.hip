@@ -409,9 +409,13 @@ __device__ __forceinline__ void copy_to_lds(const uint8_t *__restrict__ g, uint8
     }
 }
 
-// body for the segments [s_lo, s_hi) of type T (one workgroup)
-template <uint32_t T, int TPW, int TG, int KS, int P, int EPI>
+// body for the segments [s_lo, s_hi) of type T (one workgroup).  NC > 1 or
+// XF (MQ_STORE only): NC input columns share each weight load, their packs
+// side by side in LDS; with XF the workgroup packs the f32 columns a.xf
+// itself instead of copying a pack made by a previous launch.
+template <uint32_t T, int TPW, int TG, int KS, int P, int EPI, int NC = 1, bool XF = false>
 __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *lds, float *red) {
+    static_assert(NC == 1 || EPI == MQ_STORE, "several columns: store epilogue only");
     constexpr int W = TG * KS;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t tg = wave / KS, ks = wave % KS;
@@ -433,21 +437,91 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     }
     const uint32_t u_lo = ks * units / KS, u_hi = (ks + 1) * units / KS;
 
+    // XF: the first B input elements per thread of column 0 are loaded ahead
+    // of the weight prefetch, so packing them waits for these loads only
+    constexpr int B = 8;
+    float xv0[B];
+    constexpr uint32_t NT = 64 * W;  // threads of the workgroup
+    if constexpr (XF) {
+        // branch-free (clamped index, then select) so that the wait before
+        // packing counts exactly these loads
+#pragma unroll
+        for (int k = 0; k < B; k++) {
+            const uint32_t e = threadIdx.x + k * NT;
+            const float t = a.xf[e < a.n_in ? e : a.n_in - 1];
+            xv0[k] = e < a.n_in ? t : 0.f;
+        }
+    }
+
     // prefetch the first P units of this wavefront
     WReg<T> wr[P][TPW];
+    if constexpr (XF) {
+        // unconditional (a unit past this wavefront's range reads an in-range
+        // unit whose registers are never consumed), for the same reason
 #pragma unroll
-    for (int i = 0; i < P; i++)
-        if (u_lo + i < u_hi) {
+        for (int i = 0; i < P; i++) {
+            const uint32_t uu = u_lo + i < units ? u_lo + i : units - 1;
 #pragma unroll
-            for (int t = 0; t < TPW; t++) wload<T>(wr[i][t], wt[t] + (size_t)(u_lo + i) * tchunk_bytes(T), lane);
+            for (int t = 0; t < TPW; t++) wload<T>(wr[i][t], wt[t] + (size_t)uu * tchunk_bytes(T), lane);
         }
+    } else {
+#pragma unroll
+        for (int i = 0; i < P; i++)
+            if (u_lo + i < u_hi) {
+#pragma unroll
+                for (int t = 0; t < TPW; t++) wload<T>(wr[i][t], wt[t] + (size_t)(u_lo + i) * tchunk_bytes(T), lane);
+            }
+    }
 
-    // stage the input pack; fused RMSNorm: sum of squares of xres
+    // stage the input pack(s): digits of column c at c * nxb * 96, 16 zero
+    // bytes, then the meta of column c at + c * nxb * 16; fused RMSNorm: sum
+    // of squares of xres
     LPack lp;
-    lp.zero = a.nxb * 96;
+    lp.zero = NC * a.nxb * 96;
     lp.meta = lp.zero + 16;
-    copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.dig), lds, a.nxb * 96);
-    copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.meta), lds + lp.meta, a.nxb * 16);
+    if constexpr (XF) {
+        // pack_half per 32-element block (lane i of a half wavefront =
+        // element i); elements past n_in pack as zero.  B elements per
+        // thread are loaded before any is packed: the LDS stores of the pack
+        // would otherwise keep each load behind the previous store.
+        const uint32_t ne = 32 * a.nxb;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            XPack xl;
+            xl.dig = reinterpret_cast<int8_t *>(lds + c * a.nxb * 96);
+            xl.meta = reinterpret_cast<float *>(lds + lp.meta + c * a.nxb * 16);
+            xl.q8 = 0;
+            const float *xc = a.xf + (size_t)c * a.n_in;
+            uint32_t e0 = threadIdx.x;
+            if (c == 0) {
+                // the batch loaded ahead of the weights; every lane computes
+                // (no branch for the compiler to sink those loads into), the
+                // half-waves past the pack store nothing
+#pragma unroll
+                for (int k = 0; k < B; k++) {
+                    const uint32_t e = e0 + k * NT;
+                    pack_half(xv0[k], e < ne ? e >> 5 : 0, xl, e < ne);
+                }
+                e0 += B * NT;
+            }
+            for (; e0 < ne; e0 += B * NT) {
+                float v[B];
+#pragma unroll
+                for (int k = 0; k < B; k++) {
+                    const uint32_t e = e0 + k * NT;
+                    v[k] = e < a.n_in ? xc[e] : 0.f;
+                }
+#pragma unroll
+                for (int k = 0; k < B; k++) {
+                    const uint32_t e = e0 + k * NT;
+                    if (e < ne) pack_half(v[k], e >> 5, xl);  // whole half-waves
+                }
+            }
+        }
+    } else {
+        copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.dig), lds, a.nxb * 96);
+        copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.meta), lds + lp.meta, a.nxb * 16);
+    }
     if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + lp.zero)[threadIdx.x] = 0u;
     float ss = 0.f;
     if (a.xres) {
@@ -477,10 +551,25 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         __syncthreads();
     }
 
-    const ALane<T> al = alane<T>(lane, lp);
-    float acc[TPW], accm[TPW];
+    // per column: the same slot mapping over that column's pack (the zero
+    // slot is shared)
+    LPack lpc[NC];
+    ALane<T> alc[NC];
+    {
+        const ALane<T> al = alane<T>(lane, lp);
 #pragma unroll
-    for (int t = 0; t < TPW; t++) acc[t] = accm[t] = 0.f;
+        for (int c = 0; c < NC; c++) {
+            lpc[c].zero = lp.zero;
+            lpc[c].meta = lp.meta + c * a.nxb * 16;
+            alc[c] = al;
+            if (al.base != lp.zero) alc[c].base = al.base + c * a.nxb * 96;
+        }
+    }
+    float acc[NC][TPW], accm[NC][TPW];
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int t = 0; t < TPW; t++) acc[c][t] = accm[c][t] = 0.f;
 
     // steady state: every unit's successor P units ahead is in range, so the
     // loads are unconditional and each register set is refilled in place
@@ -491,7 +580,9 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     for (; u0 + 2 * P <= u_hi; u0 += P) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
-            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc, accm);
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+                udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
 #pragma unroll
             for (int t = 0; t < TPW; t++)
                 wload<T>(wr[i][t], wt[t] + (size_t)(u0 + P + i) * tchunk_bytes(T), lane);
@@ -504,7 +595,9 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
     for (int i = 0; i < P; i++) {
         if (u0 + i < u_hi) {
-            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc, accm);
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+                udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
             if (u0 + P + i < u_hi) {
 #pragma unroll
                 for (int t = 0; t < TPW; t++)
@@ -515,22 +608,29 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     u0 += P;
 #pragma unroll
     for (int i = 0; i < P; i++)
-        if (u0 + i < u_hi) udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc, accm);
+        if (u0 + i < u_hi) {
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+                udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+        }
 
     // row sums: lanes n, n+16, n+32, n+48 hold sub-block classes of row n
-    float v[TPW];
+    // red layout: [NC][W][TPW][16] partials, then [W] sums of squares
 #pragma unroll
-    for (int t = 0; t < TPW; t++) {
-        v[t] = acc[t] - accm[t];
-        v[t] += __shfl_xor(v[t], 16, 64);
-        v[t] += __shfl_xor(v[t], 32, 64);
-    }
-    // red layout: [W][TPW][16] partials, then [W] sums of squares
-    if (lane < 16) {
+    for (int c = 0; c < NC; c++) {
+        float v[TPW];
 #pragma unroll
-        for (int t = 0; t < TPW; t++) red[(wave * TPW + t) * 16 + lane] = v[t];
+        for (int t = 0; t < TPW; t++) {
+            v[t] = acc[c][t] - accm[c][t];
+            v[t] += __shfl_xor(v[t], 16, 64);
+            v[t] += __shfl_xor(v[t], 32, 64);
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int t = 0; t < TPW; t++) red[((c * W + wave) * TPW + t) * 16 + lane] = v[t];
+        }
     }
-    if (lane == 0) red[W * TPW * 16 + wave] = ss;
+    if (lane == 0) red[NC * W * TPW * 16 + wave] = ss;
     __syncthreads();
 
     // ---- epilogue: thread i owns output i of the workgroup ----
@@ -538,7 +638,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     if (a.xres) {
         float tot = 0.f;
 #pragma unroll
-        for (int w = 0; w < W; w++) tot += red[W * TPW * 16 + w];
+        for (int w = 0; w < W; w++) tot += red[NC * W * TPW * 16 + w];
         // ops.rs:56-66: 1 / sqrt(mean(x^2) + eps)
         s = 1.0f / sqrtf(tot / (float)a.n_in + a.eps);
     }
@@ -549,11 +649,12 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     constexpr bool PACK = EPI == MQ_RESID || EPI == MQ_SWIGLU;
     const uint32_t lim = PACK ? ((nout + 31) & ~31u) : EPI == MQ_STORE ? ((nout + 63) & ~63u) : nout;
     if (i >= lim) return;
-    // value of output i: sum of the KS K-slice partials of its tile group
-    auto partial = [&](uint32_t grp, uint32_t t, uint32_t n) {
+    // value of output i (column c): sum of the KS K-slice partials of its
+    // tile group
+    auto partial = [&](uint32_t grp, uint32_t t, uint32_t n, int c = 0) {
         float r = 0.f;
 #pragma unroll
-        for (int k = 0; k < KS; k++) r += red[((grp * KS + k) * TPW + t) * 16 + n];
+        for (int k = 0; k < KS; k++) r += red[((c * W + grp * KS + k) * TPW + t) * 16 + n];
         return r;
     };
     const uint32_t row = tile0 * 16 + i;
@@ -570,7 +671,18 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     const uint32_t tt = pair ? 0 : (ii >> 4) % TPW;
     float y = s * partial(grp, tt, ii & 15);
     if (sg.bias && valid) y = y + sg.bias[row];
-    if constexpr (EPI == MQ_STORE) {
+    if constexpr (NC > 1) {
+        // several columns: column c's outputs at out + c * ostride
+        if (valid) {
+            sg.out[row] = y;
+#pragma unroll
+            for (int c = 1; c < NC; c++) {
+                float yc = s * partial(grp, tt, ii & 15, c);
+                if (sg.bias) yc = yc + sg.bias[row];
+                sg.out[(size_t)c * a.ostride + row] = yc;
+            }
+        }
+    } else if constexpr (EPI == MQ_STORE) {
         if (valid) sg.out[row] = y;
         if (a.amax) {
             unsigned long long key = valid ? amax_key(y, row) : 0ull;
@@ -629,6 +741,15 @@ __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq(MqArg
         mq_body<T0, TPW, TG, KS, P, EPI>(a, si, lds, red);
     else
         mq_body<T1, TPW, TG, KS, P, EPI>(a, si, lds, red);
+}
+
+// plain matvec of NC f32 input columns (a.xf), packed by each workgroup
+template <uint32_t T, int TPW, int TG, int KS, int P, int NC>
+__global__ __launch_bounds__(64 * TG * KS)
+__attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mqx(MqArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float red[NC * TG * KS * TPW * 16 + TG * KS];
+    mq_body<T, TPW, TG, KS, P, MQ_STORE, NC, true>(a, 0, lds, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -806,8 +927,103 @@ hipError_t launch_matvec_actq(WeightView w, const float *x, float *y, uint32_t c
     return hipSuccess;
 }
 
+// ---- plain matvec of f32 columns packed in the kernel (k_mqx) ----
+template <uint32_t T, int TPW, int TG, int KS, int P>
+static MqFn pick_nc(int nc) {
+    switch (nc) {
+    case 1: return k_mqx<T, TPW, TG, KS, P, 1>;
+    case 2: return k_mqx<T, TPW, TG, KS, P, 2>;
+    case 4: return k_mqx<T, TPW, TG, KS, P, 4>;
+    case 8:
+        if constexpr (T == T_Q8_0) return k_mqx<T, TPW, TG, KS, P, 8>;
+        return nullptr;
+    default: return nullptr;
+    }
+}
+
+// the launch shapes store_geom picks (without a tuning override)
+template <uint32_t T>
+static MqFn pick_x_geom(const MqGeom &g, int nc) {
+    if constexpr (T == T_Q8_0) {
+        if (g.tpw == 1 && g.tg == 1 && g.ks == 8 && g.p == 6) return pick_nc<T, 1, 1, 8, 6>(nc);
+    } else {
+        if (g.tpw == 1 && g.tg == 2 && g.ks == 2 && g.p == 2) return pick_nc<T, 1, 2, 2, 2>(nc);
+        if (g.tpw == 1 && g.tg == 2 && g.ks == 4 && g.p == 2) return pick_nc<T, 1, 2, 4, 2>(nc);
+        if (g.tpw == 1 && g.tg == 1 && g.ks == 4 && g.p == 2) return pick_nc<T, 1, 1, 4, 2>(nc);
+    }
+    return nullptr;
+}
+
+static MqFn pick_x(uint32_t t, const MqGeom &g, int nc) {
+    switch (t) {
+    case T_Q4_K: return pick_x_geom<T_Q4_K>(g, nc);
+    case T_Q5_K: return pick_x_geom<T_Q5_K>(g, nc);
+    case T_Q6_K: return pick_x_geom<T_Q6_K>(g, nc);
+    case T_Q8_0: return pick_x_geom<T_Q8_0>(g, nc);
+    default: return nullptr;
+    }
+}
+
+// LDS bytes of k_mqx with nc columns of nxb pack blocks each; launches keep
+// 8 KB of the 160 KB for the kernel's static partial-sum array
+static size_t mqx_lds(uint32_t nxb, int nc) { return (size_t)nc * nxb * 112 + 16; }
+static constexpr size_t MQX_LDS_MAX = 152 * 1024;
+
+// In-kernel packing costs every workgroup the pack of the whole input; it
+// pays for Q8_0 (its short units leave the prologue exposed either way), for
+// several columns (each weight load serves up to 8) and for inputs whose pack
+// is one batch of 8 elements per thread, loaded ahead of the weights.  Wider
+// single K-quant columns take the staged form (a pack launch, then the matvec
+// copying that pack to LDS), which measures faster there.
+bool matvec_packs_in_kernel(WeightView w, uint32_t cols) {
+    if (!is_tiled(w.type)) return false;
+    const MqGeom g = store_geom(w.type, w.n_in, w.n_out);
+    const uint32_t nxb = pack_blocks(w.type, w.n_in);
+    if (!pick_x(w.type, g, 1) || mqx_lds(nxb, 1) > MQX_LDS_MAX) return false;
+    return w.type == T_Q8_0 || cols > 1 || 32 * nxb <= 8 * 64 * (uint32_t)(g.tg * g.ks);
+}
+
 hipError_t launch_matvec(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
                          hipStream_t s) {
+    if (!is_tiled(w.type)) return hipErrorInvalidValue;
+    const uint32_t nxb = pack_blocks(w.type, w.n_in);
+    const MqGeom g = store_geom(w.type, w.n_in, w.n_out);
+    if (matvec_packs_in_kernel(w, cols)) {
+        // up to 8 columns per launch share every weight load; each column's
+        // arithmetic is the single-column kernel's (same K-slices, same
+        // order), so the results do not depend on the grouping
+        // K-quants: at most 4 columns (8 need more than 128 VGPRs, fewer waves)
+        const int nc_max = w.type == T_Q8_0 ? 8 : 4;
+        for (uint32_t c0 = 0; c0 < cols;) {
+            int nc = nc_max;
+            while (nc > 1 && ((uint32_t)nc > cols - c0 || mqx_lds(nxb, nc) > MQX_LDS_MAX)) nc >>= 1;
+            MqArgs a = {};
+            a.n_seg = a.n_seg0 = 1;
+            a.seg[0].w = w.q;
+            a.seg[0].rows = w.n_out;
+            a.seg[0].out = y + (size_t)c0 * w.n_out;
+            a.seg[0].wg0 = 0;
+            a.n_in = w.n_in;
+            a.nxb = nxb;
+            a.xf = x + (size_t)c0 * w.n_in;
+            a.ostride = w.n_out;
+            const uint32_t per = (uint32_t)(g.tg * g.tpw);
+            const uint32_t wgs = (ttiles(w.n_out) + per - 1) / per;
+            hipLaunchKernelGGL(pick_x(w.type, g, nc), dim3(wgs), dim3(64 * g.tg * g.ks),
+                               mqx_lds(nxb, nc), s, a);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            c0 += (uint32_t)nc;
+        }
+        return hipSuccess;
+    }
+    if (!pack) return hipErrorInvalidValue;
+    return launch_matvec_staged(w, x, y, cols, pack, s);
+}
+
+// the two-launch form: pack each column into `pack`, then the matvec over it
+hipError_t launch_matvec_staged(WeightView w, const float *x, float *y, uint32_t cols, void *pack,
+                                hipStream_t s) {
     if (!is_tiled(w.type)) return hipErrorInvalidValue;
     const uint32_t nxb = pack_blocks(w.type, w.n_in);
     const XPack xp = xpack_at(pack, nxb);

@@ -78,6 +78,10 @@ struct MqArgs {
     const float *gss;
     uint32_t gblk;
     float gn;
+    // plain matvec of f32 columns packed in the kernel (k_mqx): column c of
+    // the input at xf + c * n_in, its outputs at seg[0].out + c * ostride
+    const float *xf;
+    uint32_t ostride;
 };
 
 // launch shape: TPW tiles per wavefront sharing the activation, TG tile

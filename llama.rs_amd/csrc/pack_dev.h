@@ -18,7 +18,9 @@ __device__ __forceinline__ float pk_dpp(float x) {
 // the 16-element sums reduce over rows of 16 lanes with DPP (quad_perm
 // [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then one exchange
 // between the two rows of the half.
-__device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p) {
+// With store false the half wavefront computes the block but writes nothing
+// (a half past the end of the pack, kept in step with the rest of the wave).
+__device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p, bool store = true) {
     const uint32_t i = threadIdx.x & 31;
     float amax = fabsf(v);
     amax = fmaxf(amax, pk_dpp<0xB1>(amax));
@@ -32,6 +34,7 @@ __device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p) {
         const float d = amax > 0.f ? amax / 127.0f : 0.f;
         const float di = d > 0.f ? 1.0f / d : 0.f;
         const float r = fminf(fmaxf(__builtin_rintf(v * di), -128.f), 127.f);
+        if (!store) return;
         int8_t *dg = p.dig + (size_t)blk * 96 + i;
         dg[0] = 0;
         dg[32] = 0;
@@ -55,6 +58,7 @@ __device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p) {
     const int X1 = (X - d2) >> 8;
     const int d1 = (int)(int8_t)(X1 & 255);
     const int d0 = (X1 - d1) >> 8;
+    if (!store) return;
     int8_t *dg = p.dig + (size_t)blk * 96 + i;
     dg[0] = (int8_t)d0;
     dg[32] = (int8_t)d1;

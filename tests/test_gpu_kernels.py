@@ -225,6 +225,36 @@ def test_matvec_columns_equal_single_calls(lrs, orc, ctx, t):
         assert np.array_equal(yb[c], W.matvec(xs[c]))
 
 
+# several columns per launch share each weight load (groups of 8, 4, 2, 1 as
+# the LDS allows); every launch shape of the plain matvec appears
+@pytest.mark.parametrize("t,n_in,n_out,cols", [
+    (Q4_K, 1024, 16, 19), (Q8_0, 4096, 4096, 11), (Q6_K, 5120, 4096, 9),
+    (Q5_K, 2048, 16384, 3), (Q4_K, 13824, 64, 5), (Q6_K, 768, 40, 8),
+])
+def test_matvec_columns_share_weight_loads_exactly(lrs, orc, ctx, t, n_in, n_out, cols):
+    """Columns computed together equal the same columns one at a time and the
+    staged form (pack launch + matvec launch) bit for bit, and the oracle to
+    the matvec bar."""
+    w = orc.gen_weight(t, 40 + cols, n_out, n_in)
+    W = lrs.Weight.upload(ctx, t, w, n_in, n_out)
+    xs = np.stack([orc.gen_normal(60 + c, n_in) * (1 + c % 3) for c in range(cols)])
+    yb = W.matvec(xs)
+    xd, yd = ctx.alloc(4 * n_in), ctx.alloc(4 * n_out)
+    try:
+        for c in range(cols):
+            assert np.array_equal(yb[c], W.matvec(xs[c])), c
+            xd.upload(xs[c])
+            W.matvec_dev_noalloc(xd, yd)
+            ctx.sync()
+            assert np.array_equal(yb[c], yd.download(np.float32, n_out)), c
+        ref = orc.matvec(t, w, n_in, n_out, xs, threads=THREADS)
+        for c in range(cols):
+            assert rel_l2(yb[c], ref[c]) < MATVEC_TOL, (c, rel_l2(yb[c], ref[c]))
+    finally:
+        xd.free()
+        yd.free()
+
+
 def test_matvec_zero_and_single_row(lrs, orc, ctx):
     for t in KQ:
         n_in = 256
