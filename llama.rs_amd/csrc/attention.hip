@@ -37,8 +37,16 @@ struct AttnArgs {
     float *part;              // [n_head][splits][HD + 4]: acc[HD], m, l
     const uint32_t *step;     // {token, pos}: attends positions 0..pos
     uint32_t n_head, n_kv, ctx, splits;
+    uint32_t minchunk;        // positions per split at least (short contexts use fewer splits)
     float scale;
 };
+
+// positions per split of a context of L positions: L spread over `splits`,
+// but at least `minchunk` (the splits past the last position have no work)
+__device__ __forceinline__ uint32_t attn_chunk(uint32_t L, uint32_t splits, uint32_t minchunk) {
+    const uint32_t c = (L + splits - 1) / splits;
+    return c > minchunk ? c : minchunk;
+}
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
@@ -81,8 +89,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     const uint32_t tid = threadIdx.x, sub = tid % LP, grp = tid / LP;
     const uint32_t sp = blockIdx.x, kh = blockIdx.y, h0 = kh * REP;
     const uint32_t L = a.step[1] + 1;
-    const uint32_t chunk = (L + a.splits - 1) / a.splits;
-    const uint32_t p0 = min(sp * chunk, L), n = min(p0 + chunk, L) - p0;
+    const uint32_t chunk = attn_chunk(L, a.splits, a.minchunk);
+    if (sp * chunk >= L) return;  // no position in this split (the combine skips it)
+    const uint32_t p0 = sp * chunk, n = min(p0 + chunk, L) - p0;
     const _Float16 *kb = a.kc + ((size_t)kh * a.ctx + p0) * HD + 8 * sub;
     const _Float16 *vb = a.vc + ((size_t)kh * a.ctx + p0) * HD + 8 * sub;
 
@@ -216,6 +225,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 // goes to LDS in one round trip (global_load_lds), then thread d owns dim d
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ part, uint32_t splits,
+                                                     const uint32_t *__restrict__ step,
+                                                     uint32_t minchunk,
                                                      const float *__restrict__ gate,
                                                      uint32_t gstride, XPack out) {
     extern __shared__ __attribute__((aligned(16))) float pl[];  // [splits][HD + 4]
@@ -223,6 +234,9 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     constexpr uint32_t ST = HD + 4;
     const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
     const uint8_t *src = reinterpret_cast<const uint8_t *>(part + (size_t)h * splits * ST);
+    // the splits that hold positions (the split kernel skipped the others)
+    const uint32_t L = step[1] + 1, chunk = attn_chunk(L, splits, minchunk);
+    splits = (L + chunk - 1) / chunk;
     const uint32_t bytes = splits * ST * 4;  // multiple of 16
     for (uint32_t base = wave * 1024; base < bytes; base += HD * 16) {
         const uint32_t off = base + lane * 16;
@@ -257,6 +271,12 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
 // split count: about one workgroup per CU (256 = splits x KV heads), at
 // most 32 (measured on the decode benches: 32 splits beat 64 for 4 KV heads
 // x 256 dims, and 16 / 32 tie for 8 x 128; 8 and 64 are slower)
+// at least 16 positions per split: a context of L < 16 * splits positions
+// runs ceil(L / 16) splits and the combine reads only those (measured on the
+// config-3 decode: 32 and 64 per split are no faster at 512 positions, 128
+// and 256 slower, and the config-4 attention is slower at 64)
+static uint32_t attn_minchunk() { return 16u; }
+
 uint32_t attn_splits(uint32_t n_kv) {
     const uint32_t S = 256 / n_kv;
     return S < 1 ? 1 : S > 32 ? 32 : S;
@@ -292,6 +312,7 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
     a.n_kv = n_kv;
     a.ctx = ctx;
     a.splits = splits;
+    a.minchunk = attn_minchunk();
     a.scale = 1.0f / sqrtf((float)head_dim);
     if (n_kv == 0 || n_head % n_kv || splits == 0) return hipErrorInvalidValue;
     const uint32_t rep = n_head / n_kv;
@@ -306,10 +327,11 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
     if (!fn) return hipErrorInvalidValue;
     hipLaunchKernelGGL(fn, grid, dim3(ATT_THREADS), 0, s, a);
     const size_t cl = (size_t)splits * (head_dim + 4) * sizeof(float);
+    const uint32_t mc = a.minchunk;
     switch (head_dim) {
-    case 64: hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), cl, s, part, splits, gate, gstride, out); break;
-    case 128: hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_head), dim3(128), cl, s, part, splits, gate, gstride, out); break;
-    default: hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_head), dim3(256), cl, s, part, splits, gate, gstride, out); break;
+    case 64: hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), cl, s, part, splits, step, mc, gate, gstride, out); break;
+    case 128: hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_head), dim3(128), cl, s, part, splits, step, mc, gate, gstride, out); break;
+    default: hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_head), dim3(256), cl, s, part, splits, step, mc, gate, gstride, out); break;
     }
     return hipGetLastError();
 }
