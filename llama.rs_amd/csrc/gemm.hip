@@ -111,8 +111,11 @@ __device__ __forceinline__ DeqPrep wprep(const WRaw<T> &w, uint32_t e) {
         const uint32_t jj = 2 * j + hi, sh = 8 * (jj & 3);
         const uint32_t by = (w.hd.y >> sh) & 0xFF, bz = (w.hd.z >> sh) & 0xFF,
                        bw = (w.hd.w >> sh) & 0xFF;
-        const uint32_t sc = jj < 4 ? (by & 63) : ((bw & 0xF) | ((by >> 6) << 4));
-        const uint32_t m = jj < 4 ? (bz & 63) : ((bw >> 4) | ((bz >> 6) << 4));
+        // both forms, then a mask select: a conditional here compiles to a
+        // divergent branch, which splits the step's MFMA / VALU interleaving
+        const uint32_t lowm = 0u - (uint32_t)(jj < 4);
+        const uint32_t sc = ((by & 63) & lowm) | (((bw & 0xF) | ((by >> 6) << 4)) & ~lowm);
+        const uint32_t m = ((bz & 63) & lowm) | (((bw >> 4) | ((bz >> 6) << 4)) & ~lowm);
         const float dv = h2f((uint16_t)(w.hd.x & 0xFFFF)), mv = h2f((uint16_t)(w.hd.x >> 16));
         p.a = __fmul_rn(dv, (float)sc);
         p.b = __fmul_rn(mv, (float)m);
