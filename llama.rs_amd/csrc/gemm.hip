@@ -15,7 +15,8 @@
 // output tile; each of its 8 wavefronts a 64 x 32 part = 2 MFMA tiles of
 // 32 x 32.  K advances 64 at a time: every thread stages 16 activations
 // (bf16, split from f32 once per GEMM input) and dequantizes 16 weights of
-// one row (bit-exact f32 dequant as in dequant.rs, then bf16) into a
+// one row (f32 dequant as in dequant.rs, the K-quant min term in the same
+// fused multiply-add as the scale, then bf16) into a
 // double-buffered LDS tile, and each wavefront issues 4 K16 steps x 2 tiles
 // of MFMA.  LDS rows are padded to 72 bf16 so the 32 lanes that read 32
 // different rows at one K offset hit distinct banks.
@@ -53,11 +54,13 @@ template <> struct WRaw<T_Q6_K> { u32x4 ql, qh; uint32_t sc, d; };
 template <> struct WRaw<T_Q5_K> { u32x4 hd, qh, qs; };
 template <> struct WRaw<T_Q8_0> { u32x4 qs; uint32_t d; };
 
+// rowq = the first chunk of the row's 16-row tile (hoisted out of the K
+// loop: per step only the 32-bit unit offset changes); r = row in the tile
 template <uint32_t T>
-__device__ __forceinline__ void wload(const GemmArgs &g, uint32_t n, uint32_t e, WRaw<T> &w) {
-    const uint32_t o = e & 255, r = n & 15;  // offset inside the super-block, row in the tile
-    const uint32_t l0 = o & 16;               // first or second 16 of a 32-element run
-    const uint8_t *c = g.q + ((size_t)(n >> 4) * g.units + e / tunit_elems(T)) * tchunk_bytes(T);
+__device__ __forceinline__ void wload(const uint8_t *rowq, uint32_t r, uint32_t e, WRaw<T> &w) {
+    const uint32_t o = e & 255;  // offset inside the super-block
+    const uint32_t l0 = o & 16;  // first or second 16 of a 32-element run
+    const uint8_t *c = rowq + (e / tunit_elems(T)) * tchunk_bytes(T);
     if constexpr (T == T_Q8_0) {
         // 64-element units of two blocks: piece g = 2 block + 16-byte half,
         // then the 16 rows' f16 d of both blocks (tiled.h)
@@ -87,7 +90,11 @@ __device__ __forceinline__ void wload(const GemmArgs &g, uint32_t n, uint32_t e,
     }
 }
 
-// the 16 weights in f32, exactly as ggml_cpu::dequant (dequant.rs:101-258):
+// the 16 weights in f32 as ggml_cpu::dequant (dequant.rs:101-258) computes
+// them with one fused multiply-add each: Q6_K a*q - 32a is a*(q - 32)
+// rounded once, bit-exact; Q4_K / Q5_K a*q - b skips the reference's
+// rounding of a*q (half an ulp of the product), which the bf16 rounding
+// that follows absorbs:
 // wprep decodes the run's scale (and min), wdeq4 the weights 4c..4c+3, so the
 // dequant can be spread between the matrix-core ops of a pipeline step
 struct DeqPrep {
@@ -137,26 +144,25 @@ __device__ __forceinline__ void wdeq4(const WRaw<T> &w, const DeqPrep &p, int c,
         for (int i = 0; i < 4; i++)
             v[4 * c + i] = __fmul_rn((float)(int8_t)((qw >> (8 * i)) & 0xFF), p.a);
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        // the four quants as bytes of one word (nibble select and, for Q5_K,
+        // the fifth bits: a few ops per 4 weights), then per weight one byte
+        // conversion and one fused a * q - b
         const uint32_t qw = c == 0 ? w.qs.x : c == 1 ? w.qs.y : c == 2 ? w.qs.z : w.qs.w;
-        uint32_t hw = 0;
-        if constexpr (T == T_Q5_K) hw = c == 0 ? w.qh.x : c == 1 ? w.qh.y : c == 2 ? w.qh.z : w.qh.w;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t byte = (qw >> (8 * i)) & 0xFF;
-            uint32_t q = p.sel ? (byte >> 4) : (byte & 15);
-            if constexpr (T == T_Q5_K) q += ((hw >> (8 * i + p.sub)) & 1) << 4;
-            v[4 * c + i] = __fsub_rn(__fmul_rn(p.a, (float)q), p.b);
+        uint32_t q4 = (qw >> (4 * p.sel)) & 0x0F0F0F0Fu;
+        if constexpr (T == T_Q5_K) {
+            const uint32_t hw = c == 0 ? w.qh.x : c == 1 ? w.qh.y : c == 2 ? w.qh.z : w.qh.w;
+            q4 |= ((hw >> p.sub) & 0x01010101u) << 4;
         }
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[4 * c + i] = fmaf(p.a, (float)((q4 >> (8 * i)) & 0xFF), -p.b);
     } else {  // T_Q6_K: q = (ql nibble | qh 2 bits << 4) - 32
         const uint32_t lw = c == 0 ? w.ql.x : c == 1 ? w.ql.y : c == 2 ? w.ql.z : w.ql.w;
         const uint32_t hw = c == 0 ? w.qh.x : c == 1 ? w.qh.y : c == 2 ? w.qh.z : w.qh.w;
+        const uint32_t q4 = ((lw >> (4 * (p.sel >> 1))) & 0x0F0F0F0Fu) |
+                            (((hw >> (2 * p.sel)) & 0x03030303u) << 4);
+        const float o = -32.0f * p.a;  // exact: a power-of-two multiple
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t lb = (lw >> (8 * i)) & 0xFF, hb = (hw >> (8 * i)) & 0xFF;
-            const uint32_t lo = p.sel < 2 ? (lb & 15) : (lb >> 4);
-            const int q = (int)(lo | (((hb >> (2 * p.sel)) & 3) << 4)) - 32;
-            v[4 * c + i] = __fmul_rn(p.a, (float)q);
-        }
+        for (int i = 0; i < 4; i++) v[4 * c + i] = fmaf(p.a, (float)((q4 >> (8 * i)) & 0xFF), o);
     }
 }
 
@@ -220,6 +226,7 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     for (int j = 0; j < AR; j++)
         aoff[j] = (size_t)min(m0 + sr + 128 * j, g.M - 1) * g.K + sq + (size_t)kz * kspan;
     const uint32_t kbase = kz * kspan;  // weight element offset of the slice
+    const uint8_t *rowq = g.q + (size_t)(wr >> 4) * g.units * tchunk_bytes(T);
 
     f32x16 acc[MT][NT];
 #pragma unroll
@@ -239,7 +246,7 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
                 A[p][j][0] = ap[0];                                                           \
                 A[p][j][1] = ap[1];                                                           \
             }                                                                                 \
-        wload<T>(g, wr, kbase + (K0) + sq, W);                                                \
+        wload<T>(rowq, wr & 15, kbase + (K0) + sq, W);                                       \
     } while (0)
 #define LRS_GSTAGE(BUF, A, W, K0)                                                             \
     do {                                                                                      \
