@@ -190,16 +190,23 @@ constexpr MqGeom G_HEAD = {1, 2, 2, 2};   // 2 tiles per workgroup x 2 K-slices
 constexpr MqGeom G_STORE = {1, 2, 4, 2};  // hybrid q/k/v and delta-net projections
 
 // gate+up tile pairs: 4 per workgroup x 2 K-slices while that gives >= 400
-// workgroups (27648 rows: 432), else 2 per workgroup x 4 K-slices (17408
-// rows: 544 workgroups instead of 272 on 256 CUs)
+// workgroups (27648 rows: 432); else 2 per workgroup x 4 K-slices when all of
+// them fit at once (2 workgroups of 8 wavefronts per CU: 13824 rows, 432);
+// else 2 per workgroup x 2 K-slices with one unit in flight (17408 rows: 544
+// workgroups of 4 wavefronts at 5 per CU, no second round; 21.9 against
+// 23.0 us)
 MqGeom gateup_geom(uint32_t n_ff) {
-    return ttiles(n_ff) / 4 >= 400 ? MqGeom{2, 4, 2, 2} : MqGeom{2, 2, 4, 2};
+    const uint32_t t = ttiles(n_ff);
+    if (t / 4 >= 400) return MqGeom{2, 4, 2, 2};
+    return t / 2 <= 512 ? MqGeom{2, 2, 4, 2} : MqGeom{2, 2, 2, 1};
 }
-// down (n_embd rows): 2 tiles x 6 K-slices for long K (27648), 8 below, one
-// unit in flight per wavefront (with non-temporal weight loads the deeper
-// prefetch measured ~4 % slower)
+// down (n_embd rows), one unit in flight per wavefront where that measured
+// best (with non-temporal weight loads the deeper prefetch was ~4 % slower
+// at 27648): 2 tiles x 6 K-slices for 27648, x 4 with two units in flight
+// for 16384..24575 (17408: 17.4 against 17.9 us), x 8 below
 MqGeom down_geom(uint32_t n_ff) {
-    return n_ff >= 24576 ? MqGeom{1, 2, 6, 1} : MqGeom{1, 2, 8, 1};
+    if (n_ff >= 24576) return MqGeom{1, 2, 6, 1};
+    return n_ff >= 16384 ? MqGeom{1, 2, 4, 2} : MqGeom{1, 2, 8, 1};
 }
 
 // ---- one fused op of the per-token plan, enqueued on the model stream ----

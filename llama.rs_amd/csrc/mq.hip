@@ -771,6 +771,7 @@ static MqFn pick(const MqGeom &g) {
     LRS_MQ_CASE(1, 2, 6, 1)
     LRS_MQ_CASE(1, 2, 8, 1)
     LRS_MQ_CASE(1, 2, 8, 2)
+    LRS_MQ_CASE(2, 2, 2, 1)
     // Q8_0 units are 64 elements: deeper prefetch over more K-slices
     if constexpr (T0 == T_Q8_0 && T1 == T_Q8_0 && EPI == MQ_STORE) {
         LRS_MQ_CASE(1, 1, 8, 6)

@@ -108,3 +108,29 @@ def test_config3_full_vocab_head_matvec(lrs, orc, c3):
     ref = orc.matvec(t, arr, C3_2L["n_embd"], C3_2L["vocab"], x, threads=THREADS)
     assert rel_l2(got, ref) < 1e-4, rel_l2(got, ref)
     W.free()
+
+
+# the config-4 FFN width (n_ff 17408) on a dense 2-layer model: its gate/up
+# launch shape (2 pairs x 2 K-slices, one unit in flight: 544 workgroups)
+# and down shape (2 tiles x 4 K-slices) run nowhere else at their real size
+C4_FFN = dict(C3_2L, n_ff=17408, vocab=4096)
+
+
+def test_config4_ffn_width_decode_matches_oracle(lrs, orc):
+    ctx = lrs.Context()
+    w = modelgen.host_model(orc, C4_FFN, seed=41, mode=0, d_lo=1e-3, d_hi=1e-2)
+    gm = modelgen.gpu_model(lrs, ctx, C4_FFN, w)
+    try:
+        om = orc.Model(C4_FFN, w, kv_f16=True, threads=THREADS)
+        prompt = np.random.default_rng(43).integers(0, C4_FFN["vocab"], 6).tolist()
+        for pos, t in enumerate(prompt):
+            g, o = gm.decode(t, pos), om.forward([t])
+            assert rel_l2(g, o) < LOGIT_TOL, (pos, rel_l2(g, o))
+            assert int(np.argmax(g)) == int(np.argmax(o)), pos
+        gm.reset()
+        want = modelgen.oracle_greedy(orc.Model(C4_FFN, w, kv_f16=True, threads=THREADS),
+                                      prompt, 8)
+        assert gm.generate_greedy(prompt, 8).tolist() == want
+    finally:
+        gm.close()
+        ctx.close()
