@@ -551,19 +551,19 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         __syncthreads();
     }
 
-    // per column: the same slot mapping over that column's pack (the zero
-    // slot is shared)
+    // column 0 reads the pack through lp/al; each further column c the same
+    // slot mapping over its own pack (the zero slot is shared).  Column 0
+    // stays out of the arrays: routed through them, the one-column kernels
+    // need more than 128 VGPRs and spill inside the main loop.
+    const ALane<T> al = alane<T>(lane, lp);
     LPack lpc[NC];
     ALane<T> alc[NC];
-    {
-        const ALane<T> al = alane<T>(lane, lp);
 #pragma unroll
-        for (int c = 0; c < NC; c++) {
-            lpc[c].zero = lp.zero;
-            lpc[c].meta = lp.meta + c * a.nxb * 16;
-            alc[c] = al;
-            if (al.base != lp.zero) alc[c].base = al.base + c * a.nxb * 96;
-        }
+    for (int c = 1; c < NC; c++) {
+        lpc[c].zero = lp.zero;
+        lpc[c].meta = lp.meta + c * a.nxb * 16;
+        alc[c] = al;
+        if (al.base != lp.zero) alc[c].base = al.base + c * a.nxb * 96;
     }
     float acc[NC][TPW], accm[NC][TPW];
 #pragma unroll
@@ -580,8 +580,9 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     for (; u0 + 2 * P <= u_hi; u0 += P) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
+            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
-            for (int c = 0; c < NC; c++)
+            for (int c = 1; c < NC; c++)
                 udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
 #pragma unroll
             for (int t = 0; t < TPW; t++)
@@ -595,8 +596,9 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
     for (int i = 0; i < P; i++) {
         if (u0 + i < u_hi) {
+            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
-            for (int c = 0; c < NC; c++)
+            for (int c = 1; c < NC; c++)
                 udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
             if (u0 + P + i < u_hi) {
 #pragma unroll
@@ -609,8 +611,9 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
     for (int i = 0; i < P; i++)
         if (u0 + i < u_hi) {
+            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
-            for (int c = 0; c < NC; c++)
+            for (int c = 1; c < NC; c++)
                 udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
         }
 
