@@ -110,25 +110,29 @@ def test_config3_full_vocab_head_matvec(lrs, orc, c3):
     W.free()
 
 
-# the config-4 FFN width (n_ff 17408) on a dense 2-layer model: its gate/up
-# launch shape (2 pairs x 2 K-slices, one unit in flight: 544 workgroups)
-# and down shape (2 tiles x 4 K-slices) run nowhere else at their real size
+# the other FFN widths on a dense 2-layer model, whose gate/up and down
+# launch shapes run nowhere else at their real size: config 4's 17408 (gate/up
+# 2 pairs x 2 K-slices with one unit in flight, 544 workgroups; down 2 tiles x
+# 4 K-slices) and config 2's 13824 (gate/up 2 pairs x 4 K-slices, 432
+# workgroups; down 2 tiles x 8 K-slices)
 C4_FFN = dict(C3_2L, n_ff=17408, vocab=4096)
+C2_FFN = dict(C3_2L, n_ff=13824, vocab=4096)
 
 
-def test_config4_ffn_width_decode_matches_oracle(lrs, orc):
+@pytest.mark.parametrize("cfg,seed", [(C4_FFN, 41), (C2_FFN, 47)], ids=["n_ff17408", "n_ff13824"])
+def test_ffn_width_decode_matches_oracle(lrs, orc, cfg, seed):
     ctx = lrs.Context()
-    w = modelgen.host_model(orc, C4_FFN, seed=41, mode=0, d_lo=1e-3, d_hi=1e-2)
-    gm = modelgen.gpu_model(lrs, ctx, C4_FFN, w)
+    w = modelgen.host_model(orc, cfg, seed=seed, mode=0, d_lo=1e-3, d_hi=1e-2)
+    gm = modelgen.gpu_model(lrs, ctx, cfg, w)
     try:
-        om = orc.Model(C4_FFN, w, kv_f16=True, threads=THREADS)
-        prompt = np.random.default_rng(43).integers(0, C4_FFN["vocab"], 6).tolist()
+        om = orc.Model(cfg, w, kv_f16=True, threads=THREADS)
+        prompt = np.random.default_rng(seed + 2).integers(0, cfg["vocab"], 6).tolist()
         for pos, t in enumerate(prompt):
             g, o = gm.decode(t, pos), om.forward([t])
             assert rel_l2(g, o) < LOGIT_TOL, (pos, rel_l2(g, o))
             assert int(np.argmax(g)) == int(np.argmax(o)), pos
         gm.reset()
-        want = modelgen.oracle_greedy(orc.Model(C4_FFN, w, kv_f16=True, threads=THREADS),
+        want = modelgen.oracle_greedy(orc.Model(cfg, w, kv_f16=True, threads=THREADS),
                                       prompt, 8)
         assert gm.generate_greedy(prompt, 8).tolist() == want
     finally:

@@ -34,11 +34,12 @@ def rel_l2(a, b):
 
 
 @pytest.mark.parametrize("t", [Q4_K, Q5_K, Q6_K, Q8_0])
-# (64, 256, 4096) and (96, 128, 8192) split K over workgroups (few output
-# tiles, long K); m >= 512 uses the 256-token tile at precision 1
+# (64, 256, 4096), (96, 128, 8192) and (512, 384, 4096) split K over
+# workgroups (few output tiles, long K); m >= 512 uses the 256-token tile at
+# precision 1 (ragged m and n included)
 @pytest.mark.parametrize("m,n,k", [(1, 200, 512), (7, 128, 256), (130, 300, 768), (256, 256, 1024),
                                    (64, 256, 4096), (96, 128, 8192), (512, 256, 1024),
-                                   (600, 200, 512)])
+                                   (600, 200, 512), (512, 384, 4096), (1000, 136, 2048)])
 def test_gemm_matches_oracle(lrs, orc, ctx, t, m, n, k):
     w = orc.gen_weight(t, 31 + m + n, n, k, mode=1)
     deq = orc.dequant(t, w).reshape(n, k)
