@@ -835,13 +835,66 @@ def prefill_line(a, m_tok, r):
                          "traffic": None, "mfma_work_per_flop": 3}}
 
 
+STREAM_SIZES = {  # algorithmic bytes of the config-3 decode launches
+    "o": 14807040, "qkv": 22089728, "down": 116273152, "gateup": 159404032, "head": 639318016}
+
+
+def bench_stream(ctx, steps):
+    """The read rate of a kernel that does nothing but stream (lrs_read_dev),
+    at each config-3 launch's byte count, best over 512 / 1024 / 2048
+    workgroups: windows of that size step through a 1 GiB arena, so no window
+    is still in the memory-side cache when it is read again (as in decode,
+    which streams ~20 GB per token)."""
+    arena = 1 << 30
+    buf = ctx.alloc(arena)
+    out = {}
+
+    def timed(size, nwin, nt, wg):
+        for i in range(2):  # warm-up
+            ctx.read_dev_at(buf, (i % nwin) * size, size, nt, wg)
+        ctx.sync()
+        ctx.timer_start()
+        for i in range(steps):
+            ctx.read_dev_at(buf, (i % nwin) * size, size, nt, wg)
+        return ctx.timer_stop() * 1e3 / steps
+
+    for name, size in STREAM_SIZES.items():
+        size -= size % 16
+        nwin = max(1, arena // size)
+        res = {}
+        for nt in (True, False):
+            per = {wg: timed(size, nwin, nt, wg) for wg in (512, 1024, 2048)}
+            wg = min(per, key=per.get)
+            res["nt" if nt else "plain"] = dict(us=round(per[wg], 2), workgroups=wg,
+                                                gbs=round(size / per[wg] / 1e3, 1))
+        # the same window read once with plain loads just before (memory-side
+        # cache warm), at the best non-temporal workgroup count
+        wg = res["nt"]["workgroups"]
+        tot, reps = 0.0, min(steps, 8)
+        for i in range(reps):
+            off = (i % nwin) * size
+            ctx.read_dev_at(buf, off, size, False, wg)
+            ctx.timer_start()
+            ctx.read_dev_at(buf, off, size, True, wg)
+            tot += ctx.timer_stop() * 1e3
+        us = tot / reps
+        res["nt_after_plain"] = dict(us=round(us, 2), workgroups=wg, gbs=round(size / us / 1e3, 1))
+        out[name] = dict(bytes=size, **res)
+        log(f"[bench] stream {name:7s} {size / 1e6:7.1f} MB: nt {res['nt']['us']:7.2f} us "
+            f"({res['nt']['gbs']:6.0f} GB/s, {res['nt']['workgroups']} workgroups), plain "
+            f"{res['plain']['us']:7.2f} us, nt after a plain read {us:7.2f} us "
+            f"({res['nt_after_plain']['gbs']:6.0f} GB/s)")
+    buf.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "hybrid", "q8", "layer", "gemm", "prefill", "pmc"])
+                    choices=["decode", "hybrid", "q8", "layer", "gemm", "prefill", "pmc", "stream"])
     ap.add_argument("--m", type=int, default=512,
                     help="gemm / prefill: prompt tokens (config 5: 128/512/2048)")
     ap.add_argument("--precision", type=int, default=1, choices=[1, 3],
@@ -865,6 +918,11 @@ def main():
     threads = min(16, os.cpu_count() or 1)
     if a.workload == "pmc":
         run_pmc(lrs, ctx)
+    elif a.workload == "stream":
+        r = bench_stream(ctx, a.steps)
+        print(json.dumps({"metric": "streaming read rate of a load-only kernel (lrs_read_dev)",
+                          "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "data": "uninitialised "
+                          "device memory (the values are not used)", "sizes": r}), flush=True)
     elif a.workload == "gemm":
         print(json.dumps(line_gemm(lrs, ctx, a, threads, a.m, a.precision)), flush=True)
     elif a.workload == "prefill":

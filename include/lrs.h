@@ -193,6 +193,15 @@ int lrs_capture_end(lrs_ctx *ctx, lrs_graph **out);
 int lrs_graph_launch(lrs_graph *g);
 void lrs_graph_destroy(lrs_graph *g);
 
+/* Measurement helper, no counterpart in the reference: one pass of plain
+ * (nontemporal 0) or non-temporal (1) 16-byte loads over bytes (a multiple of
+ * 16) of device memory by `workgroups` workgroups of 256 threads (1..4096,
+ * 0 = 1024), enqueued on the context stream; timed between lrs_timer_start /
+ * lrs_timer_stop it gives the read rate a kernel that does nothing but
+ * stream reaches, the practical ceiling of the matvec kernels. */
+int lrs_read_dev(lrs_ctx *ctx, const void *src_dev, size_t bytes, int nontemporal,
+                 uint32_t workgroups);
+
 /* HIP events on the context stream: start, then stop returns elapsed ms. */
 int lrs_timer_start(lrs_ctx *ctx);
 int lrs_timer_stop(lrs_ctx *ctx, float *ms);

@@ -530,6 +530,16 @@ void lrs_graph_destroy(lrs_graph *g) {
     delete g;
 }
 
+int lrs_read_dev(lrs_ctx *ctx, const void *src_dev, size_t bytes, int nontemporal,
+                 uint32_t workgroups) {
+    if (!ctx || !src_dev || bytes == 0 || bytes % 16 || workgroups > 4096)
+        return fail(LRS_E_ARG, "lrs_read_dev: null argument, bytes not a positive multiple of "
+                               "16, or more than 4096 workgroups");
+    SETDEV(ctx);
+    LRS_HIP(lrs::launch_read(src_dev, bytes, nontemporal != 0, workgroups, ctx->stream));
+    return LRS_OK;
+}
+
 int lrs_timer_start(lrs_ctx *ctx) {
     if (!ctx) return fail(LRS_E_ARG, "null ctx");
     SETDEV(ctx);

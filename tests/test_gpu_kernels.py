@@ -112,6 +112,25 @@ def test_dequant_rejects_bad_sizes(lrs, ctx):
             lrs.dequant_to_f32(ctx, t, bytes(bad))
 
 
+def test_read_probe_runs_and_rejects_bad_sizes(lrs, ctx):
+    """lrs_read_dev (the streaming-read measurement helper) reads a buffer in
+    both load forms and refuses a size that is not a multiple of 16 or runs
+    past the buffer."""
+    buf = ctx.alloc(1 << 20)
+    for nt in (True, False):
+        for wg in (0, 1, 512, 4096):
+            ctx.read_dev_at(buf, 0, 1 << 20, nt, wg)
+        ctx.read_dev_at(buf, 4096, 4096 + 16, nt)
+    ctx.sync()
+    with pytest.raises(lrs.ModelError):
+        ctx.read_dev_at(buf, 0, 24, True)
+    with pytest.raises(lrs.ModelError):
+        ctx.read_dev_at(buf, 0, 1 << 20, True, 4097)
+    with pytest.raises(AssertionError):
+        ctx.read_dev_at(buf, 16, 1 << 20, False)
+    buf.free()
+
+
 # --------------------------------------------------------------------------
 # weights: upload / download / synthetic generator
 # --------------------------------------------------------------------------
