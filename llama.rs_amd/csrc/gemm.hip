@@ -11,15 +11,16 @@
 //           lo*hi): ~2^-16 relative per product, for prefill whose logits must
 //           match the f32 reference
 //
-// Tiling.  A 512-thread workgroup owns a 128 (tokens) x 128 (weight rows)
-// output tile; each of its 8 wavefronts a 64 x 32 part = 2 MFMA tiles of
-// 32 x 32.  K advances 64 at a time: every thread stages 16 activations
+// Tiling.  A 512-thread workgroup owns a BM (tokens) x 128 (weight rows)
+// output tile: BM = 256 for bf16 operands at M >= 512 (each wavefront a
+// 64 x 64 part = 4 MFMA tiles of 32 x 32), else 128 (64 x 32 parts, 2
+// tiles).  K advances 64 at a time: every thread stages BM / 8 activations
 // (bf16, split from f32 once per GEMM input) and dequantizes 16 weights of
 // one row (f32 dequant as in dequant.rs, the K-quant min term in the same
-// fused multiply-add as the scale, then bf16) into a
-// double-buffered LDS tile, and each wavefront issues 4 K16 steps x 2 tiles
-// of MFMA.  LDS rows are padded to 72 bf16 so the 32 lanes that read 32
-// different rows at one K offset hit distinct banks.
+// fused multiply-add as the scale, then bf16) into a double-buffered LDS
+// tile, and each wavefront issues 4 K16 steps of MFMA over its tiles.  LDS
+// rows are padded to 72 bf16 so the 32 lanes that read 32 different rows at
+// one K offset hit distinct banks.
 #include "lrs_internal.h"
 #include "quant_dev.h"
 

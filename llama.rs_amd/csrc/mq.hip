@@ -34,7 +34,9 @@
 // with P units of loads in flight, then the K-slices are summed through LDS
 // and an epilogue writes the outputs (store, q/k/v with bias + RoPE + f16 KV
 // append, residual add, SwiGLU) and, for the residual and SwiGLU epilogues,
-// the pack of the next op's input.
+// the pack of the next op's input.  The plain matvec (k_mqx) instead packs
+// its f32 input inside each workgroup and runs up to NC input columns over
+// every weight load (each column bit-identical to a one-column call).
 #include "lrs_internal.h"
 #include "mq_args.h"
 #include "pack_dev.h"
