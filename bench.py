@@ -884,6 +884,23 @@ def bench_stream(ctx, steps):
             f"({res['nt']['gbs']:6.0f} GB/s, {res['nt']['workgroups']} workgroups), plain "
             f"{res['plain']['us']:7.2f} us, nt after a plain read {us:7.2f} us "
             f"({res['nt_after_plain']['gbs']:6.0f} GB/s)")
+    # the read rate of 160 workgroups (one per CU on 160 of the 256 CUs, as
+    # the decode down and o launches use) against 256, at down's size
+    size = STREAM_SIZES["down"] - STREAM_SIZES["down"] % 16
+    nwin = max(1, arena // size)
+    cap = {}
+    for wg, th in ((160, 256), (160, 768), (160, 1024), (256, 768), (256, 1024)):
+        ctx.read_dev_at(buf, 0, size, True, wg, th)
+        ctx.sync()
+        ctx.timer_start()
+        for i in range(steps):
+            ctx.read_dev_at(buf, (i % nwin) * size, size, True, wg, th)
+        us = ctx.timer_stop() * 1e3 / steps
+        cap[f"{wg}x{th}"] = dict(us=round(us, 2), gbs=round(size / us / 1e3, 1),
+                                 gbs_per_workgroup=round(size / us / 1e3 / wg, 1))
+        log(f"[bench] stream down-size, {wg} workgroups x {th} threads: {us:7.2f} us "
+            f"({size / us / 1e3:6.0f} GB/s, {size / us / 1e3 / wg:5.1f} per workgroup)")
+    out["down_by_workgroups"] = cap
     buf.free()
     return out
 

@@ -195,12 +195,13 @@ void lrs_graph_destroy(lrs_graph *g);
 
 /* Measurement helper, no counterpart in the reference: one pass of plain
  * (nontemporal 0) or non-temporal (1) 16-byte loads over bytes (a multiple of
- * 16) of device memory by `workgroups` workgroups of 256 threads (1..4096,
- * 0 = 1024), enqueued on the context stream; timed between lrs_timer_start /
- * lrs_timer_stop it gives the read rate a kernel that does nothing but
- * stream reaches, the practical ceiling of the matvec kernels. */
+ * 16) of device memory by `workgroups` workgroups (1..4096, 0 = 1024) of
+ * `threads` threads (a multiple of 64 up to 1024, 0 = 256), enqueued on the
+ * context stream; timed between lrs_timer_start / lrs_timer_stop it gives the
+ * read rate a kernel that does nothing but stream reaches, the practical
+ * ceiling of the matvec kernels. */
 int lrs_read_dev(lrs_ctx *ctx, const void *src_dev, size_t bytes, int nontemporal,
-                 uint32_t workgroups);
+                 uint32_t workgroups, uint32_t threads);
 
 /* HIP events on the context stream: start, then stop returns elapsed ms. */
 int lrs_timer_start(lrs_ctx *ctx);

@@ -80,7 +80,7 @@ def _load() -> C.CDLL:
         "lrs_capture_end": (i32, [vp, pvp]),
         "lrs_graph_launch": (i32, [vp]),
         "lrs_graph_destroy": (None, [vp]),
-        "lrs_read_dev": (i32, [vp, vp, sz, i32, u32]),
+        "lrs_read_dev": (i32, [vp, vp, sz, i32, u32, u32]),
         "lrs_timer_start": (i32, [vp]),
         "lrs_timer_stop": (i32, [vp, C.POINTER(C.c_float)]),
     }
@@ -154,12 +154,12 @@ class Context:
         return DeviceBuffer(self, nbytes)
 
     def read_dev_at(self, buf: "DeviceBuffer", offset: int, nbytes: int, nontemporal: bool,
-                    workgroups: int = 0) -> None:
+                    workgroups: int = 0, threads: int = 0) -> None:
         """One streaming read pass over nbytes of buf from offset by `workgroups`
-        workgroups (0 = 1024; lrs_read_dev)."""
+        workgroups of `threads` threads (0 = 1024 of 256; lrs_read_dev)."""
         assert 0 <= offset and offset + nbytes <= buf.nbytes
         check(lib.lrs_read_dev(self.h, buf.ptr + offset, nbytes, 1 if nontemporal else 0,
-                               workgroups))
+                               workgroups, threads))
 
     def timer_start(self) -> None:
         check(lib.lrs_timer_start(self.h))

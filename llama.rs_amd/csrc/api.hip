@@ -531,12 +531,14 @@ void lrs_graph_destroy(lrs_graph *g) {
 }
 
 int lrs_read_dev(lrs_ctx *ctx, const void *src_dev, size_t bytes, int nontemporal,
-                 uint32_t workgroups) {
-    if (!ctx || !src_dev || bytes == 0 || bytes % 16 || workgroups > 4096)
+                 uint32_t workgroups, uint32_t threads) {
+    if (!ctx || !src_dev || bytes == 0 || bytes % 16 || workgroups > 4096 || threads % 64 ||
+        threads > 1024)
         return fail(LRS_E_ARG, "lrs_read_dev: null argument, bytes not a positive multiple of "
-                               "16, or more than 4096 workgroups");
+                               "16, more than 4096 workgroups, or threads not a multiple of 64 "
+                               "up to 1024");
     SETDEV(ctx);
-    LRS_HIP(lrs::launch_read(src_dev, bytes, nontemporal != 0, workgroups, ctx->stream));
+    LRS_HIP(lrs::launch_read(src_dev, bytes, nontemporal != 0, workgroups, threads, ctx->stream));
     return LRS_OK;
 }
 

@@ -187,7 +187,7 @@ hipError_t launch_qk_prep(const float *qg, const float *kb, const float *vb, con
 // one streaming read pass over bytes (a multiple of 16) of device memory
 // (probe.hip, behind lrs_read_dev)
 hipError_t launch_read(const void *src, size_t bytes, bool nontemporal, uint32_t workgroups,
-                       hipStream_t s);
+                       uint32_t threads, hipStream_t s);
 
 }  // namespace lrs
 

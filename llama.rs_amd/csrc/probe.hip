@@ -14,10 +14,10 @@ constexpr uint32_t READ_MAX_WG = 4096;
 __device__ uint32_t g_read_sink[READ_MAX_WG];
 
 template <bool NT>
-__global__ __launch_bounds__(256) void k_read(const u32x4 *__restrict__ p, size_t n16) {
-    const size_t stride = (size_t)gridDim.x * 256;
+__global__ __launch_bounds__(1024) void k_read(const u32x4 *__restrict__ p, size_t n16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
     uint32_t acc = 0;
-    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     // four independent 16-byte loads per thread in flight
     for (; i + 3 * stride < n16; i += 4 * stride) {
         u32x4 v[4];
@@ -33,24 +33,28 @@ __global__ __launch_bounds__(256) void k_read(const u32x4 *__restrict__ p, size_
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) acc ^= __shfl_xor(acc, o, 64);
-    if (threadIdx.x == 0) g_read_sink[blockIdx.x] = acc;
+    if (threadIdx.x == 0) g_read_sink[blockIdx.x] = acc;  // one wavefront's word
 }
 
-// Workgroups of 256 threads stride over the buffer together (consecutive
-// workgroups read consecutive 4 KB), each thread with four 16-byte loads in
-// flight; the best count depends on the size (on MI355X 512 for >= 100 MB,
-// 2048 for ~20 MB), so the caller picks it (0 = 1024).
+// Workgroups of `threads` threads stride over the buffer together
+// (consecutive workgroups read consecutive 16 * threads bytes), each thread
+// with four 16-byte loads in flight.  The best workgroup count depends on the
+// size (on MI355X 512 of 256 threads for >= 100 MB, 2048 for ~20 MB), so the
+// caller picks it (0 = 1024; threads 0 = 256).
 hipError_t launch_read(const void *src, size_t bytes, bool nontemporal, uint32_t workgroups,
-                       hipStream_t s) {
-    if (!src || bytes == 0 || bytes % 16 || workgroups > READ_MAX_WG) return hipErrorInvalidValue;
+                       uint32_t threads, hipStream_t s) {
+    if (!threads) threads = 256;
+    if (!src || bytes == 0 || bytes % 16 || workgroups > READ_MAX_WG || threads % 64 ||
+        threads > 1024)
+        return hipErrorInvalidValue;
     const size_t n16 = bytes / 16;
     const uint32_t grid =
-        (uint32_t)std::min<size_t>(workgroups ? workgroups : 1024, (n16 + 255) / 256);
+        (uint32_t)std::min<size_t>(workgroups ? workgroups : 1024, (n16 + threads - 1) / threads);
     const u32x4 *p = reinterpret_cast<const u32x4 *>(src);
     if (nontemporal)
-        hipLaunchKernelGGL(k_read<true>, dim3(grid), dim3(256), 0, s, p, n16);
+        hipLaunchKernelGGL(k_read<true>, dim3(grid), dim3(threads), 0, s, p, n16);
     else
-        hipLaunchKernelGGL(k_read<false>, dim3(grid), dim3(256), 0, s, p, n16);
+        hipLaunchKernelGGL(k_read<false>, dim3(grid), dim3(threads), 0, s, p, n16);
     return hipGetLastError();
 }
 

@@ -126,6 +126,12 @@ def test_read_probe_runs_and_rejects_bad_sizes(lrs, ctx):
         ctx.read_dev_at(buf, 0, 24, True)
     with pytest.raises(lrs.ModelError):
         ctx.read_dev_at(buf, 0, 1 << 20, True, 4097)
+    for th in (64, 768, 1024):
+        ctx.read_dev_at(buf, 0, 1 << 20, True, 160, th)
+    ctx.sync()
+    for th in (96, 1088):
+        with pytest.raises(lrs.ModelError):
+            ctx.read_dev_at(buf, 0, 1 << 20, True, 160, th)
     with pytest.raises(AssertionError):
         ctx.read_dev_at(buf, 16, 1 << 20, False)
     buf.free()
