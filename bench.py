@@ -835,13 +835,15 @@ def prefill_line(a, m_tok, r):
                          "traffic": None, "mfma_work_per_flop": 3}}
 
 
-STREAM_SIZES = {  # algorithmic bytes of the config-3 decode launches
-    "o": 14807040, "qkv": 22089728, "down": 116273152, "gateup": 159404032, "head": 639318016}
+STREAM_SIZES = {  # algorithmic bytes of the decode launches (config 3, then configs 1, 2, 4)
+    "o": 14807040, "qkv": 22089728, "down": 116273152, "gateup": 159404032, "head": 639318016,
+    "q8_matvec": 17858560, "l14_gateup": 79722496, "l14_down": 58157056,
+    "hybrid_gateup": 100380672, "hybrid_down": 73224192}
 
 
 def bench_stream(ctx, steps):
     """The read rate of a kernel that does nothing but stream (lrs_read_dev),
-    at each config-3 launch's byte count, best over 512 / 1024 / 2048
+    at each decode launch's byte count, best over 512 / 1024 / 2048
     workgroups: windows of that size step through a 1 GiB arena, so no window
     is still in the memory-side cache when it is read again (as in decode,
     which streams ~20 GB per token)."""
