@@ -200,13 +200,14 @@ MqGeom gateup_geom(uint32_t n_ff) {
     if (t / 4 >= 400) return MqGeom{2, 4, 2, 2};
     return t / 2 <= 512 ? MqGeom{2, 2, 4, 2} : MqGeom{2, 2, 2, 1};
 }
-// down (n_embd rows), one unit in flight per wavefront where that measured
-// best (with non-temporal weight loads the deeper prefetch was ~4 % slower
-// at 27648): 2 tiles x 6 K-slices for 27648, x 4 with two units in flight
-// for 16384..24575 (17408: 17.4 against 17.9 us), x 8 below
+// down (n_embd rows): 2 tiles x 6 K-slices with one unit in flight per
+// wavefront (with non-temporal weight loads the deeper prefetch was ~4 %
+// slower at 27648; at 13824 it beats 8 K-slices, 14.0 against 14.3 us),
+// except x 4 K-slices with two units in flight for 16384..24575 (17408:
+// 17.4 against 17.9 us for 8 K-slices and 18.5 for 6)
 MqGeom down_geom(uint32_t n_ff) {
-    if (n_ff >= 24576) return MqGeom{1, 2, 6, 1};
-    return n_ff >= 16384 ? MqGeom{1, 2, 4, 2} : MqGeom{1, 2, 8, 1};
+    if (n_ff >= 16384 && n_ff < 24576) return MqGeom{1, 2, 4, 2};
+    return MqGeom{1, 2, 6, 1};
 }
 
 // ---- one fused op of the per-token plan, enqueued on the model stream ----

@@ -114,7 +114,7 @@ def test_config3_full_vocab_head_matvec(lrs, orc, c3):
 # launch shapes run nowhere else at their real size: config 4's 17408 (gate/up
 # 2 pairs x 2 K-slices with one unit in flight, 544 workgroups; down 2 tiles x
 # 4 K-slices) and config 2's 13824 (gate/up 2 pairs x 4 K-slices, 432
-# workgroups; down 2 tiles x 8 K-slices)
+# workgroups; down 2 tiles x 6 K-slices, as config 3's)
 C4_FFN = dict(C3_2L, n_ff=17408, vocab=4096)
 C2_FFN = dict(C3_2L, n_ff=13824, vocab=4096)
 
