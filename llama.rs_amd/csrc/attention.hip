@@ -6,11 +6,14 @@
 // GPU path keeps them (kv_pack.comp).
 //
 // Split over positions ("flash decode"): workgroup (split s, KV head kh)
-// takes positions [s*chunk, (s+1)*chunk) of 0..pos for all REP query heads
-// of the GQA group (K and V are read once for the group).  A "lane group" of
-// HD/8 lanes owns one position at a time (8 dims = one 16-byte piece of the K
-// and V rows per lane; lane group g takes positions g, g+NG, ..., with the
-// next positions' loads in flight):
+// takes the blocks of ATT_BLOCK positions s, s + S, s + 2S, ... (S = splits)
+// of 0..pos for all REP query heads of the GQA group (K and V are read once
+// for the group).  The blocks a split owns do not depend on pos, so every
+// workgroup issues its first K/V (and q) loads before the position arrives
+// from the step buffer; pos only masks.  A "lane group" of HD/8 lanes owns
+// one position at a time (8 dims = one 16-byte piece of the K and V rows per
+// lane; lane group g takes the split's positions g, g+NG, ... in block order,
+// with the next positions' loads in flight):
 //   score    q is split into f16 hi + lo halves so v_dot2_f32_f16 forms q.k
 //            from exact f16 products to 22 bits of q; the row sum over the
 //            lane group is four DPP adds
@@ -21,15 +24,17 @@
 // (acc, m, l) partial of the split.  A second kernel, one workgroup per query
 // head, merges the splits the same way (the identity of attention_split.comp
 // + attn_reduce.comp) and writes the output as the activation pack of the
-// o-projection.  The split spreads the K/V stream over ~256 workgroups: one
-// CU streams only ~35 GB/s.
+// o-projection; it loads every split's partial while the position is in
+// flight and weighs only the splits that hold positions.  The split spreads
+// the K/V stream over ~256 workgroups: one CU streams only ~35 GB/s.
 #include "lrs_internal.h"
 #include "pack_dev.h"
 
 namespace lrs {
 
 constexpr int ATT_THREADS = 256;
-constexpr int ATT_DEPTH = 4;  // positions per lane group with K and V loads in flight
+constexpr int ATT_DEPTH = 4;    // positions per lane group with K and V loads in flight
+constexpr uint32_t ATT_BLOCK = 16;  // positions per block; split s owns blocks s, s + splits, ...
 
 struct AttnArgs {
     const float *q;           // [n_head * HD], RoPE applied
@@ -37,15 +42,14 @@ struct AttnArgs {
     float *part;              // [n_head][splits][HD + 4]: acc[HD], m, l
     const uint32_t *step;     // {token, pos}: attends positions 0..pos
     uint32_t n_head, n_kv, ctx, splits;
-    uint32_t minchunk;        // positions per split at least (short contexts use fewer splits)
     float scale;
 };
 
-// positions per split of a context of L positions: L spread over `splits`,
-// but at least `minchunk` (the splits past the last position have no work)
-__device__ __forceinline__ uint32_t attn_chunk(uint32_t L, uint32_t splits, uint32_t minchunk) {
-    const uint32_t c = (L + splits - 1) / splits;
-    return c > minchunk ? c : minchunk;
+// the splits that hold positions of a context of L positions (the others
+// have no work and write no partial)
+__device__ __forceinline__ uint32_t attn_live_splits(uint32_t L, uint32_t splits) {
+    const uint32_t b = (L + ATT_BLOCK - 1) / ATT_BLOCK;
+    return b < splits ? b : splits;
 }
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -70,6 +74,16 @@ __device__ __forceinline__ float row_max(float v) {
     v = fmaxf(v, dpp_f<0x141>(v));
     return fmaxf(v, dpp_f<0x140>(v));
 }
+// max over aligned groups of N lanes (N = 8, 16, 32) in every lane
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    if constexpr (N >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+    if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return v;
+}
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
     v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
@@ -84,27 +98,43 @@ template <int HD, int REP>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     constexpr int LP = HD / 8;              // lanes per position
     constexpr int NG = ATT_THREADS / LP;    // lane groups per workgroup
+    static_assert(REP * NG <= ATT_THREADS, "one thread per (query head, lane group) in the merge");
     __shared__ float sm[NG][REP], sl[NG][REP], sw[NG][REP];
     __shared__ float sacc[NG][REP][HD];
     const uint32_t tid = threadIdx.x, sub = tid % LP, grp = tid / LP;
     const uint32_t sp = blockIdx.x, kh = blockIdx.y, h0 = kh * REP;
-    const uint32_t L = a.step[1] + 1;
-    const uint32_t chunk = attn_chunk(L, a.splits, a.minchunk);
-    if (sp * chunk >= L) return;  // no position in this split (the combine skips it)
-    const uint32_t p0 = sp * chunk, n = min(p0 + chunk, L) - p0;
-    const _Float16 *kb = a.kc + ((size_t)kh * a.ctx + p0) * HD + 8 * sub;
-    const _Float16 *vb = a.vc + ((size_t)kh * a.ctx + p0) * HD + 8 * sub;
+    const uint32_t S = a.splits * ATT_BLOCK;  // positions between two blocks of a split
+    // position of this lane group's k-th slot: slot t = k NG + grp of the
+    // split is position t % ATT_BLOCK of the split's block t / ATT_BLOCK
+    auto slot_pos = [&](uint32_t k) {
+        const uint32_t t = k * NG + grp;
+        return sp * ATT_BLOCK + (t / ATT_BLOCK) * S + t % ATT_BLOCK;
+    };
+    const _Float16 *kb = a.kc + (size_t)kh * a.ctx * HD + 8 * sub;
+    const _Float16 *vb = a.vc + (size_t)kh * a.ctx * HD + 8 * sub;
 
-    // K and V of the first ATT_DEPTH positions of every lane group in flight
+    // q of the REP heads, and K and V of the first ATT_DEPTH slots of every
+    // lane group, before the position is known (slots past the position are
+    // in the cache allocation and are never used)
+    float4 qx[REP][2];
+#pragma unroll
+    for (int r = 0; r < REP; r++) {
+        const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)(h0 + r) * HD + 8 * sub);
+        qx[r][0] = qp[0];
+        qx[r][1] = qp[1];
+    }
     uint4 kr[ATT_DEPTH], vr[ATT_DEPTH];
 #pragma unroll
     for (int i = 0; i < ATT_DEPTH; i++) {
-        const uint32_t p = grp + i * NG;
-        if (p < n) {
+        const uint32_t p = slot_pos(i);
+        if (p < a.ctx) {
             kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)p * HD);
             vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)p * HD);
         }
     }
+    const uint32_t L = a.step[1] + 1;
+    if (sp * ATT_BLOCK >= L) return;  // no position in this split (the combine skips it)
+
     // q / 2^e as f16 hi + lo pairs (dims 8 sub .. 8 sub + 7), 2^e >= max |q|
     // of the head so both halves stay in f16 range; the score is rescaled
     // by 2^e * scale (exact power of two, then the reference's 1/sqrt(HD))
@@ -112,14 +142,12 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     float sscale[REP];
 #pragma unroll
     for (int r = 0; r < REP; r++) {
-        const float4 *qp = reinterpret_cast<const float4 *>(a.q + (size_t)(h0 + r) * HD + 8 * sub);
-        const float4 x0 = qp[0], x1 = qp[1];
+        const float4 x0 = qx[r][0], x1 = qx[r][1];
         float qv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
         float qm = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) qm = fmaxf(qm, fabsf(qv[i]));
-#pragma unroll
-        for (int o = LP / 2; o >= 1; o >>= 1) qm = fmaxf(qm, __shfl_xor(qm, o, 64));
+        qm = group_max<LP>(qm);
         int e;
         frexpf(qm, &e);
         e = e < -60 ? -60 : e;
@@ -143,14 +171,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[r][e] = 0.f;
     }
-    for (uint32_t q0 = grp; q0 < n; q0 += ATT_DEPTH * NG) {
+    // slot positions grow with the slot, so the first slot past L ends the walk
+    for (uint32_t k0 = 0; slot_pos(k0) < L; k0 += ATT_DEPTH) {
 #pragma unroll
         for (int i = 0; i < ATT_DEPTH; i++) {
-            const uint32_t p = q0 + i * NG;
-            if (p < n) {  // uniform within the lane group
+            const uint32_t p = slot_pos(k0 + i);
+            if (p < L) {  // uniform within the lane group
                 const uint4 k = kr[i], v = vr[i];
-                const uint32_t pn = p + ATT_DEPTH * NG;
-                if (pn < n) {
+                const uint32_t pn = slot_pos(k0 + i + ATT_DEPTH);
+                if (pn < L) {
                     kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)pn * HD);
                     vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)pn * HD);
                 }
@@ -191,23 +220,21 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) sacc[grp][r][8 * sub + e] = acc[r][e];
     __syncthreads();
-    if (tid < REP) {
-        // head r: split max M, weights e^(m_g - M) of the lane groups (0 for a
-        // group with no position) and the denominator sum_g w_g l_g
-        const uint32_t r = tid;
-        float M = -INFINITY;
-#pragma unroll
-        for (int g = 0; g < NG; g++) M = fmaxf(M, sm[g][r]);
-        float den = 0.f;
-#pragma unroll
-        for (int g = 0; g < NG; g++) {
-            const float w = sm[g][r] == -INFINITY ? 0.f : expf(sm[g][r] - M);
-            sw[g][r] = w;
-            den = fmaf(w, sl[g][r], den);
+    if (tid < REP * NG) {
+        // thread (head r, lane group g), whole groups of NG aligned lanes:
+        // split max M of head r, weight e^(m_g - M) of group g (0 for a group
+        // with no position) and the denominator sum_g w_g l_g
+        const uint32_t r = tid / NG, g = tid % NG;
+        const float mg = sm[g][r];
+        const float M = group_max<NG>(mg);
+        const float w = mg == -INFINITY ? 0.f : expf(mg - M);
+        sw[g][r] = w;
+        const float den = group_sum<NG>(w * sl[g][r]);
+        if (g == 0) {
+            float *pp = a.part + ((size_t)(h0 + r) * a.splits + sp) * (HD + 4);
+            pp[HD] = M;
+            pp[HD + 1] = den;
         }
-        float *pp = a.part + ((size_t)(h0 + r) * a.splits + sp) * (HD + 4);
-        pp[HD] = M;  // -inf: an empty split, no weight
-        pp[HD + 1] = den;
     }
     __syncthreads();
     for (uint32_t i = tid; i < REP * HD; i += ATT_THREADS) {
@@ -222,11 +249,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
 typedef __attribute__((address_space(3))) void lds_void;
 
 // combine of the split partials of head blockIdx.x: the head's partial block
-// goes to LDS in one round trip (global_load_lds), then thread d owns dim d
+// (every split's, issued before the position arrives) goes to LDS in one
+// round trip (global_load_lds), then thread d owns dim d
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ part, uint32_t splits,
                                                      const uint32_t *__restrict__ step,
-                                                     uint32_t minchunk,
                                                      const float *__restrict__ gate,
                                                      uint32_t gstride, XPack out) {
     extern __shared__ __attribute__((aligned(16))) float pl[];  // [splits][HD + 4]
@@ -234,15 +261,15 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     constexpr uint32_t ST = HD + 4;
     const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
     const uint8_t *src = reinterpret_cast<const uint8_t *>(part + (size_t)h * splits * ST);
-    // the splits that hold positions (the split kernel skipped the others)
-    const uint32_t L = step[1] + 1, chunk = attn_chunk(L, splits, minchunk);
-    splits = (L + chunk - 1) / chunk;
     const uint32_t bytes = splits * ST * 4;  // multiple of 16
     for (uint32_t base = wave * 1024; base < bytes; base += HD * 16) {
         const uint32_t off = base + lane * 16;
         if (off < bytes)
             __builtin_amdgcn_global_load_lds(src + off, (lds_void *)(reinterpret_cast<uint8_t *>(pl) + base), 16, 0, 0);
     }
+    // the splits that hold positions (the split kernel wrote no partial for
+    // the others; what their slots hold is not used)
+    splits = attn_live_splits(step[1] + 1, splits);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     // wave 0: M = max over the splits (splits <= 64), weights, denominator
@@ -270,12 +297,11 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
 
 // split count: about one workgroup per CU (256 = splits x KV heads), at
 // most 32 (measured on the decode benches: 32 splits beat 64 for 4 KV heads
-// x 256 dims, and 16 / 32 tie for 8 x 128; 8 and 64 are slower)
-// at least 16 positions per split: a context of L < 16 * splits positions
-// runs ceil(L / 16) splits and the combine reads only those (measured on the
-// config-3 decode: 32 and 64 per split are no faster at 512 positions, 128
-// and 256 slower, and the config-4 attention is slower at 64)
-static uint32_t attn_minchunk() { return 16u; }
+// x 256 dims, and 16 / 32 tie for 8 x 128; 8 and 64 are slower).  Blocks of
+// 16 positions: a context of L < 16 * splits positions runs ceil(L / 16)
+// splits (measured on the config-3 decode as contiguous ranges of at least
+// 16 positions per split: 32 and 64 are no faster at 512 positions, 128 and
+// 256 slower, and the config-4 attention is slower at 64)
 
 uint32_t attn_splits(uint32_t n_kv) {
     const uint32_t S = 256 / n_kv;
@@ -312,7 +338,6 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
     a.n_kv = n_kv;
     a.ctx = ctx;
     a.splits = splits;
-    a.minchunk = attn_minchunk();
     a.scale = 1.0f / sqrtf((float)head_dim);
     if (n_kv == 0 || n_head % n_kv || splits == 0) return hipErrorInvalidValue;
     const uint32_t rep = n_head / n_kv;
@@ -327,11 +352,10 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
     if (!fn) return hipErrorInvalidValue;
     hipLaunchKernelGGL(fn, grid, dim3(ATT_THREADS), 0, s, a);
     const size_t cl = (size_t)splits * (head_dim + 4) * sizeof(float);
-    const uint32_t mc = a.minchunk;
     switch (head_dim) {
-    case 64: hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), cl, s, part, splits, step, mc, gate, gstride, out); break;
-    case 128: hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_head), dim3(128), cl, s, part, splits, step, mc, gate, gstride, out); break;
-    default: hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_head), dim3(256), cl, s, part, splits, step, mc, gate, gstride, out); break;
+    case 64: hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), cl, s, part, splits, step, gate, gstride, out); break;
+    case 128: hipLaunchKernelGGL(k_attn_combine<128>, dim3(n_head), dim3(128), cl, s, part, splits, step, gate, gstride, out); break;
+    default: hipLaunchKernelGGL(k_attn_combine<256>, dim3(n_head), dim3(256), cl, s, part, splits, step, gate, gstride, out); break;
     }
     return hipGetLastError();
 }

@@ -779,7 +779,7 @@ static MqFn pick(const MqGeom &g) {
     LRS_MQ_CASE(2, 2, 2, 1)
     // Q8_0 units are 64 elements: deeper prefetch over more K-slices
     if constexpr (T0 == T_Q8_0 && T1 == T_Q8_0 && EPI == MQ_STORE) {
-        LRS_MQ_CASE(1, 1, 8, 6)
+        LRS_MQ_CASE(1, 1, 16, 4)
     }
 #undef LRS_MQ_CASE
     return nullptr;
@@ -900,9 +900,11 @@ int set_matvec_geom(int tpw, int tg, int ks) {
 MqGeom store_geom(uint32_t t, uint32_t n_in, uint32_t n_out) {
     (void)n_in;
     if (g_store_override.tpw) return g_store_override;
-    // Q8_0 (config 1, 4096 x 4096): 8 K-slices with 6 of its 64-element units
-    // in flight per wavefront: 6.1 us against 9.3 us at the K-quant shape
-    if (t == T_Q8_0) return {1, 1, 8, 6};
+    // Q8_0 (config 1, 4096 x 4096): one tile x 16 K-slices with 4 of its
+    // 64-element units in flight per wavefront (every unit of a wavefront in
+    // one round of loads): 7.0 us per in-launch-packed matvec against 7.6 at
+    // 8 K-slices x 6 units and 9.3 at the K-quant shape
+    if (t == T_Q8_0) return {1, 1, 16, 4};
     const uint32_t tiles = ttiles(n_out);
     if (tiles >= 1024) return {1, 2, 2, 2};
     if (tiles >= 256) return {1, 2, 4, 2};
@@ -951,7 +953,7 @@ static MqFn pick_nc(int nc) {
 template <uint32_t T>
 static MqFn pick_x_geom(const MqGeom &g, int nc) {
     if constexpr (T == T_Q8_0) {
-        if (g.tpw == 1 && g.tg == 1 && g.ks == 8 && g.p == 6) return pick_nc<T, 1, 1, 8, 6>(nc);
+        if (g.tpw == 1 && g.tg == 1 && g.ks == 16 && g.p == 4) return pick_nc<T, 1, 1, 16, 4>(nc);
     } else {
         if (g.tpw == 1 && g.tg == 2 && g.ks == 2 && g.p == 2) return pick_nc<T, 1, 2, 2, 2>(nc);
         if (g.tpw == 1 && g.tg == 2 && g.ks == 4 && g.p == 2) return pick_nc<T, 1, 2, 4, 2>(nc);
