@@ -113,9 +113,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     const _Float16 *kb = a.kc + (size_t)kh * a.ctx * HD + 8 * sub;
     const _Float16 *vb = a.vc + (size_t)kh * a.ctx * HD + 8 * sub;
 
-    // q of the REP heads, and K and V of the first ATT_DEPTH slots of every
-    // lane group, before the position is known (slots past the position are
-    // in the cache allocation and are never used)
+    // q of the REP heads, and K and V of this lane group's slots in the
+    // split's first block, before the position is known (slots past the
+    // position are in the cache allocation and are never used; the later
+    // blocks wait for the position, so a short context reads no more than
+    // one block per split)
     float4 qx[REP][2];
 #pragma unroll
     for (int r = 0; r < REP; r++) {
@@ -127,13 +129,21 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < ATT_DEPTH; i++) {
         const uint32_t p = slot_pos(i);
-        if (p < a.ctx) {
+        if (i * NG + grp < ATT_BLOCK && p < a.ctx) {
             kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)p * HD);
             vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)p * HD);
         }
     }
     const uint32_t L = a.step[1] + 1;
     if (sp * ATT_BLOCK >= L) return;  // no position in this split (the combine skips it)
+#pragma unroll
+    for (int i = 0; i < ATT_DEPTH; i++) {
+        const uint32_t p = slot_pos(i);
+        if (i * NG + grp >= ATT_BLOCK && p < L) {
+            kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)p * HD);
+            vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)p * HD);
+        }
+    }
 
     // q / 2^e as f16 hi + lo pairs (dims 8 sub .. 8 sub + 7), 2^e >= max |q|
     // of the head so both halves stay in f16 range; the score is rescaled

@@ -58,6 +58,32 @@ def test_hybrid_decode_and_greedy_match_oracle(lrs, orc, ctx, name, cfg, mix):
     assert got == want
 
 
+def test_hybrid_long_context_decode_matches_oracle(lrs, orc, ctx):
+    """The gated attention layers (6 query heads over one 256-dim KV head,
+    k_attn<256, 6>) at cache lengths where the position splits own one and
+    two 16-position blocks; every token through decode(), checked at the
+    lengths below against the oracle."""
+    cfg = dict(modelgen.HY_MID, ctx=640)
+    checks = (1, 17, 512, 513, 600)
+    w = modelgen.hybrid_host_model(orc, cfg, seed=23)
+    gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
+    om = orc.HybridModel(cfg, w, kv_f16=True, threads=8)
+    seq = np.random.default_rng(13).integers(0, cfg["vocab"], max(checks)).tolist()
+    done, worst = 0, 0.0
+    for pos, t in enumerate(seq):
+        g = gm.decode(t, pos)
+        n = pos + 1
+        if n in checks:
+            o = om.forward(seq[done:n])
+            done = n
+            e = rel_l2(g, o)
+            worst = max(worst, e)
+            assert e < LOGIT_TOL, (n, e)
+            assert int(np.argmax(g)) == int(np.argmax(o)), n
+    gm.close()
+    print(f"hy-mid long: worst rel L2 {worst:.2e} at lengths {checks}")
+
+
 def test_hybrid_batch_reset_and_position_rule(lrs, orc, ctx):
     """decode_batch runs the prompt block through the GEMMs, the block
     delta-net kernels and the batched gated attention; the token loop and the

@@ -69,6 +69,43 @@ def test_decode_logits_and_greedy_match_oracle(lrs, orc, ctx, name, cfg, mix, mo
     assert got == want
 
 
+# cache lengths where each of the 32 position splits of the decode attention
+# owns one, two or three 16-position blocks (a split's blocks are 512
+# positions apart), and lengths one past each boundary
+LONG_CHECKS = (1, 16, 17, 511, 512, 513, 1024, 1025, 1041)
+LONG_CASES = [
+    # k_attn<128, 5>: 16 lane groups, one block per round
+    ("gqa5", dict(modelgen.GQA5, ctx=1100)),
+    # k_attn<64, 2>: 32 lane groups, two blocks per round
+    ("tiny", dict(modelgen.TINY, ctx=1100)),
+]
+
+
+@pytest.mark.parametrize("name,cfg", LONG_CASES, ids=[c[0] for c in LONG_CASES])
+def test_long_context_decode_matches_oracle(lrs, orc, ctx, name, cfg):
+    """attention.rs:76-166 over up to 1041 cached positions: every token goes
+    through decode(); the logits at the lengths of LONG_CHECKS are checked
+    against the oracle at the 1e-3 bar with the same argmax."""
+    print(f"case {name}", flush=True)
+    w = modelgen.host_model(orc, cfg, seed=29, mode=0, d_lo=1e-3, d_hi=1e-2)
+    gm = modelgen.gpu_model(lrs, ctx, cfg, w)
+    om = orc.Model(cfg, w, kv_f16=True, threads=8)
+    seq = np.random.default_rng(11).integers(0, cfg["vocab"], max(LONG_CHECKS)).tolist()
+    done, worst = 0, 0.0
+    for pos, t in enumerate(seq):
+        g = gm.decode(t, pos)
+        n = pos + 1
+        if n in LONG_CHECKS:
+            o = om.forward(seq[done:n])
+            done = n
+            e = rel_l2(g, o)
+            worst = max(worst, e)
+            assert e < LOGIT_TOL, (name, n, e)
+            assert int(np.argmax(g)) == int(np.argmax(o)), (name, n)
+    gm.close()
+    print(f"{name}: worst rel L2 {worst:.2e} at lengths {LONG_CHECKS}")
+
+
 # Q8_0 and K-quant weights sharing inputs: q/k Q8_0 with v Q6_K, o and down
 # Q8_0 after K-quant producers, a Q8_0 head
 MIXED_Q8_0 = dict(modelgen.Q4_K_M, attn_q=modelgen.Q8_0, attn_k=modelgen.Q8_0,
