@@ -277,6 +277,9 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
         if (off < bytes)
             __builtin_amdgcn_global_load_lds(src + off, (lds_void *)(reinterpret_cast<uint8_t *>(pl) + base), 16, 0, 0);
     }
+    // the output gate of (head h, dim d) for the gated attention, loaded with
+    // the partials
+    const float gv = gate ? gate[(size_t)h * gstride + d] : 0.f;
     // the splits that hold positions (the split kernel wrote no partial for
     // the others; what their slots hold is not used)
     splits = attn_live_splits(step[1] + 1, splits);
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     for (uint32_t s = 0; s < splits; s++) num = fmaf(wsh[s], pl[s * ST + d], num);
     float o = num / den;
     // gated attention (gate_quant.comp): o * sigmoid(gate of head h, dim d)
-    if (gate) o = o * (1.0f / (1.0f + expf(-gate[(size_t)h * gstride + d])));
+    if (gate) o = o * (1.0f / (1.0f + expf(-gv)));
     pack_half(o, (h * HD + d) >> 5, out);
 }
 

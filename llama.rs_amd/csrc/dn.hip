@@ -84,12 +84,14 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
     // (dn_conv.comp); the current input goes to ring slot pos % W, written
     // once per channel: q/k by workgroup 0 of value head kh, v by its owner.
     // Two channels per thread (2D + 32 <= 512); their loads, like the gate
-    // rows' below, are issued before any of them is used.
-    const uint32_t pos = a.step[1];
-    const uint32_t W = a.d_conv, wslot = pos % W;
+    // rows' below, are issued before any of them is used.  All W ring slots
+    // are loaded (none of these loads waits for the position); the position
+    // then picks the W - 1 previous inputs among them (slot pos % W, which
+    // another workgroup may be overwriting, is never picked).
+    const uint32_t W = a.d_conv;
     const bool own_qk = r == 0 && hh < a.k_heads;
     constexpr int WM = 8;  // d_conv <= 8
-    float xc[2], wt[2][WM], wn[2][WM];
+    float xc[2], wt[2][WM], wa[2][WM];
     uint32_t chs[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -102,11 +104,22 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
             xc[u] = a.qkv[ch];
 #pragma unroll
             for (int t = 0; t < WM; t++) {
-                if ((uint32_t)t < W) wt[u][t] = a.conv_w[(size_t)ch * W + t];
-                if ((uint32_t)t + 1 < W) wn[u][t] = a.win[(size_t)((pos + 1 + t) % W) * CD + ch];
+                if ((uint32_t)t < W) {
+                    wt[u][t] = a.conv_w[(size_t)ch * W + t];
+                    wa[u][t] = a.win[(size_t)t * CD + ch];
+                }
             }
         }
     }
+    // the read-out's gate z and norm weight of this workgroup's 32 rows, for
+    // the pack at the end
+    float zr = 0.f, nr = 0.f;
+    if (tid < 32) {
+        zr = a.z[(size_t)hh * D + 32 * r + tid];
+        nr = a.norm_w[32 * r + tid];
+    }
+    const uint32_t pos = a.step[1];
+    const uint32_t wslot = pos % W;
     // gate projections of hn = rmsnorm(x) * attn_norm (dn_gates.comp): every
     // load of a thread's elements is issued before the first product
     {
@@ -152,8 +165,17 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
             if (c >= 2 * D + 32) continue;
             float acc = 0.f;
 #pragma unroll
-            for (int t = 0; t < WM; t++)
-                if ((uint32_t)t + 1 < W) acc += wn[u][t] * wt[u][t];
+            for (int t = 0; t < WM; t++) {
+                if ((uint32_t)t + 1 < W) {
+                    // input pos - W + 1 + t, in ring slot (pos + 1 + t) % W
+                    const uint32_t sl = (pos + 1 + t) % W;
+                    float wn = wa[u][0];
+#pragma unroll
+                    for (int q = 1; q < WM; q++)
+                        if ((uint32_t)q == sl) wn = wa[u][q];
+                    acc += wn * wt[u][t];
+                }
+            }
             float wl = wt[u][0];
 #pragma unroll
             for (int t = 1; t < WM; t++)
@@ -239,8 +261,7 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
     if (tid < 32) {
         const uint32_t jj = 32 * r + tid;
         const float ov = so[tid];
-        const float zz = a.z[(size_t)hh * D + jj];
-        const float y = ov * (a.norm_w[jj] * (zz / (1.0f + expf(-zz))));
+        const float y = ov * (nr * (zr / (1.0f + expf(-zr))));
         pack_half(y, (hh * D + jj) >> 5, a.out);
         float p = ov * ov;
 #pragma unroll

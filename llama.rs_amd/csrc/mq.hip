@@ -525,6 +525,26 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.meta), lds + lp.meta, a.nxb * 16);
     }
     if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + lp.zero)[threadIdx.x] = 0u;
+    // the epilogue's operands of this thread's output (thread i owns output i
+    // of the workgroup): loaded here, with the weights, so that no load is
+    // left for after the main loop (the position and RoPE frequency, the
+    // bias, the residual and its norm weight)
+    const uint32_t eo = threadIdx.x, erow = tile0 * 16 + eo;
+    const bool evalid = eo < otiles_wg * 16 && erow < sg.rows;
+    float e_bias = 0.f, e_x = 0.f, e_nw = 1.f, e_freq = 0.f;
+    uint32_t e_pos = 0;
+    if (sg.bias && evalid) e_bias = sg.bias[erow];
+    if constexpr (EPI == MQ_QKV) {
+        e_pos = a.step[1];
+        const uint32_t dd = erow % a.head_dim;
+        if (evalid && sg.kind < 2 && dd < a.rope_dim) e_freq = a.freq[dd >> 1];
+    }
+    if constexpr (EPI == MQ_RESID) {
+        if (evalid) {
+            e_x = a.x[erow];
+            if (a.nw) e_nw = a.nw[erow];
+        }
+    }
     float ss = 0.f;
     if (a.xres) {
         for (uint32_t i = 4 * threadIdx.x; i < a.n_in; i += 4 * blockDim.x) {
@@ -675,7 +695,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     const uint32_t grp = pair ? (ii >> 4) : (ii >> 4) / TPW;
     const uint32_t tt = pair ? 0 : (ii >> 4) % TPW;
     float y = s * partial(grp, tt, ii & 15);
-    if (sg.bias && valid) y = y + sg.bias[row];
+    if (sg.bias && valid) y = y + e_bias;
     if constexpr (NC > 1) {
         // several columns: column c's outputs at out + c * ostride
         if (valid) {
@@ -683,7 +703,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
             for (int c = 1; c < NC; c++) {
                 float yc = s * partial(grp, tt, ii & 15, c);
-                if (sg.bias) yc = yc + sg.bias[row];
+                if (sg.bias) yc = yc + e_bias;
                 sg.out[(size_t)c * a.ostride + row] = yc;
             }
         }
@@ -700,12 +720,12 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
             if (lane == 0) a.amax[(size_t)blockIdx.x * ((otiles_wg * 16 + 63) / 64) + wave] = key;
         }
     } else if constexpr (EPI == MQ_QKV) {
-        const uint32_t pos = a.step[1];
+        const uint32_t pos = e_pos;
         // adjacent-pair RoPE (ops.rs:952-975) on q and k: theta = pos * freq[d/2]
         const float yo = __shfl_xor(y, 1, 64);
         const uint32_t dd = row % a.head_dim;
         if (sg.kind < 2 && dd < a.rope_dim) {
-            const float th = (float)pos * a.freq[dd >> 1];
+            const float th = (float)pos * e_freq;
             float sn, cs;
             sincosf(th, &sn, &cs);
             y = (row & 1) ? yo * sn + y * cs : y * cs - yo * sn;
@@ -721,10 +741,10 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     } else {  // MQ_RESID
         float xn = 0.f;
         if (valid) {
-            xn = a.x[row] + y;
+            xn = e_x + y;
             a.x[row] = xn;
         }
-        const float pv = valid ? (a.nw ? xn * a.nw[row] : xn) : 0.f;
+        const float pv = valid ? (a.nw ? xn * e_nw : xn) : 0.f;
         pack_half(pv, row >> 5, a.xout);
     }
 }
