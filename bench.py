@@ -563,6 +563,50 @@ def bench_gemm(lrs, ctx, steps, warmup, m, precision):
     return dict(per=per, us=tot_us, tflops=tot_flop / tot_us / 1e6, flop=tot_flop)
 
 
+def bench_gemm_library(steps, warmup, m):
+    """The vendor library's bf16 GEMM (torch.matmul on ROCm: hipBLASLt) at the
+    config-5 FFN shapes, its weights already dequantized to bf16: what a plain
+    bf16 GEMM of these shapes reaches on this part, as a reference for the
+    dequant-GEMM (not the product path: 2 B per weight instead of GGUF blocks,
+    no dequantization).  Each shape rotates over 4 weight copies, so every
+    weight byte comes from HBM."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    shapes = [("ffn_gate", 5120, 13824), ("ffn_up", 5120, 13824), ("ffn_down", 13824, 5120)]
+    per = {}
+    for name, n_in, n_out in shapes:
+        a = torch.randn(m, n_in, device=dev, dtype=torch.bfloat16, generator=gen)
+        ws = [torch.randn(n_out, n_in, device=dev, dtype=torch.bfloat16, generator=gen)
+              for _ in range(4)]
+        for i in range(max(1, warmup)):
+            torch.matmul(a, ws[i % 4].t())
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(steps):
+            torch.matmul(a, ws[i % 4].t())
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / steps
+        per[name] = dict(us=round(us, 2), tflops=round(2.0 * m * n_in * n_out / us / 1e6, 1))
+        log(f"[bench]   library bf16 {name:9s} {us:9.1f} us {per[name]['tflops']:8.1f} TFLOP/s")
+        del a, ws
+    tot_us = sum(v["us"] for v in per.values())
+    tot_flop = sum(2.0 * m * n_in * n_out for _, n_in, n_out in shapes)
+    return {"metric": "library bf16 GEMM TFLOP/s at the config-5 FFN shapes (reference, "
+                      "weights pre-dequantized to bf16)",
+            "value": round(tot_flop / tot_us / 1e6, 2), "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": steps, "warmup": warmup, "higher_is_better": True,
+            "dtype": "bf16 operands, f32 accumulate", "data": "synthetic (bf16 ~ N(0,1))",
+            "config": {"workload": "config5-ffn-shapes-library-bf16-gemm", "m": m,
+                       "op_us": {k: v["us"] for k, v in per.items()},
+                       "op_tflops": {k: v["tflops"] for k, v in per.items()},
+                       "frac_of_bf16_peak": round(tot_flop / tot_us / 1e6 / 2500.0, 4)}}
+
+
 def time_prompts(m, ctx, cfg, m_tok, steps, warmup):
     """Config 5 through the full 32B-shaped model: one step = an m_tok-token
     prompt at positions 0.. (decode_batch: logits of the last token)."""
@@ -913,7 +957,8 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "hybrid", "q8", "layer", "gemm", "prefill", "pmc", "stream"])
+                    choices=["decode", "hybrid", "q8", "layer", "gemm", "gemm_library", "prefill",
+                             "pmc", "stream"])
     ap.add_argument("--m", type=int, default=512,
                     help="gemm / prefill: prompt tokens (config 5: 128/512/2048)")
     ap.add_argument("--precision", type=int, default=1, choices=[1, 3],
@@ -929,6 +974,11 @@ def main():
         sys.exit(2)
     if a.steps < 1:
         raise SystemExit("--steps must be >= 1")
+    if a.workload == "gemm_library":
+        # torch's own HIP runtime in a process that has not loaded this
+        # library's (two HIP runtimes in one process see no device)
+        print(json.dumps(bench_gemm_library(a.steps, a.warmup, a.m)), flush=True)
+        return
     from pkgload import load_product
 
     lrs = load_product()

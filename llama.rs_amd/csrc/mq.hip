@@ -556,6 +556,13 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     }
+    // grouped RMS factor (below): the sum of squares of this thread's first
+    // block's group, loaded with the weights
+    float gs0 = 0.f;
+    if (a.gss && threadIdx.x < a.nxb) {
+        const uint32_t g = threadIdx.x / a.gblk;
+        for (uint32_t r = 0; r < a.gblk; r++) gs0 += a.gss[g * a.gblk + r];
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (a.gss) {
@@ -564,7 +571,11 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         for (uint32_t b = threadIdx.x; b < a.nxb; b += blockDim.x) {
             const uint32_t g = b / a.gblk;
             float t = 0.f;
-            for (uint32_t r = 0; r < a.gblk; r++) t += a.gss[g * a.gblk + r];
+            if (b == threadIdx.x) {
+                t = gs0;
+            } else {
+                for (uint32_t r = 0; r < a.gblk; r++) t += a.gss[g * a.gblk + r];
+            }
             const float f = 1.0f / sqrtf(t / a.gn + a.eps);
             float4 *mb = reinterpret_cast<float4 *>(lds + lp.meta + 16 * b);
             const float4 v = *mb;
