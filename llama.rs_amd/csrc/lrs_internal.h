@@ -126,8 +126,10 @@ size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K, int prec);
 // hi = bf16(a), lo = bf16(a - hi) (lo may be null); n a multiple of 4
 hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, hipStream_t s);
 // batched prompt block (prefill.hip)
+// Y = RMSNorm rows of X times w (Y may be null), and, when hi is given, the
+// same values as the bf16 planes of launch_split_bf16 ([n][E] hi, then lo)
 hipError_t launch_rmsnorm_rows(const float *X, const float *w, float eps, uint32_t E, uint32_t n,
-                               float *Y, hipStream_t s);
+                               float *Y, hipStream_t s, __bf16 *hi = nullptr);
 hipError_t launch_qkv_post(const float *qt, const float *kt, const float *vt, const float *bq,
                            const float *bk, const float *bv, const float *freq, float *q,
                            _Float16 *kc, _Float16 *vc, uint32_t n, uint32_t pos0, uint32_t qd,
@@ -136,7 +138,10 @@ hipError_t launch_qkv_post(const float *qt, const float *kt, const float *vt, co
 hipError_t launch_attn_prefill(const float *q, const _Float16 *kc, const _Float16 *vc, float *out,
                                uint32_t n, uint32_t pos0, uint32_t n_head, uint32_t n_kv,
                                uint32_t hd, uint32_t ctx, hipStream_t s);
-hipError_t launch_swiglu_rows(float *G, const float *U, size_t n, hipStream_t s);
+// silu(G) * U written straight to the bf16 planes of launch_split_bf16 (hi,
+// then lo = hi + n); n a multiple of 4
+hipError_t launch_swiglu_split(const float *G, const float *U, size_t n, __bf16 *hi,
+                               hipStream_t s);
 // hybrid (qwen35) mixers (dn.hip)
 struct DnArgs {
     const float *qkv;           // [conv_dim] conv input (RMSNorm already applied by the matvec)

@@ -1005,8 +1005,11 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
     LRS_HIP(launch_dequant_rows(m->embd->v, m->ptok, nb, m->pX, s));
     for (uint32_t l = 0; l < c.n_layer; l++) {
         const DevLayer &L = m->layers[l];
-        LRS_HIP(launch_rmsnorm_rows(m->pX, L.attn_norm, c.rms_eps, E, nb, m->pXN, s));
-        LRS_HIP(split(m->pXN, (size_t)nb * E));
+        // the normalised rows as GEMM planes (and in f32 for the delta-net
+        // block, which reads them for its gates)
+        const bool keep_xn = m->hybrid && L.dn;
+        LRS_HIP(launch_rmsnorm_rows(m->pX, L.attn_norm, c.rms_eps, E, nb, keep_xn ? m->pXN : nullptr,
+                                    s, hi));
         if (m->hybrid) {
             if (L.dn) {
                 // gated delta net over the block (plano_delta with n_tok = nb)
@@ -1057,12 +1060,10 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                 LRS_HIP(split(m->pATT, (size_t)nb * qd));
                 LRS_HIP(launch_gemm(L.o->v, hi, lo(nb, qd), m->pX, nb, E, P, s, true, m->pWork));
             }
-            LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, m->pXN, s));
-            LRS_HIP(split(m->pXN, (size_t)nb * E));
+            LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, nullptr, s, hi));
             LRS_HIP(launch_gemm(L.gate->v, hi, lo(nb, E), m->pG, nb, c.n_ff, P, s));
             LRS_HIP(launch_gemm(L.up->v, hi, lo(nb, E), m->pU, nb, c.n_ff, P, s));
-            LRS_HIP(launch_swiglu_rows(m->pG, m->pU, (size_t)nb * c.n_ff, s));
-            LRS_HIP(split(m->pG, (size_t)nb * c.n_ff));
+            LRS_HIP(launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s));
             LRS_HIP(launch_gemm(L.down->v, hi, lo(nb, c.n_ff), m->pX, nb, E, P, s, true, m->pWork));
             continue;
         }
@@ -1075,12 +1076,10 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                                     c.head_dim, c.ctx, s));
         LRS_HIP(split(m->pATT, (size_t)nb * qd));
         LRS_HIP(launch_gemm(L.o->v, hi, lo(nb, qd), m->pX, nb, E, P, s, true, m->pWork));
-        LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, m->pXN, s));
-        LRS_HIP(split(m->pXN, (size_t)nb * E));
+        LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, nullptr, s, hi));
         LRS_HIP(launch_gemm(L.gate->v, hi, lo(nb, E), m->pG, nb, c.n_ff, P, s));
         LRS_HIP(launch_gemm(L.up->v, hi, lo(nb, E), m->pU, nb, c.n_ff, P, s));
-        LRS_HIP(launch_swiglu_rows(m->pG, m->pU, (size_t)nb * c.n_ff, s));
-        LRS_HIP(split(m->pG, (size_t)nb * c.n_ff));
+        LRS_HIP(launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s));
         LRS_HIP(launch_gemm(L.down->v, hi, lo(nb, c.n_ff), m->pX, nb, E, P, s, true, m->pWork));
     }
     return LRS_OK;

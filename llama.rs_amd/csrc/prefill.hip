@@ -1,7 +1,8 @@
 // prefill.hip — the per-token ops of a batched prompt block (n tokens at
 // positions pos0 .. pos0+n-1) around the matrix-core GEMMs of gemm.hip:
-// RMSNorm per row, bias + RoPE + f16 KV append after the q/k/v GEMMs,
-// causal GQA attention over the cache, SwiGLU.  The formulas of the decode
+// RMSNorm per row and SwiGLU (both written straight to the bf16 input
+// planes of the next GEMM), bias + RoPE + f16 KV append after the q/k/v
+// GEMMs, causal GQA attention over the cache.  The formulas of the decode
 // kernels (Model::forward, crates/llama-model/src/model.rs:99-266; ops.rs:
 // 56-66, 952-988; attention.rs:76-166), which is what the reference's
 // prefill_residente (gpu.rs:673-697) drives in blocks of batch_size() tokens;
@@ -11,13 +12,22 @@
 
 namespace lrs {
 
-// Y[r] = (X[r] * scale_r) * w, scale_r = 1 / sqrt(mean(X[r]^2) + eps)
+// bf16 hi of v and the bf16 of the remainder (the GEMM input planes)
+__device__ __forceinline__ void split_store(float v, __bf16 *hi, __bf16 *lo) {
+    const __bf16 h = (__bf16)v;
+    *hi = h;
+    *lo = (__bf16)(v - (float)h);
+}
+
+// Y[r] = (X[r] * scale_r) * w, scale_r = 1 / sqrt(mean(X[r]^2) + eps); with
+// hi, the same values also as bf16 hi / lo planes (lo = hi + gridDim.x * E)
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ X,
                                                       const float *__restrict__ w, float eps,
-                                                      uint32_t E, float *__restrict__ Y) {
+                                                      uint32_t E, float *__restrict__ Y,
+                                                      __bf16 *__restrict__ hi) {
     __shared__ float red[4];
     const float *x = X + (size_t)blockIdx.x * E;
-    float *y = Y + (size_t)blockIdx.x * E;
+    float *y = Y ? Y + (size_t)blockIdx.x * E : nullptr;
     float ss = 0.f;
     for (uint32_t i = 4 * threadIdx.x; i < E; i += 4 * blockDim.x) {
         const float4 v = *reinterpret_cast<const float4 *>(x + i);
@@ -29,7 +39,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ 
     __syncthreads();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float scale = 1.0f / sqrtf(tot / (float)E + eps);
-    for (uint32_t i = threadIdx.x; i < E; i += blockDim.x) y[i] = (x[i] * scale) * w[i];
+    const size_t plane = (size_t)gridDim.x * E, r0 = (size_t)blockIdx.x * E;
+    for (uint32_t i = threadIdx.x; i < E; i += blockDim.x) {
+        const float v = (x[i] * scale) * w[i];
+        if (Y) y[i] = v;
+        if (hi) split_store(v, hi + r0 + i, hi + plane + r0 + i);
+    }
 }
 
 // q/k/v GEMM outputs -> bias, adjacent-pair RoPE on q and k at position
@@ -342,20 +357,10 @@ __global__ __launch_bounds__(64 * NW) void k_attn_pf_mma(AttnPre a) {
     }
 }
 
-// G = silu(G) * U elementwise (ops.rs:978-988)
-__global__ void k_swiglu_rows(float *__restrict__ G, const float *__restrict__ U, size_t n) {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const float g = G[i];
-        const float den = 1.0f + expf(-g);
-        G[i] = (g / den) * U[i];
-    }
-}
-
 hipError_t launch_rmsnorm_rows(const float *X, const float *w, float eps, uint32_t E, uint32_t n,
-                               float *Y, hipStream_t s) {
-    if (E % 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(256), 0, s, X, w, eps, E, Y);
+                               float *Y, hipStream_t s, __bf16 *hi) {
+    if (E % 4 || (!Y && !hi)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(256), 0, s, X, w, eps, E, Y, hi);
     return hipGetLastError();
 }
 
@@ -404,10 +409,35 @@ hipError_t launch_attn_prefill(const float *q, const _Float16 *kc, const _Float1
     return hipGetLastError();
 }
 
-hipError_t launch_swiglu_rows(float *G, const float *U, size_t n, hipStream_t s) {
-    size_t g = (n + 255) / 256;
-    if (g > 65536) g = 65536;
-    hipLaunchKernelGGL(k_swiglu_rows, dim3((unsigned)g), dim3(256), 0, s, G, U, n);
+// silu(G) * U (ops.rs:978-988: g / (1 + e^-g) * u), stored as the bf16 hi / lo
+// planes of the down projection's input
+__global__ __launch_bounds__(256) void k_swiglu_split(const float *__restrict__ G,
+                                                      const float *__restrict__ U, size_t n4,
+                                                      __bf16 *__restrict__ hi,
+                                                      __bf16 *__restrict__ lo) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4 g = reinterpret_cast<const float4 *>(G)[i];
+    const float4 u = reinterpret_cast<const float4 *>(U)[i];
+    const float y[4] = {(g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
+                        (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w};
+    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+    bf16x4 h, l;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        h[k] = (__bf16)y[k];
+        l[k] = (__bf16)(y[k] - (float)h[k]);
+    }
+    reinterpret_cast<bf16x4 *>(hi)[i] = h;
+    reinterpret_cast<bf16x4 *>(lo)[i] = l;
+}
+
+hipError_t launch_swiglu_split(const float *G, const float *U, size_t n, __bf16 *hi,
+                               hipStream_t s) {
+    if (n % 4) return hipErrorInvalidValue;
+    const size_t n4 = n / 4;
+    hipLaunchKernelGGL(k_swiglu_split, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, G, U,
+                       n4, hi, hi + n);
     return hipGetLastError();
 }
 
