@@ -114,6 +114,7 @@ struct lrs_model {
           *pY = nullptr;
     float2 *pGB = nullptr;
     float *pWork = nullptr;  // K-slice partials of the split GEMMs
+    size_t work_bytes = 0;
     uint32_t *ptok;
     _Float16 *kv;                // all layers' caches
     uint32_t *step_host;         // pinned
@@ -967,8 +968,9 @@ static int ensure_prefill(lrs_model *m) {
                                                 std::max<size_t>(c.n_ff, (size_t)m->hc.dn_v_heads *
                                                                              m->hc.dn_state)) * 4,
                         (void **)&m->pA16)) ||
-        // K-sliced o / down GEMMs: at most 8 slices of [rows][n_embd] partials
-        (rc = dev_alloc(m, 8 * B * c.n_embd * 4, (void **)&m->pWork)) ||
+        // K-sliced GEMMs (few output tiles: o, down, and the narrow k / v):
+        // 8 slices of [rows][n_embd] partials
+        (rc = dev_alloc(m, m->work_bytes = 8 * B * c.n_embd * 4, (void **)&m->pWork)) ||
         (rc = dev_alloc(m, B * 4, (void **)&m->ptok)))
         return rc;
     if (m->hybrid) {
@@ -1001,6 +1003,13 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
     __bf16 *const hi = m->pA16;
     auto lo = [&](uint32_t rows, uint32_t cols) { return hi + (size_t)rows * cols; };
     auto split = [&](const float *a, size_t n) { return launch_split_bf16(a, n, hi, hi + n, s); };
+    // y (+)= A W^T over the block, split over K across workgroups when the
+    // weight has too few output tiles to fill the GPU (the slices' partials
+    // must fit the work buffer)
+    auto gemm = [&](const lrs_weight *w, uint32_t K, float *y, uint32_t N, bool accum = false) {
+        float *work = gemm_work_bytes(nb, N, K, P) <= m->work_bytes ? m->pWork : nullptr;
+        return launch_gemm(w->v, hi, lo(nb, K), y, nb, N, P, s, accum, work);
+    };
     LRS_HIP(hipMemcpyAsync(m->ptok, tokens, nb * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     LRS_HIP(launch_dequant_rows(m->embd->v, m->ptok, nb, m->pX, s));
     for (uint32_t l = 0; l < c.n_layer; l++) {
@@ -1016,8 +1025,8 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                 const lrs_hybrid_config &hc = m->hc;
                 const uint32_t VD = hc.dn_v_heads * hc.dn_state;
                 const uint32_t CD = 2 * hc.dn_k_heads * hc.dn_state + VD;
-                LRS_HIP(launch_gemm(L.ssm_qkv->v, hi, lo(nb, E), m->pCI, nb, CD, P, s));
-                LRS_HIP(launch_gemm(L.ssm_gate->v, hi, lo(nb, E), m->pZ, nb, VD, P, s));
+                LRS_HIP(gemm(L.ssm_qkv, E, m->pCI, CD));
+                LRS_HIP(gemm(L.ssm_gate, E, m->pZ, VD));
                 DnBlockArgs da = {};
                 da.hn = m->pXN;
                 da.alpha = L.alpha;
@@ -1044,13 +1053,13 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                 da.eps = c.rms_eps;
                 LRS_HIP(launch_dn_prefill(da, s));
                 LRS_HIP(split(m->pY, (size_t)nb * VD));
-                LRS_HIP(launch_gemm(L.ssm_out->v, hi, lo(nb, VD), m->pX, nb, E, P, s, true, m->pWork));
+                LRS_HIP(gemm(L.ssm_out, VD, m->pX, E, true));
             } else {
                 // gated attention: Q (+ gate), k, v; QK-norm + RoPE; causal
                 // attention over the cache; sigmoid gate; o
-                LRS_HIP(launch_gemm(L.q->v, hi, lo(nb, E), m->pQG, nb, 2 * qd, P, s));
-                LRS_HIP(launch_gemm(L.k->v, hi, lo(nb, E), m->pKt, nb, kvd, P, s));
-                LRS_HIP(launch_gemm(L.v->v, hi, lo(nb, E), m->pVt, nb, kvd, P, s));
+                LRS_HIP(gemm(L.q, E, m->pQG, 2 * qd));
+                LRS_HIP(gemm(L.k, E, m->pKt, kvd));
+                LRS_HIP(gemm(L.v, E, m->pVt, kvd));
                 LRS_HIP(launch_qk_prep_rows(m->pQG, m->pKt, m->pVt, L.q_norm, L.k_norm, m->freq, m->pQ,
                                             L.kc, L.vc, nb, pos0, c.n_head, c.n_head_kv, c.head_dim,
                                             c.ctx, c.rope_dim, c.rms_eps, s));
@@ -1058,29 +1067,29 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                                             c.head_dim, c.ctx, s));
                 LRS_HIP(launch_gate_rows(m->pATT, m->pQG, nb, qd, c.head_dim, s));
                 LRS_HIP(split(m->pATT, (size_t)nb * qd));
-                LRS_HIP(launch_gemm(L.o->v, hi, lo(nb, qd), m->pX, nb, E, P, s, true, m->pWork));
+                LRS_HIP(gemm(L.o, qd, m->pX, E, true));
             }
             LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, nullptr, s, hi));
-            LRS_HIP(launch_gemm(L.gate->v, hi, lo(nb, E), m->pG, nb, c.n_ff, P, s));
-            LRS_HIP(launch_gemm(L.up->v, hi, lo(nb, E), m->pU, nb, c.n_ff, P, s));
+            LRS_HIP(gemm(L.gate, E, m->pG, c.n_ff));
+            LRS_HIP(gemm(L.up, E, m->pU, c.n_ff));
             LRS_HIP(launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s));
-            LRS_HIP(launch_gemm(L.down->v, hi, lo(nb, c.n_ff), m->pX, nb, E, P, s, true, m->pWork));
+            LRS_HIP(gemm(L.down, c.n_ff, m->pX, E, true));
             continue;
         }
-        LRS_HIP(launch_gemm(L.q->v, hi, lo(nb, E), m->pQt, nb, qd, P, s));
-        LRS_HIP(launch_gemm(L.k->v, hi, lo(nb, E), m->pKt, nb, kvd, P, s));
-        LRS_HIP(launch_gemm(L.v->v, hi, lo(nb, E), m->pVt, nb, kvd, P, s));
+        LRS_HIP(gemm(L.q, E, m->pQt, qd));
+        LRS_HIP(gemm(L.k, E, m->pKt, kvd));
+        LRS_HIP(gemm(L.v, E, m->pVt, kvd));
         LRS_HIP(launch_qkv_post(m->pQt, m->pKt, m->pVt, L.bq, L.bk, L.bv, m->freq, m->pQ, L.kc,
                                 L.vc, nb, pos0, qd, kvd, c.head_dim, c.rope_dim, c.ctx, s));
         LRS_HIP(launch_attn_prefill(m->pQ, L.kc, L.vc, m->pATT, nb, pos0, c.n_head, c.n_head_kv,
                                     c.head_dim, c.ctx, s));
         LRS_HIP(split(m->pATT, (size_t)nb * qd));
-        LRS_HIP(launch_gemm(L.o->v, hi, lo(nb, qd), m->pX, nb, E, P, s, true, m->pWork));
+        LRS_HIP(gemm(L.o, qd, m->pX, E, true));
         LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, nullptr, s, hi));
-        LRS_HIP(launch_gemm(L.gate->v, hi, lo(nb, E), m->pG, nb, c.n_ff, P, s));
-        LRS_HIP(launch_gemm(L.up->v, hi, lo(nb, E), m->pU, nb, c.n_ff, P, s));
+        LRS_HIP(gemm(L.gate, E, m->pG, c.n_ff));
+        LRS_HIP(gemm(L.up, E, m->pU, c.n_ff));
         LRS_HIP(launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s));
-        LRS_HIP(launch_gemm(L.down->v, hi, lo(nb, c.n_ff), m->pX, nb, E, P, s, true, m->pWork));
+        LRS_HIP(gemm(L.down, c.n_ff, m->pX, E, true));
     }
     return LRS_OK;
 }
