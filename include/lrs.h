@@ -162,6 +162,15 @@ int lrs_matvec_q8_0_actq_dev(lrs_ctx *ctx, const lrs_weight *w, const float *x_d
  * Weights: Q4_K, Q5_K, Q6_K, Q8_0; n_in a multiple of 256. */
 int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y_dev, uint32_t m,
                  int precision);
+/* lrs_gemm_dev for n_w (1..3) weights over the same a, as one launch over
+ * all their output tiles: y_dev[i] [m * n_out(w[i])] = a W[i]^T.  No
+ * reference counterpart (the reference dispatches one GEMM per weight); it
+ * is the form a prompt block uses for q / k / v.  The weights share n_in;
+ * at most two types, the first type's weights first, and the mixes Q4_K or
+ * Q5_K followed by Q6_K (else LRS_E_UNSUPPORTED).  Each output equals the
+ * single-weight GEMM without a split over K. */
+int lrs_gemm_group_dev(lrs_ctx *ctx, const lrs_weight *const *w, uint32_t n_w, const float *a_dev,
+                       float *const *y_dev, uint32_t m, int precision);
 
 /* Matvec launch shape override: tiles of 16 rows per wavefront, tile groups
  * per workgroup, K-slices per workgroup; one of the instantiated shapes

@@ -69,6 +69,7 @@ def _load() -> C.CDLL:
         "lrs_matvec_dev": (i32, [vp, vp, vp, vp, u32]),
         "lrs_matvec_dev_noalloc": (i32, [vp, vp, vp, vp, u32]),
         "lrs_gemm_dev": (i32, [vp, vp, vp, vp, u32, i32]),
+        "lrs_gemm_group_dev": (i32, [vp, vp, u32, vp, vp, u32, i32]),
         "lrs_quantize_q8_0_dev": (i32, [vp, vp, u32, i32, vp]),
         "lrs_matvec_q8_0_actq_dev": (i32, [vp, vp, vp, vp, u32, i32]),
         "lrs_dev_alloc": (i32, [vp, sz, pvp]),
@@ -368,6 +369,26 @@ def quantize_q8_0(ctx: Context, x: np.ndarray, half_even: bool = True) -> np.nda
     finally:
         xb.free()
         qb.free()
+
+
+def gemm_group(ctx: Context, weights, a: np.ndarray, precision: int = 1) -> list:
+    """lrs_gemm_group_dev: the GEMM of each weight over the same a [m, n_in]
+    as one launch; returns [m, n_out] f32 per weight."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    m = a.shape[0]
+    ab = ctx.alloc(a.nbytes)
+    ys = [ctx.alloc(4 * m * w.n_out) for w in weights]
+    try:
+        ab.upload(a)
+        wa = (C.c_void_p * len(weights))(*[w.h for w in weights])
+        ya = (C.c_void_p * len(weights))(*[y.ptr for y in ys])
+        check(lib.lrs_gemm_group_dev(ctx.h, wa, len(weights), ab.ptr, ya, m, precision))
+        ctx.sync()
+        return [y.download(np.float32, m * w.n_out).reshape(m, w.n_out) for y, w in zip(ys, weights)]
+    finally:
+        ab.free()
+        for y in ys:
+            y.free()
 
 
 class GpuMatmul:

@@ -439,6 +439,33 @@ int lrs_gemm_dev(lrs_ctx *ctx, const lrs_weight *w, const float *a_dev, float *y
     return LRS_OK;
 }
 
+int lrs_gemm_group_dev(lrs_ctx *ctx, const lrs_weight *const *w, uint32_t n_w, const float *a_dev,
+                       float *const *y_dev, uint32_t m, int precision) {
+    if (!ctx || !w || !a_dev || !y_dev) return fail(LRS_E_ARG, "null argument");
+    if (n_w == 0 || n_w > 3) return fail(LRS_E_ARG, "1 to 3 weights per group");
+    if (m == 0) return fail(LRS_E_ARG, "m must be >= 1");
+    if (precision != 1 && precision != 3) return fail(LRS_E_ARG, "precision must be 1 or 3");
+    WeightView wv[3];
+    uint32_t ldy[3];
+    for (uint32_t i = 0; i < n_w; i++) {
+        if (!w[i] || !y_dev[i]) return fail(LRS_E_ARG, "null weight or output");
+        wv[i] = w[i]->v;
+        ldy[i] = w[i]->v.n_out;
+        if (wv[i].n_in != wv[0].n_in) return fail(LRS_E_ARG, "the weights of a group share n_in");
+    }
+    if (wv[0].n_in % 256) return fail(LRS_E_ARG, "the GEMM needs n_in to be a multiple of 256");
+    if (!gemm_segs_supported(wv, n_w))
+        return fail(LRS_E_UNSUPPORTED, "group types: one type, or Q4_K / Q5_K weights then Q6_K");
+    SETDEV(ctx);
+    const size_t n = (size_t)m * wv[0].n_in, ab = n * 2 * (precision == 3 ? 2 : 1);
+    void *buf = nullptr;
+    if (int rc_ = ctx_scratch(ctx, ab, &buf)) return rc_;
+    __bf16 *hi = (__bf16 *)buf, *lo = precision == 3 ? hi + n : nullptr;
+    LRS_HIP(launch_split_bf16(a_dev, n, hi, lo, ctx->stream));
+    LRS_HIP(launch_gemm_segs(wv, y_dev, ldy, n_w, hi, lo, m, precision, ctx->stream));
+    return LRS_OK;
+}
+
 int lrs_matvec_set_geom(int tiles_per_wave, int tile_groups, int k_slices) {
     if (set_matvec_geom(tiles_per_wave, tile_groups, k_slices) != 0)
         return fail(LRS_E_ARG, "unsupported matvec launch shape (tiles_per_wave, tile_groups, "

@@ -33,14 +33,24 @@ typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 constexpr int GM_BN = 128, GM_BK = 64;
 constexpr int GM_LD = GM_BK + 8;  // padded LDS row (bf16 elements)
 
+// one weight of a launch: weights that share the input (a prompt block's q,
+// k and v projections) run as one launch over their concatenated output
+// tiles, segment s owning tiles [nt0, next segment's nt0) along N
+constexpr int GM_MAX_SEG = 3;
+struct GemmSeg {
+    const uint8_t *q;  // weight, tiled layout (tiled.h)
+    float *y;          // [M][ldy]
+    uint32_t N, ldy, nt0;
+};
+
 struct GemmArgs {
     const __bf16 *ahi, *alo;  // A [M][K] as bf16 (hi, and lo = bf16(a - hi) for PREC 3)
-    float *y;                 // [M][ldy]
-    const uint8_t *q;         // weight, tiled layout (tiled.h)
-    uint32_t M, N, K, units, ldy;
+    GemmSeg seg[GM_MAX_SEG];
+    uint32_t nseg, nseg0;     // segments; the first nseg0 have the kernel's type T0, the rest T1
+    uint32_t M, K;
     uint32_t accum;           // 1: y += A W^T (residual add), 0: y = A W^T
-    uint32_t nm, nn;          // output tiles along M and N
-    uint32_t ks;              // K slices: slice z writes part + z*M*N (then k_reduce_ks)
+    uint32_t nm, nn;          // output tiles along M and N (all segments)
+    uint32_t ks;              // K slices (one segment): slice z writes part + z*M*N (then k_reduce_ks)
     float *part;
 };
 
@@ -200,8 +210,13 @@ __device__ __forceinline__ void put16(__bf16 *hi, __bf16 *lo, const float (&v)[1
 // tiles are numbered M-block-major and XCD x takes the x-th contiguous run
 // of them, so the workgroups of one XCD share one or two activation blocks,
 // which stay in that XCD's L2.
+// the output tile (m0, n0 of segment sg) of K slice kz, with the weight of
+// type T; As / Ws the workgroup's LDS stages
 template <uint32_t T, int PREC, int BM>
-__global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs &g, const GemmSeg &sg, uint32_t kz,
+                                          uint32_t m0, uint32_t n0,
+                                          __bf16 (*As)[PREC == 3 ? 2 : 1][BM * GM_LD],
+                                          __bf16 (*Ws)[PREC == 3 ? 2 : 1][GM_BN * GM_LD]) {
     constexpr int NS = PREC == 3 ? 2 : 1;  // hi (+ lo) planes
     // wavefront grid: WM x WN = 8 wavefronts, each (BM / WM) x (128 / WN) of
     // the tile in MT x NT MFMA tiles of 32 x 32 (the 256-token tile uses 4 x 2
@@ -209,25 +224,18 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     constexpr int WM = BM == 256 ? 4 : 2, WN = 8 / WM;
     constexpr int MT = BM / WM / 32, NT = GM_BN / WN / 32;
     constexpr int AR = BM / 128;           // activation rows staged per thread
-    __shared__ __attribute__((aligned(16))) __bf16 As[2][NS][BM * GM_LD];
-    __shared__ __attribute__((aligned(16))) __bf16 Ws[2][NS][GM_BN * GM_LD];
-    const uint32_t ntile = g.nm * g.nn * g.ks, per = (ntile + 7) / 8;
-    const uint32_t t0 = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (t0 >= ntile) return;
-    const uint32_t kz = t0 / (g.nm * g.nn), t = t0 % (g.nm * g.nn);  // K slice, output tile
-    const uint32_t kspan = g.K / g.ks;                                 // a multiple of 256
+    const uint32_t kspan = g.K / g.ks;     // a multiple of 256
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t m0 = (t / g.nn) * BM, n0 = (t % g.nn) * GM_BN;
     const uint32_t wm = wave / WN, wn = wave % WN;
     // staging roles: thread t handles row t/4, K quarter t%4 (16 of the 64)
     const uint32_t sr = tid >> 2, sq = (tid & 3) * 16;
-    const uint32_t wr = min(n0 + sr, g.N - 1);
+    const uint32_t wr = min(n0 + sr, sg.N - 1);
     size_t aoff[AR];  // activation rows sr, sr + 128, ...
 #pragma unroll
     for (int j = 0; j < AR; j++)
         aoff[j] = (size_t)min(m0 + sr + 128 * j, g.M - 1) * g.K + sq + (size_t)kz * kspan;
     const uint32_t kbase = kz * kspan;  // weight element offset of the slice
-    const uint8_t *rowq = g.q + (size_t)(wr >> 4) * g.units * tchunk_bytes(T);
+    const uint8_t *rowq = sg.q + (size_t)(wr >> 4) * tunits(T, g.K) * tchunk_bytes(T);
 
     f32x16 acc[MT][NT];
 #pragma unroll
@@ -349,16 +357,42 @@ __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const uint32_t m = m0 + (BM / WM) * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < g.M && n < g.N) {
+                if (m < g.M && n < sg.N) {
                     if (g.ks > 1) {
-                        g.part[((size_t)kz * g.M + m) * g.N + n] = acc[i][jn][r];
+                        g.part[((size_t)kz * g.M + m) * sg.N + n] = acc[i][jn][r];
                     } else {
-                        float *o = g.y + (size_t)m * g.ldy + n;
+                        float *o = sg.y + (size_t)m * sg.ldy + n;
                         *o = g.accum ? *o + acc[i][jn][r] : acc[i][jn][r];
                     }
                 }
             }
     }
+}
+
+// workgroup b takes output tile t0 of the (K slice, M block, N tile) order;
+// the segment of its N tile picks the weight and the type (T0 for the first
+// nseg0 segments, T1 after them); MS = the most segments the instance takes
+// (1: single-weight launches)
+template <uint32_t T0, uint32_t T1, int PREC, int BM, int MS>
+__global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
+    constexpr int NS = PREC == 3 ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) __bf16 As[2][NS][BM * GM_LD];
+    __shared__ __attribute__((aligned(16))) __bf16 Ws[2][NS][GM_BN * GM_LD];
+    const uint32_t ntile = g.nm * g.nn * g.ks, per = (ntile + 7) / 8;
+    const uint32_t t0 = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (t0 >= ntile) return;
+    const uint32_t kz = t0 / (g.nm * g.nn), t = t0 % (g.nm * g.nn);  // K slice, output tile
+    const uint32_t nt = t % g.nn;
+    uint32_t si = 0;
+#pragma unroll
+    for (int i = 1; i < MS; i++)
+        if ((uint32_t)i < g.nseg && nt >= g.seg[i].nt0) si = i;
+    const GemmSeg sg = g.seg[si];
+    const uint32_t m0 = (t / g.nn) * BM, n0 = (nt - sg.nt0) * GM_BN;
+    if (T0 == T1 || si < g.nseg0)
+        gemm_tile<T0, PREC, BM>(g, sg, kz, m0, n0, As, Ws);
+    else
+        gemm_tile<T1, PREC, BM>(g, sg, kz, m0, n0, As, Ws);
 }
 
 // y[m][n] (+)= sum over the K slices of part[z][m][n], slices in order
@@ -430,6 +464,11 @@ static uint32_t ksplit_for(uint32_t tiles, uint32_t K) {
     return best;
 }
 
+uint32_t gemm_out_tiles(uint32_t M, uint32_t N, int prec) {
+    const uint32_t bm = gemm_bm(M, prec);
+    return ((M + bm - 1) / bm) * ((N + GM_BN - 1) / GM_BN);
+}
+
 uint32_t gemm_ksplit(uint32_t M, uint32_t N, uint32_t K, int prec) {
     const uint32_t bm = gemm_bm(M, prec);
     return ksplit_for(((M + bm - 1) / bm) * ((N + GM_BN - 1) / GM_BN), K);
@@ -441,43 +480,89 @@ size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K, int prec) {
     return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
 }
 
-hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
-                       uint32_t ldy, int prec, hipStream_t s, bool accum, float *work) {
-    if (M == 0 || w.n_in % (4 * GM_BK) || (prec == 3 && !alo)) return hipErrorInvalidValue;
+using GemmFn = void (*)(GemmArgs);
+
+// the kernel for weight types t0 (the first segments) and t1 (the rest)
+template <uint32_t T0>
+static GemmFn pick_gemm_t0(uint32_t t1, uint32_t nseg, int prec, uint32_t bm) {
+#define LRS_GEMM_PICK(T1, MS)                                                             \
+    return prec == 3 ? k_gemm<T0, T1, 3, 128, MS>                                         \
+                     : bm == 256 ? k_gemm<T0, T1, 1, 256, MS> : k_gemm<T0, T1, 1, 128, MS>
+    if (t1 == T0 && nseg == 1) { LRS_GEMM_PICK(T0, 1); }
+    if (t1 == T0) { LRS_GEMM_PICK(T0, GM_MAX_SEG); }
+    // a prompt block's q / k with a Q6_K v (the K-quant mixes)
+    if constexpr (T0 == T_Q4_K || T0 == T_Q5_K)
+        if (t1 == T_Q6_K) { LRS_GEMM_PICK(T_Q6_K, GM_MAX_SEG); }
+#undef LRS_GEMM_PICK
+    return nullptr;
+}
+static GemmFn pick_gemm(uint32_t t0, uint32_t t1, uint32_t nseg, int prec, uint32_t bm) {
+    switch (t0) {
+    case T_Q4_K: return pick_gemm_t0<T_Q4_K>(t1, nseg, prec, bm);
+    case T_Q5_K: return pick_gemm_t0<T_Q5_K>(t1, nseg, prec, bm);
+    case T_Q6_K: return pick_gemm_t0<T_Q6_K>(t1, nseg, prec, bm);
+    case T_Q8_0: return pick_gemm_t0<T_Q8_0>(t1, nseg, prec, bm);
+    default: return nullptr;
+    }
+}
+
+bool gemm_segs_supported(const WeightView *w, uint32_t nseg) {
+    if (nseg == 0 || nseg > (uint32_t)GM_MAX_SEG) return false;
+    uint32_t nseg0 = 1;
+    while (nseg0 < nseg && w[nseg0].type == w[0].type) nseg0++;
+    for (uint32_t i = 0; i < nseg; i++) {
+        if (w[i].n_in != w[0].n_in || !is_tiled(w[i].type)) return false;
+        if (i >= nseg0 && w[i].type != w[nseg0].type) return false;  // at most two types, in two runs
+    }
+    return pick_gemm(w[0].type, w[nseg - 1].type, nseg, 3, 128) != nullptr;
+}
+
+hipError_t launch_gemm_segs(const WeightView *w, float *const *y, const uint32_t *ldy, uint32_t nseg,
+                            const __bf16 *ahi, const __bf16 *alo, uint32_t M, int prec,
+                            hipStream_t s, bool accum, float *work) {
+    if (M == 0 || nseg == 0 || nseg > (uint32_t)GM_MAX_SEG || (prec == 3 && !alo))
+        return hipErrorInvalidValue;
+    if (!gemm_segs_supported(w, nseg) || w[0].n_in % (4 * GM_BK)) return hipErrorInvalidValue;
     const uint32_t bm = gemm_bm(M, prec);
-    GemmArgs g;
+    GemmArgs g = {};
     g.ahi = ahi;
     g.alo = alo;
-    g.y = y;
-    g.q = w.q;
+    g.nseg = nseg;
+    g.nseg0 = 1;
+    while (g.nseg0 < nseg && w[g.nseg0].type == w[0].type) g.nseg0++;
+    uint32_t nt = 0;
+    for (uint32_t i = 0; i < nseg; i++) {
+        g.seg[i].q = w[i].q;
+        g.seg[i].y = y[i];
+        g.seg[i].N = w[i].n_out;
+        g.seg[i].ldy = ldy[i];
+        g.seg[i].nt0 = nt;
+        nt += (w[i].n_out + GM_BN - 1) / GM_BN;
+    }
     g.M = M;
-    g.N = w.n_out;
-    g.K = w.n_in;
-    g.units = tunits(w.type, w.n_in);
-    g.ldy = ldy;
+    g.K = w[0].n_in;
     g.accum = accum ? 1u : 0u;
     g.nm = (M + bm - 1) / bm;
-    g.nn = (w.n_out + GM_BN - 1) / GM_BN;
-    g.ks = work ? ksplit_for(g.nm * g.nn, g.K) : 1;
+    g.nn = nt;
+    // K slices write [M][N] partials of one weight: one-segment launches only
+    g.ks = work && nseg == 1 ? ksplit_for(g.nm * g.nn, g.K) : 1;
     g.part = work;
+    const GemmFn fn = pick_gemm(w[0].type, w[nseg - 1].type, nseg, prec, bm);
+    if (!fn) return hipErrorNotSupported;
     const uint32_t grid = 8 * ((g.nm * g.nn * g.ks + 7) / 8);
-    void (*fn)(GemmArgs) = nullptr;
-#define LRS_GEMM_PICK(TT) prec == 3 ? k_gemm<TT, 3, 128> : bm == 256 ? k_gemm<TT, 1, 256> : k_gemm<TT, 1, 128>
-    switch (w.type) {
-    case T_Q4_K: fn = LRS_GEMM_PICK(T_Q4_K); break;
-    case T_Q5_K: fn = LRS_GEMM_PICK(T_Q5_K); break;
-    case T_Q6_K: fn = LRS_GEMM_PICK(T_Q6_K); break;
-    case T_Q8_0: fn = LRS_GEMM_PICK(T_Q8_0); break;
-    default: return hipErrorNotSupported;
-    }
-#undef LRS_GEMM_PICK
     hipLaunchKernelGGL(fn, dim3(grid), dim3(512), 0, s, g);
     if (g.ks > 1) {
-        const size_t n = (size_t)M * g.N;
-        hipLaunchKernelGGL(k_reduce_ks, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, work, y,
-                           M, g.N, ldy, g.ks, g.accum);
+        const size_t n = (size_t)M * g.seg[0].N;
+        hipLaunchKernelGGL(k_reduce_ks, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, work,
+                           y[0], M, g.seg[0].N, ldy[0], g.ks, g.accum);
     }
     return hipGetLastError();
+}
+
+hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
+                       uint32_t ldy, int prec, hipStream_t s, bool accum, float *work) {
+    if (!is_tiled(w.type)) return hipErrorNotSupported;
+    return launch_gemm_segs(&w, &y, &ldy, 1, ahi, alo, M, prec, s, accum, work);
 }
 
 }  // namespace lrs

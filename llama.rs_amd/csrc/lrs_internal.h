@@ -123,6 +123,16 @@ hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float
                        uint32_t ldy, int prec, hipStream_t s, bool accum = false,
                        float *work = nullptr);
 size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K, int prec);
+// several weights over the same A in one launch (their output tiles side by
+// side; y[i] [M][ldy[i]]): at most 3, the same n_in, at most two types with
+// the first type's weights first and only the pairs the kernel is built for
+// (one type; Q4_K or Q5_K then Q6_K); no K split
+bool gemm_segs_supported(const WeightView *w, uint32_t nseg);
+// output tiles (workgroups without a K split) of an M x N GEMM
+uint32_t gemm_out_tiles(uint32_t M, uint32_t N, int prec);
+hipError_t launch_gemm_segs(const WeightView *w, float *const *y, const uint32_t *ldy, uint32_t nseg,
+                            const __bf16 *ahi, const __bf16 *alo, uint32_t M, int prec,
+                            hipStream_t s, bool accum = false, float *work = nullptr);
 // hi = bf16(a), lo = bf16(a - hi) (lo may be null); n a multiple of 4
 hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, hipStream_t s);
 // batched prompt block (prefill.hip)

@@ -1010,6 +1010,25 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
         float *work = gemm_work_bytes(nb, N, K, P) <= m->work_bytes ? m->pWork : nullptr;
         return launch_gemm(w->v, hi, lo(nb, K), y, nb, N, P, s, accum, work);
     };
+    // weights over the same normalised rows (q / k / v, or the delta net's
+    // in-projections): one launch over all their output tiles when that alone
+    // keeps most CUs busy for the whole K, else one launch each (split over K)
+    auto gemm_group = [&](uint32_t n, const lrs_weight *const *w, float *const *y,
+                          const uint32_t *N) -> hipError_t {
+        WeightView wv[3];
+        uint32_t tiles = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            wv[i] = w[i]->v;
+            tiles += gemm_out_tiles(nb, N[i], P);
+        }
+        if (tiles >= 192 && gemm_segs_supported(wv, n))
+            return launch_gemm_segs(wv, y, N, n, hi, lo(nb, E), nb, P, s);
+        for (uint32_t i = 0; i < n; i++) {
+            const hipError_t e = gemm(w[i], E, y[i], N[i]);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    };
     LRS_HIP(hipMemcpyAsync(m->ptok, tokens, nb * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     LRS_HIP(launch_dequant_rows(m->embd->v, m->ptok, nb, m->pX, s));
     for (uint32_t l = 0; l < c.n_layer; l++) {
@@ -1025,8 +1044,12 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                 const lrs_hybrid_config &hc = m->hc;
                 const uint32_t VD = hc.dn_v_heads * hc.dn_state;
                 const uint32_t CD = 2 * hc.dn_k_heads * hc.dn_state + VD;
-                LRS_HIP(gemm(L.ssm_qkv, E, m->pCI, CD));
-                LRS_HIP(gemm(L.ssm_gate, E, m->pZ, VD));
+                {
+                    const lrs_weight *const w[2] = {L.ssm_qkv, L.ssm_gate};
+                    float *const y[2] = {m->pCI, m->pZ};
+                    const uint32_t N[2] = {CD, VD};
+                    LRS_HIP(gemm_group(2, w, y, N));
+                }
                 DnBlockArgs da = {};
                 da.hn = m->pXN;
                 da.alpha = L.alpha;
@@ -1057,9 +1080,12 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
             } else {
                 // gated attention: Q (+ gate), k, v; QK-norm + RoPE; causal
                 // attention over the cache; sigmoid gate; o
-                LRS_HIP(gemm(L.q, E, m->pQG, 2 * qd));
-                LRS_HIP(gemm(L.k, E, m->pKt, kvd));
-                LRS_HIP(gemm(L.v, E, m->pVt, kvd));
+                {
+                    const lrs_weight *const w[3] = {L.q, L.k, L.v};
+                    float *const y[3] = {m->pQG, m->pKt, m->pVt};
+                    const uint32_t N[3] = {2 * qd, kvd, kvd};
+                    LRS_HIP(gemm_group(3, w, y, N));
+                }
                 LRS_HIP(launch_qk_prep_rows(m->pQG, m->pKt, m->pVt, L.q_norm, L.k_norm, m->freq, m->pQ,
                                             L.kc, L.vc, nb, pos0, c.n_head, c.n_head_kv, c.head_dim,
                                             c.ctx, c.rope_dim, c.rms_eps, s));
@@ -1076,9 +1102,12 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
             LRS_HIP(gemm(L.down, c.n_ff, m->pX, E, true));
             continue;
         }
-        LRS_HIP(gemm(L.q, E, m->pQt, qd));
-        LRS_HIP(gemm(L.k, E, m->pKt, kvd));
-        LRS_HIP(gemm(L.v, E, m->pVt, kvd));
+        {
+            const lrs_weight *const w[3] = {L.q, L.k, L.v};
+            float *const y[3] = {m->pQt, m->pKt, m->pVt};
+            const uint32_t N[3] = {qd, kvd, kvd};
+            LRS_HIP(gemm_group(3, w, y, N));
+        }
         LRS_HIP(launch_qkv_post(m->pQt, m->pKt, m->pVt, L.bq, L.bk, L.bv, m->freq, m->pQ, L.kc,
                                 L.vc, nb, pos0, qd, kvd, c.head_dim, c.rope_dim, c.ctx, s));
         LRS_HIP(launch_attn_prefill(m->pQ, L.kc, L.vc, m->pATT, nb, pos0, c.n_head, c.n_head_kv,

@@ -74,3 +74,42 @@ def test_gemm_rejects_bad_arguments(lrs, orc, ctx):
     w4 = lrs.Weight.upload(ctx, Q4_K, orc.gen_weight(Q4_K, 1, 4, 256), 256, 4)
     with pytest.raises(lrs.ModelError):
         w4.gemm(np.zeros((2, 256), np.float32), precision=2)
+
+
+@pytest.mark.parametrize("types,m", [((Q4_K, Q4_K, Q6_K), 512), ((Q4_K, Q4_K, Q6_K), 130),
+                                     ((Q5_K, Q6_K), 600), ((Q8_0, Q8_0), 77), ((Q6_K,), 256)])
+def test_gemm_group_equals_single_gemms(lrs, orc, ctx, types, m):
+    """lrs_gemm_group_dev (the prompt block's q / k / v as one launch, segments
+    of ragged width and two types) against the oracle at both precisions and
+    against one lrs_gemm_dev call per weight (the same per-tile arithmetic;
+    the single calls may split K, so within 1e-6 rather than bit-exact)."""
+    k = 1024
+    widths = [200, 136, 72][:len(types)]
+    ws, deqs = [], []
+    for i, (t, n) in enumerate(zip(types, widths)):
+        w = orc.gen_weight(t, 71 + i, n, k, mode=1)
+        deqs.append(orc.dequant(t, w).reshape(n, k))
+        ws.append(lrs.Weight.upload(ctx, t, w, k, n))
+    a = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    for prec in (1, 3):
+        ys = lrs.gemm_group(ctx, ws, a, precision=prec)
+        for y, w, deq in zip(ys, ws, deqs):
+            single = w.gemm(a, precision=prec)
+            assert rel_l2(y, single) < 1e-6
+            if prec == 3:
+                ref = a.astype(np.float64) @ deq.astype(np.float64).T
+                assert rel_l2(y, ref) < 1e-4
+            else:
+                ref = bf16(a).astype(np.float64) @ bf16(deq).astype(np.float64).T
+                assert rel_l2(y, ref) < 1e-5
+
+
+def test_gemm_group_rejects_bad_groups(lrs, orc, ctx):
+    w4 = lrs.Weight.upload(ctx, Q4_K, orc.gen_weight(Q4_K, 1, 16, 512), 512, 16)
+    w6 = lrs.Weight.upload(ctx, Q6_K, orc.gen_weight(Q6_K, 2, 16, 512), 512, 16)
+    w8 = lrs.Weight.upload(ctx, Q8_0, orc.gen_weight(Q8_0, 3, 16, 512), 512, 16)
+    w4k = lrs.Weight.upload(ctx, Q4_K, orc.gen_weight(Q4_K, 4, 16, 256), 256, 16)
+    a = np.zeros((4, 512), np.float32)
+    for group in ([w6, w4], [w4, w6, w4], [w4, w8], [w4, w4k], [w4, w4, w4, w4]):
+        with pytest.raises(lrs.ModelError):
+            lrs.gemm_group(ctx, group, a)
