@@ -1010,9 +1010,11 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
         float *work = gemm_work_bytes(nb, N, K, P) <= m->work_bytes ? m->pWork : nullptr;
         return launch_gemm(w->v, hi, lo(nb, K), y, nb, N, P, s, accum, work);
     };
-    // weights over the same normalised rows (q / k / v, or the delta net's
-    // in-projections): one launch over all their output tiles when that alone
-    // keeps most CUs busy for the whole K, else one launch each (split over K)
+    // weights over the same normalised rows (q / k / v, gate / up, or the
+    // delta net's in-projections): one launch over all their output tiles
+    // when that alone keeps most CUs busy for the whole K (fewer partly
+    // filled rounds of workgroups than one launch each), else one launch
+    // each (split over K)
     auto gemm_group = [&](uint32_t n, const lrs_weight *const *w, float *const *y,
                           const uint32_t *N) -> hipError_t {
         WeightView wv[3];
@@ -1096,8 +1098,12 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                 LRS_HIP(gemm(L.o, qd, m->pX, E, true));
             }
             LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, nullptr, s, hi));
-            LRS_HIP(gemm(L.gate, E, m->pG, c.n_ff));
-            LRS_HIP(gemm(L.up, E, m->pU, c.n_ff));
+            {
+                const lrs_weight *const w[2] = {L.gate, L.up};
+                float *const y[2] = {m->pG, m->pU};
+                const uint32_t N[2] = {c.n_ff, c.n_ff};
+                LRS_HIP(gemm_group(2, w, y, N));
+            }
             LRS_HIP(launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s));
             LRS_HIP(gemm(L.down, c.n_ff, m->pX, E, true));
             continue;
@@ -1115,8 +1121,12 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
         LRS_HIP(split(m->pATT, (size_t)nb * qd));
         LRS_HIP(gemm(L.o, qd, m->pX, E, true));
         LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, nullptr, s, hi));
-        LRS_HIP(gemm(L.gate, E, m->pG, c.n_ff));
-        LRS_HIP(gemm(L.up, E, m->pU, c.n_ff));
+        {
+            const lrs_weight *const w[2] = {L.gate, L.up};
+            float *const y[2] = {m->pG, m->pU};
+            const uint32_t N[2] = {c.n_ff, c.n_ff};
+            LRS_HIP(gemm_group(2, w, y, N));
+        }
         LRS_HIP(launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s));
         LRS_HIP(gemm(L.down, c.n_ff, m->pX, E, true));
     }
