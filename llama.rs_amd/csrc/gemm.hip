@@ -204,14 +204,9 @@ __device__ __forceinline__ void put16(__bf16 *hi, __bf16 *lo, const float (&v)[1
 // load step k+3, issue step k's MFMAs, then dequantize step k+1 into the
 // other buffer (VALU work that overlaps the matrix cores), then one barrier.
 // K-quant rows are whole super-blocks (K % 256 == 0), so the loop runs four
-// steps per trip with no tail.
-//
-// Tile order: workgroup b runs on XCD b % 8 (round-robin dispatch); the
-// tiles are numbered M-block-major and XCD x takes the x-th contiguous run
-// of them, so the workgroups of one XCD share one or two activation blocks,
-// which stay in that XCD's L2.
-// the output tile (m0, n0 of segment sg) of K slice kz, with the weight of
-// type T; As / Ws the workgroup's LDS stages
+// steps per trip with no tail.  One call computes the output tile (m0, n0
+// of segment sg) of K slice kz with the weight of type T, over the
+// workgroup's LDS stages As / Ws.
 template <uint32_t T, int PREC, int BM>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const GemmSeg &sg, uint32_t kz,
                                           uint32_t m0, uint32_t n0,
@@ -372,7 +367,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const GemmSeg &sg, 
 // workgroup b takes output tile t0 of the (K slice, M block, N tile) order;
 // the segment of its N tile picks the weight and the type (T0 for the first
 // nseg0 segments, T1 after them); MS = the most segments the instance takes
-// (1: single-weight launches)
+// (1: single-weight launches).  Tile order: workgroup b runs on XCD b % 8
+// (round-robin dispatch); the tiles are numbered M-block-major and XCD x
+// takes the x-th contiguous run of them, so the workgroups of one XCD share
+// one or two activation blocks, which stay in that XCD's L2.
 template <uint32_t T0, uint32_t T1, int PREC, int BM, int MS>
 __global__ __launch_bounds__(512) void k_gemm(GemmArgs g) {
     constexpr int NS = PREC == 3 ? 2 : 1;
