@@ -75,27 +75,30 @@ def test_decode_logits_and_greedy_match_oracle(lrs, orc, ctx, name, cfg, mix, mo
 LONG_CHECKS = (1, 16, 17, 511, 512, 513, 1024, 1025, 1041)
 LONG_CASES = [
     # k_attn<128, 5>: 16 lane groups, one block per round
-    ("gqa5", dict(modelgen.GQA5, ctx=1100)),
+    ("gqa5", dict(modelgen.GQA5, ctx=1100), LONG_CHECKS),
     # k_attn<64, 2>: 32 lane groups, two blocks per round
-    ("tiny", dict(modelgen.TINY, ctx=1100)),
+    ("tiny", dict(modelgen.TINY, ctx=1100), LONG_CHECKS),
+    # the 4096-position cache of the benchmark config, filled to the last slot
+    # (each split owns 8 blocks)
+    ("gqa5-4096", dict(modelgen.GQA5, ctx=4096), (2048, 2049, 4095, 4096)),
 ]
 
 
-@pytest.mark.parametrize("name,cfg", LONG_CASES, ids=[c[0] for c in LONG_CASES])
-def test_long_context_decode_matches_oracle(lrs, orc, ctx, name, cfg):
-    """attention.rs:76-166 over up to 1041 cached positions: every token goes
-    through decode(); the logits at the lengths of LONG_CHECKS are checked
+@pytest.mark.parametrize("name,cfg,checks", LONG_CASES, ids=[c[0] for c in LONG_CASES])
+def test_long_context_decode_matches_oracle(lrs, orc, ctx, name, cfg, checks):
+    """attention.rs:76-166 over up to a full 4096-position cache: every token
+    goes through decode(); the logits at the lengths of `checks` are checked
     against the oracle at the 1e-3 bar with the same argmax."""
     print(f"case {name}", flush=True)
     w = modelgen.host_model(orc, cfg, seed=29, mode=0, d_lo=1e-3, d_hi=1e-2)
     gm = modelgen.gpu_model(lrs, ctx, cfg, w)
-    om = orc.Model(cfg, w, kv_f16=True, threads=8)
-    seq = np.random.default_rng(11).integers(0, cfg["vocab"], max(LONG_CHECKS)).tolist()
+    om = orc.Model(cfg, w, kv_f16=True, threads=16)
+    seq = np.random.default_rng(11).integers(0, cfg["vocab"], max(checks)).tolist()
     done, worst = 0, 0.0
     for pos, t in enumerate(seq):
         g = gm.decode(t, pos)
         n = pos + 1
-        if n in LONG_CHECKS:
+        if n in checks:
             o = om.forward(seq[done:n])
             done = n
             e = rel_l2(g, o)
@@ -103,7 +106,7 @@ def test_long_context_decode_matches_oracle(lrs, orc, ctx, name, cfg):
             assert e < LOGIT_TOL, (name, n, e)
             assert int(np.argmax(g)) == int(np.argmax(o)), (name, n)
     gm.close()
-    print(f"{name}: worst rel L2 {worst:.2e} at lengths {LONG_CHECKS}")
+    print(f"{name}: worst rel L2 {worst:.2e} at lengths {checks}")
 
 
 # Q8_0 and K-quant weights sharing inputs: q/k Q8_0 with v Q6_K, o and down
