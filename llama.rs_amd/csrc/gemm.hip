@@ -50,7 +50,7 @@ struct GemmArgs {
     uint32_t M, K;
     uint32_t accum;           // 1: y += A W^T (residual add), 0: y = A W^T
     uint32_t nm, nn;          // output tiles along M and N (all segments)
-    uint32_t ks;              // K slices (one segment): slice z writes part + z*M*N (then k_reduce_ks)
+    uint32_t ks;              // K slices (one segment): slice z writes part + z*M*N (then a reduce)
     float *part;
 };
 
@@ -517,7 +517,7 @@ bool gemm_segs_supported(const WeightView *w, uint32_t nseg) {
 
 hipError_t launch_gemm_segs(const WeightView *w, float *const *y, const uint32_t *ldy, uint32_t nseg,
                             const __bf16 *ahi, const __bf16 *alo, uint32_t M, int prec,
-                            hipStream_t s, bool accum, float *work) {
+                            hipStream_t s, bool accum, float *work, uint32_t *ks_out) {
     if (M == 0 || nseg == 0 || nseg > (uint32_t)GM_MAX_SEG || (prec == 3 && !alo))
         return hipErrorInvalidValue;
     if (!gemm_segs_supported(w, nseg) || w[0].n_in % (4 * GM_BK)) return hipErrorInvalidValue;
@@ -549,7 +549,9 @@ hipError_t launch_gemm_segs(const WeightView *w, float *const *y, const uint32_t
     if (!fn) return hipErrorNotSupported;
     const uint32_t grid = 8 * ((g.nm * g.nn * g.ks + 7) / 8);
     hipLaunchKernelGGL(fn, dim3(grid), dim3(512), 0, s, g);
-    if (g.ks > 1) {
+    if (ks_out) {
+        *ks_out = g.ks;  // the caller reduces the slices (launch_reduce_norm_rows)
+    } else if (g.ks > 1) {
         const size_t n = (size_t)M * g.seg[0].N;
         hipLaunchKernelGGL(k_reduce_ks, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, work,
                            y[0], M, g.seg[0].N, ldy[0], g.ks, g.accum);
@@ -558,9 +560,10 @@ hipError_t launch_gemm_segs(const WeightView *w, float *const *y, const uint32_t
 }
 
 hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
-                       uint32_t ldy, int prec, hipStream_t s, bool accum, float *work) {
+                       uint32_t ldy, int prec, hipStream_t s, bool accum, float *work,
+                       uint32_t *ks_out) {
     if (!is_tiled(w.type)) return hipErrorNotSupported;
-    return launch_gemm_segs(&w, &y, &ldy, 1, ahi, alo, M, prec, s, accum, work);
+    return launch_gemm_segs(&w, &y, &ldy, 1, ahi, alo, M, prec, s, accum, work, ks_out);
 }
 
 }  // namespace lrs

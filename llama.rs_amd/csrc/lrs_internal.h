@@ -119,9 +119,11 @@ hipError_t launch_matvec_actq(WeightView w, const float *x, float *y, uint32_t c
 // Y[M][ldy] = A[M][K] W^T on the matrix cores; A given as bf16 planes
 // (prec 1: hi only; 3: hi + lo, three products) from launch_split_bf16
 // work: gemm_work_bytes(M, N, K, prec) of scratch for the K-sliced form (null: one slice)
+// ks_out: when given, a K split leaves its ks_out slices of [M][N] partials in
+// work for the caller to reduce (ks_out 1: y written directly)
 hipError_t launch_gemm(WeightView w, const __bf16 *ahi, const __bf16 *alo, float *y, uint32_t M,
                        uint32_t ldy, int prec, hipStream_t s, bool accum = false,
-                       float *work = nullptr);
+                       float *work = nullptr, uint32_t *ks_out = nullptr);
 size_t gemm_work_bytes(uint32_t M, uint32_t N, uint32_t K, int prec);
 // several weights over the same A in one launch (their output tiles side by
 // side; y[i] [M][ldy[i]]): at most 3, the same n_in, at most two types with
@@ -132,7 +134,8 @@ bool gemm_segs_supported(const WeightView *w, uint32_t nseg);
 uint32_t gemm_out_tiles(uint32_t M, uint32_t N, int prec);
 hipError_t launch_gemm_segs(const WeightView *w, float *const *y, const uint32_t *ldy, uint32_t nseg,
                             const __bf16 *ahi, const __bf16 *alo, uint32_t M, int prec,
-                            hipStream_t s, bool accum = false, float *work = nullptr);
+                            hipStream_t s, bool accum = false, float *work = nullptr,
+                            uint32_t *ks_out = nullptr);
 // hi = bf16(a), lo = bf16(a - hi) (lo may be null); n a multiple of 4
 hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, hipStream_t s);
 // batched prompt block (prefill.hip)
@@ -140,6 +143,12 @@ hipError_t launch_split_bf16(const float *a, size_t n, __bf16 *hi, __bf16 *lo, h
 // same values as the bf16 planes of launch_split_bf16 ([n][E] hi, then lo)
 hipError_t launch_rmsnorm_rows(const float *X, const float *w, float eps, uint32_t E, uint32_t n,
                                float *Y, hipStream_t s, __bf16 *hi = nullptr);
+// X += the ks K-slice partials part[z][n][E] (slices in order, as
+// k_reduce_ks), then the RMSNorm rows of the new X times w as
+// launch_rmsnorm_rows writes them (Y may be null; hi planes)
+hipError_t launch_reduce_norm_rows(const float *part, uint32_t ks, float *X, const float *w,
+                                   float eps, uint32_t E, uint32_t n, float *Y, __bf16 *hi,
+                                   hipStream_t s);
 hipError_t launch_qkv_post(const float *qt, const float *kt, const float *vt, const float *bq,
                            const float *bk, const float *bv, const float *freq, float *q,
                            _Float16 *kc, _Float16 *vc, uint32_t n, uint32_t pos0, uint32_t qd,

@@ -1031,15 +1031,48 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
         }
         return hipSuccess;
     };
+    // pX += A W^T (o, down, the delta net's out-projection), then the
+    // RMSNorm rows of pX times nw as GEMM planes (and in f32 into xn): when
+    // the GEMM splits over K, its slices' reduce and the norm run as one
+    // kernel
+    auto gemm_resid_norm = [&](const lrs_weight *w, uint32_t K, const float *nw,
+                               float *xn) -> hipError_t {
+        float *work = gemm_work_bytes(nb, E, K, P) <= m->work_bytes ? m->pWork : nullptr;
+        uint32_t ks = 1;
+        const hipError_t e = launch_gemm(w->v, hi, lo(nb, K), m->pX, nb, E, P, s, true, work, &ks);
+        if (e != hipSuccess) return e;
+        return ks > 1 ? launch_reduce_norm_rows(m->pWork, ks, m->pX, nw, c.rms_eps, E, nb, xn, hi, s)
+                      : launch_rmsnorm_rows(m->pX, nw, c.rms_eps, E, nb, xn, s, hi);
+    };
+    // the normalised rows as GEMM planes, and in f32 for a delta-net block,
+    // which reads them for its gates
+    auto xn_for = [&](const DevLayer &L) { return m->hybrid && L.dn ? m->pXN : nullptr; };
+    // the previous layer's down GEMM already normalised the rows for this one
+    bool normed = false;
+    // the FFN of layer l: gate / up, SwiGLU, down + residual (+ the next
+    // layer's attention norm)
+    auto ffn = [&](uint32_t l) -> hipError_t {
+        const DevLayer &L = m->layers[l];
+        {
+            const lrs_weight *const w[2] = {L.gate, L.up};
+            float *const y[2] = {m->pG, m->pU};
+            const uint32_t N[2] = {c.n_ff, c.n_ff};
+            const hipError_t e = gemm_group(2, w, y, N);
+            if (e != hipSuccess) return e;
+        }
+        const hipError_t e = launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s);
+        if (e != hipSuccess) return e;
+        if (l + 1 == c.n_layer) return gemm(L.down, c.n_ff, m->pX, E, true);
+        const DevLayer &N = m->layers[l + 1];
+        normed = true;
+        return gemm_resid_norm(L.down, c.n_ff, N.attn_norm, xn_for(N));
+    };
     LRS_HIP(hipMemcpyAsync(m->ptok, tokens, nb * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     LRS_HIP(launch_dequant_rows(m->embd->v, m->ptok, nb, m->pX, s));
     for (uint32_t l = 0; l < c.n_layer; l++) {
         const DevLayer &L = m->layers[l];
-        // the normalised rows as GEMM planes (and in f32 for the delta-net
-        // block, which reads them for its gates)
-        const bool keep_xn = m->hybrid && L.dn;
-        LRS_HIP(launch_rmsnorm_rows(m->pX, L.attn_norm, c.rms_eps, E, nb, keep_xn ? m->pXN : nullptr,
-                                    s, hi));
+        if (!normed) LRS_HIP(launch_rmsnorm_rows(m->pX, L.attn_norm, c.rms_eps, E, nb, xn_for(L), s, hi));
+        normed = false;
         if (m->hybrid) {
             if (L.dn) {
                 // gated delta net over the block (plano_delta with n_tok = nb)
@@ -1078,7 +1111,7 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                 da.eps = c.rms_eps;
                 LRS_HIP(launch_dn_prefill(da, s));
                 LRS_HIP(split(m->pY, (size_t)nb * VD));
-                LRS_HIP(gemm(L.ssm_out, VD, m->pX, E, true));
+                LRS_HIP(gemm_resid_norm(L.ssm_out, VD, L.ffn_norm, nullptr));
             } else {
                 // gated attention: Q (+ gate), k, v; QK-norm + RoPE; causal
                 // attention over the cache; sigmoid gate; o
@@ -1095,17 +1128,9 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
                                             c.head_dim, c.ctx, s));
                 LRS_HIP(launch_gate_rows(m->pATT, m->pQG, nb, qd, c.head_dim, s));
                 LRS_HIP(split(m->pATT, (size_t)nb * qd));
-                LRS_HIP(gemm(L.o, qd, m->pX, E, true));
+                LRS_HIP(gemm_resid_norm(L.o, qd, L.ffn_norm, nullptr));
             }
-            LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, nullptr, s, hi));
-            {
-                const lrs_weight *const w[2] = {L.gate, L.up};
-                float *const y[2] = {m->pG, m->pU};
-                const uint32_t N[2] = {c.n_ff, c.n_ff};
-                LRS_HIP(gemm_group(2, w, y, N));
-            }
-            LRS_HIP(launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s));
-            LRS_HIP(gemm(L.down, c.n_ff, m->pX, E, true));
+            LRS_HIP(ffn(l));
             continue;
         }
         {
@@ -1119,16 +1144,8 @@ static int prefill_block(lrs_model *m, const uint32_t *tokens, uint32_t nb, uint
         LRS_HIP(launch_attn_prefill(m->pQ, L.kc, L.vc, m->pATT, nb, pos0, c.n_head, c.n_head_kv,
                                     c.head_dim, c.ctx, s));
         LRS_HIP(split(m->pATT, (size_t)nb * qd));
-        LRS_HIP(gemm(L.o, qd, m->pX, E, true));
-        LRS_HIP(launch_rmsnorm_rows(m->pX, L.ffn_norm, c.rms_eps, E, nb, nullptr, s, hi));
-        {
-            const lrs_weight *const w[2] = {L.gate, L.up};
-            float *const y[2] = {m->pG, m->pU};
-            const uint32_t N[2] = {c.n_ff, c.n_ff};
-            LRS_HIP(gemm_group(2, w, y, N));
-        }
-        LRS_HIP(launch_swiglu_split(m->pG, m->pU, (size_t)nb * c.n_ff, hi, s));
-        LRS_HIP(gemm(L.down, c.n_ff, m->pX, E, true));
+        LRS_HIP(gemm_resid_norm(L.o, qd, L.ffn_norm, nullptr));
+        LRS_HIP(ffn(l));
     }
     return LRS_OK;
 }

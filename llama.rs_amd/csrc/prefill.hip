@@ -47,6 +47,58 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float *__restrict__ 
     }
 }
 
+// X += the ks K-slice partials part[z][row][E] (summed in slice order, then
+// added to X, as k_reduce_ks does), then k_rmsnorm_rows over the new rows
+// (same sum-of-squares order, so the same scale): the residual add of a
+// K-split o / down GEMM and the norm after it in one pass over the rows
+__global__ __launch_bounds__(256) void k_reduce_norm_rows(const float *__restrict__ part,
+                                                          uint32_t ks, float *__restrict__ X,
+                                                          const float *__restrict__ w, float eps,
+                                                          uint32_t E, float *__restrict__ Y,
+                                                          __bf16 *__restrict__ hi) {
+    __shared__ float red[4];
+    const size_t plane = (size_t)gridDim.x * E, r0 = (size_t)blockIdx.x * E;
+    float *x = X + r0;
+    float ss = 0.f;
+    for (uint32_t i = 4 * threadIdx.x; i < E; i += 4 * blockDim.x) {
+        float4 p = *reinterpret_cast<const float4 *>(part + r0 + i);
+        for (uint32_t z = 1; z < ks; z++) {
+            const float4 q = *reinterpret_cast<const float4 *>(part + z * plane + r0 + i);
+            p.x += q.x;
+            p.y += q.y;
+            p.z += q.z;
+            p.w += q.w;
+        }
+        float4 v = *reinterpret_cast<const float4 *>(x + i);
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
+        *reinterpret_cast<float4 *>(x + i) = v;
+        ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float scale = 1.0f / sqrtf(tot / (float)E + eps);
+    // each thread reads back the elements it stored above
+    for (uint32_t i = 4 * threadIdx.x; i < E; i += 4 * blockDim.x) {
+        const float4 v = *reinterpret_cast<const float4 *>(x + i);
+        const float4 g = *reinterpret_cast<const float4 *>(w + i);
+        const float4 o = {(v.x * scale) * g.x, (v.y * scale) * g.y, (v.z * scale) * g.z,
+                          (v.w * scale) * g.w};
+        if (Y) *reinterpret_cast<float4 *>(Y + r0 + i) = o;
+        if (hi) {
+            split_store(o.x, hi + r0 + i, hi + plane + r0 + i);
+            split_store(o.y, hi + r0 + i + 1, hi + plane + r0 + i + 1);
+            split_store(o.z, hi + r0 + i + 2, hi + plane + r0 + i + 2);
+            split_store(o.w, hi + r0 + i + 3, hi + plane + r0 + i + 3);
+        }
+    }
+}
+
 // q/k/v GEMM outputs -> bias, adjacent-pair RoPE on q and k at position
 // pos0 + token, q to f32, k and v to the f16 cache.  One thread per pair.
 struct QkvPost {
@@ -361,6 +413,14 @@ hipError_t launch_rmsnorm_rows(const float *X, const float *w, float eps, uint32
                                float *Y, hipStream_t s, __bf16 *hi) {
     if (E % 4 || (!Y && !hi)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_rmsnorm_rows, dim3(n), dim3(256), 0, s, X, w, eps, E, Y, hi);
+    return hipGetLastError();
+}
+
+hipError_t launch_reduce_norm_rows(const float *part, uint32_t ks, float *X, const float *w,
+                                   float eps, uint32_t E, uint32_t n, float *Y, __bf16 *hi,
+                                   hipStream_t s) {
+    if (E % 4 || ks == 0 || (!Y && !hi)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_reduce_norm_rows, dim3(n), dim3(256), 0, s, part, ks, X, w, eps, E, Y, hi);
     return hipGetLastError();
 }
 
