@@ -9,6 +9,10 @@ TINY = dict(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512,
 # GQA with 5 query heads per KV head and head_dim 128, like the 32B shape
 GQA5 = dict(n_layer=2, n_embd=1280, n_head=10, n_head_kv=2, head_dim=128, n_ff=1024,
             vocab=1000, rope_dim=128, ctx=160, rms_eps=1e-6, freq_base=1e6)
+# o and down with K = 2048 over few output tiles: the prompt block splits
+# their K across workgroups and adds the slices in the fused reduce + RMSNorm
+KSPLIT = dict(n_layer=2, n_embd=512, n_head=16, n_head_kv=2, head_dim=128, n_ff=2048,
+              vocab=1000, rope_dim=128, ctx=160, rms_eps=1e-6, freq_base=1e6)
 
 Q4_K_M = dict(attn_q=Q4_K, attn_k=Q4_K, attn_v=Q6_K, attn_output=Q4_K, ffn_gate=Q4_K,
               ffn_up=Q4_K, ffn_down=Q6_K, output=Q6_K, token_embd=Q4_K)
@@ -97,6 +101,10 @@ HY_TINY = dict(n_layer=4, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=5
 HY_MID = dict(n_layer=4, n_embd=512, n_head=6, n_head_kv=1, head_dim=256, n_ff=768, vocab=1024,
               rope_dim=64, ctx=64, rms_eps=1e-6, freq_base=1e7, full_attn_interval=2,
               dn_k_heads=2, dn_v_heads=2, dn_state=128, dn_conv=4)
+# K = 2048 for o (8 x 256), ssm_out (16 x 128 state columns) and down: the
+# prompt block's K-split GEMMs and the fused reduce + RMSNorm, including the
+# f32 normalised rows a delta-net layer reads
+HY_KS = dict(HY_MID, n_head=8, n_ff=2048, dn_k_heads=4, dn_v_heads=16)
 
 HY_Q4_K_M = dict(Q4_K_M, ssm_qkv=Q4_K, ssm_gate=Q4_K, ssm_out=Q4_K)
 

@@ -114,7 +114,8 @@ def test_hybrid_batch_reset_and_position_rule(lrs, orc, ctx):
 
 
 @pytest.mark.parametrize("name,cfg", [("hy-tiny", modelgen.HY_TINY), ("hy-mid", modelgen.HY_MID),
-                                      ("hy-gqa5-256", dict(modelgen.HY_MID, n_head=5))])
+                                      ("hy-gqa5-256", dict(modelgen.HY_MID, n_head=5)),
+                                      ("hy-ksplit", modelgen.HY_KS)])
 def test_hybrid_prompt_block_matches_oracle(lrs, orc, ctx, name, cfg):
     """A 40-token prompt in one block (ring wrap, state carried across
     tokens inside the block kernel), then decode steps.  5 query heads per KV

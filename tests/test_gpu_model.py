@@ -201,6 +201,8 @@ PREFILL_CASES = [
     ("tiny-q4km-600", dict(modelgen.TINY, ctx=640), None, 600, 21),
     ("gqa5-q4km-150", modelgen.GQA5, None, 150, 21),
     ("gqa5-q4km-40", modelgen.GQA5, None, 40, 23),
+    # o / down split over K (2 slices) into the fused reduce + RMSNorm
+    ("ksplit-q4km-150", modelgen.KSPLIT, None, 150, 24),
     # every GEMM weight type: Q5_K, Q8_0, and Q8_0 beside K-quants
     ("gqa5-q5km-150", modelgen.GQA5, modelgen.Q5_K_M, 150, 21),
     ("gqa5-q8_0-150", modelgen.GQA5, modelgen.ALL_Q8_0, 150, 21),
