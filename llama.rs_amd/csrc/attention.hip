@@ -308,17 +308,18 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
     pack_half(o, (h * HD + d) >> 5, out);
 }
 
-// split count: about one workgroup per CU (256 = splits x KV heads), at
-// most 32 (measured on the decode benches: 32 splits beat 64 for 4 KV heads
-// x 256 dims, and 16 / 32 tie for 8 x 128; 8 and 64 are slower).  Blocks of
-// 16 positions: a context of L < 16 * splits positions runs ceil(L / 16)
-// splits (measured on the config-3 decode as contiguous ranges of at least
-// 16 positions per split: 32 and 64 are no faster at 512 positions, 128 and
-// 256 slower, and the config-4 attention is slower at 64)
+// split count: at most one workgroup per CU (256 >= splits x KV heads), at
+// most 40 (measured on the decode benches at 511..640 positions: 8 KV heads
+// x 128 dims run 32 splits, 40 / 48 / 64 are slower there, 16 ties; 4 KV
+// heads x 256 dims take 11.8 us with 32 splits, 10.3 with 40, 10.4 with 48,
+// and 64 is slower).  Blocks of 16 positions: a context of L < 16 * splits
+// positions runs ceil(L / 16) splits (measured on the config-3 decode as
+// contiguous ranges of at least 16 positions per split: 32 and 64 are no
+// faster at 512 positions, 128 and 256 slower)
 
 uint32_t attn_splits(uint32_t n_kv) {
     const uint32_t S = 256 / n_kv;
-    return S < 1 ? 1 : S > 32 ? 32 : S;
+    return S < 1 ? 1 : S > 40 ? 40 : S;
 }
 
 using AttnFn = void (*)(AttnArgs);
