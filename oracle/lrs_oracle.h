@@ -20,10 +20,21 @@
  *   matvec             f64 dot, one-hot columns, batched-column invariance
  *   rmsnorm/rope/swiglu/softmax/argmax/attention  reference known answers
  *                                 (ops.rs:1065-1164, attention.rs:174-200)
- *   forward            numpy float64 restatement of model.rs:99-266 on tiny
- *                      models (structure pin; no reference golden logits exist)
+ *   forward            closed-form reductions (tests/test_oracle_model_pins.py:
+ *                      zeroed mixers, one cached position, W_v = 0, FFN-only
+ *                      layer, the int8-activation head) and a numpy float64
+ *                      restatement of model.rs:99-266 (no reference golden
+ *                      logits exist)
  *   delta-net ops      reference known answers (delta_net.rs:133-255) and a
  *                      numpy restatement
+ *   hybrid forward     closed forms in tests/test_oracle_model_pins.py: the
+ *                      delta rule over two tokens from a zero state; the gated
+ *                      attention with one cached position (gate = rows
+ *                      [HD, 2HD) of each head's Q block); QK-norm scale
+ *                      invariance per head; partial RoPE leaving dims >=
+ *                      rope_dim alone; adjacent-pair scores expanded by hand
+ *                      at the closed-form frequencies 1 and base^(-1/2); a
+ *                      delta-net layer followed by an attention layer
  */
 #ifndef LRS_ORACLE_H
 #define LRS_ORACLE_H
@@ -175,9 +186,9 @@ float lrso_silu(float x);                           /* delta_net.rs:27-30 */
  * restates the GPU plan's op order (resident_forward.rs:3826-4103 with
  * plano_delta :2252-2470) with the CPU primitives of delta_net.rs and ops.rs
  * and the shader formulas of dn_gates.comp, dn_norm.comp, dn_l2_qk.comp,
- * dn_conv.comp, delta_net.comp and gate_quant.comp.  Model-level parity
- * against the reference is unpinned (no reference logits exist); the
- * structure is pinned by a float64 numpy restatement (tests/npref.py). */
+ * dn_conv.comp, delta_net.comp and gate_quant.comp.  No reference logits
+ * exist for it; both mixers are pinned by closed forms (see the top of this
+ * header) and the whole by a float64 numpy restatement (tests/npref.py). */
 typedef struct {
     lrso_config base;            /* full-attention layers use n_head, n_head_kv, head_dim */
     uint32_t full_attn_interval; /* layer l is full attention iff (l+1) % interval == 0 */
