@@ -885,45 +885,56 @@ STREAM_SIZES = {  # algorithmic bytes of the decode launches (config 3, then con
     "hybrid_gateup": 100380672, "hybrid_down": 73224192}
 
 
+def _probe_lib():
+    """liblrs_probe.so: the load-only read kernel (a measurement library built
+    beside liblrs.so, not part of the product)."""
+    import ctypes as C
+
+    path = os.path.join(REPO, "llama.rs_amd", "liblrs_probe.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} is missing: build first (python __graft_entry__.py)")
+    L = C.CDLL(path)
+    L.lrsp_read_time.restype = C.c_int
+    L.lrsp_read_time.argtypes = [C.c_int, C.c_void_p, C.c_size_t, C.c_uint32, C.c_int,
+                                 C.c_uint32, C.c_uint32, C.c_uint32, C.c_int,
+                                 C.POINTER(C.c_float)]
+
+    def read_time(device, ptr, window, n_windows, nt, workgroups=0, threads=0, reads=1,
+                  plain_first=False):
+        us = C.c_float()
+        rc = L.lrsp_read_time(device, ptr, window, n_windows, 1 if nt else 0, workgroups,
+                              threads, reads, 1 if plain_first else 0, C.byref(us))
+        if rc != 0:
+            raise RuntimeError(f"lrsp_read_time failed ({rc})")
+        return us.value
+
+    return read_time
+
+
 def bench_stream(ctx, steps):
-    """The read rate of a kernel that does nothing but stream (lrs_read_dev),
-    at each decode launch's byte count, best over 512 / 1024 / 2048
-    workgroups: windows of that size step through a 1 GiB arena, so no window
-    is still in the memory-side cache when it is read again (as in decode,
-    which streams ~20 GB per token)."""
+    """The read rate of a kernel that does nothing but stream
+    (liblrs_probe.so), at each decode launch's byte count, best over
+    512 / 1024 / 2048 workgroups: windows of that size step through a 1 GiB
+    arena, so no window is still in the memory-side cache when it is read
+    again (as in decode, which streams ~20 GB per token)."""
+    read_time = _probe_lib()
     arena = 1 << 30
     buf = ctx.alloc(arena)
+    dev = ctx.device
     out = {}
-
-    def timed(size, nwin, nt, wg):
-        for i in range(2):  # warm-up
-            ctx.read_dev_at(buf, (i % nwin) * size, size, nt, wg)
-        ctx.sync()
-        ctx.timer_start()
-        for i in range(steps):
-            ctx.read_dev_at(buf, (i % nwin) * size, size, nt, wg)
-        return ctx.timer_stop() * 1e3 / steps
-
     for name, size in STREAM_SIZES.items():
         size -= size % 16
         nwin = max(1, arena // size)
         res = {}
         for nt in (True, False):
-            per = {wg: timed(size, nwin, nt, wg) for wg in (512, 1024, 2048)}
+            per = {wg: read_time(dev, buf.ptr, size, nwin, nt, wg, 0, steps) for wg in (512, 1024, 2048)}
             wg = min(per, key=per.get)
             res["nt" if nt else "plain"] = dict(us=round(per[wg], 2), workgroups=wg,
                                                 gbs=round(size / per[wg] / 1e3, 1))
         # the same window read once with plain loads just before (memory-side
         # cache warm), at the best non-temporal workgroup count
         wg = res["nt"]["workgroups"]
-        tot, reps = 0.0, min(steps, 8)
-        for i in range(reps):
-            off = (i % nwin) * size
-            ctx.read_dev_at(buf, off, size, False, wg)
-            ctx.timer_start()
-            ctx.read_dev_at(buf, off, size, True, wg)
-            tot += ctx.timer_stop() * 1e3
-        us = tot / reps
+        us = read_time(dev, buf.ptr, size, nwin, True, wg, 0, min(steps, 8), plain_first=True)
         res["nt_after_plain"] = dict(us=round(us, 2), workgroups=wg, gbs=round(size / us / 1e3, 1))
         out[name] = dict(bytes=size, **res)
         log(f"[bench] stream {name:7s} {size / 1e6:7.1f} MB: nt {res['nt']['us']:7.2f} us "
@@ -936,12 +947,7 @@ def bench_stream(ctx, steps):
     nwin = max(1, arena // size)
     cap = {}
     for wg, th in ((160, 256), (160, 768), (160, 1024), (256, 768), (256, 1024)):
-        ctx.read_dev_at(buf, 0, size, True, wg, th)
-        ctx.sync()
-        ctx.timer_start()
-        for i in range(steps):
-            ctx.read_dev_at(buf, (i % nwin) * size, size, True, wg, th)
-        us = ctx.timer_stop() * 1e3 / steps
+        us = read_time(dev, buf.ptr, size, nwin, True, wg, th, steps)
         cap[f"{wg}x{th}"] = dict(us=round(us, 2), gbs=round(size / us / 1e3, 1),
                                  gbs_per_workgroup=round(size / us / 1e3 / wg, 1))
         log(f"[bench] stream down-size, {wg} workgroups x {th} threads: {us:7.2f} us "
@@ -982,14 +988,14 @@ def main():
     from pkgload import load_product
 
     lrs = load_product()
-    ctx = lrs.Context()
+    ctx = lrs.Context(0)
     log(f"[bench] workload={a.workload} steps={a.steps} warmup={a.warmup}")
     threads = min(16, os.cpu_count() or 1)
     if a.workload == "pmc":
         run_pmc(lrs, ctx)
     elif a.workload == "stream":
         r = bench_stream(ctx, a.steps)
-        print(json.dumps({"metric": "streaming read rate of a load-only kernel (lrs_read_dev)",
+        print(json.dumps({"metric": "streaming read rate of a load-only kernel (liblrs_probe.so)",
                           "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "data": "uninitialised "
                           "device memory (the values are not used)", "sizes": r}), flush=True)
     elif a.workload == "gemm":

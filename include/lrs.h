@@ -57,9 +57,11 @@ const char *lrs_version(void);
 /* ------------------------------------------------------------------------ */
 /* context                                                                  */
 /* ------------------------------------------------------------------------ */
-/* Opens a device and a stream.  device = -1 picks the device with the most
- * free HBM, like pick_device (resident_forward.rs:1119-1133).
- * Replaces VulkanContext::new + VulkanDevice::create (device.rs). */
+/* Opens a device and a stream.  device >= 0 opens that device only.
+ * device = -1 picks the device with the most free HBM, like pick_device
+ * (resident_forward.rs:1119-1133); to compare them it makes every visible
+ * device current once, so callers that must not touch other GPUs pass an
+ * index.  Replaces VulkanContext::new + VulkanDevice::create (device.rs). */
 int lrs_ctx_create(int device, lrs_ctx **out);
 void lrs_ctx_destroy(lrs_ctx *ctx);
 /* Blocks until all work enqueued on the context's stream has finished. */
@@ -201,16 +203,6 @@ int lrs_capture_begin(lrs_ctx *ctx);
 int lrs_capture_end(lrs_ctx *ctx, lrs_graph **out);
 int lrs_graph_launch(lrs_graph *g);
 void lrs_graph_destroy(lrs_graph *g);
-
-/* Measurement helper, no counterpart in the reference: one pass of plain
- * (nontemporal 0) or non-temporal (1) 16-byte loads over bytes (a multiple of
- * 16) of device memory by `workgroups` workgroups (1..4096, 0 = 1024) of
- * `threads` threads (a multiple of 64 up to 1024, 0 = 256), enqueued on the
- * context stream; timed between lrs_timer_start / lrs_timer_stop it gives the
- * read rate a kernel that does nothing but stream reaches, the practical
- * ceiling of the matvec kernels. */
-int lrs_read_dev(lrs_ctx *ctx, const void *src_dev, size_t bytes, int nontemporal,
-                 uint32_t workgroups, uint32_t threads);
 
 /* HIP events on the context stream: start, then stop returns elapsed ms. */
 int lrs_timer_start(lrs_ctx *ctx);

@@ -81,7 +81,6 @@ def _load() -> C.CDLL:
         "lrs_capture_end": (i32, [vp, pvp]),
         "lrs_graph_launch": (i32, [vp]),
         "lrs_graph_destroy": (None, [vp]),
-        "lrs_read_dev": (i32, [vp, vp, sz, i32, u32, u32]),
         "lrs_timer_start": (i32, [vp]),
         "lrs_timer_stop": (i32, [vp, C.POINTER(C.c_float)]),
     }
@@ -133,10 +132,14 @@ class Graph:
 class Context:
     """A device + stream (VulkanContext/VulkanDevice in the reference)."""
 
-    def __init__(self, device: int = -1):
+    def __init__(self, device: int = 0):
+        """Opens `device` (default 0: this process touches no other GPU);
+        device = -1 asks lrs_ctx_create to pick the device with the most free
+        HBM, which opens every visible device to compare them."""
         h = C.c_void_p()
         check(lib.lrs_ctx_create(device, C.byref(h)))
         self.h = h
+        self.device = device if device >= 0 else None
         # children must be released before the context (C-ABI contract):
         # models first (they reference weights), then weights and buffers
         self._models = weakref.WeakSet()
@@ -153,14 +156,6 @@ class Context:
 
     def alloc(self, nbytes: int) -> "DeviceBuffer":
         return DeviceBuffer(self, nbytes)
-
-    def read_dev_at(self, buf: "DeviceBuffer", offset: int, nbytes: int, nontemporal: bool,
-                    workgroups: int = 0, threads: int = 0) -> None:
-        """One streaming read pass over nbytes of buf from offset by `workgroups`
-        workgroups of `threads` threads (0 = 1024 of 256; lrs_read_dev)."""
-        assert 0 <= offset and offset + nbytes <= buf.nbytes
-        check(lib.lrs_read_dev(self.h, buf.ptr + offset, nbytes, 1 if nontemporal else 0,
-                               workgroups, threads))
 
     def timer_start(self) -> None:
         check(lib.lrs_timer_start(self.h))
@@ -397,7 +392,7 @@ class GpuMatmul:
     reference's ResidentGpu (crates/llama-vulkan/src/resident.rs:141-452)."""
 
     def __init__(self, ctx: Context | None = None):
-        self.ctx = ctx or Context()
+        self.ctx = ctx or Context(0)
         self._cache: dict = {}
 
     def _weight(self, t, w_bytes, n_in, n_out) -> Weight:

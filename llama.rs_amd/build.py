@@ -1,4 +1,6 @@
-"""Builds liblrs.so (all HIP sources under csrc/) for gfx950 with hipcc.
+"""Builds liblrs.so (all HIP sources under csrc/) for gfx950 with hipcc, and
+the measurement library liblrs_probe.so (probe/probe.hip, used by bench.py
+only; not part of the product).
 
 Every HIP translation unit is compiled with
   -ffp-contract=off     the dequant must round like the Rust reference
@@ -16,6 +18,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "liblrs.so")
+PROBE_SRC = os.path.join(HERE, "probe", "probe.hip")
+PROBE_OUT = os.path.join(HERE, "liblrs_probe.so")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -39,17 +43,22 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 8) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    with cf.ThreadPoolExecutor(max_workers=min(jobs, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = OUT + ".tmp"
+def _link(objs, out: str) -> None:
+    tmp = out + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
+
+
+def build(jobs: int = 8) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip"))) + [PROBE_SRC]
+    with cf.ThreadPoolExecutor(max_workers=min(jobs, len(srcs))) as ex:
+        objs = list(ex.map(_compile, srcs))
+    _link(objs[:-1], OUT)
+    _link(objs[-1:], PROBE_OUT)
     return OUT
 
 

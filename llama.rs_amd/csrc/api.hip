@@ -110,7 +110,8 @@ static int ctx_scratch(lrs_ctx *ctx, size_t bytes, void **p) {
 // element, fully rewritten by every call, so nothing has to start at zero).
 // Each GPU holds its own copy until the process ends.  In host code `scratch`
 // only names the symbol: the device address of each GPU's copy comes from
-// hipGetSymbolAddress, resolved once per device by lrs_ctx_create.
+// hipGetSymbolAddress, resolved once per device by the first
+// lrs_matvec_dev_noalloc call there (so no other entry point depends on it).
 static constexpr size_t NOALLOC_PACK_BYTES = 160 * 1024;
 static __device__ __align__(256) uint8_t scratch[NOALLOC_PACK_BYTES];
 static constexpr int NOALLOC_MAX_DEVICES = 64;
@@ -120,8 +121,8 @@ static void *g_noalloc_ptr[NOALLOC_MAX_DEVICES];
 namespace lrs {
 // with `device` current: the device address of this GPU's `scratch`
 static int noalloc_init(int device) {
-    if (device >= NOALLOC_MAX_DEVICES)
-        return fail(LRS_E_UNSUPPORTED, "device index " + std::to_string(device) + " above " +
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES)
+        return fail(LRS_E_UNSUPPORTED, "the no-allocation matvec serves device indices 0.." +
                                            std::to_string(NOALLOC_MAX_DEVICES - 1));
     std::lock_guard<std::mutex> lk(g_noalloc_mu);
     if (g_noalloc_ptr[device]) return LRS_OK;
@@ -132,9 +133,12 @@ static int noalloc_init(int device) {
     g_noalloc_ptr[device] = p;
     return LRS_OK;
 }
-static void *noalloc_ptr(int device) {
+// with `device` current: the resolved address, resolving it on first use
+static int noalloc_ptr(int device, void **p) {
+    if (int rc = noalloc_init(device)) return rc;
     std::lock_guard<std::mutex> lk(g_noalloc_mu);
-    return device >= 0 && device < NOALLOC_MAX_DEVICES ? g_noalloc_ptr[device] : nullptr;
+    *p = g_noalloc_ptr[device];
+    return LRS_OK;
 }
 }  // namespace lrs
 
@@ -169,7 +173,6 @@ int lrs_ctx_create(int device, lrs_ctx **out) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(LRS_E_UNSUPPORTED, std::string("liblrs is built for gfx950, device is ") +
                                            prop.gcnArchName);
-    if (int rc = noalloc_init(device)) return rc;
     lrs_ctx *c = new lrs_ctx();
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -364,9 +367,9 @@ int lrs_matvec_dev_noalloc(lrs_ctx *ctx, const lrs_weight *w, const float *x_dev
         return fail(LRS_E_ARG, "n_in=" + std::to_string(w->v.n_in) +
                                    " is above the no-allocation matvec's maximum of " +
                                    std::to_string(LRS_NOALLOC_MAX_N_IN));
-    void *pack = noalloc_ptr(ctx->device);
-    if (!pack) return fail(LRS_E_HIP, "static pack of this device not resolved");
     SETDEV(ctx);
+    void *pack = nullptr;
+    if (int rc_ = noalloc_ptr(ctx->device, &pack)) return rc_;
     LRS_HIP(launch_matvec_staged(w->v, x_dev, y_dev, cols, pack, ctx->stream));
     return LRS_OK;
 }
@@ -555,18 +558,6 @@ void lrs_graph_destroy(lrs_graph *g) {
         g->ctx->live_graphs--;
     }
     delete g;
-}
-
-int lrs_read_dev(lrs_ctx *ctx, const void *src_dev, size_t bytes, int nontemporal,
-                 uint32_t workgroups, uint32_t threads) {
-    if (!ctx || !src_dev || bytes == 0 || bytes % 16 || workgroups > 4096 || threads % 64 ||
-        threads > 1024)
-        return fail(LRS_E_ARG, "lrs_read_dev: null argument, bytes not a positive multiple of "
-                               "16, more than 4096 workgroups, or threads not a multiple of 64 "
-                               "up to 1024");
-    SETDEV(ctx);
-    LRS_HIP(lrs::launch_read(src_dev, bytes, nontemporal != 0, workgroups, threads, ctx->stream));
-    return LRS_OK;
 }
 
 int lrs_timer_start(lrs_ctx *ctx) {

@@ -208,11 +208,6 @@ hipError_t launch_qk_prep(const float *qg, const float *kb, const float *vb, con
                           uint32_t head_dim, uint32_t ctx, uint32_t rope_dim, float eps,
                           hipStream_t s);
 
-// one streaming read pass over bytes (a multiple of 16) of device memory
-// (probe.hip, behind lrs_read_dev)
-hipError_t launch_read(const void *src, size_t bytes, bool nontemporal, uint32_t workgroups,
-                       uint32_t threads, hipStream_t s);
-
 }  // namespace lrs
 
 struct lrs_ctx {

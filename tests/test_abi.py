@@ -35,6 +35,16 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_measurement_probe_is_a_library_of_its_own():
+    """the load-only read kernel bench.py measures with lives in
+    liblrs_probe.so, not in the product library or its header"""
+    probe = C.CDLL(os.path.join(REPO, "llama.rs_amd", "liblrs_probe.so"))
+    assert hasattr(probe, "lrsp_read_time")
+    lib = C.CDLL(LIB)
+    assert not hasattr(lib, "lrs_read_dev") and not hasattr(lib, "lrsp_read_time")
+    assert "lrs_read_dev" not in declared_symbols()
+
+
 def test_library_is_built_for_gfx950_only():
     data = open(LIB, "rb").read()
     assert b"gfx950" in data

@@ -33,7 +33,7 @@ def rel_l2(a, b):
 
 @pytest.fixture(scope="module")
 def c3(lrs, orc):
-    ctx = lrs.Context()
+    ctx = lrs.Context(0)
     w = modelgen.host_model(orc, C3_2L, seed=31, mode=0, d_lo=1e-3, d_hi=1e-2)
     gm = modelgen.gpu_model(lrs, ctx, C3_2L, w)
     prompt = np.random.default_rng(17).integers(0, C3_2L["vocab"], 12).tolist()
@@ -121,7 +121,7 @@ C2_FFN = dict(C3_2L, n_ff=13824, vocab=4096)
 
 @pytest.mark.parametrize("cfg,seed", [(C4_FFN, 41), (C2_FFN, 47)], ids=["n_ff17408", "n_ff13824"])
 def test_ffn_width_decode_matches_oracle(lrs, orc, cfg, seed):
-    ctx = lrs.Context()
+    ctx = lrs.Context(0)
     w = modelgen.host_model(orc, cfg, seed=seed, mode=0, d_lo=1e-3, d_hi=1e-2)
     gm = modelgen.gpu_model(lrs, ctx, cfg, w)
     try:

@@ -16,7 +16,7 @@ Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 
 @pytest.fixture(scope="module")
 def ctx(lrs):
-    c = lrs.Context()
+    c = lrs.Context(0)
     yield c
     c.close()
 

@@ -13,7 +13,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def ctx(lrs):
-    c = lrs.Context()
+    c = lrs.Context(0)
     yield c
     c.close()
 

@@ -20,7 +20,7 @@ MATVEC_TOL = 1e-4
 
 @pytest.fixture(scope="module")
 def ctx(lrs):
-    c = lrs.Context()
+    c = lrs.Context(0)
     yield c
     c.close()
 
@@ -112,28 +112,39 @@ def test_dequant_rejects_bad_sizes(lrs, ctx):
             lrs.dequant_to_f32(ctx, t, bytes(bad))
 
 
-def test_read_probe_runs_and_rejects_bad_sizes(lrs, ctx):
-    """lrs_read_dev (the streaming-read measurement helper) reads a buffer in
-    both load forms and refuses a size that is not a multiple of 16 or runs
-    past the buffer."""
-    buf = ctx.alloc(1 << 20)
-    for nt in (True, False):
+def test_read_probe_library_runs_and_rejects_bad_arguments(lrs, ctx):
+    """liblrs_probe.so (the load-only read kernel behind bench.py --workload
+    stream, kept out of liblrs.so) times reads in both load forms and refuses
+    sizes that are not a multiple of 16, more than 4096 workgroups and thread
+    counts that are not a multiple of 64 up to 1024, launching nothing."""
+    import ctypes as C
+    import os
+
+    L = C.CDLL(os.path.join(os.path.dirname(lrs.LIB_PATH), "liblrs_probe.so"))
+    L.lrsp_read_time.restype = C.c_int
+    L.lrsp_read_time.argtypes = [C.c_int, C.c_void_p, C.c_size_t, C.c_uint32, C.c_int,
+                                 C.c_uint32, C.c_uint32, C.c_uint32, C.c_int,
+                                 C.POINTER(C.c_float)]
+    buf = ctx.alloc(1 << 22)
+    us = C.c_float()
+
+    def run(window, nwin, nt, wg=0, th=0, reads=2, plain_first=0):
+        return L.lrsp_read_time(0, buf.ptr, window, nwin, nt, wg, th, reads, plain_first,
+                                C.byref(us))
+
+    for nt in (0, 1):
         for wg in (0, 1, 512, 4096):
-            ctx.read_dev_at(buf, 0, 1 << 20, nt, wg)
-        ctx.read_dev_at(buf, 4096, 4096 + 16, nt)
-    ctx.sync()
-    with pytest.raises(lrs.ModelError):
-        ctx.read_dev_at(buf, 0, 24, True)
-    with pytest.raises(lrs.ModelError):
-        ctx.read_dev_at(buf, 0, 1 << 20, True, 4097)
-    for th in (64, 768, 1024):
-        ctx.read_dev_at(buf, 0, 1 << 20, True, 160, th)
-    ctx.sync()
+            assert run(1 << 20, 4, nt, wg) == 0 and us.value > 0
+        assert run(4096 + 16, 1, nt) == 0
+        assert run(1 << 20, 4, nt, 160, 768, 3, 1) == 0 and us.value > 0
+    for th in (64, 1024):
+        assert run(1 << 20, 4, 1, 160, th) == 0
+    assert run(24, 1, 1) == -1
+    assert run(1 << 20, 4, 1, 4097) == -1
     for th in (96, 1088):
-        with pytest.raises(lrs.ModelError):
-            ctx.read_dev_at(buf, 0, 1 << 20, True, 160, th)
-    with pytest.raises(AssertionError):
-        ctx.read_dev_at(buf, 16, 1 << 20, False)
+        assert run(1 << 20, 4, 1, 160, th) == -1
+    assert run(1 << 20, 0, 1) == -1 and run(1 << 20, 4, 1, reads=0) == -1
+    ctx.sync()
     buf.free()
 
 
@@ -363,14 +374,16 @@ def test_scratch_growth_refused_while_a_graph_lives(lrs, orc):
     the scratch while the graph is alive fails (LRS_E_ARG) and leaves the
     buffer in place, so the graph still replays correctly; once the graph is
     destroyed the same call succeeds."""
-    c = lrs.Context()
+    c = lrs.Context(0)
     try:
-        n_in, n_out = 1024, 256
+        # one Q4_K column wider than 4096: the staged form, whose input pack
+        # lives in the context scratch (sized here, outside the capture)
+        n_in, n_out = 8192, 256
         w = lrs.Weight.upload(c, Q4_K, orc.gen_weight(Q4_K, 81, n_out, n_in, mode=1), n_in, n_out)
         x = c.alloc(4 * n_in)
         x.upload(orc.gen_normal(82, n_in))
         y = c.alloc(4 * n_out)
-        w.matvec_dev(x, y)  # sizes the scratch (1 MiB minimum) outside the capture
+        w.matvec_dev(x, y)
         c.sync()
         want = y.download(np.float32, n_out)
         g = c.capture(lambda: w.matvec_dev(x, y))
@@ -382,10 +395,19 @@ def test_scratch_growth_refused_while_a_graph_lives(lrs, orc):
         with pytest.raises(lrs.ModelError) as e:
             big.gemm_dev(a, yg, m, precision=3)
         assert e.value.code == -1 and "graph" in str(e.value)
+        # had the scratch been freed, memory allocated now could take its
+        # address and the replay (which writes the pack there) would overwrite it
+        guards = [c.alloc(1 << 20) for _ in range(4)]
+        pattern = np.arange(1 << 18, dtype=np.uint32)
+        for b in guards:
+            b.upload(pattern)
         y.upload(np.full(n_out, np.nan, np.float32))
         g.launch()
         c.sync()
         assert np.array_equal(y.download(np.float32, n_out), want)
+        for b in guards:
+            assert np.array_equal(b.download(np.uint32, 1 << 18), pattern)
+            b.free()
         g.close()
         a.upload(np.zeros(m * 4096, np.float32))
         big.gemm_dev(a, yg, m, precision=3)  # grows now

@@ -17,7 +17,7 @@ LOGIT_TOL = 1e-3
 
 @pytest.fixture(scope="module")
 def ctx(lrs):
-    c = lrs.Context()
+    c = lrs.Context(0)
     yield c
     c.close()
 
@@ -69,15 +69,22 @@ def test_decode_logits_and_greedy_match_oracle(lrs, orc, ctx, name, cfg, mix, mo
     assert got == want
 
 
-# cache lengths where each of the 32 position splits of the decode attention
-# owns one, two or three 16-position blocks (a split's blocks are 512
-# positions apart), and lengths one past each boundary
-LONG_CHECKS = (1, 16, 17, 511, 512, 513, 1024, 1025, 1041)
+# cache lengths where the S position splits of the decode attention (split s
+# owns the 16-position blocks s, s + S, ...: 16 S positions apart) first own
+# one, two or three blocks, one past each boundary, and one more inside the
+# third round; derived from the split count of the model's KV heads
+def _long_checks(cfg):
+    c = modelgen.split_block_checks(cfg["n_head_kv"])
+    return c + (c[-1] + 16,)
+
+
 LONG_CASES = [
     # k_attn<128, 5>: 16 lane groups, one block per round
-    ("gqa5", dict(modelgen.GQA5, ctx=1100), LONG_CHECKS),
+    ("gqa5", dict(modelgen.GQA5, ctx=_long_checks(modelgen.GQA5)[-1] + 8),
+     _long_checks(modelgen.GQA5)),
     # k_attn<64, 2>: 32 lane groups, two blocks per round
-    ("tiny", dict(modelgen.TINY, ctx=1100), LONG_CHECKS),
+    ("tiny", dict(modelgen.TINY, ctx=_long_checks(modelgen.TINY)[-1] + 8),
+     _long_checks(modelgen.TINY)),
     # the 4096-position cache of the benchmark config, filled to the last slot
     # (each split owns 8 blocks)
     ("gqa5-4096", dict(modelgen.GQA5, ctx=4096), (2048, 2049, 4095, 4096)),

@@ -29,7 +29,7 @@ def _case(lrs, orc, ctx, t, n_in, n_out, cols, seed):
 
 
 def test_noalloc_matvec_matches_scratch_matvec(lrs, orc):
-    c = lrs.Context()
+    c = lrs.Context(0)
     try:
         # the largest input the static pack holds, then a smaller one
         _case(lrs, orc, c, Q4_K, lrs.NOALLOC_MAX_N_IN, 96, 1, 31)
@@ -40,7 +40,7 @@ def test_noalloc_matvec_matches_scratch_matvec(lrs, orc):
 
 
 def test_noalloc_matvec_rejects_inputs_beyond_the_static_pack(lrs, orc):
-    c = lrs.Context()
+    c = lrs.Context(0)
     try:
         n_in = lrs.NOALLOC_MAX_N_IN + 256
         w = lrs.Weight.upload(c, Q4_K, orc.gen_weight(Q4_K, 41, 16, n_in, mode=1), n_in, 16)
