@@ -986,108 +986,125 @@ static void hy_rope_head(float *b, uint32_t rope_dim, const float *freq, uint32_
 
 static float hy_silu(float v) { float den = 1.0f + expf(-v); return v / den; }
 
-/* one token through the full-attention mixer; o [n_embd] */
-static void hy_attn(lrso_hybrid *m, uint32_t l, const float *h, float *o) {
+/* n_tok consecutive tokens (positions m->len ..) through the full-attention
+ * mixer of layer l; h, o [n_tok][n_embd].  The projections take all the
+ * tokens as matvec columns (bit-identical to one column at a time, the
+ * batched-column invariance of lrso_matvec); each token then runs in order,
+ * so token t's attention sees the cache rows of the tokens before it. */
+static void hy_attn(lrso_hybrid *m, uint32_t l, const float *h, uint32_t n_tok, float *o) {
     const lrso_config *b = &m->c.base;
     const lrso_hybrid_layer *L = &m->layers[l];
     const uint32_t E = b->n_embd, HD = b->head_dim, QD = b->n_head * HD, KV = b->n_head_kv * HD;
-    const uint32_t pos = m->len;
-    float *qg = (float *)malloc(sizeof(float) * 2 * QD);
+    float *qg = (float *)malloc(sizeof(float) * 2 * QD * n_tok);
+    float *k = (float *)malloc(sizeof(float) * KV * n_tok);
+    float *v = (float *)malloc(sizeof(float) * KV * n_tok);
     float *q = (float *)malloc(sizeof(float) * QD);
-    float *k = (float *)malloc(sizeof(float) * KV);
-    float *v = (float *)malloc(sizeof(float) * KV);
-    float *att = (float *)malloc(sizeof(float) * QD);
+    float *att = (float *)malloc(sizeof(float) * QD * n_tok);
     float *qn = tensor_f32(&L->q_norm, HD), *kn = tensor_f32(&L->k_norm, HD);
-    lrso_matvec(L->attn_q.type, L->attn_q.bytes, L->attn_q.len, E, 2 * QD, h, qg, 1, m->n_threads);
-    lrso_matvec(L->attn_k.type, L->attn_k.bytes, L->attn_k.len, E, KV, h, k, 1, m->n_threads);
-    lrso_matvec(L->attn_v.type, L->attn_v.bytes, L->attn_v.len, E, KV, h, v, 1, m->n_threads);
-    /* QK-norm (dn_norm mode 2, Q heads 2*head_dim apart) then RoPE */
-    for (uint32_t hh = 0; hh < b->n_head; hh++) {
-        float *qh = qg + (size_t)hh * 2 * HD;
-        hy_head_rms(qh, HD, qn, b->rms_eps);
-        hy_rope_head(qh, b->rope_dim, m->freq, pos);
-        memcpy(q + (size_t)hh * HD, qh, sizeof(float) * HD);
-    }
-    for (uint32_t hh = 0; hh < b->n_head_kv; hh++) {
-        hy_head_rms(k + (size_t)hh * HD, HD, kn, b->rms_eps);
-        hy_rope_head(k + (size_t)hh * HD, b->rope_dim, m->freq, pos);
-    }
+    lrso_matvec(L->attn_q.type, L->attn_q.bytes, L->attn_q.len, E, 2 * QD, h, qg, n_tok, m->n_threads);
+    lrso_matvec(L->attn_k.type, L->attn_k.bytes, L->attn_k.len, E, KV, h, k, n_tok, m->n_threads);
+    lrso_matvec(L->attn_v.type, L->attn_v.bytes, L->attn_v.len, E, KV, h, v, n_tok, m->n_threads);
     const size_t sl = (size_t)m->slot[l] * b->ctx * KV;
     float *kl = m->kc + sl, *vl = m->vc + sl;
-    for (uint32_t i = 0; i < KV; i++) {
-        float kk = k[i], vv = v[i];
-        if (m->kv_f16) {
-            kk = lrso_f16_to_f32(lrso_f32_to_f16(kk));
-            vv = lrso_f16_to_f32(lrso_f32_to_f16(vv));
+    for (uint32_t t = 0; t < n_tok; t++) {
+        const uint32_t pos = m->len + t;
+        float *qgt = qg + (size_t)t * 2 * QD, *kt = k + (size_t)t * KV, *vt = v + (size_t)t * KV;
+        float *at = att + (size_t)t * QD;
+        /* QK-norm (dn_norm mode 2, Q heads 2*head_dim apart) then RoPE */
+        for (uint32_t hh = 0; hh < b->n_head; hh++) {
+            float *qh = qgt + (size_t)hh * 2 * HD;
+            hy_head_rms(qh, HD, qn, b->rms_eps);
+            hy_rope_head(qh, b->rope_dim, m->freq, pos);
+            memcpy(q + (size_t)hh * HD, qh, sizeof(float) * HD);
         }
-        kl[(size_t)pos * KV + i] = kk;
-        vl[(size_t)pos * KV + i] = vv;
+        for (uint32_t hh = 0; hh < b->n_head_kv; hh++) {
+            hy_head_rms(kt + (size_t)hh * HD, HD, kn, b->rms_eps);
+            hy_rope_head(kt + (size_t)hh * HD, b->rope_dim, m->freq, pos);
+        }
+        for (uint32_t i = 0; i < KV; i++) {
+            float kk = kt[i], vv = vt[i];
+            if (m->kv_f16) {
+                kk = lrso_f16_to_f32(lrso_f32_to_f16(kk));
+                vv = lrso_f16_to_f32(lrso_f32_to_f16(vv));
+            }
+            kl[(size_t)pos * KV + i] = kk;
+            vl[(size_t)pos * KV + i] = vv;
+        }
+        lrso_attention(q, kl, vl, 1, pos, b->n_head, b->n_head_kv, HD, at);
+        /* gate_quant.comp: att * sigmoid(gate), gate = second half of the head's Q rows */
+        for (uint32_t hh = 0; hh < b->n_head; hh++)
+            for (uint32_t i = 0; i < HD; i++) {
+                float g = qgt[(size_t)hh * 2 * HD + HD + i];
+                at[(size_t)hh * HD + i] *= 1.0f / (1.0f + expf(-g));
+            }
     }
-    lrso_attention(q, kl, vl, 1, pos, b->n_head, b->n_head_kv, HD, att);
-    /* gate_quant.comp: att * sigmoid(gate), gate = second half of the head's Q rows */
-    for (uint32_t hh = 0; hh < b->n_head; hh++)
-        for (uint32_t i = 0; i < HD; i++) {
-            float g = qg[(size_t)hh * 2 * HD + HD + i];
-            att[(size_t)hh * HD + i] *= 1.0f / (1.0f + expf(-g));
-        }
-    lrso_matvec(L->attn_output.type, L->attn_output.bytes, L->attn_output.len, QD, E, att, o, 1,
-                m->n_threads);
+    lrso_matvec(L->attn_output.type, L->attn_output.bytes, L->attn_output.len, QD, E, att, o,
+                n_tok, m->n_threads);
     free(qg); free(q); free(k); free(v); free(att); free(qn); free(kn);
 }
 
-/* one token through the gated delta-net mixer (plano_delta order); o [n_embd] */
-static void hy_delta(lrso_hybrid *m, uint32_t l, const float *h, float *o) {
+/* n_tok consecutive tokens through the gated delta-net mixer of layer l
+ * (plano_delta order); h, o [n_tok][n_embd].  Projections batched as in
+ * hy_attn; the conv, gates and the delta rule run token by token. */
+static void hy_delta(lrso_hybrid *m, uint32_t l, const float *h, uint32_t n_tok, float *o) {
     const lrso_hybrid_config *c = &m->c;
     const lrso_config *b = &c->base;
     const lrso_hybrid_layer *L = &m->layers[l];
     const uint32_t E = b->n_embd, d = c->dn_state, KD = c->dn_k_heads * d, VD = c->dn_v_heads * d;
     const uint32_t CD = hy_conv_dim(c), NV = c->dn_v_heads;
-    float *qkv = (float *)malloc(sizeof(float) * CD);
+    float *qkv = (float *)malloc(sizeof(float) * CD * n_tok);
     float *cv = (float *)malloc(sizeof(float) * CD);
-    float *z = (float *)malloc(sizeof(float) * VD);
-    float *y = (float *)malloc(sizeof(float) * VD);
+    float *z = (float *)malloc(sizeof(float) * VD * n_tok);
+    float *y = (float *)malloc(sizeof(float) * VD * n_tok);
     float *al = tensor_f32(&L->ssm_alpha, E * NV), *be = tensor_f32(&L->ssm_beta, E * NV);
     float *sa = tensor_f32(&L->ssm_a, NV), *dt = tensor_f32(&L->ssm_dt, NV);
     float *cw = tensor_f32(&L->ssm_conv, CD * c->dn_conv), *nw = tensor_f32(&L->ssm_norm, d);
-    lrso_matvec(L->ssm_qkv.type, L->ssm_qkv.bytes, L->ssm_qkv.len, E, CD, h, qkv, 1, m->n_threads);
-    lrso_matvec(L->ssm_gate.type, L->ssm_gate.bytes, L->ssm_gate.len, E, VD, h, z, 1, m->n_threads);
-    /* causal conv with state, then SiLU (dn_conv.comp; delta_net.rs:51-78) */
+    lrso_matvec(L->ssm_qkv.type, L->ssm_qkv.bytes, L->ssm_qkv.len, E, CD, h, qkv, n_tok, m->n_threads);
+    lrso_matvec(L->ssm_gate.type, L->ssm_gate.bytes, L->ssm_gate.len, E, VD, h, z, n_tok, m->n_threads);
     float *win = m->win + (size_t)m->slot[l] * CD * (c->dn_conv - 1);
-    lrso_conv1d_step(win, qkv, cw, CD, c->dn_conv, cv);
-    for (uint32_t i = 0; i < CD; i++) cv[i] = hy_silu(cv[i]);
-    /* L2 norm of q and k per key head (dn_l2_qk.comp, eps = rms_eps) */
-    lrso_l2_norm_rows(cv, 2 * c->dn_k_heads, d, b->rms_eps);
     float *st = m->state + (size_t)m->slot[l] * NV * d * d;
-    for (uint32_t hh = 0; hh < NV; hh++) {
-        /* gates (dn_gates.comp): g = a * softplus(alpha.h + dt), beta = sigmoid(beta.h) */
-        float pa = -0.0f, pb = -0.0f;
-        for (uint32_t i = 0; i < E; i++) {
-            float p1 = al[(size_t)hh * E + i] * h[i], p2 = be[(size_t)hh * E + i] * h[i];
-            pa = pa + p1;
-            pb = pb + p2;
-        }
-        float g = sa[hh] * lrso_softplus(pa + dt[hh]);
-        float beta = 1.0f / (1.0f + expf(-pb));
-        /* value head hh reads key head hh % k_heads (delta_net.comp:75-85) */
-        const uint32_t kh = hh % c->dn_k_heads;
-        lrso_delta_net_step(st + (size_t)hh * d * d, cv + (size_t)kh * d, cv + KD + (size_t)kh * d,
-                            cv + 2 * KD + (size_t)hh * d, g, beta, d, y + (size_t)hh * d);
-        /* gated RMSNorm (dn_norm mode 1): (y * 1/sqrt(mean(y^2)+eps)) * (w * silu(z)) */
-        float *yh = y + (size_t)hh * d;
-        const float *zh = z + (size_t)hh * d;
-        float ss = -0.0f;
-        for (uint32_t i = 0; i < d; i++) { float sq = yh[i] * yh[i]; ss = ss + sq; }
-        float s = 1.0f / sqrtf(ss / (float)d + b->rms_eps);
-        for (uint32_t i = 0; i < d; i++) {
-            float vv = yh[i] * s;
-            float gz = nw[i] * hy_silu(zh[i]);
-            yh[i] = vv * gz;
+    for (uint32_t t = 0; t < n_tok; t++) {
+        const float *ht = h + (size_t)t * E, *zt = z + (size_t)t * VD;
+        float *yt = y + (size_t)t * VD;
+        /* causal conv with state, then SiLU (dn_conv.comp; delta_net.rs:51-78) */
+        lrso_conv1d_step(win, qkv + (size_t)t * CD, cw, CD, c->dn_conv, cv);
+        for (uint32_t i = 0; i < CD; i++) cv[i] = hy_silu(cv[i]);
+        /* L2 norm of q and k per key head (dn_l2_qk.comp, eps = rms_eps) */
+        lrso_l2_norm_rows(cv, 2 * c->dn_k_heads, d, b->rms_eps);
+        for (uint32_t hh = 0; hh < NV; hh++) {
+            /* gates (dn_gates.comp): g = a * softplus(alpha.h + dt), beta = sigmoid(beta.h) */
+            float pa = -0.0f, pb = -0.0f;
+            for (uint32_t i = 0; i < E; i++) {
+                float p1 = al[(size_t)hh * E + i] * ht[i], p2 = be[(size_t)hh * E + i] * ht[i];
+                pa = pa + p1;
+                pb = pb + p2;
+            }
+            float g = sa[hh] * lrso_softplus(pa + dt[hh]);
+            float beta = 1.0f / (1.0f + expf(-pb));
+            /* value head hh reads key head hh % k_heads (delta_net.comp:75-85) */
+            const uint32_t kh = hh % c->dn_k_heads;
+            lrso_delta_net_step(st + (size_t)hh * d * d, cv + (size_t)kh * d, cv + KD + (size_t)kh * d,
+                                cv + 2 * KD + (size_t)hh * d, g, beta, d, yt + (size_t)hh * d);
+            /* gated RMSNorm (dn_norm mode 1): (y * 1/sqrt(mean(y^2)+eps)) * (w * silu(z)) */
+            float *yh = yt + (size_t)hh * d;
+            const float *zh = zt + (size_t)hh * d;
+            float ss = -0.0f;
+            for (uint32_t i = 0; i < d; i++) { float sq = yh[i] * yh[i]; ss = ss + sq; }
+            float s = 1.0f / sqrtf(ss / (float)d + b->rms_eps);
+            for (uint32_t i = 0; i < d; i++) {
+                float vv = yh[i] * s;
+                float gz = nw[i] * hy_silu(zh[i]);
+                yh[i] = vv * gz;
+            }
         }
     }
-    lrso_matvec(L->ssm_out.type, L->ssm_out.bytes, L->ssm_out.len, VD, E, y, o, 1, m->n_threads);
+    lrso_matvec(L->ssm_out.type, L->ssm_out.bytes, L->ssm_out.len, VD, E, y, o, n_tok, m->n_threads);
     free(qkv); free(cv); free(z); free(y); free(al); free(be); free(sa); free(dt); free(cw); free(nw);
 }
 
+/* The tokens go through the model layer by layer (every token of layer l
+ * before layer l + 1), each op's per-token arithmetic unchanged, so the
+ * result equals feeding them one at a time. */
 int lrso_hybrid_forward(lrso_hybrid *m, const uint32_t *tokens, uint32_t n_tok, float *logits) {
     const lrso_config *b = &m->c.base;
     const uint32_t E = b->n_embd;
@@ -1096,36 +1113,37 @@ int lrso_hybrid_forward(lrso_hybrid *m, const uint32_t *tokens, uint32_t n_tok, 
     for (uint32_t t = 0; t < n_tok; t++)
         if (tokens[t] >= b->vocab) return -4;
     size_t row_bytes = m->embd.len / b->vocab;
-    float *x = (float *)malloc(sizeof(float) * E);
-    float *h = (float *)malloc(sizeof(float) * E);
-    float *o = (float *)malloc(sizeof(float) * E);
-    float *g = (float *)malloc(sizeof(float) * b->n_ff);
-    float *u = (float *)malloc(sizeof(float) * b->n_ff);
-    for (uint32_t t = 0; t < n_tok; t++) {
-        lrso_dequant(m->embd.type, m->embd.bytes + (size_t)tokens[t] * row_bytes, row_bytes, x);
-        for (uint32_t l = 0; l < b->n_layer; l++) {
-            lrso_hybrid_layer *L = &m->layers[l];
-            float *an = tensor_f32(&L->attn_norm, E), *pn = tensor_f32(&L->post_norm, E);
-            lrso_rmsnorm_scale(x, an, 1, E, b->rms_eps, h);
-            if (hy_full(&m->c, l)) hy_attn(m, l, h, o);
-            else hy_delta(m, l, h, o);
-            for (uint32_t i = 0; i < E; i++) x[i] += o[i];
-            lrso_rmsnorm_scale(x, pn, 1, E, b->rms_eps, h);
-            lrso_matvec(L->ffn_gate.type, L->ffn_gate.bytes, L->ffn_gate.len, E, b->n_ff, h, g, 1,
-                        m->n_threads);
-            lrso_matvec(L->ffn_up.type, L->ffn_up.bytes, L->ffn_up.len, E, b->n_ff, h, u, 1,
-                        m->n_threads);
-            lrso_swiglu(g, u, b->n_ff, g);
-            lrso_matvec(L->ffn_down.type, L->ffn_down.bytes, L->ffn_down.len, b->n_ff, E, g, o, 1,
-                        m->n_threads);
-            for (uint32_t i = 0; i < E; i++) x[i] += o[i];
-            free(an); free(pn);
-        }
-        m->len++;
+    float *x = (float *)malloc(sizeof(float) * E * n_tok);
+    float *h = (float *)malloc(sizeof(float) * E * n_tok);
+    float *o = (float *)malloc(sizeof(float) * E * n_tok);
+    float *g = (float *)malloc(sizeof(float) * b->n_ff * n_tok);
+    float *u = (float *)malloc(sizeof(float) * b->n_ff * n_tok);
+    for (uint32_t t = 0; t < n_tok; t++)
+        lrso_dequant(m->embd.type, m->embd.bytes + (size_t)tokens[t] * row_bytes, row_bytes,
+                     x + (size_t)t * E);
+    const size_t xe = (size_t)E * n_tok;
+    for (uint32_t l = 0; l < b->n_layer; l++) {
+        lrso_hybrid_layer *L = &m->layers[l];
+        float *an = tensor_f32(&L->attn_norm, E), *pn = tensor_f32(&L->post_norm, E);
+        lrso_rmsnorm_scale(x, an, n_tok, E, b->rms_eps, h);
+        if (hy_full(&m->c, l)) hy_attn(m, l, h, n_tok, o);
+        else hy_delta(m, l, h, n_tok, o);
+        for (size_t i = 0; i < xe; i++) x[i] += o[i];
+        lrso_rmsnorm_scale(x, pn, n_tok, E, b->rms_eps, h);
+        lrso_matvec(L->ffn_gate.type, L->ffn_gate.bytes, L->ffn_gate.len, E, b->n_ff, h, g, n_tok,
+                    m->n_threads);
+        lrso_matvec(L->ffn_up.type, L->ffn_up.bytes, L->ffn_up.len, E, b->n_ff, h, u, n_tok,
+                    m->n_threads);
+        lrso_swiglu(g, u, b->n_ff * n_tok, g);
+        lrso_matvec(L->ffn_down.type, L->ffn_down.bytes, L->ffn_down.len, b->n_ff, E, g, o, n_tok,
+                    m->n_threads);
+        for (size_t i = 0; i < xe; i++) x[i] += o[i];
+        free(an); free(pn);
     }
+    m->len += n_tok;
     if (logits) {
         float *on = tensor_f32(&m->onorm, E);
-        lrso_rmsnorm_scale(x, on, 1, E, b->rms_eps, h);
+        lrso_rmsnorm_scale(x + (size_t)(n_tok - 1) * E, on, 1, E, b->rms_eps, h);
         lrso_matvec(m->out.type, m->out.bytes, m->out.len, E, b->vocab, h, logits, 1, m->n_threads);
         free(on);
     }

@@ -73,6 +73,23 @@ def gpu_model(lrs, ctx, cfg, w):
     return ResidentForward(ctx, cfg, layers, emb, w["output_norm"][1], out)
 
 
+def attn_splits(n_kv):
+    """position splits of the decode attention per KV head (attention.hip
+    attn_splits): 256 / n_kv workgroups, at least 1 and at most 40"""
+    return max(1, min(40, 256 // n_kv))
+
+
+def split_block_checks(n_kv, rounds=2):
+    """cache lengths at which the decode attention's splits (split s owns the
+    16-position blocks s, s + S, s + 2S, ...) first own 1 .. rounds + 1 blocks:
+    16 S r and 16 S r + 1 for r = 1 .. rounds, plus 1, 16 and 17"""
+    S = attn_splits(n_kv)
+    out = [1, 16, 17]
+    for r in range(1, rounds + 1):
+        out += [16 * S * r, 16 * S * r + 1]
+    return tuple(out)
+
+
 def oracle_greedy(model, prompt, n_gen):
     """Model::generate with greedy sampling: forward(prompt), then one token
     at a time (generate.rs:13-43)."""
@@ -161,6 +178,38 @@ def hybrid_host_model(orc, cfg, seed=1, mix=None, mode=1, d_lo=2e-4, d_hi=2e-3):
                                                   cfg["n_embd"], mode=mode, d_lo=d_lo, d_hi=d_hi))
     w["output_norm"] = (F32, orc.gen_uniform(seed * 5 + 3, cfg["n_embd"], 0.9, 1.1))
     return w
+
+
+def hybrid_device_model(lrs, ctx, orc, cfg, seed=1, mix=None, mode=1, d_lo=2e-4, d_hi=2e-3):
+    """The weights of hybrid_host_model(orc, cfg, seed, mix, mode, d_lo, d_hi),
+    the quantized ones generated on the GPU (the device generator writes the
+    oracle generator's bytes; test_device_generator_matches_host_generator)
+    and downloaded for the oracle.  Returns (host weight dict, GPU model) on
+    the same bytes; much faster than host generation at full width."""
+    from llama_rs_amd.model import HybridForward
+
+    mix = dict(HY_Q4_K_M, **(mix or {}))
+    w, layers = {}, []
+    for l in range(cfg["n_layer"]):
+        L = {}
+        for i, (name, (n_in, n_out)) in enumerate(sorted(hybrid_shapes(cfg, l).items())):
+            t = mix[name]
+            L[name] = lrs.Weight.generate(ctx, t, seed * 1000 + l * 32 + i, n_in, n_out,
+                                          mode=mode, d_lo=d_lo, d_hi=d_hi)
+            w[f"blk.{l}.{name}"] = (t, L[name].download())
+        for i, (name, (n, lo, hi)) in enumerate(sorted(hybrid_f32_shapes(cfg, l).items())):
+            w[f"blk.{l}.{name}"] = (F32, orc.gen_uniform(seed * 77 + 32 * l + i, n, lo, hi))
+            L[name] = w[f"blk.{l}.{name}"][1]
+        layers.append(L)
+    te, ot = mix["token_embd"], mix["output"]
+    emb = lrs.Weight.generate(ctx, te, seed * 5 + 1, cfg["n_embd"], cfg["vocab"], mode=mode,
+                              d_lo=d_lo * 20, d_hi=d_hi * 20)
+    out = lrs.Weight.generate(ctx, ot, seed * 5 + 2, cfg["n_embd"], cfg["vocab"], mode=mode,
+                              d_lo=d_lo, d_hi=d_hi)
+    w["token_embd"] = (te, emb.download())
+    w["output"] = (ot, out.download())
+    w["output_norm"] = (F32, orc.gen_uniform(seed * 5 + 3, cfg["n_embd"], 0.9, 1.1))
+    return w, HybridForward(ctx, cfg, layers, emb, w["output_norm"][1], out)
 
 
 def gpu_hybrid_model(lrs, ctx, cfg, w):

@@ -15,7 +15,7 @@ LOGIT_TOL = 1e-3
 
 @pytest.fixture(scope="module")
 def ctx(lrs):
-    c = lrs.Context()
+    c = lrs.Context(0)
     yield c
     c.close()
 
@@ -60,11 +60,12 @@ def test_hybrid_decode_and_greedy_match_oracle(lrs, orc, ctx, name, cfg, mix):
 
 def test_hybrid_long_context_decode_matches_oracle(lrs, orc, ctx):
     """The gated attention layers (6 query heads over one 256-dim KV head,
-    k_attn<256, 6>) at cache lengths where the position splits own one and
-    two 16-position blocks; every token through decode(), checked at the
-    lengths below against the oracle."""
-    cfg = dict(modelgen.HY_MID, ctx=640)
-    checks = (1, 17, 512, 513, 600)
+    k_attn<256, 6>) at the cache lengths where the position splits first own
+    one, two and three 16-position blocks and one past each (computed from the
+    split count, so a change of it moves the checks along); every token
+    through decode(), checked at those lengths against the oracle."""
+    checks = modelgen.split_block_checks(modelgen.HY_MID["n_head_kv"])
+    cfg = dict(modelgen.HY_MID, ctx=max(checks) + 8)
     w = modelgen.hybrid_host_model(orc, cfg, seed=23)
     gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
     om = orc.HybridModel(cfg, w, kv_f16=True, threads=8)

@@ -94,3 +94,23 @@ def test_hybrid_context_overflow_and_shapes(orc):
     bad["blk.0.ssm_a"] = (0, np.zeros(cfg["dn_v_heads"] + 1, np.float32))
     with pytest.raises(ValueError):
         orc.HybridModel(cfg, bad)
+
+
+@pytest.mark.parametrize("cfg", [modelgen.HY_TINY, modelgen.HY_KS], ids=["tiny", "ks"])
+def test_hybrid_prompt_batch_equals_token_by_token(orc, cfg):
+    """lrso_hybrid_forward runs a prompt layer by layer with every projection
+    over all its tokens as matvec columns; the result is bit-identical to
+    feeding the tokens one at a time (the batched-column invariance of the
+    matvec, and each token's attention / conv / delta rule in order)."""
+    w = modelgen.hybrid_host_model(orc, cfg, seed=61)
+    toks = np.random.default_rng(4).integers(0, cfg["vocab"], 21).tolist()
+    a = orc.HybridModel(cfg, w, threads=4)
+    b = orc.HybridModel(cfg, w, threads=4)
+    for t in toks[:-1]:
+        a.forward([t])
+    la = a.forward([toks[-1]])
+    lb = b.forward(toks)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    # and the states it leaves carry on identically
+    for t in (7, 300 % cfg["vocab"]):
+        assert np.array_equal(a.forward([t]).view(np.uint32), b.forward([t]).view(np.uint32))
