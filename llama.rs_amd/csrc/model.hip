@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -88,6 +89,10 @@ struct lrs_model {
     float *output_norm, *freq;
     // activations: residual, q after RoPE, logits, attention split partials
     float *x, *qbuf, *logits, *pa;
+    // partial sums and arrival counts of the matvecs split over K across
+    // workgroups (down, o): [n_embd / 32 blocks][8 slices][32], [blocks]
+    float *xpart = nullptr;
+    uint32_t *xcnt = nullptr;
     uint32_t a_splits;
     // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
     // SwiGLU output
@@ -201,14 +206,35 @@ MqGeom gateup_geom(uint32_t n_ff) {
     if (t / 4 >= 400) return MqGeom{2, 4, 2, 2};
     return t / 2 <= 512 ? MqGeom{2, 2, 4, 2} : MqGeom{2, 2, 2, 1};
 }
-// down (n_embd rows): 2 tiles x 6 K-slices with one unit in flight per
-// wavefront (with non-temporal weight loads the deeper prefetch was ~4 %
-// slower at 27648; at 13824 it beats 8 K-slices, 14.0 against 14.3 us),
-// except x 4 K-slices with two units in flight for 16384..24575 (17408:
-// 17.4 against 17.9 us for 8 K-slices and 18.5 for 6)
+// down (n_embd rows, K = n_ff): one 32-row block per workgroup leaves 96 of
+// the 256 CUs idle, and one CU streams ~35-40 GB/s, so wide down projections
+// split K over 3 workgroups per block (480 workgroups; the last slice to
+// arrive adds the partials and runs the residual + pack epilogue):
+//   n_ff >= 24576: 2 tiles x 4 K-slices x 2 units in flight x 3 slices
+//     (27648: 22.3 against 23.6 us unsplit at 2 tiles x 6 K-slices x 1 unit);
+//   16384..24575: x 4 K-slices x 1 unit x 3 slices (17408: 16.4 against 17.2 us
+//     unsplit at x 4 K-slices x 2 units);
+//   below: 2 tiles x 6 K-slices x 1 unit, unsplit (13824: 13.6 us; the best
+//     split 13.9).
 MqGeom down_geom(uint32_t n_ff) {
-    if (n_ff >= 16384 && n_ff < 24576) return MqGeom{1, 2, 4, 2};
+    if (n_ff >= 24576) return MqGeom{1, 2, 4, 2, 3};
+    if (n_ff >= 16384) return MqGeom{1, 2, 4, 1, 3};
     return MqGeom{1, 2, 6, 1};
+}
+
+// A launch-shape override from the environment, "tpw,tg,ks,p[,xs]" (the
+// LLAMA_RS_MATVEC_GEOM knob of resident_forward.rs:164-176, per op here):
+// LRS_GEOM_DOWN, LRS_GEOM_O.  Read when the op is enqueued (graphs: at
+// capture); a shape the kernels do not have fails the launch.
+MqGeom env_geom(const char *name, MqGeom dflt) {
+    const char *v = getenv(name);
+    if (!v || !v[0]) return dflt;
+    MqGeom g = {0, 0, 0, 0};
+    int xs = 1;
+    const int n = sscanf(v, "%d,%d,%d,%d,%d", &g.tpw, &g.tg, &g.ks, &g.p, &xs);
+    if (n < 4) return dflt;
+    g.xs = xs;
+    return g;
 }
 
 // ---- one fused op of the per-token plan, enqueued on the model stream ----
@@ -323,7 +349,10 @@ hipError_t op_o(lrs_model *m, uint32_t l) {
         a.gn = (float)m->hc.dn_state;
         a.eps = c.rms_eps;
     }
-    return launch_mq(a, wo->v.type, wo->v.type, G_O, MQ_RESID, m->ctx->stream);
+    a.xpart = m->xpart;
+    a.xcnt = m->xcnt;
+    return launch_mq(a, wo->v.type, wo->v.type, env_geom("LRS_GEOM_O", G_O), MQ_RESID,
+                     m->ctx->stream);
 }
 
 // outs[i] = W_i (rmsnorm(x) * attn_norm) for n weights (f32 rows out): one
@@ -469,8 +498,10 @@ hipError_t op_down(lrs_model *m, uint32_t l) {
     a.x = m->x;
     a.nw = l + 1 < c.n_layer ? m->layers[l + 1].attn_norm : m->output_norm;
     a.xout = m->pk_n;
-    return launch_mq(a, L.down->v.type, L.down->v.type, down_geom(c.n_ff), MQ_RESID,
-                     m->ctx->stream);
+    a.xpart = m->xpart;
+    a.xcnt = m->xcnt;
+    return launch_mq(a, L.down->v.type, L.down->v.type, env_geom("LRS_GEOM_DOWN", down_geom(c.n_ff)),
+                     MQ_RESID, m->ctx->stream);
 }
 
 // the FFN of layer l: gate/up + SwiGLU, then down + residual
@@ -641,6 +672,16 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         m->pk_q8.q8 = 1;
     }
     if (hipMemset(m->step, 0, 4 * sizeof(uint32_t)) != hipSuccess) return fail(LRS_E_HIP, "memset");
+    {
+        // the split matvecs' arrival counts start at zero and every launch
+        // leaves them at zero (the last slice to arrive resets its block's)
+        const size_t nb = c.n_embd / 32;
+        if ((rc = dev_alloc(m, nb * 8 * 32 * sizeof(float), (void **)&m->xpart)) ||
+            (rc = dev_alloc(m, nb * sizeof(uint32_t), (void **)&m->xcnt)))
+            return rc;
+        if (hipMemset(m->xcnt, 0, nb * sizeof(uint32_t)) != hipSuccess)
+            return fail(LRS_E_HIP, "memset");
+    }
     if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=

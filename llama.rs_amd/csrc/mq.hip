@@ -428,7 +428,11 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     // output tiles of this workgroup: TG tile groups of TPW tiles (pairs: one
     // output tile per group, its gate and up weights)
     const uint32_t otiles_wg = pair ? TG : TG * TPW;
-    const uint32_t tile0 = (blockIdx.x - sg.wg0) * otiles_wg;
+    // MQ_RESID split over K: workgroup b is slice b % xs of output block b / xs
+    const uint32_t XSN = (EPI == MQ_RESID && a.xsplit > 1) ? a.xsplit : 1u;
+    const uint32_t wrel = blockIdx.x - sg.wg0;
+    const uint32_t blk = wrel / XSN, xsl = wrel % XSN;
+    const uint32_t tile0 = blk * otiles_wg;
     const uint32_t ntiles = ttiles(sg.rows);
     const uint8_t *wt[TPW];
 #pragma unroll
@@ -437,7 +441,12 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         if (tile >= ntiles) tile = ntiles - 1;  // duplicate reads, results dropped
         wt[t] = (pair && t == 1 ? sg.w2 : sg.w) + (size_t)tile * tstride;
     }
-    const uint32_t u_lo = ks * units / KS, u_hi = (ks + 1) * units / KS;
+    // this workgroup's units [ub, ue) (all of them without the split); the
+    // input pack is staged from block ub * BPU on, so LDS offsets use u - ub
+    const uint32_t ub = xsl * units / XSN, ue = (xsl + 1) * units / XSN, nu = ue - ub;
+    constexpr uint32_t BPU = T == T_Q8_0 ? 2u : 8u;  // pack blocks per unit
+    const uint32_t nxl = XSN > 1 ? nu * BPU : a.nxb;  // pack blocks staged
+    const uint32_t u_lo = ub + ks * nu / KS, u_hi = ub + (ks + 1) * nu / KS;
 
     // XF: the first B input elements per thread of column 0 are loaded ahead
     // of the weight prefetch, so packing them waits for these loads only
@@ -479,7 +488,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     // bytes, then the meta of column c at + c * nxb * 16; fused RMSNorm: sum
     // of squares of xres
     LPack lp;
-    lp.zero = NC * a.nxb * 96;
+    lp.zero = NC * nxl * 96;
     lp.meta = lp.zero + 16;
     if constexpr (XF) {
         // pack_half per 32-element block (lane i of a half wavefront =
@@ -521,8 +530,10 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
             }
         }
     } else {
-        copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.dig), lds, a.nxb * 96);
-        copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.meta), lds + lp.meta, a.nxb * 16);
+        const uint32_t bb0 = XSN > 1 ? ub * BPU : 0u;
+        copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.dig) + (size_t)bb0 * 96, lds, nxl * 96);
+        copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.meta + 4 * (size_t)bb0), lds + lp.meta,
+                    nxl * 16);
     }
     if (threadIdx.x < 4) reinterpret_cast<uint32_t *>(lds + lp.zero)[threadIdx.x] = 0u;
     // the epilogue's operands of this thread's output (thread i owns output i
@@ -558,9 +569,10 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     }
     // grouped RMS factor (below): the sum of squares of this thread's first
     // block's group, loaded with the weights
+    const uint32_t gb0 = XSN > 1 ? ub * BPU : 0u;  // first staged block
     float gs0 = 0.f;
-    if (a.gss && threadIdx.x < a.nxb) {
-        const uint32_t g = threadIdx.x / a.gblk;
+    if (a.gss && threadIdx.x < nxl) {
+        const uint32_t g = (threadIdx.x + gb0) / a.gblk;
         for (uint32_t r = 0; r < a.gblk; r++) gs0 += a.gss[g * a.gblk + r];
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -568,8 +580,8 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     if (a.gss) {
         // the producer packed each group without its RMS factor; the pack is
         // linear in the block scale and sums, so the factor scales the meta
-        for (uint32_t b = threadIdx.x; b < a.nxb; b += blockDim.x) {
-            const uint32_t g = b / a.gblk;
+        for (uint32_t b = threadIdx.x; b < nxl; b += blockDim.x) {
+            const uint32_t g = (b + gb0) / a.gblk;
             float t = 0.f;
             if (b == threadIdx.x) {
                 t = gs0;
@@ -613,10 +625,10 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     for (; u0 + 2 * P <= u_hi; u0 += P) {
 #pragma unroll
         for (int i = 0; i < P; i++) {
-            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc[0], accm[0]);
+            udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
             for (int c = 1; c < NC; c++)
-                udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+                udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
 #pragma unroll
             for (int t = 0; t < TPW; t++)
                 wload<T>(wr[i][t], wt[t] + (size_t)(u0 + P + i) * tchunk_bytes(T), lane);
@@ -629,10 +641,10 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
     for (int i = 0; i < P; i++) {
         if (u0 + i < u_hi) {
-            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc[0], accm[0]);
+            udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
             for (int c = 1; c < NC; c++)
-                udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+                udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
             if (u0 + P + i < u_hi) {
 #pragma unroll
                 for (int t = 0; t < TPW; t++)
@@ -644,10 +656,10 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
     for (int i = 0; i < P; i++)
         if (u0 + i < u_hi) {
-            udot<T, TPW>(wr[i], u0 + i, lds, lp, al, lane, acc[0], accm[0]);
+            udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
             for (int c = 1; c < NC; c++)
-                udot<T, TPW>(wr[i], u0 + i, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+                udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
         }
 
     // row sums: lanes n, n+16, n+32, n+48 hold sub-block classes of row n
@@ -684,7 +696,6 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     // (one 32-element block each), the argmax keeps whole wavefronts
     constexpr bool PACK = EPI == MQ_RESID || EPI == MQ_SWIGLU;
     const uint32_t lim = PACK ? ((nout + 31) & ~31u) : EPI == MQ_STORE ? ((nout + 63) & ~63u) : nout;
-    if (i >= lim) return;
     // value of output i (column c): sum of the KS K-slice partials of its
     // tile group
     auto partial = [&](uint32_t grp, uint32_t t, uint32_t n, int c = 0) {
@@ -696,6 +707,44 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     const uint32_t row = tile0 * 16 + i;
     const bool valid = i < nout && row < sg.rows;
     const uint32_t ii = i < nout ? i : nout - 1;
+    const uint32_t grp = pair ? (ii >> 4) : (ii >> 4) / TPW;
+    const uint32_t tt = pair ? 0 : (ii >> 4) % TPW;
+    float ysum = 0.f;
+    if constexpr (EPI == MQ_RESID) {
+        ysum = partial(grp, tt, ii & 15);
+        if (XSN > 1) {
+            // every thread reaches both barriers; slices other than the last
+            // to arrive leave after counting themselves.  Partials go out as
+            // agent-scope stores (written through to memory), and the wait
+            // for their completion comes before the count, so the last
+            // arriver's agent-scope loads see every slice's partials.
+            float *mine = a.xpart + ((size_t)blk * XSN + xsl) * 32;
+            if (i < nout) __hip_atomic_store(mine + i, ysum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores are complete
+            __syncthreads();
+            uint32_t *flag = reinterpret_cast<uint32_t *>(red + NC * W * TPW * 16 + W);
+            if (threadIdx.x == 0) {
+                const uint32_t before =
+                    __hip_atomic_fetch_add(a.xcnt + blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint32_t last = before == XSN - 1;
+                // every slice has counted itself: ready for the next launch
+                if (last) __hip_atomic_store(a.xcnt + blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *flag = last;
+            }
+            __syncthreads();
+            if (*flag == 0) return;
+            if (i < nout) {
+                // the slices in order, whichever arrived last
+                float r = 0.f;
+                for (uint32_t k = 0; k < XSN; k++)
+                    r += k == xsl ? ysum
+                                  : __hip_atomic_load(a.xpart + ((size_t)blk * XSN + k) * 32 + i,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ysum = r;
+            }
+        }
+    }
+    if (i >= lim) return;
     if constexpr (EPI == MQ_SWIGLU) {
         const uint32_t grp = ii >> 4, n = ii & 15;
         const float gv = s * partial(grp, 0, n), uv = s * partial(grp, TPW - 1, n);
@@ -703,9 +752,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         pack_half(act, row >> 5, a.xout);
         return;
     }
-    const uint32_t grp = pair ? (ii >> 4) : (ii >> 4) / TPW;
-    const uint32_t tt = pair ? 0 : (ii >> 4) % TPW;
-    float y = s * partial(grp, tt, ii & 15);
+    float y = s * (EPI == MQ_RESID ? ysum : partial(grp, tt, ii & 15));
     if (sg.bias && valid) y = y + e_bias;
     if constexpr (NC > 1) {
         // several columns: column c's outputs at out + c * ostride
@@ -768,7 +815,7 @@ template <uint32_t T0, uint32_t T1, int TPW, int TG, int KS, int P, int EPI>
 __global__ __launch_bounds__(64 * TG * KS)
 __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq(MqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ float red[TG * KS * TPW * 16 + TG * KS];
+    __shared__ float red[TG * KS * TPW * 16 + TG * KS + 1];
     uint32_t si = 0;
 #pragma unroll
     for (int s = 1; s < MQ_MAX_SEG; s++)
@@ -784,7 +831,7 @@ template <uint32_t T, int TPW, int TG, int KS, int P, int NC>
 __global__ __launch_bounds__(64 * TG * KS)
 __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mqx(MqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ float red[NC * TG * KS * TPW * 16 + TG * KS];
+    __shared__ float red[NC * TG * KS * TPW * 16 + TG * KS + 1];
     mq_body<T, TPW, TG, KS, P, MQ_STORE, NC, true>(a, 0, lds, red);
 }
 
@@ -808,6 +855,8 @@ static MqFn pick(const MqGeom &g) {
     LRS_MQ_CASE(1, 2, 8, 1)
     LRS_MQ_CASE(1, 2, 8, 2)
     LRS_MQ_CASE(2, 2, 2, 1)
+    LRS_MQ_CASE(1, 2, 4, 1)
+    LRS_MQ_CASE(1, 2, 2, 1)
     // Q8_0 units are 64 elements: deeper prefetch over more K-slices
     if constexpr (T0 == T_Q8_0 && T1 == T_Q8_0 && EPI == MQ_STORE) {
         LRS_MQ_CASE(1, 1, 16, 4)
@@ -841,13 +890,22 @@ hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int e
     MqArgs a = in;
     if (a.n_seg == 0 || a.n_seg > MQ_MAX_SEG) return hipErrorInvalidValue;
     if (t0 == t1) a.n_seg0 = a.n_seg;
+    // K split across workgroups: one segment, residual epilogue, 32-row
+    // output blocks, at least one unit per K-slice of every workgroup
+    const uint32_t xs = g.xs > 1 ? (uint32_t)g.xs : 1u;
+    if (xs > 1) {
+        if (epi != MQ_RESID || a.n_seg != 1 || a.seg[0].w2 || !a.xpart || !a.xcnt ||
+            g.tg * g.tpw != 2 || t0 != t1 || xs > 8 || tunits(t0, a.n_in) < xs * (uint32_t)g.ks)
+            return hipErrorInvalidValue;
+    }
+    a.xsplit = xs;
     uint32_t wgs = 0;
     for (uint32_t i = 0; i < a.n_seg; i++) {
         const bool pair = a.seg[i].w2 != nullptr;
         const uint32_t per = pair ? (uint32_t)g.tg : (uint32_t)(g.tg * g.tpw);
         if (pair && g.tpw != 2) return hipErrorInvalidValue;
         a.seg[i].wg0 = wgs;
-        wgs += (ttiles(a.seg[i].rows) + per - 1) / per;
+        wgs += (ttiles(a.seg[i].rows) + per - 1) / per * xs;
     }
     // output packs need whole 32-row blocks per workgroup
     if (epi == MQ_RESID || epi == MQ_SWIGLU) {
@@ -865,7 +923,10 @@ hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int e
     default: return hipErrorInvalidValue;
     }
     if (!fn) return hipErrorNotSupported;
-    const size_t lds = (size_t)a.nxb * 96 + 16 + (size_t)a.nxb * 16;
+    // staged pack: all nxb blocks, or the largest slice's blocks
+    const uint32_t units = tunits(t0, a.n_in), bpu = t0 == T_Q8_0 ? 2u : 8u;
+    const size_t nxl = xs > 1 ? (size_t)((units + xs - 1) / xs) * bpu : a.nxb;
+    const size_t lds = nxl * 96 + 16 + nxl * 16;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if (wgs_out) *wgs_out = wgs;
     if (keys_per_wg) {
