@@ -90,7 +90,8 @@ struct lrs_model {
     // activations: residual, q after RoPE, logits, attention split partials
     float *x, *qbuf, *logits, *pa;
     // partial sums and arrival counts of the matvecs split over K across
-    // workgroups (down, o): [n_embd / 32 blocks][8 slices][32], [blocks]
+    // workgroups (down, o, gate/up): [blocks][8 slices][64], [blocks], for
+    // max(n_embd, n_ff) / 32 output blocks
     float *xpart = nullptr;
     uint32_t *xcnt = nullptr;
     uint32_t a_splits;
@@ -224,7 +225,7 @@ MqGeom down_geom(uint32_t n_ff) {
 
 // A launch-shape override from the environment, "tpw,tg,ks,p[,xs]" (the
 // LLAMA_RS_MATVEC_GEOM knob of resident_forward.rs:164-176, per op here):
-// LRS_GEOM_DOWN, LRS_GEOM_O.  Read when the op is enqueued (graphs: at
+// LRS_GEOM_DOWN, LRS_GEOM_O, LRS_GEOM_GATEUP.  Read when the op is enqueued (graphs: at
 // capture); a shape the kernels do not have fails the launch.
 MqGeom env_geom(const char *name, MqGeom dflt) {
     const char *v = getenv(name);
@@ -481,8 +482,10 @@ hipError_t op_gateup(lrs_model *m, uint32_t l) {
     }
     a.xout = m->pk_s;
     a.xout.q8 = L.down_q8;
-    return launch_mq(a, L.gate->v.type, L.gate->v.type, gateup_geom(c.n_ff), MQ_SWIGLU,
-                     m->ctx->stream);
+    a.xpart = m->xpart;
+    a.xcnt = m->xcnt;
+    return launch_mq(a, L.gate->v.type, L.gate->v.type, env_geom("LRS_GEOM_GATEUP", gateup_geom(c.n_ff)),
+                     MQ_SWIGLU, m->ctx->stream);
 }
 
 // x += W_down act; pack of x * (next layer's attn_norm, or output_norm)
@@ -675,8 +678,8 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
     {
         // the split matvecs' arrival counts start at zero and every launch
         // leaves them at zero (the last slice to arrive resets its block's)
-        const size_t nb = c.n_embd / 32;
-        if ((rc = dev_alloc(m, nb * 8 * 32 * sizeof(float), (void **)&m->xpart)) ||
+        const size_t nb = (c.n_embd > c.n_ff ? c.n_embd : c.n_ff) / 32;
+        if ((rc = dev_alloc(m, nb * 8 * 64 * sizeof(float), (void **)&m->xpart)) ||
             (rc = dev_alloc(m, nb * sizeof(uint32_t), (void **)&m->xcnt)))
             return rc;
         if (hipMemset(m->xcnt, 0, nb * sizeof(uint32_t)) != hipSuccess)

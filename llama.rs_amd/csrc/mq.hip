@@ -428,8 +428,9 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     // output tiles of this workgroup: TG tile groups of TPW tiles (pairs: one
     // output tile per group, its gate and up weights)
     const uint32_t otiles_wg = pair ? TG : TG * TPW;
-    // MQ_RESID split over K: workgroup b is slice b % xs of output block b / xs
-    const uint32_t XSN = (EPI == MQ_RESID && a.xsplit > 1) ? a.xsplit : 1u;
+    // MQ_RESID / MQ_SWIGLU split over K: workgroup b is slice b % xs of
+    // output block b / xs
+    const uint32_t XSN = ((EPI == MQ_RESID || EPI == MQ_SWIGLU) && a.xsplit > 1) ? a.xsplit : 1u;
     const uint32_t wrel = blockIdx.x - sg.wg0;
     const uint32_t blk = wrel / XSN, xsl = wrel % XSN;
     const uint32_t tile0 = blk * otiles_wg;
@@ -709,17 +710,29 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     const uint32_t ii = i < nout ? i : nout - 1;
     const uint32_t grp = pair ? (ii >> 4) : (ii >> 4) / TPW;
     const uint32_t tt = pair ? 0 : (ii >> 4) % TPW;
-    float ysum = 0.f;
-    if constexpr (EPI == MQ_RESID) {
-        ysum = partial(grp, tt, ii & 15);
+    // the K-slice sums of output i: (value) or, for SwiGLU, (gate, up)
+    float ysum = 0.f, usum = 0.f;
+    if constexpr (EPI == MQ_RESID || EPI == MQ_SWIGLU) {
+        if constexpr (EPI == MQ_SWIGLU) {
+            ysum = partial(ii >> 4, 0, ii & 15);
+            usum = partial(ii >> 4, TPW - 1, ii & 15);
+        } else {
+            ysum = partial(grp, tt, ii & 15);
+        }
         if (XSN > 1) {
             // every thread reaches both barriers; slices other than the last
             // to arrive leave after counting themselves.  Partials go out as
             // agent-scope stores (written through to memory), and the wait
             // for their completion comes before the count, so the last
             // arriver's agent-scope loads see every slice's partials.
-            float *mine = a.xpart + ((size_t)blk * XSN + xsl) * 32;
-            if (i < nout) __hip_atomic_store(mine + i, ysum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // Slice k of block b: [32 values] or [32 gate][32 up] floats.
+            constexpr uint32_t NXV = EPI == MQ_SWIGLU ? 64u : 32u;
+            float *mine = a.xpart + ((size_t)blk * XSN + xsl) * NXV;
+            if (i < nout) {
+                __hip_atomic_store(mine + i, ysum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if constexpr (EPI == MQ_SWIGLU)
+                    __hip_atomic_store(mine + 32 + i, usum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the stores are complete
             __syncthreads();
             uint32_t *flag = reinterpret_cast<uint32_t *>(red + NC * W * TPW * 16 + W);
@@ -735,19 +748,22 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
             if (*flag == 0) return;
             if (i < nout) {
                 // the slices in order, whichever arrived last
-                float r = 0.f;
-                for (uint32_t k = 0; k < XSN; k++)
-                    r += k == xsl ? ysum
-                                  : __hip_atomic_load(a.xpart + ((size_t)blk * XSN + k) * 32 + i,
-                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                float r = 0.f, ru = 0.f;
+                for (uint32_t k = 0; k < XSN; k++) {
+                    const float *pk = a.xpart + ((size_t)blk * XSN + k) * NXV;
+                    r += k == xsl ? ysum : __hip_atomic_load(pk + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if constexpr (EPI == MQ_SWIGLU)
+                        ru += k == xsl ? usum
+                                       : __hip_atomic_load(pk + 32 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
                 ysum = r;
+                usum = ru;
             }
         }
     }
     if (i >= lim) return;
     if constexpr (EPI == MQ_SWIGLU) {
-        const uint32_t grp = ii >> 4, n = ii & 15;
-        const float gv = s * partial(grp, 0, n), uv = s * partial(grp, TPW - 1, n);
+        const float gv = s * ysum, uv = s * usum;
         const float act = valid ? silu_mul(gv, uv) : 0.f;
         pack_half(act, row >> 5, a.xout);
         return;
@@ -855,6 +871,7 @@ static MqFn pick(const MqGeom &g) {
     LRS_MQ_CASE(1, 2, 8, 1)
     LRS_MQ_CASE(1, 2, 8, 2)
     LRS_MQ_CASE(2, 2, 2, 1)
+    LRS_MQ_CASE(2, 2, 2, 2)
     LRS_MQ_CASE(1, 2, 4, 1)
     LRS_MQ_CASE(1, 2, 2, 1)
     // Q8_0 units are 64 elements: deeper prefetch over more K-slices
@@ -894,8 +911,11 @@ hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int e
     // output blocks, at least one unit per K-slice of every workgroup
     const uint32_t xs = g.xs > 1 ? (uint32_t)g.xs : 1u;
     if (xs > 1) {
-        if (epi != MQ_RESID || a.n_seg != 1 || a.seg[0].w2 || !a.xpart || !a.xcnt ||
-            g.tg * g.tpw != 2 || t0 != t1 || xs > 8 || tunits(t0, a.n_in) < xs * (uint32_t)g.ks)
+        // 32 outputs per workgroup: 2 tiles (residual) or 2 tile pairs (SwiGLU)
+        const bool resid = epi == MQ_RESID && !a.seg[0].w2 && g.tg * g.tpw == 2;
+        const bool swiglu = epi == MQ_SWIGLU && a.seg[0].w2 && g.tpw == 2 && g.tg == 2;
+        if (!(resid || swiglu) || a.n_seg != 1 || !a.xpart || !a.xcnt || t0 != t1 || xs > 8 ||
+            tunits(t0, a.n_in) < xs * (uint32_t)g.ks)
             return hipErrorInvalidValue;
     }
     a.xsplit = xs;

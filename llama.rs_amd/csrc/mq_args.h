@@ -82,12 +82,13 @@ struct MqArgs {
     // the input at xf + c * n_in, its outputs at seg[0].out + c * ostride
     const float *xf;
     uint32_t ostride;
-    // MQ_RESID split over K across workgroups: xsplit workgroups per output
-    // block, each over its own contiguous share of the units; each writes its
-    // partial sums to xpart[(block * xsplit + slice) * 32 + i] and counts
-    // itself in xcnt[block]; the last to arrive adds the partials in slice
-    // order, runs the epilogue and sets xcnt[block] back to 0 (so xcnt must
-    // start at zero, and does again after every launch)
+    // MQ_RESID / MQ_SWIGLU split over K across workgroups: xsplit workgroups
+    // per 32-output block, each over its own contiguous share of the units;
+    // each writes its partial sums to xpart[(block * xsplit + slice) * 32 + i]
+    // (SwiGLU: * 64, gate then up) and counts itself in xcnt[block]; the last
+    // to arrive adds the partials in slice order, runs the epilogue and sets
+    // xcnt[block] back to 0 (so xcnt must start at zero, and does again after
+    // every launch)
     uint32_t xsplit;
     float *xpart;
     uint32_t *xcnt;

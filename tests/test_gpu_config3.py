@@ -99,19 +99,21 @@ def test_config3_prompt_block_matches_oracle(orc, c3):
     assert rel_l2(g, o) < LOGIT_TOL
 
 
-# down and o split over K across workgroups (each slice stages its share of
-# the input pack; the last slice to arrive adds the partials in slice order
-# and runs the residual + pack epilogue): other slice counts than the
-# default's (down at n_ff 27648 splits over 3 workgroups per block, o does
-# not split), including down unsplit and 8 slices of down with 5 of o
-SPLITS = [("1,2,6,1,1", "1,2,2,2,2"), ("1,2,2,1,8", "1,2,2,1,5"), ("1,2,6,1,2", "1,2,4,1,2")]
+# down, o and gate/up split over K across workgroups (each slice stages its
+# share of the input pack; the last slice to arrive adds the partials in
+# slice order and runs the residual + pack or SwiGLU + pack epilogue): other
+# slice counts than the defaults', including down unsplit and 8 slices of
+# down and gate/up with 5 of o
+SPLITS = [("1,2,6,1,1", "1,2,2,2,2", "2,2,2,1,3"), ("1,2,2,1,8", "1,2,2,1,5", "2,2,2,2,8"),
+          ("1,2,6,1,2", "1,2,4,1,2", "2,4,2,2,1")]
 
 
-@pytest.mark.parametrize("down,o", SPLITS, ids=[f"down{d}-o{o}" for d, o in SPLITS])
-def test_config3_k_split_matvecs_match_oracle(lrs, orc, c3, monkeypatch, down, o):
+@pytest.mark.parametrize("down,o,gu", SPLITS, ids=[f"down{d}-o{o}-gu{g}" for d, o, g in SPLITS])
+def test_config3_k_split_matvecs_match_oracle(lrs, orc, c3, monkeypatch, down, o, gu):
     ctx, w, _, prompt = c3
     monkeypatch.setenv("LRS_GEOM_DOWN", down)
     monkeypatch.setenv("LRS_GEOM_O", o)
+    monkeypatch.setenv("LRS_GEOM_GATEUP", gu)
     gm = modelgen.gpu_model(lrs, ctx, C3_2L, w)
     try:
         om = orc.Model(C3_2L, w, kv_f16=True, threads=THREADS)
@@ -128,7 +130,7 @@ def test_config3_k_split_matvecs_match_oracle(lrs, orc, c3, monkeypatch, down, o
         a = gm.generate_greedy(prompt[:4], 8).tolist()
         gm.reset()
         assert gm.generate_greedy(prompt[:4], 8).tolist() == a
-        print(f"split down {down} o {o}: worst rel L2 {worst:.2e}")
+        print(f"split down {down} o {o} gate/up {gu}: worst rel L2 {worst:.2e}")
     finally:
         gm.close()
 
