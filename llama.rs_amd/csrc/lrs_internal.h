@@ -81,7 +81,8 @@ hipError_t launch_dequant_rows(WeightView w, const uint32_t *rows_dev, uint32_t 
                                float *out, hipStream_t s);
 // matrix-core matvec (mq.hip)
 hipError_t launch_xpack(const float *x, const float *nw, uint32_t n, uint32_t nxb, XPack p,
-                        hipStream_t s);
+                        hipStream_t s,
+                        float *xsq = nullptr);
 hipError_t launch_mq(const MqArgs &a, uint32_t t0, uint32_t t1, MqGeom g, int epi, hipStream_t s,
                      uint32_t *wgs_out = nullptr, uint32_t *keys_per_wg = nullptr);
 bool mq_geom_supported(const MqGeom &g);

@@ -50,7 +50,7 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
 // and the pack of x * nw for the first layer's q/k/v
 __global__ __launch_bounds__(256) void k_embed(WeightView w, const uint32_t *__restrict__ step,
                                                const float *__restrict__ nw, float *__restrict__ x,
-                                               XPack p) {
+                                               XPack p, float *__restrict__ xsq) {
     const uint32_t be = (uint32_t)block_elems(w.type);
     uint32_t tok = step[0];
     if (tok >= w.n_out) tok = w.n_out - 1;  // ids are validated on the host
@@ -59,6 +59,8 @@ __global__ __launch_bounds__(256) void k_embed(WeightView w, const uint32_t *__r
     const float v = deq_elem(w, e / be, (uint32_t)(e % be));
     x[i] = v;
     pack_half(v * nw[i], i >> 5, p);
+    const float sq = half_sum(v * v);  // the first RMSNorm's block sums
+    if ((i & 31) == 0) xsq[i >> 5] = sq;
 }
 
 }  // namespace lrs
@@ -89,6 +91,9 @@ struct lrs_model {
     float *output_norm, *freq;
     // activations: residual, q after RoPE, logits, attention split partials
     float *x, *qbuf, *logits, *pa;
+    // sum(x^2) of each 32-element block of x, written with x (embed, the
+    // residual epilogues) and read by the fused RMSNorm of the next matvec
+    float *xsq = nullptr;
     // partial sums and arrival counts of the matvecs split over K across
     // workgroups (down, o, gate/up): [blocks][8 slices][64], [blocks], for
     // max(n_embd, n_ff) / 32 output blocks
@@ -241,7 +246,7 @@ MqGeom env_geom(const char *name, MqGeom dflt) {
 // ---- one fused op of the per-token plan, enqueued on the model stream ----
 hipError_t op_embed(lrs_model *m) {
     hipLaunchKernelGGL(k_embed, dim3(m->cfg.n_embd / 256), dim3(256), 0, m->ctx->stream,
-                       m->embd->v, m->step, m->layers[0].attn_norm, m->x, m->pk_n);
+                       m->embd->v, m->step, m->layers[0].attn_norm, m->x, m->pk_n, m->xsq);
     return hipGetLastError();
 }
 
@@ -254,7 +259,7 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
     MqArgs a = {};
     a.n_in = c.n_embd;
     a.xin = m->pk_n;
-    a.xres = m->x;
+    a.xsq = m->xsq;
     a.eps = c.rms_eps;
     a.step = m->step;
     a.freq = m->freq;
@@ -308,7 +313,7 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
         a.nxb = pack_blocks(t, c.n_embd);
         const bool q8 = L.qkv_q8 && t == T_Q8_0;
         a.xin = q8 ? m->pk_q8 : m->pk_n;
-        a.xres = q8 ? nullptr : m->x;
+        a.xsq = q8 ? nullptr : m->xsq;
         hipError_t e = launch_mq(a, t, t, G_QKV, MQ_QKV, m->ctx->stream);
         if (e != hipSuccess) return e;
     }
@@ -341,6 +346,7 @@ hipError_t op_o(lrs_model *m, uint32_t l) {
     a.nxb = pack_blocks(wo->v.type, a.n_in);
     a.xin = m->pk_a;
     a.x = m->x;
+    a.xsq_out = m->xsq;
     a.nw = L.ffn_norm;
     a.xout = m->pk_f;
     if (L.dn) {
@@ -363,7 +369,7 @@ hipError_t op_store(lrs_model *m, const lrs_weight *const *ws, float *const *out
     MqArgs a = {};
     a.n_in = c.n_embd;
     a.xin = m->pk_n;
-    a.xres = m->x;
+    a.xsq = m->xsq;
     a.eps = c.rms_eps;
     bool q4 = false, q6 = false, other = false;
     for (int i = 0; i < n; i++) {
@@ -471,14 +477,14 @@ hipError_t op_gateup(lrs_model *m, uint32_t l) {
     a.n_in = c.n_embd;
     a.nxb = pack_blocks(L.gate->v.type, c.n_embd);
     a.xin = m->pk_f;
-    a.xres = m->x;
+    a.xsq = m->xsq;
     a.eps = c.rms_eps;
     if (L.ffn_q8) {
         hipError_t e = launch_q8norm(m->x, L.ffn_norm, c.n_embd, c.rms_eps, m->pk_q8,
                                      m->ctx->stream);
         if (e != hipSuccess) return e;
         a.xin = m->pk_q8;
-        a.xres = nullptr;
+        a.xsq = nullptr;
     }
     a.xout = m->pk_s;
     a.xout.q8 = L.down_q8;
@@ -499,6 +505,7 @@ hipError_t op_down(lrs_model *m, uint32_t l) {
     a.nxb = pack_blocks(L.down->v.type, c.n_ff);
     a.xin = m->pk_s;
     a.x = m->x;
+    a.xsq_out = m->xsq;
     a.nw = l + 1 < c.n_layer ? m->layers[l + 1].attn_norm : m->output_norm;
     a.xout = m->pk_n;
     a.xpart = m->xpart;
@@ -524,14 +531,14 @@ hipError_t op_head(lrs_model *m, bool greedy) {
     a.n_in = c.n_embd;
     a.nxb = pack_blocks(m->output->v.type, c.n_embd);
     a.xin = m->pk_n;
-    a.xres = m->x;
+    a.xsq = m->xsq;
     a.eps = c.rms_eps;
     if (m->head_q8) {
         hipError_t e = launch_q8norm(m->x, m->output_norm, c.n_embd, c.rms_eps, m->pk_q8,
                                      m->ctx->stream);
         if (e != hipSuccess) return e;
         a.xin = m->pk_q8;
-        a.xres = nullptr;
+        a.xsq = nullptr;
     }
     if (greedy) a.amax = m->amax;
     uint32_t wgs = 0, kpw = 0;
@@ -650,6 +657,7 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
     if ((rc = dev_alloc(m, (size_t)c.n_head * m->a_splits * (c.head_dim + 4) * sizeof(float),
                         (void **)&m->pa)) ||
         (rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
+        (rc = dev_alloc(m, c.n_embd / 32 * sizeof(float), (void **)&m->xsq)) ||
         (rc = dev_alloc(m, qd * sizeof(float), (void **)&m->qbuf)) ||
         (rc = dev_alloc(m, c.vocab * sizeof(float), (void **)&m->logits)) ||
         (rc = dev_alloc(m, 4 * sizeof(uint32_t), (void **)&m->step)) ||
@@ -1210,7 +1218,8 @@ static int prefill(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t po
     if (!head) return LRS_OK;
     LRS_HIP(hipMemcpyAsync(m->x, m->pX + (size_t)(nb - 1) * m->cfg.n_embd,
                            m->cfg.n_embd * sizeof(float), hipMemcpyDeviceToDevice, s));
-    LRS_HIP(launch_xpack(m->x, m->output_norm, m->cfg.n_embd, m->cfg.n_embd / 32, m->pk_n, s));
+    LRS_HIP(launch_xpack(m->x, m->output_norm, m->cfg.n_embd, m->cfg.n_embd / 32, m->pk_n, s,
+                         m->xsq));
     LRS_HIP(op_head(m, false));
     return LRS_OK;
 }

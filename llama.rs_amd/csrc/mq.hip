@@ -78,20 +78,29 @@ __device__ __forceinline__ float cfold(v4i c) {
 // ---------------------------------------------------------------------------
 // x-pack of x (times nw when given) for blocks [0, nxb); elements >= n pack
 // as zero (padding of the K dimension to whole units)
+// xsq (optional): sum(x^2) of each 32-element block
 __global__ __launch_bounds__(256) void k_xpack(const float *__restrict__ x,
                                                const float *__restrict__ nw, uint32_t n,
-                                               uint32_t nxb, XPack p) {
+                                               uint32_t nxb, XPack p, float *__restrict__ xsq) {
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= 32 * nxb) return;  // whole half-waves leave together
-    float v = 0.f;
-    if (e < n) v = nw ? x[e] * nw[e] : x[e];
+    float v = 0.f, xv = 0.f;
+    if (e < n) {
+        xv = x[e];
+        v = nw ? xv * nw[e] : xv;
+    }
     pack_half(v, e >> 5, p);
+    if (xsq) {
+        const float sq = half_sum(xv * xv);
+        if ((e & 31) == 0) xsq[e >> 5] = sq;
+    }
 }
 
 hipError_t launch_xpack(const float *x, const float *nw, uint32_t n, uint32_t nxb, XPack p,
-                        hipStream_t s) {
+                        hipStream_t s, float *xsq) {
     const uint32_t threads = 32 * nxb;
-    hipLaunchKernelGGL(k_xpack, dim3((threads + 255) / 256), dim3(256), 0, s, x, nw, n, nxb, p);
+    hipLaunchKernelGGL(k_xpack, dim3((threads + 255) / 256), dim3(256), 0, s, x, nw, n, nxb, p,
+                       xsq);
     return hipGetLastError();
 }
 
@@ -487,7 +496,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 
     // stage the input pack(s): digits of column c at c * nxb * 96, 16 zero
     // bytes, then the meta of column c at + c * nxb * 16; fused RMSNorm: sum
-    // of squares of xres
+    // of the block sums of squares
     LPack lp;
     lp.zero = NC * nxl * 96;
     lp.meta = lp.zero + 16;
@@ -558,11 +567,9 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         }
     }
     float ss = 0.f;
-    if (a.xres) {
-        for (uint32_t i = 4 * threadIdx.x; i < a.n_in; i += 4 * blockDim.x) {
-            const float4 v = *reinterpret_cast<const float4 *>(a.xres + i);
-            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-        }
+    if (a.xsq) {
+        // the block sums of squares x's producer wrote (n_in / 32 of them)
+        for (uint32_t b = threadIdx.x; b < a.n_in / 32; b += blockDim.x) ss += a.xsq[b];
         // the wavefront's sum now, while the weight and pack loads are in
         // flight, not in the epilogue
 #pragma unroll
@@ -684,7 +691,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 
     // ---- epilogue: thread i owns output i of the workgroup ----
     float s = 1.0f;
-    if (a.xres) {
+    if (a.xsq) {
         float tot = 0.f;
 #pragma unroll
         for (int w = 0; w < W; w++) tot += red[NC * W * TPW * 16 + w];
@@ -820,6 +827,10 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         }
         const float pv = valid ? (a.nw ? xn * e_nw : xn) : 0.f;
         pack_half(pv, row >> 5, a.xout);
+        if (a.xsq_out) {
+            const float sq = half_sum(xn * xn);
+            if ((i & 31) == 0 && valid) a.xsq_out[row >> 5] = sq;
+        }
     }
 }
 

@@ -60,10 +60,13 @@ struct MqArgs {
     uint32_t n_in;           // K (elements)
     uint32_t nxb;            // 32-element blocks of the input pack (K padded to units)
     XPack xin;               // input pack
-    const float *xres;       // fused RMSNorm: the f32 vector whose rms scales the result
+    // fused RMSNorm: sum(x^2) of each 32-element block of the f32 vector x whose
+    // rms scales the result ([n_in / 32], written by x's producer), or null
+    const float *xsq;
     float eps;
     // MQ_RESID
     float *x;                // residual [rows]
+    float *xsq_out;          // sum(x_new^2) of each 32-row block of x, or null
     const float *nw;         // norm weight folded into the output pack (null: 1)
     XPack xout;              // output pack (RESID / SWIGLU)
     // MQ_QKV

@@ -70,6 +70,18 @@ __device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p, bool s
     }
 }
 
+// Sum over the 32 lanes of a half wavefront, in every lane of the half (the
+// same DPP rows of 16, then one exchange between the rows): the producers of
+// the residual x store sum(x^2) per 32-element block with it, so that a
+// fused RMSNorm reads n / 32 block sums instead of the n elements.
+__device__ __forceinline__ float half_sum(float v) {
+    v += pk_dpp<0xB1>(v);
+    v += pk_dpp<0x4E>(v);
+    v += pk_dpp<0x141>(v);
+    v += pk_dpp<0x140>(v);
+    return v + __shfl_xor(v, 16, 64);
+}
+
 // orderable 64-bit argmax key of value v at index r: the larger value wins,
 // ties go to the smaller index (the first max of ops.rs:1035-1045); NaN
 // never wins
