@@ -204,13 +204,24 @@ constexpr MqGeom G_STORE = {1, 2, 4, 2};  // hybrid q/k/v and delta-net projecti
 // gate+up tile pairs: 4 per workgroup x 2 K-slices while that gives >= 400
 // workgroups (27648 rows: 432); else 2 per workgroup x 4 K-slices when all of
 // them fit at once (2 workgroups of 8 wavefronts per CU: 13824 rows, 432);
-// else 2 per workgroup x 2 K-slices with one unit in flight (17408 rows: 544
-// workgroups of 4 wavefronts at 5 per CU, no second round; 21.9 against
-// 23.0 us)
+// else 2 per workgroup x 2 K-slices (unsplit with one unit in flight: 544
+// workgroups of 4 wavefronts at 5 per CU, 21.9 against 23.0 us for x 4
+// K-slices), with a split tail when the block count just passes 512
 MqGeom gateup_geom(uint32_t n_ff) {
     const uint32_t t = ttiles(n_ff);
     if (t / 4 >= 400) return MqGeom{2, 4, 2, 2};
-    return t / 2 <= 512 ? MqGeom{2, 2, 4, 2} : MqGeom{2, 2, 2, 1};
+    if (t / 2 <= 512) return MqGeom{2, 2, 4, 2};
+    // more blocks of 2 tile pairs than twice the 256 CUs: a few CUs would
+    // stream a third whole block (17408 rows: 544 blocks, 32 CUs with 3), so
+    // the blocks past the last multiple of 256 split over K in 6 workgroups
+    // each (21.1 -> 18.4 us at 17408, two units in flight)
+    const uint32_t blocks = t / 2, tail = blocks % 256;
+    if (tail && tail <= 64) {
+        MqGeom g = {2, 2, 2, 2, 6};
+        g.xfull = (int)(blocks - tail);
+        return g;
+    }
+    return MqGeom{2, 2, 2, 1};
 }
 // down (n_embd rows, K = n_ff): one 32-row block per workgroup leaves 96 of
 // the 256 CUs idle, and one CU streams ~35-40 GB/s, so wide down projections
@@ -228,7 +239,7 @@ MqGeom down_geom(uint32_t n_ff) {
     return MqGeom{1, 2, 6, 1};
 }
 
-// A launch-shape override from the environment, "tpw,tg,ks,p[,xs]" (the
+// A launch-shape override from the environment, "tpw,tg,ks,p[,xs[,xfull]]" (the
 // LLAMA_RS_MATVEC_GEOM knob of resident_forward.rs:164-176, per op here):
 // LRS_GEOM_DOWN, LRS_GEOM_O, LRS_GEOM_GATEUP.  Read when the op is enqueued (graphs: at
 // capture); a shape the kernels do not have fails the launch.
@@ -237,9 +248,11 @@ MqGeom env_geom(const char *name, MqGeom dflt) {
     if (!v || !v[0]) return dflt;
     MqGeom g = {0, 0, 0, 0};
     int xs = 1;
-    const int n = sscanf(v, "%d,%d,%d,%d,%d", &g.tpw, &g.tg, &g.ks, &g.p, &xs);
+    int xfull = 0;
+    const int n = sscanf(v, "%d,%d,%d,%d,%d,%d", &g.tpw, &g.tg, &g.ks, &g.p, &xs, &xfull);
     if (n < 4) return dflt;
     g.xs = xs;
+    g.xfull = xfull;
     return g;
 }
 

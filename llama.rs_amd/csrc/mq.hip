@@ -438,10 +438,13 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     // output tile per group, its gate and up weights)
     const uint32_t otiles_wg = pair ? TG : TG * TPW;
     // MQ_RESID / MQ_SWIGLU split over K: workgroup b is slice b % xs of
-    // output block b / xs
-    const uint32_t XSN = ((EPI == MQ_RESID || EPI == MQ_SWIGLU) && a.xsplit > 1) ? a.xsplit : 1u;
+    // output block b / xs (past the xfull whole blocks when those are set)
+    const uint32_t xs_all = ((EPI == MQ_RESID || EPI == MQ_SWIGLU) && a.xsplit > 1) ? a.xsplit : 1u;
     const uint32_t wrel = blockIdx.x - sg.wg0;
-    const uint32_t blk = wrel / XSN, xsl = wrel % XSN;
+    const bool whole = xs_all == 1 || wrel < a.xfull;
+    const uint32_t XSN = whole ? 1u : xs_all;
+    const uint32_t blk = whole ? wrel : a.xfull + (wrel - a.xfull) / xs_all;
+    const uint32_t xsl = whole ? 0u : (wrel - a.xfull) % xs_all;
     const uint32_t tile0 = blk * otiles_wg;
     const uint32_t ntiles = ttiles(sg.rows);
     const uint8_t *wt[TPW];
@@ -930,13 +933,16 @@ hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int e
             return hipErrorInvalidValue;
     }
     a.xsplit = xs;
+    a.xfull = xs > 1 ? (uint32_t)g.xfull : 0u;
     uint32_t wgs = 0;
     for (uint32_t i = 0; i < a.n_seg; i++) {
         const bool pair = a.seg[i].w2 != nullptr;
         const uint32_t per = pair ? (uint32_t)g.tg : (uint32_t)(g.tg * g.tpw);
         if (pair && g.tpw != 2) return hipErrorInvalidValue;
         a.seg[i].wg0 = wgs;
-        wgs += (ttiles(a.seg[i].rows) + per - 1) / per * xs;
+        const uint32_t blocks = (ttiles(a.seg[i].rows) + per - 1) / per;
+        if (a.xfull >= blocks) return hipErrorInvalidValue;
+        wgs += a.xfull + (blocks - a.xfull) * xs;
     }
     // output packs need whole 32-row blocks per workgroup
     if (epi == MQ_RESID || epi == MQ_SWIGLU) {
@@ -956,7 +962,7 @@ hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int e
     if (!fn) return hipErrorNotSupported;
     // staged pack: all nxb blocks, or the largest slice's blocks
     const uint32_t units = tunits(t0, a.n_in), bpu = t0 == T_Q8_0 ? 2u : 8u;
-    const size_t nxl = xs > 1 ? (size_t)((units + xs - 1) / xs) * bpu : a.nxb;
+    const size_t nxl = xs > 1 && !a.xfull ? (size_t)((units + xs - 1) / xs) * bpu : a.nxb;
     const size_t lds = nxl * 96 + 16 + nxl * 16;
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if (wgs_out) *wgs_out = wgs;

@@ -92,7 +92,10 @@ struct MqArgs {
     // to arrive adds the partials in slice order, runs the epilogue and sets
     // xcnt[block] back to 0 (so xcnt must start at zero, and does again after
     // every launch)
-    uint32_t xsplit;
+    // With xfull > 0 only the blocks from xfull on are split (workgroups
+    // [0, xfull) take one whole block each, the rest xsplit per block): a
+    // block count that is not a multiple of the CUs gets its tail spread.
+    uint32_t xsplit, xfull;
     float *xpart;
     uint32_t *xcnt;
 };
@@ -103,6 +106,7 @@ struct MqArgs {
 struct MqGeom {
     int tpw, tg, ks, p;
     int xs = 1;
+    int xfull = 0;  // with xs > 1: blocks before the split tail (0: every block split)
 };
 
 }  // namespace lrs

@@ -105,7 +105,9 @@ def test_config3_prompt_block_matches_oracle(orc, c3):
 # slice counts than the defaults', including down unsplit and 8 slices of
 # down and gate/up with 5 of o
 SPLITS = [("1,2,6,1,1", "1,2,2,2,2", "2,2,2,1,3"), ("1,2,2,1,8", "1,2,2,1,5", "2,2,2,2,8"),
-          ("1,2,6,1,2", "1,2,4,1,2", "2,4,2,2,1")]
+          ("1,2,6,1,2", "1,2,4,1,2", "2,4,2,2,1"),
+          # only a tail of the blocks split (xfull whole blocks first)
+          ("1,2,4,1,4,100", "1,2,4,2,3,150", "2,2,2,1,8,800")]
 
 
 @pytest.mark.parametrize("down,o,gu", SPLITS, ids=[f"down{d}-o{o}-gu{g}" for d, o, g in SPLITS])
