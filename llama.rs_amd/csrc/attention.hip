@@ -27,6 +27,7 @@
 // o-projection; it loads every split's partial while the position is in
 // flight and weighs only the splits that hold positions.  The split spreads
 // the K/V stream over ~256 workgroups: one CU streams only ~35 GB/s.
+#include "attn_dev.h"
 #include "lrs_internal.h"
 #include "pack_dev.h"
 
@@ -34,7 +35,6 @@ namespace lrs {
 
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_DEPTH = 4;    // positions per lane group with K and V loads in flight
-constexpr uint32_t ATT_BLOCK = 16;  // positions per block; split s owns blocks s, s + splits, ...
 
 struct AttnArgs {
     const float *q;           // [n_head * HD], RoPE applied
@@ -45,53 +45,12 @@ struct AttnArgs {
     float scale;
 };
 
-// the splits that hold positions of a context of L positions (the others
-// have no work and write no partial)
-__device__ __forceinline__ uint32_t attn_live_splits(uint32_t L, uint32_t splits) {
-    const uint32_t b = (L + ATT_BLOCK - 1) / ATT_BLOCK;
-    return b < splits ? b : splits;
-}
-
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ half2_t as_h2(uint32_t v) {
     half2_t r;
     __builtin_memcpy(&r, &v, 4);
     return r;
-}
-
-// sum over aligned groups of N lanes (N = 8, 16, 32) in every lane: DPP
-// within a row of 16 (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
-// row_mirror), a lane shuffle across rows
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-// max over each row of 16 lanes, in every lane of the row
-__device__ __forceinline__ float row_max(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    return fmaxf(v, dpp_f<0x140>(v));
-}
-// max over aligned groups of N lanes (N = 8, 16, 32) in every lane
-template <int N>
-__device__ __forceinline__ float group_max(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    if constexpr (N >= 16) v = fmaxf(v, dpp_f<0x140>(v));
-    if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return v;
-}
-template <int N>
-__device__ __forceinline__ float group_sum(float v) {
-    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
-    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp_f<0x141>(v);  // row_half_mirror
-    if constexpr (N >= 16) v += dpp_f<0x140>(v);  // row_mirror
-    if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
-    return v;
 }
 
 template <int HD, int REP>
@@ -256,11 +215,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     }
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// combine of the split partials of head blockIdx.x: the head's partial block
-// (every split's, issued before the position arrives) goes to LDS in one
-// round trip (global_load_lds), then thread d owns dim d
+// combine of the split partials of head blockIdx.x (attn_combine_head)
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ part, uint32_t splits,
                                                      const uint32_t *__restrict__ step,
@@ -268,44 +223,7 @@ __global__ __launch_bounds__(HD) void k_attn_combine(const float *__restrict__ p
                                                      uint32_t gstride, XPack out) {
     extern __shared__ __attribute__((aligned(16))) float pl[];  // [splits][HD + 4]
     __shared__ float wsh[64], red[1];
-    constexpr uint32_t ST = HD + 4;
-    const uint32_t h = blockIdx.x, d = threadIdx.x, lane = d & 63, wave = d >> 6;
-    const uint8_t *src = reinterpret_cast<const uint8_t *>(part + (size_t)h * splits * ST);
-    const uint32_t bytes = splits * ST * 4;  // multiple of 16
-    for (uint32_t base = wave * 1024; base < bytes; base += HD * 16) {
-        const uint32_t off = base + lane * 16;
-        if (off < bytes)
-            __builtin_amdgcn_global_load_lds(src + off, (lds_void *)(reinterpret_cast<uint8_t *>(pl) + base), 16, 0, 0);
-    }
-    // the output gate of (head h, dim d) for the gated attention, loaded with
-    // the partials
-    const float gv = gate ? gate[(size_t)h * gstride + d] : 0.f;
-    // the splits that hold positions (the split kernel wrote no partial for
-    // the others; what their slots hold is not used)
-    splits = attn_live_splits(step[1] + 1, splits);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    // wave 0: M = max over the splits (splits <= 64), weights, denominator
-    if (wave == 0) {
-        const float ms = lane < splits ? pl[lane * ST + HD] : -INFINITY;
-        float M = row_max(ms);  // rows of 16 by DPP, then across the rows
-        M = fmaxf(M, __shfl_xor(M, 16, 64));
-        M = fmaxf(M, __shfl_xor(M, 32, 64));
-        const float w = ms == -INFINITY ? 0.f : expf(ms - M);  // empty splits weigh 0
-        float den = group_sum<16>(lane < splits ? w * pl[lane * ST + HD + 1] : 0.f);
-        den += __shfl_xor(den, 16, 64);
-        den += __shfl_xor(den, 32, 64);
-        if (lane < splits) wsh[lane] = w;
-        if (lane == 0) red[0] = den;
-    }
-    __syncthreads();
-    const float den = red[0];
-    float num = 0.f;
-    for (uint32_t s = 0; s < splits; s++) num = fmaf(wsh[s], pl[s * ST + d], num);
-    float o = num / den;
-    // gated attention (gate_quant.comp): o * sigmoid(gate of head h, dim d)
-    if (gate) o = o * (1.0f / (1.0f + expf(-gv)));
-    pack_half(o, (h * HD + d) >> 5, out);
+    attn_combine_head<false>(part, splits, HD, step, gate, gstride, out, blockIdx.x, pl, wsh, red);
 }
 
 // split count: at most one workgroup per CU (256 >= splits x KV heads), at
@@ -341,7 +259,7 @@ static AttnFn pick_rep(uint32_t rep) {
 hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *part,
                             XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
                             uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s,
-                            const float *gate, uint32_t gstride) {
+                            const float *gate, uint32_t gstride, bool combine) {
     AttnArgs a;
     a.q = q;
     a.kc = kc;
@@ -365,6 +283,7 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
     }
     if (!fn) return hipErrorInvalidValue;
     hipLaunchKernelGGL(fn, grid, dim3(ATT_THREADS), 0, s, a);
+    if (!combine) return hipGetLastError();  // the o launch merges the splits (k_mq_ao)
     const size_t cl = (size_t)splits * (head_dim + 4) * sizeof(float);
     switch (head_dim) {
     case 64: hipLaunchKernelGGL(k_attn_combine<64>, dim3(n_head), dim3(64), cl, s, part, splits, step, gate, gstride, out); break;

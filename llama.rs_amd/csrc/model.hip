@@ -44,7 +44,8 @@ uint32_t attn_splits(uint32_t n_kv);
 hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *part,
                             XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
                             uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s,
-                            const float *gate = nullptr, uint32_t gstride = 0);
+                            const float *gate = nullptr, uint32_t gstride = 0,
+                            bool combine = true);
 
 // x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304),
 // and the pack of x * nw for the first layer's q/k/v
@@ -100,6 +101,11 @@ struct lrs_model {
     float *xpart = nullptr;
     uint32_t *xcnt = nullptr;
     uint32_t a_splits;
+    // attention combine in the o launch (k_mq_ao; LRS_AO=0 turns it off):
+    // producer count at [0], the consumers' wait-error word at [32], then
+    // one flag per o workgroup 32 words apart; all zero between launches
+    bool ao_on = true;
+    uint32_t *ao_sync = nullptr;
     // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
     // SwiGLU output
     XPack pk_n, pk_f, pk_a, pk_s;
@@ -333,8 +339,17 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
     return hipSuccess;
 }
 
+// whether layer l's attention combine runs in its o launch (k_mq_ao):
+// attention layers whose o weight has the kernel and takes the 22-bit pack
+bool ao_fused(const lrs_model *m, const DevLayer &L) {
+    const lrs_config &c = m->cfg;
+    return m->ao_on && m->ao_sync && !L.dn && L.o && !L.o_q8 &&
+           mq_ao_supported(L.o->v.type, L.o->v.n_in, c.n_embd, c.head_dim, m->a_splits);
+}
+
 // attention over the f16 cache; hybrid layers gate the output with
-// sigmoid(second half of each head's Q rows) before packing it
+// sigmoid(second half of each head's Q rows) before packing it (the combine
+// in the o launch when ao_fused)
 hipError_t op_attn(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
@@ -343,7 +358,7 @@ hipError_t op_attn(lrs_model *m, uint32_t l) {
     out.q8 = L.o_q8;
     return launch_attention(m->qbuf, L.kc, L.vc, m->pa, out, m->step, c.n_head, c.n_head_kv,
                             c.head_dim, c.ctx, m->a_splits, m->ctx->stream, gate,
-                            2 * c.head_dim);
+                            2 * c.head_dim, !ao_fused(m, L));
 }
 
 // x += W_o att (or W_ssm_out y of a delta-net layer); pack of x * ffn_norm
@@ -371,6 +386,21 @@ hipError_t op_o(lrs_model *m, uint32_t l) {
     }
     a.xpart = m->xpart;
     a.xcnt = m->xcnt;
+    if (ao_fused(m, L)) {
+        // the attention combine's workgroups (one per query head) ahead of o's
+        AoArgs ao = {};
+        ao.part = m->pa;
+        ao.gate = m->hybrid ? m->qg + c.head_dim : nullptr;
+        ao.splits = m->a_splits;
+        ao.head_dim = c.head_dim;
+        ao.gstride = 2 * c.head_dim;
+        ao.n_prod = c.n_head;
+        ao.cnt = m->ao_sync;
+        a.werr = m->ao_sync + 32;
+        a.wflag = m->ao_sync + 64;
+        a.step = m->step;
+        return launch_mq_ao(a, ao, wo->v.type, m->ctx->stream);
+    }
     return launch_mq(a, wo->v.type, wo->v.type, env_geom("LRS_GEOM_O", G_O), MQ_RESID,
                      m->ctx->stream);
 }
@@ -667,6 +697,13 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
     if ((rc = upload_vec(m, fr.data(), fr.size(), &m->freq))) return rc;
     m->gen_cap = 1u << 16;
     m->a_splits = attn_splits(c.n_head_kv);
+    {
+        // LRS_ATTN_SPLITS: the decode attention's position splits per KV head
+        // (tuning knob; at most the default's 256 / n_head_kv, 40)
+        const char *v = getenv("LRS_ATTN_SPLITS");
+        const int n = v ? atoi(v) : 0;
+        if (n > 0 && (uint32_t)n < m->a_splits) m->a_splits = (uint32_t)n;
+    }
     if ((rc = dev_alloc(m, (size_t)c.n_head * m->a_splits * (c.head_dim + 4) * sizeof(float),
                         (void **)&m->pa)) ||
         (rc = dev_alloc(m, c.n_embd * sizeof(float), (void **)&m->x)) ||
@@ -705,8 +742,16 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
             return rc;
         if (hipMemset(m->xcnt, 0, nb * sizeof(uint32_t)) != hipSuccess)
             return fail(LRS_E_HIP, "memset");
+        // count, error word and one flag per 32 rows of o's output
+        const size_t aw = 64 + 32 * (size_t)(c.n_embd / 32);
+        if ((rc = dev_alloc(m, aw * sizeof(uint32_t), (void **)&m->ao_sync))) return rc;
+        if (hipMemset(m->ao_sync, 0, aw * sizeof(uint32_t)) != hipSuccess)
+            return fail(LRS_E_HIP, "memset");
+        const char *v = getenv("LRS_AO");
+        m->ao_on = !(v && (strcmp(v, "0") == 0 || strcasecmp(v, "false") == 0));
     }
-    if (hipHostMalloc((void **)&m->step_host, 4 * 1024 * sizeof(uint32_t), hipHostMallocDefault) !=
+    // 1024 step slots of 4 words (enqueue_tokens), then the wait-error word
+    if (hipHostMalloc((void **)&m->step_host, (4 * 1024 + 4) * sizeof(uint32_t), hipHostMallocDefault) !=
             hipSuccess ||
         hipHostMalloc((void **)&m->logits_host, c.vocab * sizeof(float), hipHostMallocDefault) !=
             hipSuccess ||
@@ -976,6 +1021,22 @@ static int check_continue(lrs_model *m, uint32_t pos0) {
     return LRS_OK;
 }
 
+// the wait-error word of the combine + o launches (a matvec workgroup that
+// ran out of polls went on without its input): copied out with each call's
+// results, checked after the call's synchronisation
+static constexpr uint32_t AO_ERR_WORD = 4 * 1024;  // past the step slots of step_host
+static hipError_t ao_err_fetch(lrs_model *m, hipStream_t s) {
+    m->step_host[AO_ERR_WORD] = 0;
+    if (!m->ao_sync) return hipSuccess;
+    return hipMemcpyAsync(m->step_host + AO_ERR_WORD, m->ao_sync + 32, sizeof(uint32_t),
+                          hipMemcpyDeviceToHost, s);
+}
+static int ao_err_check(lrs_model *m) {
+    if (m->step_host[AO_ERR_WORD] == 0) return LRS_OK;
+    (void)hipMemset(m->ao_sync + 32, 0, sizeof(uint32_t));
+    return fail(LRS_E_HIP, "attention output launch: a workgroup's wait for its input ran out");
+}
+
 static int check_step(lrs_model *m, uint32_t token, uint32_t pos) {
     if (token >= m->cfg.vocab)
         return fail(LRS_E_ARG, "token " + std::to_string(token) + " outside the vocabulary");
@@ -1241,6 +1302,7 @@ static int prefill(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t po
 // {token, pos} goes through its own pinned slot, and the stream is drained
 // whenever the slots run out
 static constexpr uint32_t STEP_SLOTS = 1024;
+static_assert(4 * STEP_SLOTS <= AO_ERR_WORD, "the wait-error word follows the step slots");
 
 static int enqueue_tokens(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t pos0) {
     for (uint32_t i = 0; i < n; i++) {
@@ -1276,7 +1338,9 @@ int lrs_decode(lrs_model *m, uint32_t token, uint32_t pos, float *logits) {
     LRS_HIP(run_forward(m, false));
     LRS_HIP(hipMemcpyAsync(m->logits_host, m->logits, m->cfg.vocab * sizeof(float),
                            hipMemcpyDeviceToHost, s));
+    LRS_HIP(ao_err_fetch(m, s));
     LRS_HIP(hipStreamSynchronize(s));
+    if (int e = ao_err_check(m)) return e;
     memcpy(logits, m->logits_host, m->cfg.vocab * sizeof(float));
     m->len = pos + 1;
     return LRS_OK;
@@ -1306,7 +1370,9 @@ int lrs_decode_batch(lrs_model *m, const uint32_t *tokens, uint32_t n, uint32_t 
     hipStream_t s = m->ctx->stream;
     LRS_HIP(hipMemcpyAsync(m->logits_host, m->logits, m->cfg.vocab * sizeof(float),
                            hipMemcpyDeviceToHost, s));
+    LRS_HIP(ao_err_fetch(m, s));
     LRS_HIP(hipStreamSynchronize(s));
+    if (int e = ao_err_check(m)) return e;
     memcpy(logits, m->logits_host, m->cfg.vocab * sizeof(float));
     m->len = pos0 + n;
     return LRS_OK;
@@ -1347,7 +1413,9 @@ int lrs_decode_greedy(lrs_model *m, uint32_t token, uint32_t pos, uint32_t *next
     LRS_HIP(hipMemcpyAsync(m->step, m->step_host, 3 * sizeof(uint32_t), hipMemcpyHostToDevice, s));
     LRS_HIP(run_forward(m, true));
     LRS_HIP(hipMemcpyAsync(m->step_host + 4, m->step, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    LRS_HIP(ao_err_fetch(m, s));
     LRS_HIP(hipStreamSynchronize(s));
+    if (int e = ao_err_check(m)) return e;
     *next = m->step_host[4];
     m->len = pos + 1;
     return LRS_OK;
@@ -1382,7 +1450,9 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
     for (uint32_t i = 0; i < n_gen; i++) LRS_HIP(run_forward(m, true));
     // through the pinned buffer: the caller's memory is pageable
     LRS_HIP(hipMemcpyAsync(m->gen_host, m->gen, n_gen * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    LRS_HIP(ao_err_fetch(m, s));
     LRS_HIP(hipStreamSynchronize(s));
+    if (int e = ao_err_check(m)) return e;
     memcpy(out_tokens, m->gen_host, n_gen * sizeof(uint32_t));
     m->len = pos0 + n_prompt + n_gen - 1;
     return LRS_OK;

@@ -37,6 +37,7 @@
 // the pack of the next op's input.  The plain matvec (k_mqx) instead packs
 // its f32 input inside each workgroup and runs up to NC input columns over
 // every weight load (each column bit-identical to a one-column call).
+#include "attn_dev.h"
 #include "lrs_internal.h"
 #include "mq_args.h"
 #include "pack_dev.h"
@@ -410,21 +411,36 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
-// copies `bytes` (multiple of 16) from global memory to LDS, 16 B per lane
+// cache policy of a load that must see agent-scope stores made in the same
+// launch by another XCD (sc1: the memory model's agent-scope load)
+constexpr int CPOL_SC1 = 16;
+
+// copies `bytes` (multiple of 16) from global memory to LDS, 16 B per lane,
+// with cache policy CP
+template <int CP = 0>
 __device__ __forceinline__ void copy_to_lds(const uint8_t *__restrict__ g, uint8_t *lds,
                                             uint32_t bytes) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     for (uint32_t base = wave * 1024; base < bytes; base += nw * 1024) {
         const uint32_t off = base + lane * 16;
-        if (off < bytes) __builtin_amdgcn_global_load_lds(g + off, (lds_void *)(lds + base), 16, 0, 0);
+        if (off < bytes) __builtin_amdgcn_global_load_lds(g + off, (lds_void *)(lds + base), 16, 0, CP);
     }
 }
+
+// polls of a matvec workgroup waiting for its input pack (k_mq_ao) before it
+// gives up: each is a memory round trip plus a short sleep (~0.5-2 us), so
+// 40-130 ms in all, against the few microseconds the producers take
+constexpr uint32_t MQ_WAIT_POLLS = 1u << 16;
 
 // body for the segments [s_lo, s_hi) of type T (one workgroup).  NC > 1 or
 // XF (MQ_STORE only): NC input columns share each weight load, their packs
 // side by side in LDS; with XF the workgroup packs the f32 columns a.xf
-// itself instead of copying a pack made by a previous launch.
-template <uint32_t T, int TPW, int TG, int KS, int P, int EPI, int NC = 1, bool XF = false>
+// itself instead of copying a pack made by a previous launch.  WT: the pack
+// is written by producers in the same launch; the workgroup issues its
+// weight loads and the epilogue's operand loads, then waits for its flag
+// (a.wflag) and stages the pack with agent-scope loads.
+template <uint32_t T, int TPW, int TG, int KS, int P, int EPI, int NC = 1, bool XF = false,
+          bool WT = false>
 __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *lds, float *red) {
     static_assert(NC == 1 || EPI == MQ_STORE, "several columns: store epilogue only");
     constexpr int W = TG * KS;
@@ -542,7 +558,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
                 }
             }
         }
-    } else {
+    } else if constexpr (!WT) {
         const uint32_t bb0 = XSN > 1 ? ub * BPU : 0u;
         copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.dig) + (size_t)bb0 * 96, lds, nxl * 96);
         copy_to_lds(reinterpret_cast<const uint8_t *>(a.xin.meta + 4 * (size_t)bb0), lds + lp.meta,
@@ -585,6 +601,26 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     if (a.gss && threadIdx.x < nxl) {
         const uint32_t g = (threadIdx.x + gb0) / a.gblk;
         for (uint32_t r = 0; r < a.gblk; r++) gs0 += a.gss[g * a.gblk + r];
+    }
+    if constexpr (WT) {
+        // every load above is in flight; thread 0 waits for this workgroup's
+        // flag (bounded), clears it for the next launch, then the workgroup
+        // stages the pack with loads that see the producers' stores
+        if (threadIdx.x == 0) {
+            uint32_t *f = a.wflag + 32 * (size_t)wrel;
+            uint32_t n = 0;
+            while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+                if (++n >= MQ_WAIT_POLLS) {
+                    __hip_atomic_store(a.werr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(4);
+            }
+            __hip_atomic_store(f, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        copy_to_lds<CPOL_SC1>(reinterpret_cast<const uint8_t *>(a.xin.dig), lds, nxl * 96);
+        copy_to_lds<CPOL_SC1>(reinterpret_cast<const uint8_t *>(a.xin.meta), lds + lp.meta, nxl * 16);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -856,6 +892,45 @@ __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq(MqArg
         mq_body<T1, TPW, TG, KS, P, EPI>(a, si, lds, red);
 }
 
+// The attention combine and the o-projection in one launch.  Workgroups
+// [0, c.n_prod) merge one query head's split partials each into the o input
+// pack (attn_combine_head, agent-scope stores), wait for those stores to
+// complete and count themselves in c.cnt; the last to count sets the count
+// back to 0 and raises one flag per o workgroup.  The o workgroups (from
+// c.n_prod on: seg[0].wg0) prefetch all their weight units (P covers a
+// wavefront's share of K), so the weight stream runs while the producers
+// do; then they wait for their flag and stage the pack (mq_body, WT).
+// Workgroups are dispatched in id order, so no producer waits behind a
+// consumer; a consumer's wait is bounded all the same (a.werr).
+template <uint32_t T, int TPW, int TG, int KS, int P>
+__global__ __launch_bounds__(64 * TG * KS)
+__attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq_ao(MqArgs a, AoArgs c) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float red[TG * KS * TPW * 16 + TG * KS + 1];
+    __shared__ float wsh[64];
+    if (blockIdx.x < c.n_prod) {
+        attn_combine_head<true>(c.part, c.splits, c.head_dim, a.step, c.gate, c.gstride, a.xin,
+                                blockIdx.x, reinterpret_cast<float *>(lds), wsh, red);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's pack stores are complete
+        __syncthreads();
+        uint32_t *last = reinterpret_cast<uint32_t *>(red + 1);
+        if (threadIdx.x == 0) {
+            const uint32_t before =
+                __hip_atomic_fetch_add(c.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t l = before == c.n_prod - 1;
+            if (l) __hip_atomic_store(c.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *last = l;
+        }
+        __syncthreads();
+        if (*last)
+            for (uint32_t t = threadIdx.x; t < c.n_cons; t += blockDim.x)
+                __hip_atomic_store(a.wflag + 32 * (size_t)t, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    mq_body<T, TPW, TG, KS, P, MQ_RESID, 1, false, true>(a, 0, lds, red);
+}
+
 // plain matvec of NC f32 input columns (a.xf), packed by each workgroup
 template <uint32_t T, int TPW, int TG, int KS, int P, int NC>
 __global__ __launch_bounds__(64 * TG * KS)
@@ -971,6 +1046,72 @@ hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int e
         *keys_per_wg = (outs + 63) / 64;
     }
     hipLaunchKernelGGL(fn, dim3(wgs), dim3(64 * g.tg * g.ks), lds, s, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// attention combine + o-projection (k_mq_ao): shape (1, 2, 4, P), one 32-row
+// block per matvec workgroup, P = a wavefront's share of the units (at least
+// 2; at most 6 for Q4_K, 4 for Q5_K and 3 for Q6_K, whose units hold more
+// registers: the largest P that compiles without spilling)
+// ---------------------------------------------------------------------------
+using MqAoFn = void (*)(MqArgs, AoArgs);
+constexpr int AO_TG = 2, AO_KS = 4;
+
+static int ao_units_per_wave(uint32_t t, uint32_t n_in) {
+    const uint32_t w = (tunits(t, n_in) + AO_KS - 1) / AO_KS;
+    return w < 2 ? 2 : (int)w;
+}
+
+template <uint32_t T>
+static MqAoFn pick_ao_p(int p) {
+    switch (p) {
+    case 2: return k_mq_ao<T, 1, AO_TG, AO_KS, 2>;
+    case 3: return k_mq_ao<T, 1, AO_TG, AO_KS, 3>;
+    case 4: if constexpr (T != T_Q6_K) return k_mq_ao<T, 1, AO_TG, AO_KS, 4>; else return nullptr;
+    case 5: if constexpr (T == T_Q4_K) return k_mq_ao<T, 1, AO_TG, AO_KS, 5>; else return nullptr;
+    case 6: if constexpr (T == T_Q4_K) return k_mq_ao<T, 1, AO_TG, AO_KS, 6>; else return nullptr;
+    default: return nullptr;
+    }
+}
+
+static MqAoFn pick_ao(uint32_t t, uint32_t n_in) {
+    const int p = ao_units_per_wave(t, n_in);
+    switch (t) {
+    case T_Q4_K: return pick_ao_p<T_Q4_K>(p);
+    case T_Q5_K: return pick_ao_p<T_Q5_K>(p);
+    case T_Q6_K: return pick_ao_p<T_Q6_K>(p);
+    default: return nullptr;
+    }
+}
+
+static size_t ao_lds(uint32_t nxb, uint32_t head_dim, uint32_t splits) {
+    const size_t mq = (size_t)nxb * 96 + 16 + (size_t)nxb * 16;
+    const size_t cb = (size_t)splits * (head_dim + 4) * sizeof(float);
+    return mq > cb ? mq : cb;
+}
+
+bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits) {
+    return pick_ao(t, n_in) != nullptr && rows % 32 == 0 && rows > 0 &&
+           (head_dim == 64 || head_dim == 128 || head_dim == 256) && splits >= 1 && splits <= 64 &&
+           ao_lds(pack_blocks(t, n_in), head_dim, splits) <= 160 * 1024;
+}
+
+hipError_t launch_mq_ao(const MqArgs &in, const AoArgs &cin, uint32_t t, hipStream_t s) {
+    MqArgs a = in;
+    AoArgs c = cin;
+    if (a.n_seg != 1 || a.seg[0].w2 || !a.wflag || !a.werr || !c.cnt || !c.part || a.xin.q8 ||
+        c.n_prod == 0 || a.nxb != pack_blocks(t, a.n_in))
+        return hipErrorInvalidValue;
+    if (!mq_ao_supported(t, a.n_in, a.seg[0].rows, c.head_dim, c.splits)) return hipErrorNotSupported;
+    MqAoFn fn = pick_ao(t, a.n_in);
+    a.n_seg0 = 1;
+    a.xsplit = 1;
+    a.xfull = 0;
+    a.seg[0].wg0 = c.n_prod;
+    c.n_cons = a.seg[0].rows / 32;  // one 32-row block (two tiles) per workgroup
+    hipLaunchKernelGGL(fn, dim3(c.n_prod + c.n_cons), dim3(64 * AO_TG * AO_KS),
+                       ao_lds(a.nxb, c.head_dim, c.splits), s, a, c);
     return hipGetLastError();
 }
 

@@ -98,6 +98,22 @@ struct MqArgs {
     uint32_t xsplit, xfull;
     float *xpart;
     uint32_t *xcnt;
+    // input pack written in the same launch (k_mq_ao): workgroup w of the
+    // matvec waits until wflag[32 w] is non-zero (set by the producers, one
+    // flag per 128-byte line), clears it, then stages xin; a wait that runs
+    // out of polls sets werr to 1 and goes on
+    uint32_t *wflag, *werr;
+};
+
+// the attention combine ahead of the o-projection in one launch (k_mq_ao):
+// workgroups [0, n_prod) merge query head blockIdx.x's split partials into
+// the o input pack; the last of them to count itself in cnt (which it sets
+// back to 0) raises the matvec workgroups' flags
+struct AoArgs {
+    const float *part;   // [n_head][splits][head_dim + 4]
+    const float *gate;   // gated attention: sigmoid gate at gate[h * gstride + d], or null
+    uint32_t splits, head_dim, gstride, n_prod, n_cons;
+    uint32_t *cnt;
 };
 
 // launch shape: TPW tiles per wavefront sharing the activation, TG tile

@@ -12,6 +12,27 @@ __device__ __forceinline__ float pk_dpp(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
 }
 
+// pack stores: plain, or (AG) agent-scope stores, written through to memory,
+// for a reader in the same launch on another XCD
+template <bool AG>
+__device__ __forceinline__ void st_dig(int8_t *p, int v) {
+    if constexpr (AG)
+        __hip_atomic_store(p, (int8_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = (int8_t)v;
+}
+template <bool AG>
+__device__ __forceinline__ void st_meta(float *p, float a, float b, float c, float d) {
+    if constexpr (AG) {
+        __hip_atomic_store(p, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 2, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 3, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *reinterpret_cast<float4 *>(p) = make_float4(a, b, c, d);
+    }
+}
+
 // Packs one 32-element block held one element per lane by the 32 lanes of a
 // half wavefront (lane i of the half = element i).  Writes the 3 digit bytes
 // of the element and, from lane 0 of the half, the block's meta.  The max and
@@ -20,6 +41,8 @@ __device__ __forceinline__ float pk_dpp(float x) {
 // between the two rows of the half.
 // With store false the half wavefront computes the block but writes nothing
 // (a half past the end of the pack, kept in step with the rest of the wave).
+// AG: agent-scope stores (st_dig / st_meta).
+template <bool AG = false>
 __device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p, bool store = true) {
     const uint32_t i = threadIdx.x & 31;
     float amax = fabsf(v);
@@ -36,12 +59,10 @@ __device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p, bool s
         const float r = fminf(fmaxf(__builtin_rintf(v * di), -128.f), 127.f);
         if (!store) return;
         int8_t *dg = p.dig + (size_t)blk * 96 + i;
-        dg[0] = 0;
-        dg[32] = 0;
-        dg[64] = (int8_t)(int)r;
-        if (i == 0)
-            *reinterpret_cast<float4 *>(p.meta + 4 * (size_t)blk) =
-                make_float4((float)(_Float16)d, 0.f, 0.f, 0.f);
+        st_dig<AG>(dg, 0);
+        st_dig<AG>(dg + 32, 0);
+        st_dig<AG>(dg + 64, (int)r);
+        if (i == 0) st_meta<AG>(p.meta + 4 * (size_t)blk, (float)(_Float16)d, 0.f, 0.f, 0.f);
         return;
     }
     float r16 = v;  // sum of this lane's 16-element run
@@ -60,14 +81,11 @@ __device__ __forceinline__ void pack_half(float v, uint32_t blk, XPack p, bool s
     const int d0 = (X1 - d1) >> 8;
     if (!store) return;
     int8_t *dg = p.dig + (size_t)blk * 96 + i;
-    dg[0] = (int8_t)d0;
-    dg[32] = (int8_t)d1;
-    dg[64] = (int8_t)d2;
-    if (i == 0) {
-        // r16 = sum of elements 0..15, other = sum of 16..31
-        *reinterpret_cast<float4 *>(p.meta + 4 * (size_t)blk) =
-            make_float4(ldexpf(1.0f, e - 21), r16 + other, r16, other);
-    }
+    st_dig<AG>(dg, d0);
+    st_dig<AG>(dg + 32, d1);
+    st_dig<AG>(dg + 64, d2);
+    // r16 = sum of elements 0..15, other = sum of 16..31
+    if (i == 0) st_meta<AG>(p.meta + 4 * (size_t)blk, ldexpf(1.0f, e - 21), r16 + other, r16, other);
 }
 
 // Sum over the 32 lanes of a half wavefront, in every lane of the half (the

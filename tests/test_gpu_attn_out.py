@@ -1,0 +1,108 @@
+"""The attention combine in the o-projection's launch (k_mq_ao, the decode
+default) against the two-launch form (the combine kernel, then the o matvec:
+LRS_AO=0 at model creation) on the same weights.  Both run the same
+arithmetic in the same order (the combine's merge, the pack, the matvec's
+units and K-slice sums), so the logits must be bit-identical: token by
+token, over greedy chains, and at cache lengths where the position splits
+of the attention first own one, two and three blocks.  The cases cover every
+o weight type the launch has (Q4_K / Q5_K / Q6_K), head dims 64 / 128 / 256,
+the gated attention of the hybrid model, and the benchmark widths (40 query
+heads over 5120 inputs; 24 x 256 over 6144), so each P instance of the
+launch that a benchmark runs is here.  Their parity with the CPU oracle is
+the rest of the GPU suite, which runs this launch by default."""
+import numpy as np
+import pytest
+
+import modelgen
+
+pytestmark = pytest.mark.gpu
+
+# the config-3 attention and o shapes with a small FFN and vocabulary
+C3W = dict(n_layer=2, n_embd=5120, n_head=40, n_head_kv=8, head_dim=128, n_ff=1024,
+           vocab=1024, rope_dim=128, ctx=1400, rms_eps=1e-6, freq_base=1e6)
+# the config-4 gated attention (24 / 4 heads x 256 over 5120) after one
+# delta-net layer, small FFN and vocabulary
+C4W = dict(n_layer=2, n_embd=5120, n_head=24, n_head_kv=4, head_dim=256, n_ff=1024,
+           vocab=1024, rope_dim=64, ctx=64, rms_eps=1e-6, freq_base=1e7,
+           full_attn_interval=2, dn_k_heads=16, dn_v_heads=16, dn_state=128, dn_conv=4)
+
+DENSE = [
+    ("tiny-q4km", modelgen.TINY, modelgen.Q4_K_M),
+    ("tiny-q5km", modelgen.TINY, modelgen.Q5_K_M),
+    ("gqa5-o-q6k", modelgen.GQA5, dict(modelgen.Q4_K_M, attn_output=modelgen.Q6_K)),
+    ("c3-width", C3W, modelgen.Q4_K_M),
+]
+
+
+@pytest.fixture(scope="module")
+def ctx(lrs):
+    c = lrs.Context(0)
+    yield c
+    c.close()
+
+
+def _pair(monkeypatch, make):
+    """(fused, two-launch) models built by make() with and without LRS_AO=0."""
+    monkeypatch.delenv("LRS_AO", raising=False)
+    fused = make()
+    monkeypatch.setenv("LRS_AO", "0")
+    try:
+        split = make()
+    finally:
+        monkeypatch.delenv("LRS_AO")
+    return fused, split
+
+
+@pytest.mark.parametrize("name,cfg,mix", DENSE, ids=[c[0] for c in DENSE])
+def test_combine_in_o_launch_is_bit_identical(lrs, orc, ctx, monkeypatch, name, cfg, mix):
+    w = modelgen.host_model(orc, cfg, seed=23, mix=mix, mode=0, d_lo=1e-3, d_hi=1e-2)
+    fused, split = _pair(monkeypatch, lambda: modelgen.gpu_model(lrs, ctx, cfg, w))
+    try:
+        rng = np.random.default_rng(29)
+        prompt = rng.integers(0, cfg["vocab"], 10).tolist()
+        for pos, t in enumerate(prompt):
+            a, b = fused.decode(t, pos), split.decode(t, pos)
+            assert np.array_equal(a, b), (name, pos, float(np.max(np.abs(a - b))))
+        fused.reset()
+        split.reset()
+        assert fused.generate_greedy(prompt, 16).tolist() == split.generate_greedy(prompt, 16).tolist()
+    finally:
+        fused.close()
+        split.close()
+
+
+def test_combine_in_o_launch_at_split_boundaries(lrs, orc, ctx, monkeypatch):
+    """C3W (8 KV heads: 32 splits, blocks 512 positions apart): every decode
+    step up to the cache length where the splits first own a third block,
+    so the combine weighs 1..32 live splits, then splits of two and three
+    blocks."""
+    cfg = C3W
+    w = modelgen.host_model(orc, cfg, seed=37, mode=0, d_lo=1e-3, d_hi=1e-2)
+    fused, split = _pair(monkeypatch, lambda: modelgen.gpu_model(lrs, ctx, cfg, w))
+    try:
+        last = modelgen.split_block_checks(cfg["n_head_kv"])[-1]  # a cache length
+        assert last <= cfg["ctx"]
+        toks = np.random.default_rng(41).integers(0, cfg["vocab"], last).tolist()
+        for pos in range(last):
+            a, b = fused.decode(toks[pos], pos), split.decode(toks[pos], pos)
+            assert np.array_equal(a, b), (pos, float(np.max(np.abs(a - b))))
+    finally:
+        fused.close()
+        split.close()
+
+
+@pytest.mark.parametrize("name,cfg", [("hy-mid", modelgen.HY_MID), ("c4-width", C4W)])
+def test_gated_combine_in_o_launch_is_bit_identical(lrs, orc, ctx, monkeypatch, name, cfg):
+    w = modelgen.hybrid_host_model(orc, cfg, seed=43, mode=0, d_lo=1e-3, d_hi=1e-2)
+    fused, split = _pair(monkeypatch, lambda: modelgen.gpu_hybrid_model(lrs, ctx, cfg, w))
+    try:
+        prompt = np.random.default_rng(47).integers(0, cfg["vocab"], 10).tolist()
+        for pos, t in enumerate(prompt):
+            a, b = fused.decode(t, pos), split.decode(t, pos)
+            assert np.array_equal(a, b), (name, pos, float(np.max(np.abs(a - b))))
+        fused.reset()
+        split.reset()
+        assert fused.generate_greedy(prompt, 16).tolist() == split.generate_greedy(prompt, 16).tolist()
+    finally:
+        fused.close()
+        split.close()
