@@ -87,7 +87,8 @@ hipError_t launch_mq(const MqArgs &a, uint32_t t0, uint32_t t1, MqGeom g, int ep
                      uint32_t *wgs_out = nullptr, uint32_t *keys_per_wg = nullptr);
 bool mq_geom_supported(const MqGeom &g);
 // the attention combine and the o-projection (RESID) in one launch
-bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits);
+bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits,
+                     uint32_t n_head);
 hipError_t launch_mq_ao(const MqArgs &a, const AoArgs &c, uint32_t t, hipStream_t s);
 MqGeom store_geom(uint32_t t, uint32_t n_in, uint32_t n_out);
 // plain-matvec launch shape override (tiles per wave, tile groups, K-slices; all 0 = automatic)

@@ -102,8 +102,9 @@ struct lrs_model {
     uint32_t *xcnt = nullptr;
     uint32_t a_splits;
     // attention combine in the o launch (k_mq_ao; LRS_AO=0 turns it off):
-    // producer count at [0], the consumers' wait-error word at [32], then
-    // one flag per o workgroup 32 words apart; all zero between launches
+    // the consumers' wait-error word at [32], then the flag matrix from [64]
+    // (a row of 64 words per o workgroup, one word per producer); all zero
+    // between launches
     bool ao_on = true;
     uint32_t *ao_sync = nullptr;
     // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
@@ -344,7 +345,7 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
 bool ao_fused(const lrs_model *m, const DevLayer &L) {
     const lrs_config &c = m->cfg;
     return m->ao_on && m->ao_sync && !L.dn && L.o && !L.o_q8 &&
-           mq_ao_supported(L.o->v.type, L.o->v.n_in, c.n_embd, c.head_dim, m->a_splits);
+           mq_ao_supported(L.o->v.type, L.o->v.n_in, c.n_embd, c.head_dim, m->a_splits, c.n_head);
 }
 
 // attention over the f16 cache; hybrid layers gate the output with
@@ -395,7 +396,6 @@ hipError_t op_o(lrs_model *m, uint32_t l) {
         ao.head_dim = c.head_dim;
         ao.gstride = 2 * c.head_dim;
         ao.n_prod = c.n_head;
-        ao.cnt = m->ao_sync;
         a.werr = m->ao_sync + 32;
         a.wflag = m->ao_sync + 64;
         a.step = m->step;
@@ -742,8 +742,8 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
             return rc;
         if (hipMemset(m->xcnt, 0, nb * sizeof(uint32_t)) != hipSuccess)
             return fail(LRS_E_HIP, "memset");
-        // count, error word and one flag per 32 rows of o's output
-        const size_t aw = 64 + 32 * (size_t)(c.n_embd / 32);
+        // error word and a row of flags per 32 rows of o's output
+        const size_t aw = 64 + 64 * (size_t)(c.n_embd / 32);
         if ((rc = dev_alloc(m, aw * sizeof(uint32_t), (void **)&m->ao_sync))) return rc;
         if (hipMemset(m->ao_sync, 0, aw * sizeof(uint32_t)) != hipSuccess)
             return fail(LRS_E_HIP, "memset");

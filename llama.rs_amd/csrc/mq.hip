@@ -603,20 +603,27 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         for (uint32_t r = 0; r < a.gblk; r++) gs0 += a.gss[g * a.gblk + r];
     }
     if constexpr (WT) {
-        // every load above is in flight; thread 0 waits for this workgroup's
-        // flag (bounded), clears it for the next launch, then the workgroup
-        // stages the pack with loads that see the producers' stores
-        if (threadIdx.x == 0) {
-            uint32_t *f = a.wflag + 32 * (size_t)wrel;
+        // every load above is in flight; wavefront 0 waits for this
+        // workgroup's n_wait producer flags (lane i polls flag i, one load
+        // per poll for the wavefront; bounded), clears them for the next
+        // launch, then the workgroup stages the pack with loads that see the
+        // producers' stores
+        if (wave == 0) {
+            uint32_t *f = a.wflag + 64 * (size_t)wrel + lane;
+            const bool mine = lane < a.n_wait;
             uint32_t n = 0;
-            while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+            for (;;) {
+                const uint32_t v =
+                    mine ? __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1u;
+                if (__all(v != 0u)) break;
                 if (++n >= MQ_WAIT_POLLS) {
-                    __hip_atomic_store(a.werr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (lane == 0)
+                        __hip_atomic_store(a.werr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }
-                __builtin_amdgcn_s_sleep(4);
+                __builtin_amdgcn_s_sleep(2);
             }
-            __hip_atomic_store(f, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (mine) __hip_atomic_store(f, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
         copy_to_lds<CPOL_SC1>(reinterpret_cast<const uint8_t *>(a.xin.dig), lds, nxl * 96);
@@ -895,13 +902,13 @@ __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq(MqArg
 // The attention combine and the o-projection in one launch.  Workgroups
 // [0, c.n_prod) merge one query head's split partials each into the o input
 // pack (attn_combine_head, agent-scope stores), wait for those stores to
-// complete and count themselves in c.cnt; the last to count sets the count
-// back to 0 and raises one flag per o workgroup.  The o workgroups (from
-// c.n_prod on: seg[0].wg0) prefetch all their weight units (P covers a
-// wavefront's share of K), so the weight stream runs while the producers
-// do; then they wait for their flag and stage the pack (mq_body, WT).
-// Workgroups are dispatched in id order, so no producer waits behind a
-// consumer; a consumer's wait is bounded all the same (a.werr).
+// complete, then raise their flag in every o workgroup's row of the flag
+// matrix (a.wflag).  The o workgroups (from c.n_prod on: seg[0].wg0)
+// prefetch all their weight units (P covers a wavefront's share of K), so
+// the weight stream runs while the producers do; then they wait for their
+// row of flags and stage the pack (mq_body, WT).  Workgroups are dispatched
+// in id order, so no producer waits behind a consumer; a consumer's wait is
+// bounded all the same (a.werr).
 template <uint32_t T, int TPW, int TG, int KS, int P>
 __global__ __launch_bounds__(64 * TG * KS)
 __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq_ao(MqArgs a, AoArgs c) {
@@ -913,19 +920,9 @@ __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq_ao(Mq
                                 blockIdx.x, reinterpret_cast<float *>(lds), wsh, red);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's pack stores are complete
         __syncthreads();
-        uint32_t *last = reinterpret_cast<uint32_t *>(red + 1);
-        if (threadIdx.x == 0) {
-            const uint32_t before =
-                __hip_atomic_fetch_add(c.cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint32_t l = before == c.n_prod - 1;
-            if (l) __hip_atomic_store(c.cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *last = l;
-        }
-        __syncthreads();
-        if (*last)
-            for (uint32_t t = threadIdx.x; t < c.n_cons; t += blockDim.x)
-                __hip_atomic_store(a.wflag + 32 * (size_t)t, 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        for (uint32_t t = threadIdx.x; t < c.n_cons; t += blockDim.x)
+            __hip_atomic_store(a.wflag + 64 * (size_t)t + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     mq_body<T, TPW, TG, KS, P, MQ_RESID, 1, false, true>(a, 0, lds, red);
@@ -1091,8 +1088,9 @@ static size_t ao_lds(uint32_t nxb, uint32_t head_dim, uint32_t splits) {
     return mq > cb ? mq : cb;
 }
 
-bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits) {
-    return pick_ao(t, n_in) != nullptr && rows % 32 == 0 && rows > 0 &&
+bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits,
+                     uint32_t n_head) {
+    return pick_ao(t, n_in) != nullptr && rows % 32 == 0 && rows > 0 && n_head >= 1 && n_head <= 64 &&
            (head_dim == 64 || head_dim == 128 || head_dim == 256) && splits >= 1 && splits <= 64 &&
            ao_lds(pack_blocks(t, n_in), head_dim, splits) <= 160 * 1024;
 }
@@ -1100,16 +1098,18 @@ bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim
 hipError_t launch_mq_ao(const MqArgs &in, const AoArgs &cin, uint32_t t, hipStream_t s) {
     MqArgs a = in;
     AoArgs c = cin;
-    if (a.n_seg != 1 || a.seg[0].w2 || !a.wflag || !a.werr || !c.cnt || !c.part || a.xin.q8 ||
+    if (a.n_seg != 1 || a.seg[0].w2 || !a.wflag || !a.werr || !c.part || a.xin.q8 ||
         c.n_prod == 0 || a.nxb != pack_blocks(t, a.n_in))
         return hipErrorInvalidValue;
-    if (!mq_ao_supported(t, a.n_in, a.seg[0].rows, c.head_dim, c.splits)) return hipErrorNotSupported;
+    if (!mq_ao_supported(t, a.n_in, a.seg[0].rows, c.head_dim, c.splits, c.n_prod))
+        return hipErrorNotSupported;
     MqAoFn fn = pick_ao(t, a.n_in);
     a.n_seg0 = 1;
     a.xsplit = 1;
     a.xfull = 0;
     a.seg[0].wg0 = c.n_prod;
     c.n_cons = a.seg[0].rows / 32;  // one 32-row block (two tiles) per workgroup
+    a.n_wait = c.n_prod;
     hipLaunchKernelGGL(fn, dim3(c.n_prod + c.n_cons), dim3(64 * AO_TG * AO_KS),
                        ao_lds(a.nxb, c.head_dim, c.splits), s, a, c);
     return hipGetLastError();

@@ -99,21 +99,21 @@ struct MqArgs {
     float *xpart;
     uint32_t *xcnt;
     // input pack written in the same launch (k_mq_ao): workgroup w of the
-    // matvec waits until wflag[32 w] is non-zero (set by the producers, one
-    // flag per 128-byte line), clears it, then stages xin; a wait that runs
-    // out of polls sets werr to 1 and goes on
+    // matvec waits until the n_wait flags wflag[64 w + i] (producer i sets
+    // flag i) are all non-zero, clears them, then stages xin; a wait that
+    // runs out of polls sets werr to 1 and goes on
     uint32_t *wflag, *werr;
+    uint32_t n_wait;
 };
 
 // the attention combine ahead of the o-projection in one launch (k_mq_ao):
 // workgroups [0, n_prod) merge query head blockIdx.x's split partials into
-// the o input pack; the last of them to count itself in cnt (which it sets
-// back to 0) raises the matvec workgroups' flags
+// the o input pack, then each raises its flag in every matvec workgroup's
+// row of the flag matrix (MqArgs::wflag)
 struct AoArgs {
     const float *part;   // [n_head][splits][head_dim + 4]
     const float *gate;   // gated attention: sigmoid gate at gate[h * gstride + d], or null
     uint32_t splits, head_dim, gstride, n_prod, n_cons;
-    uint32_t *cnt;
 };
 
 // launch shape: TPW tiles per wavefront sharing the activation, TG tile
