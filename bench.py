@@ -458,16 +458,31 @@ CFG14_SET = [(Q4_K, 5120, 5120), (Q4_K, 5120, 1024), (Q6_K, 5120, 1024), (Q4_K, 
              (Q4_K, 5120, 13824), (Q4_K, 5120, 13824), (Q6_K, 13824, 5120)]
 
 
+def layer14_model(ctx):
+    """The config-2 model with the o-projection as a plain matvec launch: the
+    decode runs the attention combine in the o launch (LRS_AO), which is not
+    part of the layer's matvec set."""
+    from llama_rs_amd.model import synthetic_model
+
+    old = os.environ.get("LRS_AO")
+    os.environ["LRS_AO"] = "0"
+    try:
+        return synthetic_model(ctx, CFG14, seed=2, mode=0, d_lo=1e-3, d_hi=1e-2)
+    finally:
+        if old is None:
+            del os.environ["LRS_AO"]
+        else:
+            os.environ["LRS_AO"] = old
+
+
 def bench_layer(lrs, ctx, steps, warmup):
     """Config 2 through the token plan's fused launches: a 4-layer model of the
     14B shape (4 x 174 MB of weights, beyond the 256 MB MALL); a step is one
     layer's q/k/v, o, gate/up and down launches (lrs_model_profile
     LRS_OP_MATVECS, rotating over the layers).  Also timed, as a labelled
     second figure: the 7 matvecs as separate lrs_matvec_dev calls."""
-    from llama_rs_amd.model import synthetic_model
-
     cfg = CFG14
-    m = synthetic_model(ctx, cfg, seed=2, mode=0, d_lo=1e-3, d_hi=1e-2)
+    m = layer14_model(ctx)
     m.decode_batch(np.arange(8, dtype=np.uint32), 0)  # a valid cache position
     nl = cfg["n_layer"]
     m.profile("matvecs", max(nl, warmup))
@@ -699,7 +714,7 @@ def run_pmc(lrs, ctx):
     for w in ws:
         w.free()
     marker("layer14")
-    lm = synthetic_model(ctx, CFG14, seed=2, mode=0, d_lo=1e-3, d_hi=1e-2)
+    lm = layer14_model(ctx)
     lm.decode_batch(np.arange(8, dtype=np.uint32), 0)
     for op in ("qkv", "o", "gateup", "down"):
         us, b = lm.profile(op, 8)
