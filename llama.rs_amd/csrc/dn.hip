@@ -26,6 +26,7 @@
 // The conv inputs live in a ring of W slots indexed by position, so the slot
 // being written (pos % W) is never one being read: workgroups that share a
 // key head need no ordering.
+#include "dn_dev.h"
 #include "lrs_internal.h"
 #include "pack_dev.h"
 
@@ -43,11 +44,7 @@ __device__ __forceinline__ float sum8(float v) {
     v += dn_dpp<0x141>(v);  // row_half_mirror
     return v;
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return dn_wave_sum(v); }
 
 template <int D>
 __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
@@ -121,40 +118,16 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
     const uint32_t pos = a.step[1];
     const uint32_t wslot = pos % W;
     // gate projections of hn = rmsnorm(x) * attn_norm (dn_gates.comp): every
-    // load of a thread's elements is issued before the first product
-    {
-        constexpr int GI = 8;  // float4 per thread per row: n_embd <= 8192
-        const float *al = a.alpha + (size_t)hh * a.n_embd, *be = a.beta + (size_t)hh * a.n_embd;
-        float4 xv[GI], wv[GI], av[GI], bv[GI];
-#pragma unroll
-        for (int g = 0; g < GI; g++) {
-            const uint32_t i = 4 * tid + 1024 * g;
-            if (i < a.n_embd) {
-                xv[g] = *reinterpret_cast<const float4 *>(a.x + i);
-                wv[g] = *reinterpret_cast<const float4 *>(a.attn_norm + i);
-                av[g] = *reinterpret_cast<const float4 *>(al + i);
-                bv[g] = *reinterpret_cast<const float4 *>(be + i);
-            }
-        }
-        float ss = 0.f, pa = 0.f, pb = 0.f;
-#pragma unroll
-        for (int g = 0; g < GI; g++) {
-            if (4 * tid + 1024 * g < a.n_embd) {
-                const float4 xq = xv[g], wq = wv[g], aq = av[g], bq = bv[g];
-                ss += (xq.x * xq.x + xq.y * xq.y) + (xq.z * xq.z + xq.w * xq.w);
-                const float h0 = xq.x * wq.x, h1 = xq.y * wq.y, h2 = xq.z * wq.z, h3 = xq.w * wq.w;
-                pa += (aq.x * h0 + aq.y * h1) + (aq.z * h2 + aq.w * h3);
-                pb += (bq.x * h0 + bq.y * h1) + (bq.z * h2 + bq.w * h3);
-            }
-        }
-        ss = wave_sum(ss);
-        pa = wave_sum(pa);
-        pb = wave_sum(pb);
-        if (lane == 0) {
-            red[0][wave] = ss;
-            red[1][wave] = pa;
-            red[2][wave] = pb;
-        }
+    // load of a thread's elements is issued before the first product; with
+    // a.gates the projection launch computed them (its spare workgroups)
+    float2 gpre = make_float2(0.f, 0.f);
+    if (a.gates) {
+        if (tid == 0) gpre = a.gates[hh];
+    } else {
+        DnGateRegs g;
+        dn_gate_load(g, a.x, a.attn_norm, a.alpha + (size_t)hh * a.n_embd,
+                     a.beta + (size_t)hh * a.n_embd, a.n_embd, tid);
+        dn_gate_reduce(g, a.n_embd, tid, red);
     }
 
     // conv + SiLU
@@ -191,14 +164,9 @@ __global__ __launch_bounds__(256) void k_dn_step(DnArgs a) {
     __syncthreads();
 
     if (tid == 0) {
-        const float ss = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
-        const float pa = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-        const float pb = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
-        const float s = 1.0f / sqrtf(ss / (float)a.n_embd + a.eps);
-        const float zz = pa * s + a.dt[hh];
-        const float sp = zz > 20.0f ? zz : log1pf(expf(zz));  // delta_net.rs:13-20
-        gb[0] = expf(a.a[hh] * sp);                          // decay e^g
-        gb[1] = 1.0f / (1.0f + expf(-(pb * s)));             // beta
+        const float2 d = a.gates ? gpre : dn_gate_final(red, a.a[hh], a.dt[hh], a.n_embd, a.eps);
+        gb[0] = d.x;  // decay e^g
+        gb[1] = d.y;  // beta
     }
     // L2 norms of q and k (dn_l2_qk.comp); 1/sqrt(D) of the read-out folded into q
     {

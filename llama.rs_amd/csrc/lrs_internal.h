@@ -83,8 +83,14 @@ hipError_t launch_dequant_rows(WeightView w, const uint32_t *rows_dev, uint32_t 
 hipError_t launch_xpack(const float *x, const float *nw, uint32_t n, uint32_t nxb, XPack p,
                         hipStream_t s,
                         float *xsq = nullptr);
+// gates (MQ_STORE, two Q4_K segments, shape (1, 2, 4, 2) only): one more
+// workgroup per value head computes the delta net's gate projections into
+// gates->out (the step then reads them; dn_dev.h)
+struct DnGateArgs;
 hipError_t launch_mq(const MqArgs &a, uint32_t t0, uint32_t t1, MqGeom g, int epi, hipStream_t s,
-                     uint32_t *wgs_out = nullptr, uint32_t *keys_per_wg = nullptr);
+                     uint32_t *wgs_out = nullptr, uint32_t *keys_per_wg = nullptr,
+                     const DnGateArgs *gates = nullptr);
+bool mq_gates_supported(uint32_t t0, uint32_t t1, const MqGeom &g);
 bool mq_geom_supported(const MqGeom &g);
 // the attention combine and the o-projection (RESID) in one launch
 bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits,
@@ -183,6 +189,10 @@ struct DnArgs {
     const uint32_t *step;       // {token, pos}
     uint32_t n_embd, k_heads, v_heads, d_conv;
     float eps;
+    // {e^g, beta} per value head computed by the projection launch
+    // (launch_mq_gates), or null: the step computes them from x, attn_norm,
+    // alpha, beta, a and dt
+    const float2 *gates;
 };
 hipError_t launch_dn_step(const DnArgs &a, uint32_t d_state, hipStream_t s);
 // delta-net layer of a prompt block of nb tokens at pos0 (after the qkv / z GEMMs)

@@ -26,6 +26,7 @@
 // The step's token and position live in device memory, so the same graph is
 // replayed for every token; a greedy generation loop runs as back-to-back
 // graph launches with no host round trip.
+#include "dn_dev.h"
 #include "lrs_internal.h"
 #include "pack_dev.h"
 #include "quant_dev.h"
@@ -150,6 +151,9 @@ struct lrs_model {
     lrs_hybrid_config hc = {};
     float *qg = nullptr, *kb = nullptr, *vb = nullptr, *dn_qkv = nullptr, *dn_z = nullptr,
           *dn_part = nullptr;
+    // {e^g, beta} per value head from the projection launch (LRS_DN_GATES=0:
+    // null, the step computes them)
+    float2 *dn_gates = nullptr;
     void *rec = nullptr;
     size_t rec_bytes = 0;
     // weights the model owns (built by lrs_model_load_gguf), freed with it
@@ -474,10 +478,47 @@ hipError_t op_qk_prep(lrs_model *m, uint32_t l) {
 }
 
 // delta-net layer: conv input (q | k | v channels) and output gate z
+// whether delta-net layer L's gate projections run in its projection launch
+// (launch_mq with gates) rather than in every workgroup of the step
+bool dn_gates_fused(const lrs_model *m, const DevLayer &L) {
+    return m->dn_gates && L.dn && L.ssm_qkv->v.type == L.ssm_gate->v.type &&
+           mq_gates_supported(L.ssm_qkv->v.type, L.ssm_gate->v.type, G_STORE) &&
+           m->cfg.n_embd % 4 == 0 && m->cfg.n_embd <= 4 * DN_GATE_THREADS * DN_GI;
+}
+
 hipError_t op_dn_proj(lrs_model *m, uint32_t l) {
     const DevLayer &L = m->layers[l];
     const lrs_weight *ws[2] = {L.ssm_qkv, L.ssm_gate};
     float *outs[2] = {m->dn_qkv, m->dn_z};
+    if (dn_gates_fused(m, L)) {
+        // ssm_qkv and ssm_gate (one type) in one launch, then one workgroup
+        // per value head for the gate projections
+        const lrs_config &c = m->cfg;
+        MqArgs a = {};
+        a.n_in = c.n_embd;
+        a.xin = m->pk_n;
+        a.xsq = m->xsq;
+        a.eps = c.rms_eps;
+        a.n_seg = 2;
+        for (int i = 0; i < 2; i++) {
+            a.seg[i] = mseg(ws[i], ws[i]->v.n_out);
+            a.seg[i].out = outs[i];
+        }
+        a.nxb = pack_blocks(ws[0]->v.type, c.n_embd);
+        DnGateArgs g = {};
+        g.x = m->x;
+        g.attn_norm = L.attn_norm;
+        g.alpha = L.alpha;
+        g.beta = L.beta;
+        g.a = L.ssm_a;
+        g.dt = L.ssm_dt;
+        g.out = m->dn_gates;
+        g.n_embd = c.n_embd;
+        g.v_heads = m->hc.dn_v_heads;
+        g.eps = c.rms_eps;
+        return launch_mq(a, ws[0]->v.type, ws[1]->v.type, G_STORE, MQ_STORE, m->ctx->stream,
+                         nullptr, nullptr, &g);
+    }
     return op_store(m, ws, outs, 2);
 }
 
@@ -505,6 +546,7 @@ hipError_t op_dn_step(lrs_model *m, uint32_t l) {
     a.v_heads = m->hc.dn_v_heads;
     a.d_conv = m->hc.dn_conv;
     a.eps = m->cfg.rms_eps;
+    a.gates = dn_gates_fused(m, L) ? m->dn_gates : nullptr;
     return launch_dn_step(a, m->hc.dn_state, m->ctx->stream);
 }
 
@@ -939,8 +981,13 @@ int lrs_hybrid_create(lrs_ctx *ctx, const lrs_hybrid_config *hcfg, const lrs_hyb
         (rc = dev_alloc(m, kvd * sizeof(float), (void **)&m->vb)) ||
         (rc = dev_alloc(m, CD * sizeof(float), (void **)&m->dn_qkv)) ||
         (rc = dev_alloc(m, VD * sizeof(float), (void **)&m->dn_z)) ||
-        (rc = dev_alloc(m, (size_t)hc.dn_v_heads * (D / 32) * sizeof(float), (void **)&m->dn_part)))
+        (rc = dev_alloc(m, (size_t)hc.dn_v_heads * (D / 32) * sizeof(float), (void **)&m->dn_part)) ||
+        (rc = dev_alloc(m, (size_t)hc.dn_v_heads * sizeof(float2), (void **)&m->dn_gates)))
         return bail(rc);
+    {
+        const char *v = getenv("LRS_DN_GATES");
+        if (v && (strcmp(v, "0") == 0 || strcasecmp(v, "false") == 0)) m->dn_gates = nullptr;
+    }
     if (hipMemset(m->kv, 0, kv_layer * 2 * n_attn * sizeof(_Float16)) != hipSuccess ||
         hipMemset(m->rec, 0, m->rec_bytes) != hipSuccess)
         return bail(fail(LRS_E_HIP, "memset"));

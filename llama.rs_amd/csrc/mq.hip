@@ -38,6 +38,7 @@
 // its f32 input inside each workgroup and runs up to NC input columns over
 // every weight load (each column bit-identical to a one-column call).
 #include "attn_dev.h"
+#include "dn_dev.h"
 #include "lrs_internal.h"
 #include "mq_args.h"
 #include "pack_dev.h"
@@ -928,6 +929,38 @@ __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq_ao(Mq
     mq_body<T, TPW, TG, KS, P, MQ_RESID, 1, false, true>(a, 0, lds, red);
 }
 
+// The delta-net projections (MQ_STORE over ssm_qkv and ssm_gate) with the
+// layer's gate projections in the same launch: the workgroups past the
+// matvec's (n_mq of them), one per value head, compute the head's
+// {e^g, beta} with threads 0..255 exactly as the step kernel would, which
+// then reads two floats instead of 40 KB of gate rows per workgroup.
+template <uint32_t T0, uint32_t T1, int TPW, int TG, int KS, int P>
+__global__ __launch_bounds__(64 * TG * KS)
+__attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq_gates(MqArgs a, DnGateArgs g,
+                                                                                    uint32_t n_mq) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float red[TG * KS * TPW * 16 + TG * KS + 1];
+    static_assert(TG * KS * 64 >= DN_GATE_THREADS && sizeof(red) >= 12 * sizeof(float), "gate role");
+    if (blockIdx.x >= n_mq) {
+        const uint32_t hh = blockIdx.x - n_mq;
+        float(*r4)[4] = reinterpret_cast<float(*)[4]>(red);
+        if (threadIdx.x < DN_GATE_THREADS)
+            dn_gate_two_rounds(g.x, g.attn_norm, g.alpha + (size_t)hh * g.n_embd,
+                               g.beta + (size_t)hh * g.n_embd, g.n_embd, threadIdx.x, r4);
+        __syncthreads();
+        if (threadIdx.x == 0) g.out[hh] = dn_gate_final(r4, g.a[hh], g.dt[hh], g.n_embd, g.eps);
+        return;
+    }
+    uint32_t si = 0;
+#pragma unroll
+    for (int s = 1; s < MQ_MAX_SEG; s++)
+        if ((uint32_t)s < a.n_seg && blockIdx.x >= a.seg[s].wg0) si = s;
+    if (T0 == T1 || si < a.n_seg0)
+        mq_body<T0, TPW, TG, KS, P, MQ_STORE>(a, si, lds, red);
+    else
+        mq_body<T1, TPW, TG, KS, P, MQ_STORE>(a, si, lds, red);
+}
+
 // plain matvec of NC f32 input columns (a.xf), packed by each workgroup
 template <uint32_t T, int TPW, int TG, int KS, int P, int NC>
 __global__ __launch_bounds__(64 * TG * KS)
@@ -988,8 +1021,19 @@ bool mq_geom_supported(const MqGeom &g) {
     return pick<T_Q4_K, T_Q4_K, MQ_STORE>(g) != nullptr;
 }
 
+using MqGatesFn = void (*)(MqArgs, DnGateArgs, uint32_t);
+static MqGatesFn pick_gates(uint32_t t0, uint32_t t1, const MqGeom &g) {
+    if (t0 == T_Q4_K && t1 == T_Q4_K && g.tpw == 1 && g.tg == 2 && g.ks == 4 && g.p == 2 && g.xs <= 1)
+        return k_mq_gates<T_Q4_K, T_Q4_K, 1, 2, 4, 2>;
+    return nullptr;
+}
+
+bool mq_gates_supported(uint32_t t0, uint32_t t1, const MqGeom &g) {
+    return pick_gates(t0, t1, g) != nullptr;
+}
+
 hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int epi, hipStream_t s,
-                     uint32_t *wgs_out, uint32_t *keys_per_wg) {
+                     uint32_t *wgs_out, uint32_t *keys_per_wg, const DnGateArgs *gates) {
     MqArgs a = in;
     if (a.n_seg == 0 || a.n_seg > MQ_MAX_SEG) return hipErrorInvalidValue;
     if (t0 == t1) a.n_seg0 = a.n_seg;
@@ -1041,6 +1085,15 @@ hipError_t launch_mq(const MqArgs &in, uint32_t t0, uint32_t t1, MqGeom g, int e
     if (keys_per_wg) {
         const uint32_t outs = (uint32_t)(g.tg * g.tpw) * 16;
         *keys_per_wg = (outs + 63) / 64;
+    }
+    if (gates) {
+        MqGatesFn gf = epi == MQ_STORE && !a.amax ? pick_gates(t0, t1, g) : nullptr;
+        if (!gf) return hipErrorNotSupported;
+        if (gates->n_embd % 4 || gates->n_embd > 4 * DN_GATE_THREADS * DN_GI || !gates->out)
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(gf, dim3(wgs + gates->v_heads), dim3(64 * g.tg * g.ks), lds, s, a, *gates,
+                           wgs);
+        return hipGetLastError();
     }
     hipLaunchKernelGGL(fn, dim3(wgs), dim3(64 * g.tg * g.ks), lds, s, a);
     return hipGetLastError();

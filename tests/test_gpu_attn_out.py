@@ -1,15 +1,20 @@
-"""The attention combine in the o-projection's launch (k_mq_ao, the decode
-default) against the two-launch form (the combine kernel, then the o matvec:
-LRS_AO=0 at model creation) on the same weights.  Both run the same
-arithmetic in the same order (the combine's merge, the pack, the matvec's
-units and K-slice sums), so the logits must be bit-identical: token by
-token, over greedy chains, and at cache lengths where the position splits
-of the attention first own one, two and three blocks.  The cases cover every
-o weight type the launch has (Q4_K / Q5_K / Q6_K), head dims 64 / 128 / 256,
-the gated attention of the hybrid model, and the benchmark widths (40 query
-heads over 5120 inputs; 24 x 256 over 6144), so each P instance of the
-launch that a benchmark runs is here.  Their parity with the CPU oracle is
-the rest of the GPU suite, which runs this launch by default."""
+"""The decode's fused launches against their separate forms on the same
+weights (the variables set to 0 at model creation):
+- the attention combine in the o-projection's launch (k_mq_ao) against the
+  combine kernel then the o matvec (LRS_AO=0);
+- the hybrid's delta-net gate projections in the projection launch
+  (k_mq_gates) against the step kernel computing them (LRS_DN_GATES=0).
+Each runs the same arithmetic in the same order (the combine's merge, the
+pack, the matvec's units and K-slice sums; the gate dots' per-thread sums,
+wavefront sums and their combination), so the logits must be bit-identical:
+token by token, over greedy chains, and at cache lengths where the position
+splits of the attention first own one, two and three blocks.  The cases
+cover every o weight type k_mq_ao has (Q4_K / Q5_K / Q6_K), head dims 64 /
+128 / 256, the gated attention of the hybrid model, and the benchmark widths
+(40 query heads over 5120 inputs; 24 x 256 over 6144; 16 value heads over
+5120), so each instance of the fused launches that a benchmark runs is
+here.  Their parity with the CPU oracle is the rest of the GPU suite, which
+runs them by default."""
 import numpy as np
 import pytest
 
@@ -41,15 +46,22 @@ def ctx(lrs):
     c.close()
 
 
-def _pair(monkeypatch, make):
-    """(fused, two-launch) models built by make() with and without LRS_AO=0."""
-    monkeypatch.delenv("LRS_AO", raising=False)
+SWITCHES = ("LRS_AO", "LRS_DN_GATES")
+
+
+def _pair(monkeypatch, make, off=("LRS_AO",)):
+    """(fused, separate) models built by make(): the default, then with the
+    variables `off` set to 0."""
+    for v in SWITCHES:
+        monkeypatch.delenv(v, raising=False)
     fused = make()
-    monkeypatch.setenv("LRS_AO", "0")
+    for v in off:
+        monkeypatch.setenv(v, "0")
     try:
         split = make()
     finally:
-        monkeypatch.delenv("LRS_AO")
+        for v in off:
+            monkeypatch.delenv(v)
     return fused, split
 
 
@@ -91,10 +103,16 @@ def test_combine_in_o_launch_at_split_boundaries(lrs, orc, ctx, monkeypatch):
         split.close()
 
 
-@pytest.mark.parametrize("name,cfg", [("hy-mid", modelgen.HY_MID), ("c4-width", C4W)])
-def test_gated_combine_in_o_launch_is_bit_identical(lrs, orc, ctx, monkeypatch, name, cfg):
+HYBRID_OFF = {"ao": ("LRS_AO",), "gates": ("LRS_DN_GATES",), "both": SWITCHES}
+
+
+@pytest.mark.parametrize("off", sorted(HYBRID_OFF))
+@pytest.mark.parametrize("name,cfg", [("hy-tiny", modelgen.HY_TINY), ("hy-mid", modelgen.HY_MID),
+                                      ("c4-width", C4W)])
+def test_hybrid_fused_launches_are_bit_identical(lrs, orc, ctx, monkeypatch, name, cfg, off):
     w = modelgen.hybrid_host_model(orc, cfg, seed=43, mode=0, d_lo=1e-3, d_hi=1e-2)
-    fused, split = _pair(monkeypatch, lambda: modelgen.gpu_hybrid_model(lrs, ctx, cfg, w))
+    fused, split = _pair(monkeypatch, lambda: modelgen.gpu_hybrid_model(lrs, ctx, cfg, w),
+                         HYBRID_OFF[off])
     try:
         prompt = np.random.default_rng(47).integers(0, cfg["vocab"], 10).tolist()
         for pos, t in enumerate(prompt):
