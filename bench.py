@@ -173,8 +173,8 @@ def bench_decode(lrs, ctx, steps, warmup, prefill_ms=()):
 
 HY_OPS = ("dn_proj", "dn_step", "dn_out", "qkv", "qk_prep", "attn", "o", "gateup", "down",
           "head")
-OP_NAMES.update({"dn_proj": "fused RMSNorm + delta-net qkv/z Q4_K matvec",
-                 "dn_step": "delta-net step: gates, conv, L2, delta rule, gated norm",
+OP_NAMES.update({"dn_proj": "fused RMSNorm + delta-net qkv/z Q4_K matvec + gate projections",
+                 "dn_step": "delta-net step: conv, L2, delta rule, gated norm",
                  "dn_out": "delta-net ssm_out matvec + residual add",
                  "qk_prep": "QK-norm + RoPE + f16 KV append (gated attention layers)"})
 

@@ -1543,13 +1543,18 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
                     (D.bq ? qd4 + (size_t)kvd * 8 : 0);
             break;
         case LRS_OP_QK_PREP: b = 2 * qd4 + (size_t)kvd * 8 + qd4 + (size_t)kvd * 4; break;
-        case LRS_OP_DN_PROJ: b = wbytes(D.ssm_qkv) + wbytes(D.ssm_gate) + 2 * E4 + CD4 + VD4; break;
+        case LRS_OP_DN_PROJ:
+            // plus the f32 gate rows when the launch computes the gates
+            b = wbytes(D.ssm_qkv) + wbytes(D.ssm_gate) + 2 * E4 + CD4 + VD4 +
+                (dn_gates_fused(m, D) ? 2 * (size_t)hc.dn_v_heads * E4 : 0);
+            break;
         case LRS_OP_DN_STEP:
-            // state read + written, f32 gate rows, conv weights and window,
-            // inputs, the y pack (3.5 B per element)
+            // state read + written, f32 gate rows (unless the projection
+            // launch read them), conv weights and window, inputs, the y pack
+            // (3.5 B per element)
             b = 2 * (size_t)hc.dn_v_heads * dnD * dnD * 4 +
-                2 * (size_t)hc.dn_v_heads * E4 + CD4 * hc.dn_conv + CD4 * hc.dn_conv + CD4 +
-                VD4 + 2 * E4 + VD4 / 4 * 7 / 2;
+                (dn_gates_fused(m, D) ? 0 : 2 * (size_t)hc.dn_v_heads * E4) + CD4 * hc.dn_conv +
+                CD4 * hc.dn_conv + CD4 + VD4 + 2 * E4 + VD4 / 4 * 7 / 2;
             break;
         case LRS_OP_DN_OUT: b = wbytes(D.ssm_out) + VD4 + 2 * E4; break;
         case LRS_OP_ATTN: b = (size_t)L * kvd * 2 * sizeof(_Float16) + 2 * qd4; break;
