@@ -107,7 +107,9 @@ struct lrs_model {
     // (a row of 64 words per o workgroup, one word per producer); all zero
     // between launches
     bool ao_on = true;
+    bool ao_wait_test = false;
     uint32_t *ao_sync = nullptr;
+    size_t ao_sync_bytes = 0;
     // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
     // SwiGLU output
     XPack pk_n, pk_f, pk_a, pk_s;
@@ -400,6 +402,12 @@ hipError_t op_o(lrs_model *m, uint32_t l) {
         ao.head_dim = c.head_dim;
         ao.gstride = 2 * c.head_dim;
         ao.n_prod = c.n_head;
+        if (m->ao_wait_test) {
+            // LRS_AO_WAIT_TEST: no flags are raised and each wait gives up
+            // after 16 polls, so the call must report the error
+            ao.no_signal = 1;
+            a.wait_polls = 16;
+        }
         a.werr = m->ao_sync + 32;
         a.wflag = m->ao_sync + 64;
         a.step = m->step;
@@ -787,10 +795,12 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         // error word and a row of flags per 32 rows of o's output
         const size_t aw = 64 + 64 * (size_t)(c.n_embd / 32);
         if ((rc = dev_alloc(m, aw * sizeof(uint32_t), (void **)&m->ao_sync))) return rc;
+        m->ao_sync_bytes = aw * sizeof(uint32_t);
         if (hipMemset(m->ao_sync, 0, aw * sizeof(uint32_t)) != hipSuccess)
             return fail(LRS_E_HIP, "memset");
         const char *v = getenv("LRS_AO");
         m->ao_on = !(v && (strcmp(v, "0") == 0 || strcasecmp(v, "false") == 0));
+        m->ao_wait_test = env_on("LRS_AO_WAIT_TEST");
     }
     // 1024 step slots of 4 words (enqueue_tokens), then the wait-error word
     if (hipHostMalloc((void **)&m->step_host, (4 * 1024 + 4) * sizeof(uint32_t), hipHostMallocDefault) !=
@@ -1080,7 +1090,9 @@ static hipError_t ao_err_fetch(lrs_model *m, hipStream_t s) {
 }
 static int ao_err_check(lrs_model *m) {
     if (m->step_host[AO_ERR_WORD] == 0) return LRS_OK;
-    (void)hipMemset(m->ao_sync + 32, 0, sizeof(uint32_t));
+    // the word and the whole flag matrix back to zero: flags a late producer
+    // raised after its consumer gave up must not release the next launch's
+    (void)hipMemset(m->ao_sync, 0, m->ao_sync_bytes);
     return fail(LRS_E_HIP, "attention output launch: a workgroup's wait for its input ran out");
 }
 
@@ -1602,7 +1614,10 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
     LRS_HIP(hipEventRecord(m->ctx->ev0, s));
     for (uint32_t i = 0; i < iters; i++) LRS_HIP(one(i));
     LRS_HIP(hipEventRecord(m->ctx->ev1, s));
+    LRS_HIP(ao_err_fetch(m, s));
     LRS_HIP(hipEventSynchronize(m->ctx->ev1));
+    LRS_HIP(hipStreamSynchronize(s));
+    if (int e = ao_err_check(m)) return e;
     float ms = 0.f;
     LRS_HIP(hipEventElapsedTime(&ms, m->ctx->ev0, m->ctx->ev1));
     *avg_us = ms * 1000.f / (float)iters;

@@ -429,8 +429,9 @@ __device__ __forceinline__ void copy_to_lds(const uint8_t *__restrict__ g, uint8
 }
 
 // polls of a matvec workgroup waiting for its input pack (k_mq_ao) before it
-// gives up: each is a memory round trip plus a short sleep (~0.5-2 us), so
-// 40-130 ms in all, against the few microseconds the producers take
+// gives up (MqArgs::wait_polls 0): each is a memory round trip plus a short
+// sleep (~0.5-2 us), so 40-130 ms in all, against the few microseconds the
+// producers take
 constexpr uint32_t MQ_WAIT_POLLS = 1u << 16;
 
 // body for the segments [s_lo, s_hi) of type T (one workgroup).  NC > 1 or
@@ -612,12 +613,13 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         if (wave == 0) {
             uint32_t *f = a.wflag + 64 * (size_t)wrel + lane;
             const bool mine = lane < a.n_wait;
+            const uint32_t limit = a.wait_polls ? a.wait_polls : MQ_WAIT_POLLS;
             uint32_t n = 0;
             for (;;) {
                 const uint32_t v =
                     mine ? __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1u;
                 if (__all(v != 0u)) break;
-                if (++n >= MQ_WAIT_POLLS) {
+                if (++n >= limit) {
                     if (lane == 0)
                         __hip_atomic_store(a.werr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
@@ -921,9 +923,10 @@ __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq_ao(Mq
                                 blockIdx.x, reinterpret_cast<float *>(lds), wsh, red);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's pack stores are complete
         __syncthreads();
-        for (uint32_t t = threadIdx.x; t < c.n_cons; t += blockDim.x)
-            __hip_atomic_store(a.wflag + 64 * (size_t)t + blockIdx.x, 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        if (!c.no_signal)
+            for (uint32_t t = threadIdx.x; t < c.n_cons; t += blockDim.x)
+                __hip_atomic_store(a.wflag + 64 * (size_t)t + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     mq_body<T, TPW, TG, KS, P, MQ_RESID, 1, false, true>(a, 0, lds, red);

@@ -104,6 +104,7 @@ struct MqArgs {
     // runs out of polls sets werr to 1 and goes on
     uint32_t *wflag, *werr;
     uint32_t n_wait;
+    uint32_t wait_polls;  // the wait's poll limit (0: the default, about a second)
 };
 
 // the attention combine ahead of the o-projection in one launch (k_mq_ao):
@@ -114,6 +115,9 @@ struct AoArgs {
     const float *part;   // [n_head][splits][head_dim + 4]
     const float *gate;   // gated attention: sigmoid gate at gate[h * gstride + d], or null
     uint32_t splits, head_dim, gstride, n_prod, n_cons;
+    // the producers raise no flags (a test of the wait's bound: the host sets
+    // it together with a small MqArgs::wait_polls, so every wait runs out)
+    uint32_t no_signal;
 };
 
 // launch shape: TPW tiles per wavefront sharing the activation, TG tile

@@ -124,3 +124,31 @@ def test_hybrid_fused_launches_are_bit_identical(lrs, orc, ctx, monkeypatch, nam
     finally:
         fused.close()
         split.close()
+
+
+def test_wait_bound_reports_an_error(lrs, orc, ctx, monkeypatch):
+    """The o workgroups' wait for the combine's flags is bounded.  With
+    LRS_AO_WAIT_TEST the combine workgroups raise no flags and every wait
+    gives up after 16 polls (each kernel still ends), so decoding must fail
+    with the library's HIP error instead of returning logits; a model made
+    without the switch decodes normally."""
+    cfg = modelgen.TINY
+    w = modelgen.host_model(orc, cfg, seed=23, mode=0, d_lo=1e-3, d_hi=1e-2)
+    monkeypatch.setenv("LRS_AO_WAIT_TEST", "1")
+    try:
+        bad = modelgen.gpu_model(lrs, ctx, cfg, w)
+    finally:
+        monkeypatch.delenv("LRS_AO_WAIT_TEST")
+    try:
+        for call in (lambda: bad.decode(1, 0), lambda: bad.generate_greedy([1, 2, 3], 4)):
+            bad.reset()
+            with pytest.raises(lrs.ModelError) as err:
+                call()
+            assert err.value.code == -2 and "ran out" in str(err.value), err.value
+    finally:
+        bad.close()
+    good = modelgen.gpu_model(lrs, ctx, cfg, w)
+    try:
+        assert np.all(np.isfinite(good.decode(1, 0)))
+    finally:
+        good.close()
