@@ -31,7 +31,8 @@ extern "C" {
 
 #define LRS_OK 0
 #define LRS_E_ARG (-1)          /* bad argument / shape (gpu.rs:149-164 checks) */
-#define LRS_E_HIP (-2)          /* HIP runtime error */
+#define LRS_E_HIP (-2)          /* HIP runtime error; also a model call whose launch's bounded
+                                   wait between its workgroups ran out (outputs not valid) */
 #define LRS_E_OOM (-3)          /* device allocation failed */
 #define LRS_E_CTX_OVERFLOW (-4) /* KV cache full (attention.rs:36-40) */
 #define LRS_E_UNSUPPORTED (-5)  /* type / shape not supported */
