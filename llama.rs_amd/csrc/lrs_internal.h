@@ -173,6 +173,18 @@ hipError_t launch_attn_prefill(const float *q, const _Float16 *kc, const _Float1
 hipError_t launch_swiglu_split(const float *G, const float *U, size_t n, __bf16 *hi,
                                hipStream_t s);
 // hybrid (qwen35) mixers (dn.hip)
+// QK-norm + RoPE of the hybrid's gated attention run by the split kernel
+// (attention.hip, QP): query rows from the projection's q + gate rows, the
+// current position's K / V rows from its k / v outputs
+struct QkPrep {
+    const float *qg, *kb, *vb;    // [n_head][2 HD] q | gate, [n_kv][HD] k, v
+    const float *q_norm, *k_norm;  // [HD]
+    const float2 *rope;            // [HD / 2] {cos, sin} of pair i at the position ({1, 0} past rope_dim)
+    _Float16 *kc, *vc;             // the layer's caches: the current row is written here
+    float eps;
+};
+// the split kernel can do the QK-norm + RoPE for this head shape
+bool attn_qp_supported(uint32_t head_dim, uint32_t rep);
 struct DnArgs {
     const float *qkv;           // [conv_dim] conv input (RMSNorm already applied by the matvec)
     const float *z;             // [v_heads * D] output gate

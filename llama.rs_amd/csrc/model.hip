@@ -46,17 +46,31 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
                             XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
                             uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s,
                             const float *gate = nullptr, uint32_t gstride = 0,
-                            bool combine = true);
+                            bool combine = true, const QkPrep *qp = nullptr);
 
 // x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304),
-// and the pack of x * nw for the first layer's q/k/v
+// and the pack of x * nw for the first layer's q/k/v.  rope (n_pairs > 0):
+// {cos, sin} of pos * freq[i] for the position step[1], pair i <
+// rope_pairs (the arithmetic of the QK-prep launch's rotation), {1, 0} for
+// the other pairs up to n_pairs, for the attention splits that rotate q and
+// k themselves
 __global__ __launch_bounds__(256) void k_embed(WeightView w, const uint32_t *__restrict__ step,
                                                const float *__restrict__ nw, float *__restrict__ x,
-                                               XPack p, float *__restrict__ xsq) {
+                                               XPack p, float *__restrict__ xsq,
+                                               const float *__restrict__ freq, float2 *__restrict__ rope,
+                                               uint32_t n_pairs, uint32_t rope_pairs) {
     const uint32_t be = (uint32_t)block_elems(w.type);
     uint32_t tok = step[0];
     if (tok >= w.n_out) tok = w.n_out - 1;  // ids are validated on the host
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;  // n_in is a multiple of 256
+    if (i < n_pairs) {
+        float sn = 0.f, cs = 1.f;
+        if (i < rope_pairs) {
+            const float th = (float)step[1] * freq[i];
+            sincosf(th, &sn, &cs);
+        }
+        rope[i] = make_float2(cs, sn);
+    }
     const uint64_t e = (uint64_t)tok * w.n_in + i;
     const float v = deq_elem(w, e / be, (uint32_t)(e % be));
     x[i] = v;
@@ -107,6 +121,10 @@ struct lrs_model {
     // (a row of 64 words per o workgroup, one word per producer); all zero
     // between launches
     bool ao_on = true;
+    // the hybrid's QK-norm + RoPE in the attention split (LRS_QKP=0: a launch
+    // of its own): the {cos, sin} table of the token's position, written by
+    // the embed kernel, head_dim / 2 pairs; null when off
+    float2 *rope_cs = nullptr;
     bool ao_wait_test = false;
     uint32_t *ao_sync = nullptr;
     size_t ao_sync_bytes = 0;
@@ -271,8 +289,13 @@ MqGeom env_geom(const char *name, MqGeom dflt) {
 
 // ---- one fused op of the per-token plan, enqueued on the model stream ----
 hipError_t op_embed(lrs_model *m) {
-    hipLaunchKernelGGL(k_embed, dim3(m->cfg.n_embd / 256), dim3(256), 0, m->ctx->stream,
-                       m->embd->v, m->step, m->layers[0].attn_norm, m->x, m->pk_n, m->xsq);
+    const lrs_config &c = m->cfg;
+    // the rotation table when an attention split rotates q and k itself
+    const uint32_t n_pairs = m->rope_cs ? c.head_dim / 2 : 0;
+    if (n_pairs > c.n_embd) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed, dim3(c.n_embd / 256), dim3(256), 0, m->ctx->stream, m->embd->v,
+                       m->step, m->layers[0].attn_norm, m->x, m->pk_n, m->xsq, m->freq, m->rope_cs,
+                       n_pairs, c.rope_dim / 2);
     return hipGetLastError();
 }
 
@@ -348,6 +371,10 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
 
 // whether layer l's attention combine runs in its o launch (k_mq_ao):
 // attention layers whose o weight has the kernel and takes the 22-bit pack
+// whether layer L's QK-norm + RoPE run in its attention split (the gated
+// attention of the hybrid model; LRS_QKP=0 keeps the separate launch)
+bool qkp_fused(const lrs_model *m, const DevLayer &L) { return !L.dn && m->rope_cs; }
+
 bool ao_fused(const lrs_model *m, const DevLayer &L) {
     const lrs_config &c = m->cfg;
     return m->ao_on && m->ao_sync && !L.dn && L.o && !L.o_q8 &&
@@ -363,9 +390,21 @@ hipError_t op_attn(lrs_model *m, uint32_t l) {
     const float *gate = m->hybrid ? m->qg + c.head_dim : nullptr;
     XPack out = m->pk_a;
     out.q8 = L.o_q8;
+    QkPrep qp = {};
+    if (qkp_fused(m, L)) {
+        qp.qg = m->qg;
+        qp.kb = m->kb;
+        qp.vb = m->vb;
+        qp.q_norm = L.q_norm;
+        qp.k_norm = L.k_norm;
+        qp.rope = m->rope_cs;
+        qp.kc = L.kc;
+        qp.vc = L.vc;
+        qp.eps = c.rms_eps;
+    }
     return launch_attention(m->qbuf, L.kc, L.vc, m->pa, out, m->step, c.n_head, c.n_head_kv,
                             c.head_dim, c.ctx, m->a_splits, m->ctx->stream, gate,
-                            2 * c.head_dim, !ao_fused(m, L));
+                            2 * c.head_dim, !ao_fused(m, L), qkp_fused(m, L) ? &qp : nullptr);
 }
 
 // x += W_o att (or W_ssm_out y of a delta-net layer); pack of x * ffn_norm
@@ -480,6 +519,7 @@ hipError_t op_hattn_proj(lrs_model *m, uint32_t l) {
 hipError_t op_qk_prep(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
+    if (qkp_fused(m, L)) return hipSuccess;  // in the split (op_attn)
     return launch_qk_prep(m->qg, m->kb, m->vb, L.q_norm, L.k_norm, m->freq, m->step, m->qbuf, L.kc,
                           L.vc, c.n_head, c.n_head_kv, c.head_dim, c.ctx, c.rope_dim, c.rms_eps,
                           m->ctx->stream);
@@ -801,6 +841,13 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         const char *v = getenv("LRS_AO");
         m->ao_on = !(v && (strcmp(v, "0") == 0 || strcasecmp(v, "false") == 0));
         m->ao_wait_test = env_on("LRS_AO_WAIT_TEST");
+        const char *vq = getenv("LRS_QKP");
+        const bool qkp_on = !(vq && (strcmp(vq, "0") == 0 || strcasecmp(vq, "false") == 0));
+        if (m->hybrid && qkp_on && attn_qp_supported(c.head_dim, c.n_head / c.n_head_kv)) {
+            const size_t rb = c.head_dim / 2 * sizeof(float2);
+            if ((rc = dev_alloc(m, rb, (void **)&m->rope_cs))) return rc;
+            if (hipMemset(m->rope_cs, 0, rb) != hipSuccess) return fail(LRS_E_HIP, "memset");
+        }
     }
     // 1024 step slots of 4 words (enqueue_tokens), then the wait-error word
     if (hipHostMalloc((void **)&m->step_host, (4 * 1024 + 4) * sizeof(uint32_t), hipHostMallocDefault) !=
@@ -1554,7 +1601,15 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
                 b = wbytes(D.q) + wbytes(D.k) + wbytes(D.v) + 2 * E4 + qd4 + (size_t)kvd * 2 * 2 +
                     (D.bq ? qd4 + (size_t)kvd * 8 : 0);
             break;
-        case LRS_OP_QK_PREP: b = 2 * qd4 + (size_t)kvd * 8 + qd4 + (size_t)kvd * 4; break;
+        case LRS_OP_QK_PREP:
+            // nothing of its own when the attention split does it
+            if (qkp_fused(m, D)) {
+                *avg_us = 0.f;
+                if (bytes) *bytes = 0;
+                return LRS_OK;
+            }
+            b = 2 * qd4 + (size_t)kvd * 8 + qd4 + (size_t)kvd * 4;
+            break;
         case LRS_OP_DN_PROJ:
             // plus the f32 gate rows when the launch computes the gates
             b = wbytes(D.ssm_qkv) + wbytes(D.ssm_gate) + 2 * E4 + CD4 + VD4 +
@@ -1569,7 +1624,13 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
                 CD4 * hc.dn_conv + CD4 + VD4 + 2 * E4 + VD4 / 4 * 7 / 2;
             break;
         case LRS_OP_DN_OUT: b = wbytes(D.ssm_out) + VD4 + 2 * E4; break;
-        case LRS_OP_ATTN: b = (size_t)L * kvd * 2 * sizeof(_Float16) + 2 * qd4; break;
+        case LRS_OP_ATTN:
+            // plus, with the QK-norm + RoPE in the split (which reads the
+            // query rows in place of the q buffer), the new k / v rows, the
+            // two norm weights, the rotation table and the f16 K/V append
+            b = (size_t)L * kvd * 2 * sizeof(_Float16) + 2 * qd4 +
+                (qkp_fused(m, D) ? (size_t)kvd * 8 + 3 * (size_t)c.head_dim * 4 + (size_t)kvd * 4 : 0);
+            break;
         case LRS_OP_O: b = wbytes(D.o) + qd4 + 2 * E4; break;
         case LRS_OP_GATEUP: b = wbytes(D.gate) + wbytes(D.up) + 2 * E4 + (size_t)c.n_ff * 4; break;
         case LRS_OP_DOWN: b = wbytes(D.down) + (size_t)c.n_ff * 4 + 2 * E4; break;

@@ -4,9 +4,12 @@ weights (the variables set to 0 at model creation):
   combine kernel then the o matvec (LRS_AO=0);
 - the hybrid's delta-net gate projections in the projection launch
   (k_mq_gates) against the step kernel computing them (LRS_DN_GATES=0).
-Each runs the same arithmetic in the same order (the combine's merge, the
-pack, the matvec's units and K-slice sums; the gate dots' per-thread sums,
-wavefront sums and their combination), so the logits must be bit-identical:
+- the hybrid's QK-norm + RoPE in the attention split kernel against its own
+  launch (LRS_QKP=0), within a tolerance (see below).
+The first two run the same arithmetic in the same order (the combine's
+merge, the pack, the matvec's units and K-slice sums; the gate dots'
+per-thread sums, wavefront sums and their combination), so the logits must
+be bit-identical:
 token by token, over greedy chains, and at cache lengths where the position
 splits of the attention first own one, two and three blocks.  The cases
 cover every o weight type k_mq_ao has (Q4_K / Q5_K / Q6_K), head dims 64 /
@@ -46,7 +49,7 @@ def ctx(lrs):
     c.close()
 
 
-SWITCHES = ("LRS_AO", "LRS_DN_GATES")
+SWITCHES = ("LRS_AO", "LRS_DN_GATES", "LRS_QKP")
 
 
 def _pair(monkeypatch, make, off=("LRS_AO",)):
@@ -103,7 +106,7 @@ def test_combine_in_o_launch_at_split_boundaries(lrs, orc, ctx, monkeypatch):
         split.close()
 
 
-HYBRID_OFF = {"ao": ("LRS_AO",), "gates": ("LRS_DN_GATES",), "both": SWITCHES}
+HYBRID_OFF = {"ao": ("LRS_AO",), "gates": ("LRS_DN_GATES",), "both": ("LRS_AO", "LRS_DN_GATES")}
 
 
 @pytest.mark.parametrize("off", sorted(HYBRID_OFF))
@@ -121,6 +124,53 @@ def test_hybrid_fused_launches_are_bit_identical(lrs, orc, ctx, monkeypatch, nam
         fused.reset()
         split.reset()
         assert fused.generate_greedy(prompt, 16).tolist() == split.generate_greedy(prompt, 16).tolist()
+    finally:
+        fused.close()
+        split.close()
+
+
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("splits", [0, 3], ids=["default-splits", "3-splits"])
+@pytest.mark.parametrize("name,cfg", [("hy-tiny", modelgen.HY_TINY), ("hy-mid", modelgen.HY_MID),
+                                      ("c4-width", C4W)])
+def test_qk_prep_in_split_matches_its_launch(lrs, orc, ctx, monkeypatch, name, cfg, splits):
+    """The split kernel normalises q and k with a lane-group sum of squares
+    where the separate launch sums by wavefronts, so the two differ by float
+    rounding (a k element can then round to the neighbouring f16): logits
+    within 1e-5 relative L2 of each other at every position, the same
+    greedy chain, and both within the GPU suite's 1e-3 of the oracle at the
+    last position.  The split that owns the current position changes every
+    16 positions; with the default split count the positions cover the
+    first block of every split, with 3 splits (LRS_ATTN_SPLITS) 150
+    positions cover three blocks of each, so the current row is built in a
+    split's first, second and third block."""
+    n = 150 if splits else 16 * modelgen.attn_splits(cfg["n_head_kv"]) + 8
+    cfg = dict(cfg, ctx=max(cfg["ctx"], n + 24))
+    w = modelgen.hybrid_host_model(orc, cfg, seed=53, mode=0, d_lo=1e-3, d_hi=1e-2)
+    if splits:
+        monkeypatch.setenv("LRS_ATTN_SPLITS", str(splits))
+    fused, split = _pair(monkeypatch, lambda: modelgen.gpu_hybrid_model(lrs, ctx, cfg, w),
+                         ("LRS_QKP",))
+    try:
+        seq = np.random.default_rng(59).integers(0, cfg["vocab"], n).tolist()
+        worst = 0.0
+        for pos, t in enumerate(seq):
+            a, b = fused.decode(t, pos), split.decode(t, pos)
+            e = rel_l2(a, b)
+            worst = max(worst, e)
+            assert e < 1e-5, (name, pos, e)
+        om = orc.HybridModel(cfg, w, kv_f16=True, threads=8)
+        o = om.forward(seq)
+        assert rel_l2(a, o) < 1e-3 and rel_l2(b, o) < 1e-3, (rel_l2(a, o), rel_l2(b, o))
+        fused.reset()
+        split.reset()
+        prompt = seq[:10]
+        assert fused.generate_greedy(prompt, 16).tolist() == split.generate_greedy(prompt, 16).tolist()
+        print(f"{name}: {n} positions, worst rel L2 {worst:.2e}")
     finally:
         fused.close()
         split.close()

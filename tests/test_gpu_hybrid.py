@@ -145,12 +145,28 @@ def test_hybrid_rejects_bad_shapes(lrs, orc, ctx):
         modelgen.gpu_hybrid_model(lrs, ctx, dict(cfg, dn_k_heads=3), w)
 
 
-def test_hybrid_profile_ops(lrs, orc, ctx):
+def test_hybrid_profile_ops(lrs, orc, ctx, monkeypatch):
+    """Every op times and counts bytes; the QK-norm + RoPE runs inside the
+    attention split by default (qk_prep then reports nothing of its own and
+    attn counts its bytes) and in a launch of its own with LRS_QKP=0."""
     cfg = modelgen.HY_MID
     w = modelgen.hybrid_host_model(orc, cfg, seed=24)
-    gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
-    gm.decode(1, 0)
-    for op in ("dn_proj", "dn_step", "dn_out", "qkv", "qk_prep", "attn", "o", "gateup",
-               "down", "head"):
-        us, b = gm.profile(op, 4)
-        assert us > 0 and b > 0, op
+    attn_b = {}
+    for qkp in ("1", "0"):
+        monkeypatch.setenv("LRS_QKP", qkp)
+        gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
+        try:
+            gm.decode(1, 0)
+            for op in ("dn_proj", "dn_step", "dn_out", "qkv", "qk_prep", "attn", "o", "gateup",
+                       "down", "head"):
+                us, b = gm.profile(op, 4)
+                if op == "qk_prep" and qkp == "1":
+                    assert us == 0 and b == 0
+                else:
+                    assert us > 0 and b > 0, (op, qkp)
+                if op == "attn":
+                    attn_b[qkp] = b
+        finally:
+            gm.close()
+    kvd = cfg["n_head_kv"] * cfg["head_dim"]
+    assert attn_b["1"] - attn_b["0"] == kvd * 12 + 3 * cfg["head_dim"] * 4
