@@ -176,7 +176,8 @@ HY_OPS = ("dn_proj", "dn_step", "dn_out", "qkv", "qk_prep", "attn", "o", "gateup
 OP_NAMES.update({"dn_proj": "fused RMSNorm + delta-net qkv/z Q4_K matvec + gate projections",
                  "dn_step": "delta-net step: conv, L2, delta rule, gated norm",
                  "dn_out": "delta-net ssm_out matvec + residual add",
-                 "qk_prep": "QK-norm + RoPE + f16 KV append (gated attention layers)"})
+                 "qk_prep": "QK-norm + RoPE + f16 KV append (gated attention layers; 0 when the "
+                            "attention split does it, the default)"})
 
 
 def bench_hybrid(lrs, ctx, steps, warmup):
