@@ -124,17 +124,20 @@ __device__ __forceinline__ void ld8(float (&v)[8], T *p) {
 // current row replaces what its slot's load returned.  The rotation's
 // cosines / sines for the position come from a.qp.rope (written by the
 // token's first kernel), so every lane group does one row's work.
-template <int HD, int REP, bool QP = false>
+template <int HD, int REP, bool QP = false, bool DQ = false>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     constexpr int LP = HD / 8;              // lanes per position
     constexpr int NG = ATT_THREADS / LP;    // lane groups per workgroup
+    // DIST: lane group g < REP splits query head g alone and shares it
+    // through LDS (QP always; DQ: the same for the dense model's q)
+    constexpr bool DIST = QP || DQ;
     static_assert(REP * NG <= ATT_THREADS, "one thread per (query head, lane group) in the merge");
     static_assert(!QP || REP < NG, "QP: a lane group per query head and one for k");
     __shared__ float sm[NG][REP], sl[NG][REP], sw[NG][REP];
     __shared__ float sacc[NG][REP][HD];
-    // QP: the query heads' hi / lo pairs and score factors, the current K / V row
-    __shared__ uint4 sqp[QP ? REP : 1][2][LP];
-    __shared__ float ssc[QP ? REP : 1];
+    // DIST: the query heads' hi / lo pairs and score factors; QP: the current K / V row
+    __shared__ uint4 sqp[DIST ? REP : 1][2][LP];
+    __shared__ float ssc[DIST ? REP : 1];
     __shared__ uint4 skv[QP ? 2 : 1][LP];
     const uint32_t tid = threadIdx.x, sub = tid % LP, grp = tid / LP;
     const uint32_t sp = blockIdx.x, kh = blockIdx.y, h0 = kh * REP;
@@ -153,12 +156,12 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     // the position is known (slots past the position are in the cache
     // allocation and are never used; the later blocks wait for the
     // position, so a short context reads no more than one block per split)
-    const uint32_t pos0 = QP ? a.step[1] : 0;
-    float4 qx[QP ? 1 : REP][2];
-    const uint32_t role = grp < REP ? grp : REP;  // QP: query head, or REP = k
+    const uint32_t pos0 = DIST ? a.step[1] : 0;
+    float4 qx[DIST ? 1 : REP][2];
+    const uint32_t role = grp < REP ? grp : REP;  // DIST: query head, or REP = k (QP) / none
     float rw[8] = {}, nw[8] = {}, vnew[8] = {}, cs[4] = {}, sn[4] = {};
+    if constexpr (DIST) __builtin_assume(tid < ATT_THREADS);
     if constexpr (QP) {
-        __builtin_assume(tid < ATT_THREADS);
         // the pointers as values (else the compiler selects between the
         // argument slots and loads the pointer per lane before the data),
         // kept global so the loads count on the vector memory counter alone
@@ -174,6 +177,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
         const float4 r0 = rp[0], r1 = rp[1];
         cs[0] = r0.x; sn[0] = r0.y; cs[1] = r0.z; sn[1] = r0.w;
         cs[2] = r1.x; sn[2] = r1.y; cs[3] = r1.z; sn[3] = r1.w;
+    } else if constexpr (DQ) {
+        // this lane group's head (groups past REP load the last one, unused)
+        const uint32_t hq = role < REP ? role : REP - 1;
+        ld8(rw, a.q + (size_t)(h0 + hq) * HD + 8 * sub);
     } else {
 #pragma unroll
         for (int r = 0; r < REP; r++) {
@@ -186,11 +193,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < ATT_DEPTH; i++) {
         const uint32_t p = slot_pos(i);
-        if (QP && (i + 1) * NG <= ATT_BLOCK) {
-            // QP: slots of the first block in every lane group, loaded with
+        if (DIST && (i + 1) * NG <= ATT_BLOCK) {
+            // DIST: slots of the first block in every lane group, loaded with
             // no branch (position clamped into the cache), so the row loads
-            // before them can be waited for alone and the QK-norm + RoPE
-            // overlaps these loads
+            // before them can be waited for alone and the q work (QP: the
+            // QK-norm + RoPE) overlaps these loads
             const uint32_t pc = p < a.ctx ? p : a.ctx - 1;
             kr[i] = *reinterpret_cast<const uint4 *>(kb + (size_t)pc * HD);
             vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)pc * HD);
@@ -199,11 +206,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
             vr[i] = *reinterpret_cast<const uint4 *>(vb + (size_t)p * HD);
         }
     }
-    // QP: the position was read first (a scalar load); the barrier keeps
+    // DIST: the position was read first (a scalar load); the barrier keeps
     // the compiler from sinking the loads above below the exit, which
     // would issue them only once the position is known
-    if constexpr (QP) __asm__ volatile("" ::: "memory");
-    const uint32_t L = (QP ? pos0 : a.step[1]) + 1;
+    if constexpr (DIST) __asm__ volatile("" ::: "memory");
+    const uint32_t L = (DIST ? pos0 : a.step[1]) + 1;
     if (sp * ATT_BLOCK >= L) return;  // no position in this split (the combine skips it)
     const bool owner = QP && ((L - 1) / ATT_BLOCK) % a.splits == sp;  // uniform over the workgroup
     // (QP: the current position's slot, if loaded here, is replaced below)
@@ -222,15 +229,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     half2_t qh[REP][4], ql[REP][4];
     float sscale[REP];
     uint4 kcur = {}, vcur = {};
-    if constexpr (QP) {
-        qk_norm_rope<LP>(rw, nw, cs, sn, HD, a.qp.eps);
+    if constexpr (DIST) {
+        if constexpr (QP) qk_norm_rope<LP>(rw, nw, cs, sn, HD, a.qp.eps);
         if (role < REP) {
             half2_t h[4], lo[4];
             const float f = q_split<LP>(rw, h, lo, a.scale);
             sqp[role][0][sub] = __builtin_bit_cast(uint4, h);
             sqp[role][1][sub] = __builtin_bit_cast(uint4, lo);
             if (sub == 0) ssc[role] = f;
-        } else if (owner && grp == REP) {
+        } else if (QP && owner && grp == REP) {
             uint32_t kw[4], vw[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -256,7 +263,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
             }
             sscale[r] = ssc[r];
         }
-        if (owner) {
+        if (QP && owner) {
             kcur = skv[0][sub];
             vcur = skv[1][sub];
         }
@@ -396,24 +403,28 @@ uint32_t attn_splits(uint32_t n_kv) {
 
 using AttnFn = void (*)(AttnArgs);
 // QP needs a lane group per query head plus one for k: REP < 2048 / HD
-template <int HD, int REP, bool QP>
+template <int HD, int REP, bool QP, bool DQ>
 static AttnFn rep_fn() {
     if constexpr (QP && REP >= ATT_THREADS / (HD / 8)) return nullptr;
-    else return k_attn<HD, REP, QP>;
+    else return k_attn<HD, REP, QP, DQ>;
 }
-template <int HD, bool QP = false>
+template <int HD, bool QP = false, bool DQ = false>
 static AttnFn pick_rep(uint32_t rep) {
     switch (rep) {
-    case 1: return rep_fn<HD, 1, QP>();
-    case 2: return rep_fn<HD, 2, QP>();
-    case 3: return rep_fn<HD, 3, QP>();
-    case 4: return rep_fn<HD, 4, QP>();
-    case 5: return rep_fn<HD, 5, QP>();
-    case 6: return rep_fn<HD, 6, QP>();
-    case 7: return rep_fn<HD, 7, QP>();
-    case 8: return rep_fn<HD, 8, QP>();
+    case 1: return rep_fn<HD, 1, QP, DQ>();
+    case 2: return rep_fn<HD, 2, QP, DQ>();
+    case 3: return rep_fn<HD, 3, QP, DQ>();
+    case 4: return rep_fn<HD, 4, QP, DQ>();
+    case 5: return rep_fn<HD, 5, QP, DQ>();
+    case 6: return rep_fn<HD, 6, QP, DQ>();
+    case 7: return rep_fn<HD, 7, QP, DQ>();
+    case 8: return rep_fn<HD, 8, QP, DQ>();
     default: return nullptr;
     }
+}
+template <int HD>
+static AttnFn pick_hd(uint32_t rep, bool qp, bool dq) {
+    return qp ? pick_rep<HD, true>(rep) : dq ? pick_rep<HD, false, true>(rep) : pick_rep<HD>(rep);
 }
 
 bool attn_qp_supported(uint32_t head_dim, uint32_t rep) {
@@ -424,7 +435,8 @@ bool attn_qp_supported(uint32_t head_dim, uint32_t rep) {
 hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *vc, float *part,
                             XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
                             uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s,
-                            const float *gate, uint32_t gstride, bool combine, const QkPrep *qp) {
+                            const float *gate, uint32_t gstride, bool combine, const QkPrep *qp,
+                            bool dq) {
     AttnArgs a;
     a.q = q;
     a.kc = kc;
@@ -448,9 +460,9 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
         a.qp = *qp;
     }
     switch (head_dim) {
-    case 64: fn = qp ? pick_rep<64, true>(rep) : pick_rep<64>(rep); break;
-    case 128: fn = qp ? pick_rep<128, true>(rep) : pick_rep<128>(rep); break;
-    case 256: fn = qp ? pick_rep<256, true>(rep) : pick_rep<256>(rep); break;
+    case 64: fn = pick_hd<64>(rep, qp, dq); break;
+    case 128: fn = pick_hd<128>(rep, qp, dq); break;
+    case 256: fn = pick_hd<256>(rep, qp, dq); break;
     default: return hipErrorInvalidValue;
     }
     if (!fn) return hipErrorInvalidValue;

@@ -46,7 +46,7 @@ hipError_t launch_attention(const float *q, const _Float16 *kc, const _Float16 *
                             XPack out, const uint32_t *step, uint32_t n_head, uint32_t n_kv,
                             uint32_t head_dim, uint32_t ctx, uint32_t splits, hipStream_t s,
                             const float *gate = nullptr, uint32_t gstride = 0,
-                            bool combine = true, const QkPrep *qp = nullptr);
+                            bool combine = true, const QkPrep *qp = nullptr, bool dq = false);
 
 // x = dequant(token_embd row step[0])  (TokenEmbd::linha, gpu.rs:297-304),
 // and the pack of x * nw for the first layer's q/k/v.  rope (n_pairs > 0):
@@ -125,6 +125,10 @@ struct lrs_model {
     // of its own): the {cos, sin} table of the token's position, written by
     // the embed kernel, head_dim / 2 pairs; null when off
     float2 *rope_cs = nullptr;
+    // the split attention's query heads split into f16 pairs by one lane
+    // group each and shared through LDS (LRS_ATTN_DQ=0: every lane group
+    // splits every head)
+    bool attn_dq = true;
     bool ao_wait_test = false;
     uint32_t *ao_sync = nullptr;
     size_t ao_sync_bytes = 0;
@@ -404,7 +408,8 @@ hipError_t op_attn(lrs_model *m, uint32_t l) {
     }
     return launch_attention(m->qbuf, L.kc, L.vc, m->pa, out, m->step, c.n_head, c.n_head_kv,
                             c.head_dim, c.ctx, m->a_splits, m->ctx->stream, gate,
-                            2 * c.head_dim, !ao_fused(m, L), qkp_fused(m, L) ? &qp : nullptr);
+                            2 * c.head_dim, !ao_fused(m, L), qkp_fused(m, L) ? &qp : nullptr,
+                            m->attn_dq);
 }
 
 // x += W_o att (or W_ssm_out y of a delta-net layer); pack of x * ffn_norm
@@ -841,6 +846,8 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         const char *v = getenv("LRS_AO");
         m->ao_on = !(v && (strcmp(v, "0") == 0 || strcasecmp(v, "false") == 0));
         m->ao_wait_test = env_on("LRS_AO_WAIT_TEST");
+        const char *vd = getenv("LRS_ATTN_DQ");
+        m->attn_dq = !(vd && (strcmp(vd, "0") == 0 || strcasecmp(vd, "false") == 0));
         const char *vq = getenv("LRS_QKP");
         const bool qkp_on = !(vq && (strcmp(vq, "0") == 0 || strcasecmp(vq, "false") == 0));
         if (m->hybrid && qkp_on && attn_qp_supported(c.head_dim, c.n_head / c.n_head_kv)) {

@@ -4,9 +4,11 @@ weights (the variables set to 0 at model creation):
   combine kernel then the o matvec (LRS_AO=0);
 - the hybrid's delta-net gate projections in the projection launch
   (k_mq_gates) against the step kernel computing them (LRS_DN_GATES=0).
+- the split kernel's query heads split by one lane group each and shared
+  through LDS against every lane group splitting every head (LRS_ATTN_DQ=0);
 - the hybrid's QK-norm + RoPE in the attention split kernel against its own
   launch (LRS_QKP=0), within a tolerance (see below).
-The first two run the same arithmetic in the same order (the combine's
+The first three run the same arithmetic in the same order (the combine's
 merge, the pack, the matvec's units and K-slice sums; the gate dots'
 per-thread sums, wavefront sums and their combination), so the logits must
 be bit-identical:
@@ -49,7 +51,7 @@ def ctx(lrs):
     c.close()
 
 
-SWITCHES = ("LRS_AO", "LRS_DN_GATES", "LRS_QKP")
+SWITCHES = ("LRS_AO", "LRS_DN_GATES", "LRS_QKP", "LRS_ATTN_DQ")
 
 
 def _pair(monkeypatch, make, off=("LRS_AO",)):
@@ -81,6 +83,25 @@ def test_combine_in_o_launch_is_bit_identical(lrs, orc, ctx, monkeypatch, name, 
         fused.reset()
         split.reset()
         assert fused.generate_greedy(prompt, 16).tolist() == split.generate_greedy(prompt, 16).tolist()
+    finally:
+        fused.close()
+        split.close()
+
+
+@pytest.mark.parametrize("name,cfg,mix", DENSE, ids=[c[0] for c in DENSE])
+def test_split_query_heads_shared_through_lds_is_bit_identical(lrs, orc, ctx, monkeypatch, name,
+                                                               cfg, mix):
+    """The split kernel's query heads split into f16 hi / lo pairs by one
+    lane group each and shared through LDS (the default) against every lane
+    group splitting every head (LRS_ATTN_DQ=0): the same per-head arithmetic
+    over the same lanes, so the logits are bit-identical."""
+    w = modelgen.host_model(orc, cfg, seed=31, mix=mix, mode=0, d_lo=1e-3, d_hi=1e-2)
+    fused, split = _pair(monkeypatch, lambda: modelgen.gpu_model(lrs, ctx, cfg, w), ("LRS_ATTN_DQ",))
+    try:
+        toks = np.random.default_rng(33).integers(0, cfg["vocab"], 40).tolist()
+        for pos, t in enumerate(toks):
+            a, b = fused.decode(t, pos), split.decode(t, pos)
+            assert np.array_equal(a, b), (name, pos, float(np.max(np.abs(a - b))))
     finally:
         fused.close()
         split.close()
