@@ -327,6 +327,16 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
                         s = __builtin_amdgcn_fdot2(qh[r][j], as_h2(kw[j]), s, false);
                     }
                     s = group_sum<LP>(s) * sscale[r];  // attention.rs: (q.k) / sqrt(head_dim)
+                    if (k0 == 0 && i == 0) {
+                        // the lane group's first position (slot 0 is its
+                        // smallest): the update below from m = -inf, l = 0,
+                        // acc = 0 gives exactly m = s, l = 1, acc = v
+                        m[r] = s;
+                        l[r] = 1.f;
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc[r][e] = vf[e];
+                        continue;
+                    }
                     const float mn = fmaxf(m[r], s);
                     const float c = expf(m[r] - mn), pe = expf(s - mn);
                     l[r] = fmaf(l[r], c, pe);
