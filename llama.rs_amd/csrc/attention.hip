@@ -237,19 +237,22 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
             sqp[role][0][sub] = __builtin_bit_cast(uint4, h);
             sqp[role][1][sub] = __builtin_bit_cast(uint4, lo);
             if (sub == 0) ssc[role] = f;
-        } else if (QP && owner && grp == REP) {
-            uint32_t kw[4], vw[4];
+        }
+        if constexpr (QP) {
+            if (owner && grp == REP) {
+                uint32_t kw[4], vw[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                kw[i] = __builtin_bit_cast(uint32_t, half2_t{(_Float16)rw[2 * i], (_Float16)rw[2 * i + 1]});
-                vw[i] = __builtin_bit_cast(uint32_t, half2_t{(_Float16)vnew[2 * i], (_Float16)vnew[2 * i + 1]});
+                for (int i = 0; i < 4; i++) {
+                    kw[i] = __builtin_bit_cast(uint32_t, half2_t{(_Float16)rw[2 * i], (_Float16)rw[2 * i + 1]});
+                    vw[i] = __builtin_bit_cast(uint32_t, half2_t{(_Float16)vnew[2 * i], (_Float16)vnew[2 * i + 1]});
+                }
+                const uint4 k4 = make_uint4(kw[0], kw[1], kw[2], kw[3]), v4 = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+                skv[0][sub] = k4;
+                skv[1][sub] = v4;
+                const size_t o = ((size_t)kh * a.ctx + (L - 1)) * HD + 8 * sub;
+                *reinterpret_cast<uint4 *>(a.qp.kc + o) = k4;
+                *reinterpret_cast<uint4 *>(a.qp.vc + o) = v4;
             }
-            const uint4 k4 = make_uint4(kw[0], kw[1], kw[2], kw[3]), v4 = make_uint4(vw[0], vw[1], vw[2], vw[3]);
-            skv[0][sub] = k4;
-            skv[1][sub] = v4;
-            const size_t o = ((size_t)kh * a.ctx + (L - 1)) * HD + 8 * sub;
-            *reinterpret_cast<uint4 *>(a.qp.kc + o) = k4;
-            *reinterpret_cast<uint4 *>(a.qp.vc + o) = v4;
         }
         __syncthreads();
 #pragma unroll

@@ -121,10 +121,13 @@ struct lrs_model {
     // (a row of 64 words per o workgroup, one word per producer); all zero
     // between launches
     bool ao_on = true;
-    // the hybrid's QK-norm + RoPE in the attention split (LRS_QKP=0: a launch
-    // of its own): the {cos, sin} table of the token's position, written by
-    // the embed kernel, head_dim / 2 pairs; null when off
+    // the {cos, sin} table of the token's position, written by the embed
+    // kernel, head_dim / 2 pairs: read by the hybrid's attention split when
+    // it does the QK-norm + RoPE (LRS_QKP=0: a launch of its own), and by the
+    // dense model's q/k/v epilogue (rope_qkv; LRS_ROPE_TABLE=0: sincosf
+    // there); null when neither uses it
     float2 *rope_cs = nullptr;
+    bool rope_qkv = false;
     // the split attention's query heads split into f16 pairs by one lane
     // group each and shared through LDS (LRS_ATTN_DQ=0: every lane group
     // splits every head)
@@ -316,6 +319,7 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
     a.eps = c.rms_eps;
     a.step = m->step;
     a.freq = m->freq;
+    a.rope = m->rope_qkv ? reinterpret_cast<const float *>(m->rope_cs) : nullptr;
     a.head_dim = c.head_dim;
     a.rope_dim = c.rope_dim;
     a.ctx = c.ctx;
@@ -377,7 +381,7 @@ hipError_t op_qkv(lrs_model *m, uint32_t l) {
 // attention layers whose o weight has the kernel and takes the 22-bit pack
 // whether layer L's QK-norm + RoPE run in its attention split (the gated
 // attention of the hybrid model; LRS_QKP=0 keeps the separate launch)
-bool qkp_fused(const lrs_model *m, const DevLayer &L) { return !L.dn && m->rope_cs; }
+bool qkp_fused(const lrs_model *m, const DevLayer &L) { return m->hybrid && !L.dn && m->rope_cs; }
 
 bool ao_fused(const lrs_model *m, const DevLayer &L) {
     const lrs_config &c = m->cfg;
@@ -850,7 +854,10 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         m->attn_dq = !(vd && (strcmp(vd, "0") == 0 || strcasecmp(vd, "false") == 0));
         const char *vq = getenv("LRS_QKP");
         const bool qkp_on = !(vq && (strcmp(vq, "0") == 0 || strcasecmp(vq, "false") == 0));
-        if (m->hybrid && qkp_on && attn_qp_supported(c.head_dim, c.n_head / c.n_head_kv)) {
+        const char *vr = getenv("LRS_ROPE_TABLE");
+        m->rope_qkv = !m->hybrid && !(vr && (strcmp(vr, "0") == 0 || strcasecmp(vr, "false") == 0));
+        if ((m->hybrid && qkp_on && attn_qp_supported(c.head_dim, c.n_head / c.n_head_kv)) ||
+            m->rope_qkv) {
             const size_t rb = c.head_dim / 2 * sizeof(float2);
             if ((rc = dev_alloc(m, rb, (void **)&m->rope_cs))) return rc;
             if (hipMemset(m->rope_cs, 0, rb) != hipSuccess) return fail(LRS_E_HIP, "memset");

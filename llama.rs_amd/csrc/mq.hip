@@ -573,13 +573,20 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     // bias, the residual and its norm weight)
     const uint32_t eo = threadIdx.x, erow = tile0 * 16 + eo;
     const bool evalid = eo < otiles_wg * 16 && erow < sg.rows;
-    float e_bias = 0.f, e_x = 0.f, e_nw = 1.f, e_freq = 0.f;
+    float e_bias = 0.f, e_x = 0.f, e_nw = 1.f, e_freq = 0.f, e_cs = 1.f, e_sn = 0.f;
     uint32_t e_pos = 0;
     if (sg.bias && evalid) e_bias = sg.bias[erow];
     if constexpr (EPI == MQ_QKV) {
         e_pos = a.step[1];
         const uint32_t dd = erow % a.head_dim;
-        if (evalid && sg.kind < 2 && dd < a.rope_dim) e_freq = a.freq[dd >> 1];
+        if (evalid && sg.kind < 2 && dd < a.rope_dim) {
+            if (a.rope) {
+                e_cs = a.rope[2 * (dd >> 1)];
+                e_sn = a.rope[2 * (dd >> 1) + 1];
+            } else {
+                e_freq = a.freq[dd >> 1];
+            }
+        }
     }
     if constexpr (EPI == MQ_RESID) {
         if (evalid) {
@@ -855,9 +862,11 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         const float yo = __shfl_xor(y, 1, 64);
         const uint32_t dd = row % a.head_dim;
         if (sg.kind < 2 && dd < a.rope_dim) {
-            const float th = (float)pos * e_freq;
-            float sn, cs;
-            sincosf(th, &sn, &cs);
+            float sn = e_sn, cs = e_cs;
+            if (!a.rope) {
+                const float th = (float)pos * e_freq;
+                sincosf(th, &sn, &cs);
+            }
             y = (row & 1) ? yo * sn + y * cs : y * cs - yo * sn;
         }
         if (valid) {

@@ -72,6 +72,10 @@ struct MqArgs {
     // MQ_QKV
     const uint32_t *step;    // device {token, pos}
     const float *freq;       // RoPE frequencies [rope_dim / 2]
+    // optional: {cos, sin} of the position's angle for each pair (floats
+    // 2i, 2i + 1), written by the token's first kernel with the same
+    // expression (then no sincosf here)
+    const float *rope;
     uint32_t head_dim, rope_dim, ctx;
     // greedy (MQ_STORE)
     unsigned long long *amax;  // [workgroups] argmax keys of the rows, or null

@@ -6,9 +6,11 @@ weights (the variables set to 0 at model creation):
   (k_mq_gates) against the step kernel computing them (LRS_DN_GATES=0).
 - the split kernel's query heads split by one lane group each and shared
   through LDS against every lane group splitting every head (LRS_ATTN_DQ=0);
+- the dense q/k/v epilogue's RoPE angles from the embed kernel's table
+  against sincosf in the epilogue (LRS_ROPE_TABLE=0);
 - the hybrid's QK-norm + RoPE in the attention split kernel against its own
   launch (LRS_QKP=0), within a tolerance (see below).
-The first three run the same arithmetic in the same order (the combine's
+The first four run the same arithmetic in the same order (the combine's
 merge, the pack, the matvec's units and K-slice sums; the gate dots'
 per-thread sums, wavefront sums and their combination), so the logits must
 be bit-identical:
@@ -51,7 +53,7 @@ def ctx(lrs):
     c.close()
 
 
-SWITCHES = ("LRS_AO", "LRS_DN_GATES", "LRS_QKP", "LRS_ATTN_DQ")
+SWITCHES = ("LRS_AO", "LRS_DN_GATES", "LRS_QKP", "LRS_ATTN_DQ", "LRS_ROPE_TABLE")
 
 
 def _pair(monkeypatch, make, off=("LRS_AO",)):
@@ -102,6 +104,28 @@ def test_split_query_heads_shared_through_lds_is_bit_identical(lrs, orc, ctx, mo
         for pos, t in enumerate(toks):
             a, b = fused.decode(t, pos), split.decode(t, pos)
             assert np.array_equal(a, b), (name, pos, float(np.max(np.abs(a - b))))
+    finally:
+        fused.close()
+        split.close()
+
+
+@pytest.mark.parametrize("name,cfg,mix", DENSE, ids=[c[0] for c in DENSE])
+def test_rope_table_in_qkv_epilogue_is_bit_identical(lrs, orc, ctx, monkeypatch, name, cfg, mix):
+    """The q/k/v epilogue's RoPE cosines and sines from the table the embed
+    kernel writes (the default) against sincosf in the epilogue
+    (LRS_ROPE_TABLE=0): the same expression on the same operands, so the
+    logits are bit-identical over 40 positions (angles up to 39 rad)."""
+    w = modelgen.host_model(orc, cfg, seed=35, mix=mix, mode=0, d_lo=1e-3, d_hi=1e-2)
+    fused, split = _pair(monkeypatch, lambda: modelgen.gpu_model(lrs, ctx, cfg, w),
+                         ("LRS_ROPE_TABLE",))
+    try:
+        toks = np.random.default_rng(37).integers(0, cfg["vocab"], 40).tolist()
+        for pos, t in enumerate(toks):
+            a, b = fused.decode(t, pos), split.decode(t, pos)
+            assert np.array_equal(a, b), (name, pos, float(np.max(np.abs(a - b))))
+        fused.reset()
+        split.reset()
+        assert fused.generate_greedy(toks[:8], 16).tolist() == split.generate_greedy(toks[:8], 16).tolist()
     finally:
         fused.close()
         split.close()
