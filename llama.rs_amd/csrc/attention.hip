@@ -123,7 +123,10 @@ __device__ __forceinline__ void ld8(float (&v)[8], T *p) {
 // reads that position).  Both go through LDS to every lane group; the
 // current row replaces what its slot's load returned.  The rotation's
 // cosines / sines for the position come from a.qp.rope (written by the
-// token's first kernel), so every lane group does one row's work.
+// token's first kernel), so every lane group does one row's work.  DQ (q
+// already normalised and rotated, the dense model): lane group g < REP
+// alone splits query head g into its f16 pairs and shares them through LDS,
+// as QP does; without either, every lane group splits every head itself.
 template <int HD, int REP, bool QP = false, bool DQ = false>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn(AttnArgs a) {
     constexpr int LP = HD / 8;              // lanes per position
