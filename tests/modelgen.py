@@ -9,6 +9,10 @@ TINY = dict(n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512,
 # GQA with 5 query heads per KV head and head_dim 128, like the 32B shape
 GQA5 = dict(n_layer=2, n_embd=1280, n_head=10, n_head_kv=2, head_dim=128, n_ff=1024,
             vocab=1000, rope_dim=128, ctx=160, rms_eps=1e-6, freq_base=1e6)
+# head_dim 256 with 8 query heads per KV head: the split kernel's lane
+# groups (8 at head_dim 256) each take one query head
+HD256R8 = dict(n_layer=2, n_embd=512, n_head=8, n_head_kv=1, head_dim=256, n_ff=512, vocab=512,
+               rope_dim=256, ctx=96, rms_eps=1e-6, freq_base=1e4)
 # o and down with K = 2048 over few output tiles: the prompt block splits
 # their K across workgroups and adds the slices in the fused reduce + RMSNorm
 KSPLIT = dict(n_layer=2, n_embd=512, n_head=16, n_head_kv=2, head_dim=128, n_ff=2048,

@@ -43,6 +43,7 @@ DENSE = [
     ("tiny-q5km", modelgen.TINY, modelgen.Q5_K_M),
     ("gqa5-o-q6k", modelgen.GQA5, dict(modelgen.Q4_K_M, attn_output=modelgen.Q6_K)),
     ("c3-width", C3W, modelgen.Q4_K_M),
+    ("hd256-rep8", modelgen.HD256R8, modelgen.Q4_K_M),
 ]
 
 

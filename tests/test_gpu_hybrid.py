@@ -85,6 +85,33 @@ def test_hybrid_long_context_decode_matches_oracle(lrs, orc, ctx):
     print(f"hy-mid long: worst rel L2 {worst:.2e} at lengths {checks}")
 
 
+def test_hybrid_decode_fills_the_cache(lrs, orc, ctx):
+    """Every position of a 64-position cache through decode() (the split
+    kernel clamps its first block's loads into the cache and writes the
+    current K/V row itself), checked against the oracle at the last
+    positions and greedy-continued from a reset."""
+    cfg = modelgen.HY_TINY
+    w = modelgen.hybrid_host_model(orc, cfg, seed=29)
+    gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
+    om = orc.HybridModel(cfg, w, kv_f16=True, threads=8)
+    seq = np.random.default_rng(31).integers(0, cfg["vocab"], cfg["ctx"]).tolist()
+    try:
+        done = 0
+        for pos, t in enumerate(seq):
+            g = gm.decode(t, pos)
+            if pos + 1 in (cfg["ctx"] - 1, cfg["ctx"]):
+                o = om.forward(seq[done:pos + 1])
+                done = pos + 1
+                assert rel_l2(g, o) < LOGIT_TOL, (pos, rel_l2(g, o))
+                assert int(np.argmax(g)) == int(np.argmax(o)), pos
+        gm.reset()
+        om2 = orc.HybridModel(cfg, w, kv_f16=True, threads=8)
+        want = modelgen.oracle_greedy(om2, seq[:8], cfg["ctx"] - 8)
+        assert gm.generate_greedy(seq[:8], cfg["ctx"] - 8).tolist() == want
+    finally:
+        gm.close()
+
+
 def test_hybrid_batch_reset_and_position_rule(lrs, orc, ctx):
     """decode_batch runs the prompt block through the GEMMs, the block
     delta-net kernels and the batched gated attention; the token loop and the

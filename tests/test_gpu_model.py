@@ -34,6 +34,7 @@ CASES = [
 
     ("gqa5-q4km", modelgen.GQA5, modelgen.Q4_K_M, 1),
     ("gqa5-q4km-baseline-dist", modelgen.GQA5, modelgen.Q4_K_M, 0),
+    ("hd256-rep8-q4km", modelgen.HD256R8, modelgen.Q4_K_M, 1),
 ]
 
 
