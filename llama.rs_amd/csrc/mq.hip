@@ -485,12 +485,14 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
     float xv0[B];
     constexpr uint32_t NT = 64 * W;  // threads of the workgroup
     if constexpr (XF) {
-        // branch-free (clamped index, then select) so that the wait before
-        // packing counts exactly these loads
+        // branch-free (index wrapped into the input, then select) so that
+        // the wait before packing counts exactly these loads; wrapped, not
+        // clamped: every workgroup's lanes past the input would otherwise
+        // all read the input's last line
 #pragma unroll
         for (int k = 0; k < B; k++) {
             const uint32_t e = threadIdx.x + k * NT;
-            const float t = a.xf[e < a.n_in ? e : a.n_in - 1];
+            const float t = a.xf[e < a.n_in ? e : e % a.n_in];
             xv0[k] = e < a.n_in ? t : 0.f;
         }
     }
@@ -541,6 +543,9 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
                 // half-waves past the pack store nothing
 #pragma unroll
                 for (int k = 0; k < B; k++) {
+                    // batches past the input store nothing: skipped whole
+                    // (a branch uniform over the workgroup)
+                    if (k * NT >= ne) break;
                     const uint32_t e = e0 + k * NT;
                     pack_half(xv0[k], e < ne ? e >> 5 : 0, xl, e < ne);
                 }
