@@ -63,6 +63,19 @@ __global__ __launch_bounds__(256) void k_embed(WeightView w, const uint32_t *__r
     uint32_t tok = step[0];
     if (tok >= w.n_out) tok = w.n_out - 1;  // ids are validated on the host
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;  // n_in is a multiple of 256
+    // block types: the GGUF blocks of this workgroup's 256 elements staged
+    // in LDS first, one byte per thread (each element then reads its
+    // block's bytes from LDS, not 4-17 separate loads from the weights)
+    __shared__ uint8_t blk[8 * 210];  // 256 elements: one K-quant block or 8 Q8_0 / Q4_0 blocks
+    const bool staged = w.type != T_F16 && w.type != T_F32;
+    const uint32_t bb = (uint32_t)block_bytes(w.type);
+    const uint32_t b0 = blockIdx.x * blockDim.x / be;  // first block in the row
+    if (staged) {
+        const uint32_t nbytes = 256 / be * bb;
+        for (uint32_t t = threadIdx.x; t < nbytes; t += blockDim.x)
+            blk[t] = gbyte(w, tok, b0 + t / bb, t % bb);
+        __syncthreads();
+    }
     if (i < n_pairs) {
         float sn = 0.f, cs = 1.f;
         if (i < rope_pairs) {
@@ -71,8 +84,14 @@ __global__ __launch_bounds__(256) void k_embed(WeightView w, const uint32_t *__r
         }
         rope[i] = make_float2(cs, sn);
     }
-    const uint64_t e = (uint64_t)tok * w.n_in + i;
-    const float v = deq_elem(w, e / be, (uint32_t)(e % be));
+    float v;
+    if (staged) {
+        const uint8_t *bp = blk + (threadIdx.x / be) * bb;
+        v = deq_block_elem(w.type, threadIdx.x % be, [&](uint32_t o) { return bp[o]; });
+    } else {
+        const uint64_t e = (uint64_t)tok * w.n_in + i;
+        v = deq_elem(w, e / be, (uint32_t)(e % be));
+    }
     x[i] = v;
     pack_half(v * nw[i], i >> 5, p);
     const float sq = half_sum(v * v);  // the first RMSNorm's block sums

@@ -36,20 +36,18 @@ __device__ __forceinline__ uint8_t gbyte(const WeightView &w, uint32_t row, uint
     return w.q[((size_t)row * w.nb + blk) * (size_t)block_bytes(w.type) + o];
 }
 
-// element e (0..255) of GGUF block b (= row * nb + block in row) of a resident weight
-__device__ __forceinline__ float deq_elem(const WeightView &w, uint64_t b, uint32_t e) {
-    if (w.type == T_F16) return h2f(reinterpret_cast<const uint16_t *>(w.q)[b]);
-    if (w.type == T_F32) return reinterpret_cast<const float *>(w.q)[b];
-    const uint32_t row = (uint32_t)(b / w.nb), blk = (uint32_t)(b % w.nb);
-    auto B = [&](uint32_t o) { return gbyte(w, row, blk, o); };
-    switch (w.type) {
+// element e (0..255) of one GGUF block of a block type (Q8_0, Q4_0, Q4_K,
+// Q5_K, Q6_K) whose byte o is B(o)
+template <typename BF>
+__device__ __forceinline__ float deq_block_elem(uint32_t type, uint32_t e, BF B) {
+    switch (type) {
     case T_Q8_0:
         // dequant.rs:58-76
         return __fmul_rn((float)(int8_t)B(2 + e), h2f((uint16_t)(B(0) | (B(1) << 8))));
     case T_Q4_K:
     case T_Q5_K: {
         // dequant.rs:112-150 / 157-203
-        const bool q5 = w.type == T_Q5_K;
+        const bool q5 = type == T_Q5_K;
         const float dv = h2f((uint16_t)(B(0) | (B(1) << 8)));
         const float mv = h2f((uint16_t)(B(2) | (B(3) << 8)));
         const uint32_t grp = e >> 6, within = e & 63, l = within & 31, hi = within >> 5;
@@ -84,6 +82,14 @@ __device__ __forceinline__ float deq_elem(const WeightView &w, uint64_t b, uint3
     default:
         return 0.0f;
     }
+}
+
+// element e (0..255) of GGUF block b (= row * nb + block in row) of a resident weight
+__device__ __forceinline__ float deq_elem(const WeightView &w, uint64_t b, uint32_t e) {
+    if (w.type == T_F16) return h2f(reinterpret_cast<const uint16_t *>(w.q)[b]);
+    if (w.type == T_F32) return reinterpret_cast<const float *>(w.q)[b];
+    const uint32_t row = (uint32_t)(b / w.nb), blk = (uint32_t)(b % w.nb);
+    return deq_block_elem(w.type, e, [&](uint32_t o) { return gbyte(w, row, blk, o); });
 }
 
 }  // namespace lrs
