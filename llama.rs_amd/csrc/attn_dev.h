@@ -60,10 +60,12 @@ __device__ __forceinline__ float group_sum(float v) {
 // position arrives); then wave 0 forms the split weights and thread d < hd
 // owns dim d.  Gated attention (gate non-null, gate_quant.comp): the output
 // is multiplied by sigmoid(gate[h * gstride + d]).  AG: the pack is written
-// with agent-scope stores, for a reader in the same launch.
+// with agent-scope stores, for a reader in the same launch.  CP: cache
+// policy of the partials' loads (agent scope when the splits ran in the
+// same launch).
 // pl: LDS for splits * (hd + 4) floats (16-byte aligned); wsh: 64 floats;
 // red: 1 float.  splits <= 64; hd a multiple of 64, at most blockDim.x.
-template <bool AG>
+template <bool AG, int CP = 0>
 __device__ __forceinline__ void attn_combine_head(const float *__restrict__ part, uint32_t splits,
                                                   uint32_t hd, const uint32_t *__restrict__ step,
                                                   const float *__restrict__ gate, uint32_t gstride,
@@ -77,7 +79,7 @@ __device__ __forceinline__ void attn_combine_head(const float *__restrict__ part
     for (uint32_t base = wave * 1024; base < bytes; base += blockDim.x * 16) {
         const uint32_t off = base + lane * 16;
         if (off < bytes)
-            __builtin_amdgcn_global_load_lds(src + off, (lds_v *)(reinterpret_cast<uint8_t *>(pl) + base), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src + off, (lds_v *)(reinterpret_cast<uint8_t *>(pl) + base), 16, 0, CP);
     }
     // the output gate of (head h, dim d), loaded with the partials
     const float gv = gate && d < hd ? gate[(size_t)h * gstride + d] : 0.f;

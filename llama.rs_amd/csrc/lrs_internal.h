@@ -96,6 +96,14 @@ bool mq_geom_supported(const MqGeom &g);
 bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits,
                      uint32_t n_head);
 hipError_t launch_mq_ao(const MqArgs &a, const AoArgs &c, uint32_t t, hipStream_t s);
+struct QkPrep;
+// the attention split, its combine and the o-projection in one launch
+// (k_mq_sao); c.n_prod = n_head, c.sflag: 64 zeroed words per query head
+bool attn_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits,
+                       uint32_t n_head, uint32_t n_kv, bool qp, bool dq);
+hipError_t launch_attn_ao(const float *q, const _Float16 *kc, const _Float16 *vc, uint32_t n_kv,
+                          uint32_t ctx, const QkPrep *qp, bool dq, const MqArgs &a, const AoArgs &c,
+                          uint32_t t, hipStream_t s);
 MqGeom store_geom(uint32_t t, uint32_t n_in, uint32_t n_out);
 // plain-matvec launch shape override (tiles per wave, tile groups, K-slices; all 0 = automatic)
 int set_matvec_geom(int tpw, int tg, int ks);

@@ -152,6 +152,7 @@ struct lrs_model {
     // splits every head)
     bool attn_dq = true;
     bool ao_wait_test = false;
+    bool sao_on = true;  // attention split + combine + o in one launch (k_mq_sao; LRS_SAO=0: two launches)
     uint32_t *ao_sync = nullptr;
     size_t ao_sync_bytes = 0;
     // packs: x*attn_norm (or x*output_norm), x*ffn_norm, attention output,
@@ -408,27 +409,40 @@ bool ao_fused(const lrs_model *m, const DevLayer &L) {
            mq_ao_supported(L.o->v.type, L.o->v.n_in, c.n_embd, c.head_dim, m->a_splits, c.n_head);
 }
 
+// whether layer L's attention split runs in the o launch too (k_mq_sao)
+bool sao_fused(const lrs_model *m, const DevLayer &L) {
+    const lrs_config &c = m->cfg;
+    return m->sao_on && ao_fused(m, L) &&
+           attn_ao_supported(L.o->v.type, L.o->v.n_in, c.n_embd, c.head_dim, m->a_splits, c.n_head,
+                             c.n_head_kv, qkp_fused(m, L), m->attn_dq);
+}
+
+// QK-norm + RoPE inputs of layer L's split (qkp_fused)
+QkPrep qk_prep(const lrs_model *m, const DevLayer &L) {
+    QkPrep qp = {};
+    qp.qg = m->qg;
+    qp.kb = m->kb;
+    qp.vb = m->vb;
+    qp.q_norm = L.q_norm;
+    qp.k_norm = L.k_norm;
+    qp.rope = m->rope_cs;
+    qp.kc = L.kc;
+    qp.vc = L.vc;
+    qp.eps = m->cfg.rms_eps;
+    return qp;
+}
+
 // attention over the f16 cache; hybrid layers gate the output with
 // sigmoid(second half of each head's Q rows) before packing it (the combine
 // in the o launch when ao_fused)
 hipError_t op_attn(lrs_model *m, uint32_t l) {
     const lrs_config &c = m->cfg;
     const DevLayer &L = m->layers[l];
+    if (sao_fused(m, L)) return hipSuccess;  // the o launch runs the split
     const float *gate = m->hybrid ? m->qg + c.head_dim : nullptr;
     XPack out = m->pk_a;
     out.q8 = L.o_q8;
-    QkPrep qp = {};
-    if (qkp_fused(m, L)) {
-        qp.qg = m->qg;
-        qp.kb = m->kb;
-        qp.vb = m->vb;
-        qp.q_norm = L.q_norm;
-        qp.k_norm = L.k_norm;
-        qp.rope = m->rope_cs;
-        qp.kc = L.kc;
-        qp.vc = L.vc;
-        qp.eps = c.rms_eps;
-    }
+    const QkPrep qp = qkp_fused(m, L) ? qk_prep(m, L) : QkPrep{};
     return launch_attention(m->qbuf, L.kc, L.vc, m->pa, out, m->step, c.n_head, c.n_head_kv,
                             c.head_dim, c.ctx, m->a_splits, m->ctx->stream, gate,
                             2 * c.head_dim, !ao_fused(m, L), qkp_fused(m, L) ? &qp : nullptr,
@@ -478,6 +492,12 @@ hipError_t op_o(lrs_model *m, uint32_t l) {
         a.werr = m->ao_sync + 32;
         a.wflag = m->ao_sync + 64;
         a.step = m->step;
+        if (sao_fused(m, L)) {
+            ao.sflag = m->ao_sync + 64 + 64 * (size_t)(c.n_embd / 32);
+            const QkPrep qp = qk_prep(m, L);
+            return launch_attn_ao(m->qbuf, L.kc, L.vc, c.n_head_kv, c.ctx, qkp_fused(m, L) ? &qp : nullptr,
+                                  m->attn_dq, a, ao, wo->v.type, m->ctx->stream);
+        }
         return launch_mq_ao(a, ao, wo->v.type, m->ctx->stream);
     }
     return launch_mq(a, wo->v.type, wo->v.type, env_geom("LRS_GEOM_O", G_O), MQ_RESID,
@@ -860,8 +880,9 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
             return rc;
         if (hipMemset(m->xcnt, 0, nb * sizeof(uint32_t)) != hipSuccess)
             return fail(LRS_E_HIP, "memset");
-        // error word and a row of flags per 32 rows of o's output
-        const size_t aw = 64 + 64 * (size_t)(c.n_embd / 32);
+        // error word, a row of flags per 32 rows of o's output, then a row
+        // per query head (the splits' flags of k_mq_sao)
+        const size_t aw = 64 + 64 * (size_t)(c.n_embd / 32) + 64 * (size_t)c.n_head;
         if ((rc = dev_alloc(m, aw * sizeof(uint32_t), (void **)&m->ao_sync))) return rc;
         m->ao_sync_bytes = aw * sizeof(uint32_t);
         if (hipMemset(m->ao_sync, 0, aw * sizeof(uint32_t)) != hipSuccess)
@@ -869,6 +890,8 @@ int finish_model(lrs_model *m, const float *output_norm, const std::vector<float
         const char *v = getenv("LRS_AO");
         m->ao_on = !(v && (strcmp(v, "0") == 0 || strcasecmp(v, "false") == 0));
         m->ao_wait_test = env_on("LRS_AO_WAIT_TEST");
+        const char *vs = getenv("LRS_SAO");
+        m->sao_on = !(vs && (strcmp(vs, "0") == 0 || strcasecmp(vs, "false") == 0));
         const char *vd = getenv("LRS_ATTN_DQ");
         m->attn_dq = !(vd && (strcmp(vd, "0") == 0 || strcasecmp(vd, "false") == 0));
         const char *vq = getenv("LRS_QKP");

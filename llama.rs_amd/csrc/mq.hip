@@ -38,6 +38,7 @@
 // its f32 input inside each workgroup and runs up to NC input columns over
 // every weight load (each column bit-identical to a one-column call).
 #include "attn_dev.h"
+#include "attn_split_dev.h"
 #include "dn_dev.h"
 #include "lrs_internal.h"
 #include "mq_args.h"
@@ -434,6 +435,28 @@ __device__ __forceinline__ void copy_to_lds(const uint8_t *__restrict__ g, uint8
 // producers take
 constexpr uint32_t MQ_WAIT_POLLS = 1u << 16;
 
+// one wavefront waits until flags row[0..n) (n <= 64) are all non-zero (lane
+// i polls flag i: one load per poll for the wavefront), then clears them
+// for the next launch; after `polls` polls (0: MQ_WAIT_POLLS) it sets *werr
+// to 1 and goes on
+__device__ __forceinline__ void wait_flags(uint32_t *row, uint32_t n, uint32_t polls, uint32_t *werr) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t *f = row + lane;
+    const bool mine = lane < n;
+    const uint32_t limit = polls ? polls : MQ_WAIT_POLLS;
+    uint32_t k = 0;
+    for (;;) {
+        const uint32_t v = mine ? __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1u;
+        if (__all(v != 0u)) break;
+        if (++k >= limit) {
+            if (lane == 0) __hip_atomic_store(werr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    if (mine) __hip_atomic_store(f, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // body for the segments [s_lo, s_hi) of type T (one workgroup).  NC > 1 or
 // XF (MQ_STORE only): NC input columns share each weight load, their packs
 // side by side in LDS; with XF the workgroup packs the f32 columns a.xf
@@ -622,24 +645,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         // per poll for the wavefront; bounded), clears them for the next
         // launch, then the workgroup stages the pack with loads that see the
         // producers' stores
-        if (wave == 0) {
-            uint32_t *f = a.wflag + 64 * (size_t)wrel + lane;
-            const bool mine = lane < a.n_wait;
-            const uint32_t limit = a.wait_polls ? a.wait_polls : MQ_WAIT_POLLS;
-            uint32_t n = 0;
-            for (;;) {
-                const uint32_t v =
-                    mine ? __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1u;
-                if (__all(v != 0u)) break;
-                if (++n >= limit) {
-                    if (lane == 0)
-                        __hip_atomic_store(a.werr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-            }
-            if (mine) __hip_atomic_store(f, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (wave == 0) wait_flags(a.wflag + 64 * (size_t)wrel, a.n_wait, a.wait_polls, a.werr);
         __syncthreads();
         copy_to_lds<CPOL_SC1>(reinterpret_cast<const uint8_t *>(a.xin.dig), lds, nxl * 96);
         copy_to_lds<CPOL_SC1>(reinterpret_cast<const uint8_t *>(a.xin.meta), lds + lp.meta, nxl * 16);
@@ -946,6 +952,53 @@ __attribute__((amdgpu_waves_per_eu(mq_waves_per_eu<TG * KS>()))) void k_mq_ao(Mq
     mq_body<T, TPW, TG, KS, P, MQ_RESID, 1, false, true>(a, 0, lds, red);
 }
 
+// The attention split, the combine and the o-projection in one launch, so
+// that o's weight stream runs while the splits and the combine do.
+// Workgroups [0, splits * n_kv) are the splits (threads 0..ATT_THREADS-1;
+// the rest leave at once): partials with agent-scope stores, then, once
+// they are complete, flag sp in the rows of the group's REP query heads
+// (c.sflag).  Workgroups [.., + c.n_prod) are the combine of k_mq_ao, each
+// first waiting (wavefront 0, bounded) for its head's live splits and
+// loading their partials with agent-scope loads; the o workgroups follow
+// (mq_body, WT).  Every wait is on workgroups with lower ids, which are
+// dispatched first.
+template <uint32_t T, int TPW, int TG, int KS, int P, int HD, int REP, bool QP, bool DQ>
+__global__ __launch_bounds__(64 * TG * KS) void k_mq_sao(MqArgs a, AoArgs c, AttnArgs s) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float red[TG * KS * TPW * 16 + TG * KS + 1];
+    __shared__ float wsh[64];
+    static_assert(64 * TG * KS >= ATT_THREADS, "the split role takes ATT_THREADS threads");
+    const uint32_t nsw = s.splits * s.n_kv;
+    if (blockIdx.x < nsw) {
+        if (threadIdx.x >= ATT_THREADS) return;  // whole wavefronts
+        const uint32_t sp = blockIdx.x % s.splits, kh = blockIdx.x / s.splits;
+        if (!attn_split<HD, REP, QP, DQ, true>(s, sp, kh, *reinterpret_cast<AttnLds<HD, REP, QP, DQ> *>(lds)))
+            return;  // no position in this split: no partial, no flag
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's partial stores are complete
+        __syncthreads();
+        if (!c.no_signal && threadIdx.x < REP)
+            __hip_atomic_store(c.sflag + 64 * (size_t)(kh * REP + threadIdx.x) + sp, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (blockIdx.x < nsw + c.n_prod) {
+        const uint32_t h = blockIdx.x - nsw;
+        if (threadIdx.x < 64)
+            wait_flags(c.sflag + 64 * (size_t)h, attn_live_splits(a.step[1] + 1, c.splits), a.wait_polls,
+                       a.werr);
+        __syncthreads();
+        attn_combine_head<true, CPOL_SC1>(c.part, c.splits, c.head_dim, a.step, c.gate, c.gstride, a.xin, h,
+                                          reinterpret_cast<float *>(lds), wsh, red);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's pack stores are complete
+        __syncthreads();
+        if (!c.no_signal)
+            for (uint32_t t = threadIdx.x; t < c.n_cons; t += blockDim.x)
+                __hip_atomic_store(a.wflag + 64 * (size_t)t + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    mq_body<T, TPW, TG, KS, P, MQ_RESID, 1, false, true>(a, 0, lds, red);
+}
+
 // The delta-net projections (MQ_STORE over ssm_qkv and ssm_gate) with the
 // layer's gate projections in the same launch: the workgroups past the
 // matvec's (n_mq of them), one per value head, compute the head's
@@ -1163,6 +1216,86 @@ bool mq_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim
     return pick_ao(t, n_in) != nullptr && rows % 32 == 0 && rows > 0 && n_head >= 1 && n_head <= 64 &&
            (head_dim == 64 || head_dim == 128 || head_dim == 256) && splits >= 1 && splits <= 64 &&
            ao_lds(pack_blocks(t, n_in), head_dim, splits) <= 160 * 1024;
+}
+
+// ---------------------------------------------------------------------------
+// attention split + combine + o-projection (k_mq_sao): the o weight in Q4_K,
+// shape (1, 2, 4, P) as k_mq_ao; the head shapes built (HD, REP, QK-norm +
+// RoPE in the split or the dense model's shared q split, P)
+// ---------------------------------------------------------------------------
+using MqSaoFn = void (*)(MqArgs, AoArgs, AttnArgs);
+struct SaoShape {
+    uint32_t hd, rep;
+    bool qp, dq;
+    int p;
+    MqSaoFn fn;
+    size_t lds;
+};
+#define LRS_SAO(HD, REP, QP, DQ, P)                                                                  \
+    SaoShape{HD, REP, QP, DQ, P, k_mq_sao<T_Q4_K, 1, AO_TG, AO_KS, P, HD, REP, QP, DQ>,               \
+             sizeof(AttnLds<HD, REP, QP, DQ>)}
+static const SaoShape SAO_SHAPES[] = {
+    LRS_SAO(128, 5, false, true, 5),  // 32B shape: 40 / 8 heads x 128, o 5120 wide
+    LRS_SAO(256, 6, true, false, 6),  // the hybrid's gated attention: 24 / 4 x 256, o 6144 wide
+    LRS_SAO(64, 2, false, true, 2),   LRS_SAO(64, 2, true, false, 2),  LRS_SAO(128, 5, false, true, 2),
+    LRS_SAO(128, 8, false, true, 2),  LRS_SAO(256, 8, false, true, 2), LRS_SAO(256, 6, true, false, 2),
+};
+#undef LRS_SAO
+
+static const SaoShape *pick_sao(uint32_t t, uint32_t n_in, uint32_t hd, uint32_t rep, bool qp, bool dq) {
+    if (t != T_Q4_K) return nullptr;
+    const int p = ao_units_per_wave(t, n_in);
+    for (const SaoShape &x : SAO_SHAPES)
+        if (x.hd == hd && x.rep == rep && x.qp == qp && x.dq == (dq && !qp) && x.p == p) return &x;
+    return nullptr;
+}
+
+bool attn_ao_supported(uint32_t t, uint32_t n_in, uint32_t rows, uint32_t head_dim, uint32_t splits,
+                       uint32_t n_head, uint32_t n_kv, bool qp, bool dq) {
+    if (n_kv == 0 || n_head % n_kv || !mq_ao_supported(t, n_in, rows, head_dim, splits, n_head)) return false;
+    const SaoShape *x = pick_sao(t, n_in, head_dim, n_head / n_kv, qp, dq);
+    return x && (qp || dq) && x->lds <= 160 * 1024;
+}
+
+hipError_t launch_attn_ao(const float *q, const _Float16 *kc, const _Float16 *vc, uint32_t n_kv,
+                          uint32_t ctx, const QkPrep *qp, bool dq, const MqArgs &in, const AoArgs &cin,
+                          uint32_t t, hipStream_t s) {
+    MqArgs a = in;
+    AoArgs c = cin;
+    const uint32_t n_head = c.n_prod;
+    if (a.n_seg != 1 || a.seg[0].w2 || !a.wflag || !a.werr || !c.part || !c.sflag || a.xin.q8 ||
+        n_head == 0 || a.nxb != pack_blocks(t, a.n_in) || !a.step)
+        return hipErrorInvalidValue;
+    if (!attn_ao_supported(t, a.n_in, a.seg[0].rows, c.head_dim, c.splits, n_head, n_kv, qp != nullptr, dq))
+        return hipErrorNotSupported;
+    const SaoShape *x = pick_sao(t, a.n_in, c.head_dim, n_head / n_kv, qp != nullptr, dq);
+    AttnArgs at = {};
+    at.q = q;
+    at.kc = kc;
+    at.vc = vc;
+    at.part = const_cast<float *>(c.part);
+    at.step = a.step;
+    at.n_head = n_head;
+    at.n_kv = n_kv;
+    at.ctx = ctx;
+    at.splits = c.splits;
+    at.scale = 1.0f / sqrtf((float)c.head_dim);
+    if (qp) {
+        if (!qp->qg || !qp->kb || !qp->vb || !qp->q_norm || !qp->k_norm || !qp->rope || !qp->kc || !qp->vc)
+            return hipErrorInvalidValue;
+        at.qp = *qp;
+    }
+    const uint32_t nsw = c.splits * n_kv;
+    a.n_seg0 = 1;
+    a.xsplit = 1;
+    a.xfull = 0;
+    a.seg[0].wg0 = nsw + n_head;
+    c.n_cons = a.seg[0].rows / 32;  // one 32-row block (two tiles) per workgroup
+    a.n_wait = n_head;
+    const size_t ml = ao_lds(a.nxb, c.head_dim, c.splits);
+    hipLaunchKernelGGL(x->fn, dim3(nsw + n_head + c.n_cons), dim3(64 * AO_TG * AO_KS), ml > x->lds ? ml : x->lds,
+                       s, a, c, at);
+    return hipGetLastError();
 }
 
 hipError_t launch_mq_ao(const MqArgs &in, const AoArgs &cin, uint32_t t, hipStream_t s) {

@@ -119,6 +119,10 @@ struct AoArgs {
     const float *part;   // [n_head][splits][head_dim + 4]
     const float *gate;   // gated attention: sigmoid gate at gate[h * gstride + d], or null
     uint32_t splits, head_dim, gstride, n_prod, n_cons;
+    // split, combine and o in one launch (k_mq_sao): split s of KV head g
+    // raises flag s of row h of sflag (64 words per query head h of the
+    // group); combine workgroup h waits for its row's live splits
+    uint32_t *sflag;
     // the producers raise no flags (a test of the wait's bound: the host sets
     // it together with a small MqArgs::wait_polls, so every wait runs out)
     uint32_t no_signal;

@@ -54,7 +54,7 @@ def ctx(lrs):
     c.close()
 
 
-SWITCHES = ("LRS_AO", "LRS_DN_GATES", "LRS_QKP", "LRS_ATTN_DQ", "LRS_ROPE_TABLE")
+SWITCHES = ("LRS_AO", "LRS_DN_GATES", "LRS_QKP", "LRS_ATTN_DQ", "LRS_ROPE_TABLE", "LRS_SAO")
 
 
 def _pair(monkeypatch, make, off=("LRS_AO",)):
@@ -144,6 +144,82 @@ def test_combine_in_o_launch_at_split_boundaries(lrs, orc, ctx, monkeypatch):
         last = modelgen.split_block_checks(cfg["n_head_kv"])[-1]  # a cache length
         assert last <= cfg["ctx"]
         toks = np.random.default_rng(41).integers(0, cfg["vocab"], last).tolist()
+        for pos in range(last):
+            a, b = fused.decode(toks[pos], pos), split.decode(toks[pos], pos)
+            assert np.array_equal(a, b), (pos, float(np.max(np.abs(a - b))))
+    finally:
+        fused.close()
+        split.close()
+
+
+def _pair_sao(monkeypatch, make):
+    """(split in the o launch, split launch then combine + o) models built
+    by make(): LRS_SAO=1, then LRS_SAO=0."""
+    for v in SWITCHES:
+        monkeypatch.delenv(v, raising=False)
+    monkeypatch.setenv("LRS_SAO", "1")
+    try:
+        fused = make()
+        monkeypatch.setenv("LRS_SAO", "0")
+        split = make()
+    finally:
+        monkeypatch.delenv("LRS_SAO")
+    return fused, split
+
+
+SAO_CASES = [
+    ("tiny-q4km", modelgen.TINY, modelgen.Q4_K_M, False),
+    ("gqa5-q4km", modelgen.GQA5, modelgen.Q4_K_M, False),
+    ("ksplit-rep8", modelgen.KSPLIT, modelgen.Q4_K_M, False),
+    ("c3-width", C3W, modelgen.Q4_K_M, False),
+    ("hd256-rep8", modelgen.HD256R8, modelgen.Q4_K_M, False),
+    ("hy-tiny", modelgen.HY_TINY, None, True),
+    ("hy-mid", modelgen.HY_MID, None, True),
+    ("c4-width", C4W, None, True),
+]
+
+
+@pytest.mark.parametrize("name,cfg,mix,hybrid", SAO_CASES, ids=[c[0] for c in SAO_CASES])
+def test_split_in_o_launch_is_bit_identical(lrs, orc, ctx, monkeypatch, name, cfg, mix, hybrid):
+    """The attention split, the combine and the o-projection in one launch
+    (k_mq_sao; the splits' partials reach the combine through agent-scope
+    stores and per-head flags) against the split launch then the combine + o
+    launch: the same arithmetic in the same order, so the logits are
+    bit-identical token by token and over a greedy chain.  The cases are
+    every head shape the launch is built for: 64 / 128 / 256 dims with 2, 5
+    and 8 query heads per KV head, the dense model's shared query split and
+    the hybrid's QK-norm + RoPE in the split, at the benchmark widths too."""
+    if hybrid:
+        w = modelgen.hybrid_host_model(orc, cfg, seed=61, mode=0, d_lo=1e-3, d_hi=1e-2)
+        make = lambda: modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
+    else:
+        w = modelgen.host_model(orc, cfg, seed=61, mix=mix, mode=0, d_lo=1e-3, d_hi=1e-2)
+        make = lambda: modelgen.gpu_model(lrs, ctx, cfg, w)
+    fused, split = _pair_sao(monkeypatch, make)
+    try:
+        toks = np.random.default_rng(67).integers(0, cfg["vocab"], 24).tolist()
+        for pos, t in enumerate(toks):
+            a, b = fused.decode(t, pos), split.decode(t, pos)
+            assert np.array_equal(a, b), (name, pos, float(np.max(np.abs(a - b))))
+        fused.reset()
+        split.reset()
+        assert fused.generate_greedy(toks[:8], 16).tolist() == split.generate_greedy(toks[:8], 16).tolist()
+    finally:
+        fused.close()
+        split.close()
+
+
+def test_split_in_o_launch_at_split_boundaries(lrs, orc, ctx, monkeypatch):
+    """C3W with the split in the o launch: every decode step up to the cache
+    length where the splits first own a third block, so the combine waits
+    for 1..32 live splits' flags, then for splits of two and three blocks."""
+    cfg = C3W
+    w = modelgen.host_model(orc, cfg, seed=71, mode=0, d_lo=1e-3, d_hi=1e-2)
+    fused, split = _pair_sao(monkeypatch, lambda: modelgen.gpu_model(lrs, ctx, cfg, w))
+    try:
+        last = modelgen.split_block_checks(cfg["n_head_kv"])[-1]
+        assert last <= cfg["ctx"]
+        toks = np.random.default_rng(73).integers(0, cfg["vocab"], last).tolist()
         for pos in range(last):
             a, b = fused.decode(toks[pos], pos), split.decode(toks[pos], pos)
             assert np.array_equal(a, b), (pos, float(np.max(np.abs(a - b))))
