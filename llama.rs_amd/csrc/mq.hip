@@ -650,7 +650,17 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
         copy_to_lds<CPOL_SC1>(reinterpret_cast<const uint8_t *>(a.xin.dig), lds, nxl * 96);
         copy_to_lds<CPOL_SC1>(reinterpret_cast<const uint8_t *>(a.xin.meta), lds + lp.meta, nxl * 16);
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (XF) {
+        // the pack was written to LDS from registers: wait for those stores
+        // only (lgkmcnt(0)), not for the weight loads in flight, so the
+        // matrix-core work starts on each unit as it arrives (the compiler
+        // waits for a unit's registers before their first use)
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+    } else {
+        // the pack arrives in LDS through global_load_lds, counted by vmcnt
+        // behind the weight loads issued before it
+        __builtin_amdgcn_s_waitcnt(0);
+    }
     __syncthreads();
     if (a.gss) {
         // the producer packed each group without its RMS factor; the pack is
@@ -691,51 +701,69 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, uint32_t si, uint8_t *l
 #pragma unroll
         for (int t = 0; t < TPW; t++) acc[c][t] = accm[c][t] = 0.f;
 
-    // steady state: every unit's successor P units ahead is in range, so the
-    // loads are unconditional and each register set is refilled in place
-    // right after its unit is consumed (P units stay in flight; a
-    // conditional refill would make the compiler copy the sets at the loop
-    // back-edge and wait for every load there)
-    uint32_t u0 = u_lo;
-    for (; u0 + 2 * P <= u_hi; u0 += P) {
+    // XF with every unit of the wavefront already in flight (the prefetch
+    // covered its range): no refills and no loop, so the wait before each
+    // unit's work is for that unit's registers alone, and the first units
+    // are consumed while the last are still arriving (through the loop below
+    // the compiler waits for every load before the first unit)
+    bool all_in_flight = false;
+    if constexpr (XF) all_in_flight = u_hi - u_lo <= (uint32_t)P;
+    if (all_in_flight) {
 #pragma unroll
-        for (int i = 0; i < P; i++) {
-            udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
+        for (int i = 0; i < P; i++)
+            if (u_lo + i < u_hi) {
+                udot<T, TPW>(wr[i], u_lo + i - ub, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
-            for (int c = 1; c < NC; c++)
-                udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+                for (int c = 1; c < NC; c++)
+                    udot<T, TPW>(wr[i], u_lo + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+            }
+    } else {
+        // steady state: every unit's successor P units ahead is in range, so the
+        // loads are unconditional and each register set is refilled in place
+        // right after its unit is consumed (P units stay in flight; a
+        // conditional refill would make the compiler copy the sets at the loop
+        // back-edge and wait for every load there)
+        uint32_t u0 = u_lo;
+        for (; u0 + 2 * P <= u_hi; u0 += P) {
 #pragma unroll
-            for (int t = 0; t < TPW; t++)
-                wload<T>(wr[i][t], wt[t] + (size_t)(u0 + P + i) * tchunk_bytes(T), lane);
-            // keep the refill here: the scheduler would otherwise sink every
-            // refill to the end of the loop body and drain the queue first
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    // tail: fewer than 2P units left, the last refills
+            for (int i = 0; i < P; i++) {
+                udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
-    for (int i = 0; i < P; i++) {
-        if (u0 + i < u_hi) {
-            udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
-#pragma unroll
-            for (int c = 1; c < NC; c++)
-                udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
-            if (u0 + P + i < u_hi) {
+                for (int c = 1; c < NC; c++)
+                    udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
 #pragma unroll
                 for (int t = 0; t < TPW; t++)
                     wload<T>(wr[i][t], wt[t] + (size_t)(u0 + P + i) * tchunk_bytes(T), lane);
+                // keep the refill here: the scheduler would otherwise sink every
+                // refill to the end of the loop body and drain the queue first
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-    }
-    u0 += P;
+        // tail: fewer than 2P units left, the last refills
 #pragma unroll
-    for (int i = 0; i < P; i++)
-        if (u0 + i < u_hi) {
-            udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
+        for (int i = 0; i < P; i++) {
+            if (u0 + i < u_hi) {
+                udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
 #pragma unroll
-            for (int c = 1; c < NC; c++)
-                udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+                for (int c = 1; c < NC; c++)
+                    udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+                if (u0 + P + i < u_hi) {
+#pragma unroll
+                    for (int t = 0; t < TPW; t++)
+                        wload<T>(wr[i][t], wt[t] + (size_t)(u0 + P + i) * tchunk_bytes(T), lane);
+                }
+            }
         }
+        u0 += P;
+#pragma unroll
+        for (int i = 0; i < P; i++)
+            if (u0 + i < u_hi) {
+                udot<T, TPW>(wr[i], u0 + i - ub, lds, lp, al, lane, acc[0], accm[0]);
+#pragma unroll
+                for (int c = 1; c < NC; c++)
+                    udot<T, TPW>(wr[i], u0 + i - ub, lds, lpc[c], alc[c], lane, acc[c], accm[c]);
+            }
+    }
 
     // row sums: lanes n, n+16, n+32, n+48 hold sub-block classes of row n
     // red layout: [NC][W][TPW][16] partials, then [W] sums of squares
