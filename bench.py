@@ -64,7 +64,7 @@ F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 8, 12, 13, 14
 TS = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 BS = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
 OP_NAMES = {"qkv": "fused RMSNorm + q/k/v matvec + bias + RoPE + f16 KV append",
-            "attn": "split-K GQA attention over the f16 KV cache (in the o launch by default: ~0)",
+            "attn": "split-K GQA attention over the f16 KV cache (run in the o launch by default, then 0 here)",
             "o": "attention split + combine + attn_output matvec + residual add (one launch)",
             "gateup": "fused RMSNorm + ffn_gate/ffn_up Q4_K matvec + SwiGLU",
             "down": "ffn_down Q6_K matvec + residual add",

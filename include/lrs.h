@@ -341,7 +341,10 @@ int lrs_generate_greedy(lrs_model *m, const uint32_t *prompt, uint32_t n_prompt,
  * LRS_OP_QKV / ATTN / O then time the attention layers' ops.  The
  * attention split kernel does the QK-norm + RoPE by default (then
  * LRS_OP_QK_PREP reports 0 us and 0 bytes and LRS_OP_ATTN includes it);
- * LRS_QKP=0 at model creation gives it a launch of its own. */
+ * LRS_QKP=0 at model creation gives it a launch of its own.  Likewise the
+ * o launch runs the attention split and combine by default: LRS_OP_ATTN
+ * then reports 0 us and 0 bytes and LRS_OP_O includes both (LRS_SAO=0 at
+ * model creation keeps the split launch). */
 #define LRS_OP_DN_PROJ 6u
 #define LRS_OP_DN_STEP 7u
 #define LRS_OP_DN_OUT 8u

@@ -417,6 +417,18 @@ bool sao_fused(const lrs_model *m, const DevLayer &L) {
                              c.n_head_kv, qkp_fused(m, L), m->attn_dq);
 }
 
+// algorithmic bytes of layer L's attention over a cache of L positions
+// (lrs_model_profile): the f16 K/V rows and q read, the partials' pack out;
+// with the QK-norm + RoPE in the split (which reads the query rows in place
+// of the q buffer), the new k / v rows, the two norm weights, the rotation
+// table and the f16 K/V append
+size_t attn_bytes(const lrs_model *m, const DevLayer &D, uint32_t len) {
+    const lrs_config &c = m->cfg;
+    const size_t qd4 = (size_t)c.n_head * c.head_dim * 4, kvd = (size_t)c.n_head_kv * c.head_dim;
+    return (size_t)len * kvd * 2 * sizeof(_Float16) + 2 * qd4 +
+           (qkp_fused(m, D) ? kvd * 8 + 3 * (size_t)c.head_dim * 4 + kvd * 4 : 0);
+}
+
 // QK-norm + RoPE inputs of layer L's split (qkp_fused)
 QkPrep qk_prep(const lrs_model *m, const DevLayer &L) {
     QkPrep qp = {};
@@ -1681,13 +1693,15 @@ int lrs_model_profile(lrs_model *m, uint32_t op, uint32_t iters, float *avg_us, 
             break;
         case LRS_OP_DN_OUT: b = wbytes(D.ssm_out) + VD4 + 2 * E4; break;
         case LRS_OP_ATTN:
-            // plus, with the QK-norm + RoPE in the split (which reads the
-            // query rows in place of the q buffer), the new k / v rows, the
-            // two norm weights, the rotation table and the f16 K/V append
-            b = (size_t)L * kvd * 2 * sizeof(_Float16) + 2 * qd4 +
-                (qkp_fused(m, D) ? (size_t)kvd * 8 + 3 * (size_t)c.head_dim * 4 + (size_t)kvd * 4 : 0);
+            // nothing of its own when the o launch runs the split
+            if (sao_fused(m, D)) {
+                *avg_us = 0.f;
+                if (bytes) *bytes = 0;
+                return LRS_OK;
+            }
+            b = attn_bytes(m, D, L);
             break;
-        case LRS_OP_O: b = wbytes(D.o) + qd4 + 2 * E4; break;
+        case LRS_OP_O: b = wbytes(D.o) + qd4 + 2 * E4 + (sao_fused(m, D) ? attn_bytes(m, D, L) : 0); break;
         case LRS_OP_GATEUP: b = wbytes(D.gate) + wbytes(D.up) + 2 * E4 + (size_t)c.n_ff * 4; break;
         case LRS_OP_DOWN: b = wbytes(D.down) + (size_t)c.n_ff * 4 + 2 * E4; break;
         case LRS_OP_FFN: b = wbytes(D.gate) + wbytes(D.up) + wbytes(D.down) + 3 * E4; break;

@@ -173,27 +173,34 @@ def test_hybrid_rejects_bad_shapes(lrs, orc, ctx):
 
 
 def test_hybrid_profile_ops(lrs, orc, ctx, monkeypatch):
-    """Every op times and counts bytes; the QK-norm + RoPE runs inside the
-    attention split by default (qk_prep then reports nothing of its own and
-    attn counts its bytes) and in a launch of its own with LRS_QKP=0."""
+    """Every op times and counts bytes.  With the split in a launch of its
+    own (LRS_SAO=0), the QK-norm + RoPE runs inside the attention split by
+    default (qk_prep then reports nothing of its own and attn counts its
+    bytes) and in a launch of its own with LRS_QKP=0.  By default the o
+    launch also runs the split: attn reports nothing of its own and o counts
+    both ops' bytes."""
     cfg = modelgen.HY_MID
     w = modelgen.hybrid_host_model(orc, cfg, seed=24)
-    attn_b = {}
-    for qkp in ("1", "0"):
+    attn_b, o_b = {}, {}
+    for qkp, sao in (("1", "0"), ("0", "0"), ("1", "1")):
         monkeypatch.setenv("LRS_QKP", qkp)
+        monkeypatch.setenv("LRS_SAO", sao)
         gm = modelgen.gpu_hybrid_model(lrs, ctx, cfg, w)
         try:
             gm.decode(1, 0)
             for op in ("dn_proj", "dn_step", "dn_out", "qkv", "qk_prep", "attn", "o", "gateup",
                        "down", "head"):
                 us, b = gm.profile(op, 4)
-                if op == "qk_prep" and qkp == "1":
-                    assert us == 0 and b == 0
+                if (op == "qk_prep" and qkp == "1") or (op == "attn" and sao == "1"):
+                    assert us == 0 and b == 0, (op, qkp, sao)
                 else:
-                    assert us > 0 and b > 0, (op, qkp)
+                    assert us > 0 and b > 0, (op, qkp, sao)
                 if op == "attn":
-                    attn_b[qkp] = b
+                    attn_b[qkp + sao] = b
+                if op == "o":
+                    o_b[qkp + sao] = b
         finally:
             gm.close()
     kvd = cfg["n_head_kv"] * cfg["head_dim"]
-    assert attn_b["1"] - attn_b["0"] == kvd * 12 + 3 * cfg["head_dim"] * 4
+    assert attn_b["10"] - attn_b["00"] == kvd * 12 + 3 * cfg["head_dim"] * 4
+    assert o_b["11"] == o_b["10"] + attn_b["10"]
