@@ -90,20 +90,6 @@ __device__ __forceinline__ void ld8(float (&v)[8], T *p) {
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-// QP: the hybrid's gated attention with its QK-norm + RoPE in the split (no
-// separate launch).  Lane group g < REP normalises and rotates query head
-// h0 + g from the projection's rows (a.qp.qg: query then gate, 2 HD per
-// head) and splits it into the f16 hi / lo pairs of the scores; lane group
-// REP, in the split that owns the current position's block, builds that
-// position's K / V row from a.qp.kb / vb (k normalised and rotated), rounded
-// to f16 as the cache holds it, and writes it to the cache (no other split
-// reads that position).  Both go through LDS to every lane group; the
-// current row replaces what its slot's load returned.  The rotation's
-// cosines / sines for the position come from a.qp.rope (written by the
-// token's first kernel), so every lane group does one row's work.  DQ (q
-// already normalised and rotated, the dense model): lane group g < REP
-// alone splits query head g into its f16 pairs and shares them through LDS,
-// as QP does; without either, every lane group splits every head itself.
 // LDS of one split workgroup
 template <int HD, int REP, bool QP, bool DQ>
 struct AttnLds {
@@ -125,7 +111,22 @@ __device__ __forceinline__ void st_part(float *p, float v) {
     else *p = v;
 }
 
-// split sp of KV head kh (threads 0..ATT_THREADS-1 of the workgroup): the
+// QP: the hybrid's gated attention with its QK-norm + RoPE in the split (no
+// separate launch).  Lane group g < REP normalises and rotates query head
+// h0 + g from the projection's rows (a.qp.qg: query then gate, 2 HD per
+// head) and splits it into the f16 hi / lo pairs of the scores; lane group
+// REP, in the split that owns the current position's block, builds that
+// position's K / V row from a.qp.kb / vb (k normalised and rotated), rounded
+// to f16 as the cache holds it, and writes it to the cache (no other split
+// reads that position).  Both go through LDS to every lane group; the
+// current row replaces what its slot's load returned.  The rotation's
+// cosines / sines for the position come from a.qp.rope (written by the
+// token's first kernel), so every lane group does one row's work.  DQ (q
+// already normalised and rotated, the dense model): lane group g < REP
+// alone splits query head g into its f16 pairs and shares them through LDS,
+// as QP does; without either, every lane group splits every head itself.
+//
+// Split sp of KV head kh (threads 0..ATT_THREADS-1 of the workgroup): the
 // REP query heads' partials of the split's positions; false (nothing
 // written) when the split holds no position
 template <int HD, int REP, bool QP, bool DQ, bool AG>
